@@ -1,0 +1,169 @@
+// Shared device helpers for the gfx950 kernels of the EdgeFM hot path.
+//
+// Activations and weights are stored as raw bf16 bit patterns (uint16_t) and all
+// arithmetic is fp32. Conversions are written out here so the rounding rule
+// (round-to-nearest-even, quiet NaN) is explicit and identical in every kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "edgefm_hip.h"
+
+namespace efm {
+
+constexpr int kWave = 64;
+
+typedef uint16_t bf16_t;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16; NaN inputs map to a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return (u >> 16) | 0x40u;
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float round_bf16(float f) {
+    return bf16_to_f32(f32_to_bf16(f));
+}
+
+// Low and high bf16 halves of a packed 32-bit word, as fp32.
+__device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+}
+
+// Unpack 8 bf16 (one 16-byte vector) into fp32.
+__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
+    f[0] = lo_f32(v.x); f[1] = hi_f32(v.x);
+    f[2] = lo_f32(v.y); f[3] = hi_f32(v.y);
+    f[4] = lo_f32(v.z); f[5] = hi_f32(v.z);
+    f[6] = lo_f32(v.w); f[7] = hi_f32(v.w);
+}
+
+__device__ __forceinline__ uint4 pack8(const float* f) {
+    uint4 v;
+    v.x = pack_bf16x2(f[0], f[1]);
+    v.y = pack_bf16x2(f[2], f[3]);
+    v.z = pack_bf16x2(f[4], f[5]);
+    v.w = pack_bf16x2(f[6], f[7]);
+    return v;
+}
+
+// 8-wide bf16 dot product accumulated in fp32.
+__device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float acc) {
+    acc = fmaf(lo_f32(a.x), lo_f32(b.x), acc);
+    acc = fmaf(hi_f32(a.x), hi_f32(b.x), acc);
+    acc = fmaf(lo_f32(a.y), lo_f32(b.y), acc);
+    acc = fmaf(hi_f32(a.y), hi_f32(b.y), acc);
+    acc = fmaf(lo_f32(a.z), lo_f32(b.z), acc);
+    acc = fmaf(hi_f32(a.z), hi_f32(b.z), acc);
+    acc = fmaf(lo_f32(a.w), lo_f32(b.w), acc);
+    acc = fmaf(hi_f32(a.w), hi_f32(b.w), acc);
+    return acc;
+}
+
+// Streaming 16-byte load for data read exactly once per step (weights, KV):
+// marked non-temporal so it does not evict the small activation working set.
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+    const uint4* q = reinterpret_cast<const uint4*>(p);
+    uint4 v;
+    v.x = __builtin_nontemporal_load(&q->x);
+    v.y = __builtin_nontemporal_load(&q->y);
+    v.z = __builtin_nontemporal_load(&q->z);
+    v.w = __builtin_nontemporal_load(&q->w);
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        v += __shfl_xor(v, off, kWave);
+    }
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        v = fmaxf(v, __shfl_xor(v, off, kWave));
+    }
+    return v;
+}
+
+// Sum over groups of `width` consecutive lanes (width a power of two <= 64).
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = width / 2; off >= 1; off >>= 1) {
+        v += __shfl_xor(v, off, kWave);
+    }
+    return v;
+}
+
+// (value, index) argmax with ties resolved to the lowest index
+// (src/layers/sampler.cu:21-26, src/layers/linear.cu:155-160).
+struct ArgMax {
+    float v;
+    int32_t i;
+};
+
+__device__ __forceinline__ ArgMax argmax_pick(ArgMax a, ArgMax b) {
+    if (a.v > b.v) return a;
+    if (b.v > a.v) return b;
+    return (a.i <= b.i) ? a : b;
+}
+
+__device__ __forceinline__ ArgMax wave_argmax(ArgMax a) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        ArgMax o;
+        o.v = __shfl_xor(a.v, off, kWave);
+        o.i = __shfl_xor(a.i, off, kWave);
+        a = argmax_pick(a, o);
+    }
+    return a;
+}
+
+// Block-wide fp32 sum for a 1-D block of `nthreads` (multiple of 64) threads.
+// `scratch` must hold nthreads/64 floats. Result is valid in every thread.
+template <int nthreads>
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+    constexpr int nw = nthreads / kWave;
+    v = wave_sum(v);
+    const int w = threadIdx.x / kWave;
+    const int l = threadIdx.x % kWave;
+    __syncthreads();
+    if (l == 0) scratch[w] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < nw; ++i) t += scratch[i];
+    return t;
+}
+
+// RoPE inverse frequency for pair index d of a head of size head_dim:
+// (1/rope_scale) / theta^(2d/head_dim), evaluated in double and rounded once to
+// fp32. The rotation angle is then fp32(pos) * inv_freq in fp32.
+// (src/operators/attention_op.cu:363-364, src/layers/attention.cu:57-60)
+__device__ __forceinline__ float rope_inv_freq(int d, int head_dim, float theta, float rcp_scale) {
+    const double e = (2.0 * (double)d) / (double)head_dim;
+    return (float)(exp(-e * log((double)theta)) * (double)rcp_scale);
+}
+
+}  // namespace efm
+
+// Error reporting shared by every entry point of the C ABI.
+namespace efm {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace efm

@@ -1,0 +1,205 @@
+/*
+ * edgefm_hip.h — C ABI of the MI355X (gfx950) kernels behind EdgeFM's operator layer.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t, launches
+ * asynchronously on that stream, never synchronises, never allocates device memory
+ * (scratch comes in through explicit workspace arguments) and is therefore safe to
+ * record into a HIP graph. Activations and weights are bf16 (raw 16-bit patterns),
+ * accumulation is fp32. Return value: EFM_OK or an EFM_ERR_* code; the message of the
+ * most recent failure on the calling thread is available from efm_last_error().
+ *
+ * Each declaration names the reference interface it replaces (file:line in the
+ * EdgeFM sources). The C++ operator adapters in edge-fm-x_amd/host map the status
+ * codes onto EdgeFM's exception types (ConfigurationError, InvalidRequestError,
+ * DeviceError).
+ */
+#ifndef EDGEFM_HIP_H_
+#define EDGEFM_HIP_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define EFM_OK 0
+#define EFM_ERR_INVALID_ARGUMENT 1 /* bad shape/pointer -> InvalidRequestError      */
+#define EFM_ERR_UNSUPPORTED 2      /* config outside the kernel -> ConfigurationError */
+#define EFM_ERR_DEVICE 3           /* HIP runtime failure -> DeviceError              */
+#define EFM_ERR_WORKSPACE 4        /* workspace missing or too small                 */
+
+/* DType ordinals, identical to edge_fm::DType (include/edge-fm/core.h:17-25). */
+#define EFM_DTYPE_F32 0
+#define EFM_DTYPE_F16 1
+#define EFM_DTYPE_BF16 2
+#define EFM_DTYPE_I32 3
+
+/* Positional encoding applied inside attention (src/operators/attention_op.h:15-18). */
+#define EFM_POS_NONE 0
+#define EFM_POS_ROPE_LLAMA 1
+
+/* Activation input layouts (src/operators/activation_op.h:18-21). */
+#define EFM_LAYOUT_GATE_UP 0
+#define EFM_LAYOUT_UP_GATE 1
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* efm_last_error(void);
+
+/* Library version string. */
+const char* efm_version(void);
+
+/* ------------------------------------------------------------------------------------
+ * Attention.  Mirrors edge_fm::AttentionOpContext (src/operators/attention_op.h:20-39).
+ * Strides are in elements; 0 means contiguous ([n, heads, head_dim] NHD layout).
+ * ---------------------------------------------------------------------------------- */
+typedef struct efm_attention_ctx {
+    uint32_t num_qo_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t q_stride_n;
+    uint32_t q_stride_h;
+    uint32_t k_stride_n;
+    uint32_t k_stride_h;
+    uint32_t kv_stride_n; /* V strides (the reference's kv_stride_*) */
+    uint32_t kv_stride_h;
+    float rope_scale;
+    float rope_theta;
+    uint32_t q_rope_pos_offset;
+    uint32_t k_rope_pos_offset;
+    int32_t dtype;        /* EFM_DTYPE_BF16 only */
+    int32_t pos_encoding; /* EFM_POS_NONE | EFM_POS_ROPE_LLAMA */
+    int32_t k_already_prerotated;
+} efm_attention_ctx;
+
+/* Bytes of workspace efm_attention_decode needs for caches of up to max_kv_len rows. */
+size_t efm_attention_decode_workspace_bytes(const efm_attention_ctx* ctx, uint32_t max_kv_len);
+
+/* Single-query GQA decode attention, split-KV with an in-kernel log-sum-exp merge.
+ * q [1, Hq, hd]; k, v [>= kv rows, Hkv, hd]; o [1, Hq, hd].
+ * The number of attended rows is *d_kv_len when d_kv_len != NULL (device-resident,
+ * graph-stable; then max_kv_len bounds it), else kv_len. With EFM_POS_ROPE_LLAMA, q is
+ * rotated at position (L - 1 + q_rope_pos_offset) and key j at (j + k_rope_pos_offset)
+ * on read; the cache holds un-rotated K. sm_scale = 1/sqrt(hd).
+ * Replaces AttentionOp::forward_decode (src/operators/attention_op.h:53-61,
+ * FlashInferAttentionOp::forward_decode, src/operators/attention_op.cu:1565-1604). */
+int efm_attention_decode(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v,
+                         void* o, uint32_t kv_len, const uint32_t* d_kv_len, uint32_t max_kv_len,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------
+ * RMSNorm (src/operators/norm_op.h:14-55, FlashInfer norm::RMSNorm / FusedAddRMSNorm
+ * called at src/operators/norm_op.cu:33-90).
+ * ---------------------------------------------------------------------------------- */
+/* out[b,:] = bf16(in * rsqrt(mean(in^2) + eps) * w). */
+int efm_rms_norm(uint32_t batch, uint32_t hidden, float eps, const void* input, const void* weight,
+                 void* output, hipStream_t stream);
+
+/* s = inout + residual (fp32); residual <- bf16(s); inout <- bf16(s * rsqrt(mean(s^2)+eps) * w). */
+int efm_fused_add_rms_norm(uint32_t batch, uint32_t hidden, float eps, void* inout, void* residual,
+                           const void* weight, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------
+ * SiLU-and-mul (src/operators/activation_op.h:23-42, act_and_mul_kernel_layout at
+ * src/operators/activation_op.cu:36-76). input [batch, 2*hidden] in the given layout,
+ * out[b, i] = bf16(silu(gate) * up), silu(x) = x / (1 + exp(-x)).
+ * ---------------------------------------------------------------------------------- */
+int efm_act_and_mul(int64_t batch, int64_t hidden, int32_t layout, const void* input, void* output,
+                    hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------
+ * Linear: y[m, out] = x[m, in] . W[out, in]^T (+ bias[out]), fp32 accumulate,
+ * output bf16 (EFM_DTYPE_BF16) or fp32 (EFM_DTYPE_F32, the LM-head logits).
+ * m == 1 runs the bandwidth-bound GEMV, m > 1 the MFMA GEMM.
+ * Replaces LinearLayer::LinearImpl::forward (src/layers/linear.h:131-153) backed by
+ * LinearCublasLtImpl (src/operators/linear_impl.cu:315-480).
+ * ---------------------------------------------------------------------------------- */
+int efm_linear(int64_t m, int64_t in_features, int64_t out_features, const void* x, const void* w,
+               const void* bias, void* y, int32_t out_dtype, hipStream_t stream);
+
+/* Fused gate/up projection + SwiGLU: W is the fused [up; gate] matrix [2*inter, hidden]
+ * (src/layers/linear.cu:1923-1943); out[m, i] = bf16(silu(bf16(g_i)) * bf16(u_i)).
+ * Replaces FusedGateUpActivationOp::run / TrtLlmDecodeSwigluOp
+ * (src/operators/fused_gate_up_activation_op.h:14-61, .cu:675-782) and the two-stage
+ * gate_up GEMM + act_and_mul fallback (src/layers/gated_mlp.cu:19-67). */
+int efm_fused_gate_up_swiglu(int64_t m, int64_t hidden, int64_t inter, const void* x,
+                             const void* w_up_gate, void* out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------
+ * LM head with fused greedy top-1 (src/layers/linear.cu:140-276, 2288-2369):
+ * token_out[0] = argmax_v (x . W[v,:]) with ties to the lowest id.
+ * ---------------------------------------------------------------------------------- */
+size_t efm_lm_head_top1_workspace_bytes(int64_t vocab);
+int efm_lm_head_top1(int64_t hidden, int64_t vocab, const void* x, const void* w, int32_t* token_out,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------
+ * Greedy sampler (src/layers/sampler.cu:146-249): out[r] = argmax(logits[r, :]),
+ * ties to the lowest index. logits fp32 [rows, vocab].
+ * ---------------------------------------------------------------------------------- */
+size_t efm_sampler_greedy_workspace_bytes(int64_t rows, int64_t vocab);
+int efm_sampler_greedy(int64_t rows, int64_t vocab, const float* logits, int32_t* out, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------
+ * Embedding lookup (src/layers/embed_head.cu:23-164). out[t,:] = table[ids[t],:];
+ * ids in [embed_token_id, embed_token_id + n_custom) take custom_embeddings rows when
+ * custom_embeddings != NULL and embed_token_id >= 0; ids outside the vocabulary give
+ * zero rows.
+ * ---------------------------------------------------------------------------------- */
+int efm_embedding_lookup(int64_t n_tokens, int64_t hidden, int64_t vocab, const int32_t* ids,
+                         const void* table, const void* custom_embeddings, int64_t n_custom,
+                         int32_t embed_token_id, void* out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------
+ * Decode runtime kernels (src/engine/tasks/token_generation/cuda/kernels/
+ * decode_runtime_kernels.h:9-56).
+ * ---------------------------------------------------------------------------------- */
+/* Copy one K row and one V row into cache slot (*d_kv_len - 1); no-op when *d_kv_len == 0. */
+int efm_copy_decode_kv_cache_slots(const void* k_src, const void* v_src, void* k_cache, void* v_cache,
+                                   int32_t k_elems, int32_t v_elems, const uint32_t* d_kv_len,
+                                   hipStream_t stream);
+/* response_token[0] = sampled_token[0] (if both non-NULL); *d_kv_len += 1 (if non-NULL). */
+int efm_finalize_decode_token(const int32_t* sampled_token, int32_t* response_token, uint32_t* d_kv_len,
+                              hipStream_t stream);
+/* values[0..2] += 1 (decode M-RoPE positions). */
+int efm_increment_int32_triplet(int32_t* values, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------
+ * Fused decode-step kernels. Each one replaces a short sequence of the reference's
+ * per-token operator calls inside Qwen2_5::forward_impl (src/models/qwen2_5/
+ * qwen2_5.cpp:552-930) with a single launch; their results equal the unfused
+ * sequence under the same rounding points.
+ * ---------------------------------------------------------------------------------- */
+
+/* Input norm + QKV projection + bias + KV-slot write (qwen2_5.cpp:564-597, 624-638).
+ * If residual_in == NULL (layer 0): s = h; else s = h + residual_in (fp32).
+ * residual_out <- bf16(s); x = bf16(s * rsqrt(mean(s^2)+eps) * norm_w);
+ * qkv = x . W_qkv^T + b (W_qkv = [Q; K; V] rows [q_dim + 2*kv_dim, hidden]);
+ * q_out <- bf16(qkv[0:q_dim]); K/V rows -> cache slot (*d_kv_len - 1), un-rotated.
+ * residual_out must not alias h or residual_in. */
+int efm_decode_norm_qkv(int32_t hidden, int32_t q_dim, int32_t kv_dim, float eps, const void* h,
+                        const void* residual_in, void* residual_out, const void* norm_w,
+                        const void* w_qkv, const void* b_qkv, void* q_out, void* k_cache,
+                        void* v_cache, const uint32_t* d_kv_len, hipStream_t stream);
+
+/* Post-attention fused add-norm + gate/up projection + SwiGLU (qwen2_5.cpp:849-875):
+ * s = a + residual_in; residual_out <- bf16(s); x = bf16(s * rsqrt(...) * norm_w);
+ * out[i] = bf16(silu(bf16(x.W_gate[i])) * bf16(x.W_up[i])) with W = [up; gate]. */
+int efm_decode_norm_gate_up_swiglu(int32_t hidden, int32_t inter, float eps, const void* a,
+                                   const void* residual_in, void* residual_out, const void* norm_w,
+                                   const void* w_up_gate, void* out, hipStream_t stream);
+
+/* Final fused add-norm + LM head + greedy top-1 (qwen2_5.cpp:883-922). */
+int efm_decode_norm_lm_head_top1(int32_t hidden, int64_t vocab, float eps, const void* h,
+                                 const void* residual_in, const void* norm_w, const void* w_lm,
+                                 int32_t* token_out, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EDGEFM_HIP_H_ */

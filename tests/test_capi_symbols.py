@@ -1,0 +1,48 @@
+"""CPU test: the C-ABI library loads and exports every entry point include/*.h
+declares, and the ctypes binding declares exactly the same set (no compute calls)."""
+import ctypes
+import glob
+import os
+import re
+
+import efm_capi as C
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(efm_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(C.LIB_PATH)
+    declared = _declared()
+    assert len(declared) >= 20
+    missing = [n for n in sorted(declared) if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_ctypes_binding_covers_header():
+    assert set(C.SIGNATURES) == _declared()
+
+
+def test_version_and_error_strings():
+    lib = C.load()
+    assert lib.efm_version().decode().startswith("edgefm-hip")
+    assert isinstance(lib.efm_last_error(), bytes)
+
+
+def test_host_side_validation_without_gpu():
+    """Argument checks run on the host before any launch, so they work without a GPU."""
+    lib = C.load()
+    ctx = C.make_attention_ctx(10, 2, 128)  # GQA group 5: unsupported (attention_op.cu:41)
+    rc = lib.efm_attention_decode(ctx, 1, 1, 1, 1, 1, None, 0, 1, 1 << 20, None)
+    assert rc == C.EFM_ERR_UNSUPPORTED and b"group size" in lib.efm_last_error()
+    rc = lib.efm_linear(1, 1530, 8, 16, 16, None, 16, C.EFM_DTYPE_BF16, None)
+    assert rc == C.EFM_ERR_UNSUPPORTED
+    assert lib.efm_attention_decode_workspace_bytes(C.make_attention_ctx(12, 2, 128), 4096) > 0

@@ -1,0 +1,375 @@
+"""GPU parity tests of every C-ABI operator against the CPU oracle on identical seeded
+inputs (ctypes through include/edgefm_hip.h). Shapes are the BASELINE head / layer
+shapes: Qwen2.5-0.5B (14/2, hd 64), 1.5B (12/2, hd 128), 3B (16/2), 7B (28/4).
+Mirrors tests/operators/test_attention_decode.py, test_norm_sampler.py,
+test_decode_linear.py and test_fused_gate_up_activation.py of the reference."""
+import math
+
+import pytest
+import torch
+
+import efm_capi as C
+from oracle import efm_oracle as O
+from _util import assert_close_bf16, ptr, stream
+
+pytestmark = pytest.mark.gpu
+
+HEAD_CASES = [
+    pytest.param(14, 2, 64, id="0p5b"),
+    pytest.param(12, 2, 128, id="1p5b"),
+    pytest.param(16, 2, 128, id="3b"),
+    pytest.param(28, 4, 128, id="7b"),
+]
+
+
+def _decode(ctx, q, k, v, kv_len, d_kv_len=None, max_kv_len=0):
+    ws_bytes = C.load().efm_attention_decode_workspace_bytes(ctx, max_kv_len if d_kv_len is not None else kv_len)
+    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=q.device)
+    o = torch.empty_like(q)
+    C.call("efm_attention_decode", ctx, ptr(q), ptr(k), ptr(v), ptr(o), kv_len, ptr(d_kv_len), max_kv_len,
+           ptr(ws), ws.numel(), stream())
+    torch.cuda.synchronize()
+    return o, ws
+
+
+@pytest.mark.parametrize("hq,hkv,hd", HEAD_CASES)
+@pytest.mark.parametrize("kv_len", [1, 7, 33, 512, 1024, 2048])
+def test_attention_decode_matches_oracle(gpu, hq, hkv, hd, kv_len):
+    torch.manual_seed(0)
+    q = torch.randn(1, hq, hd, dtype=torch.bfloat16)
+    k = torch.randn(kv_len, hkv, hd, dtype=torch.bfloat16)
+    v = torch.randn(kv_len, hkv, hd, dtype=torch.bfloat16)
+    ref = O.attention_decode(q, k, v, kv_len, O.AttnCtx(hq, hkv, hd))
+    ctx = C.make_attention_ctx(hq, hkv, hd)
+    out, _ = _decode(ctx, q.to(gpu), k.to(gpu), v.to(gpu), kv_len)
+    assert_close_bf16(out, ref, what=f"decode hq={hq} hkv={hkv} hd={hd} kv={kv_len}")
+
+
+@pytest.mark.parametrize("hq,hkv,hd", [pytest.param(28, 4, 128, id="7b")])
+def test_attention_decode_long_context(gpu, hq, hkv, hd):
+    torch.manual_seed(1)
+    kv_len = 16385
+    q = torch.randn(1, hq, hd, dtype=torch.bfloat16)
+    k = torch.randn(kv_len, hkv, hd, dtype=torch.bfloat16)
+    v = torch.randn(kv_len, hkv, hd, dtype=torch.bfloat16)
+    ref = O.attention_decode(q, k, v, kv_len, O.AttnCtx(hq, hkv, hd))
+    out, _ = _decode(C.make_attention_ctx(hq, hkv, hd), q.to(gpu), k.to(gpu), v.to(gpu), kv_len)
+    assert_close_bf16(out, ref, what="decode 16k")
+
+
+@pytest.mark.parametrize("hq,hkv,hd", HEAD_CASES)
+@pytest.mark.parametrize("kv_len", [512, 1024, 2048])
+def test_attention_decode_graph_like_path_matches_plain(gpu, hq, hkv, hd, kv_len):
+    """d_kv_len + max_kv_len over a larger cache == plain call on the first kv_len rows
+    (tests/operators/test_attention_decode.py:155-179). Called twice to check that the
+    in-workspace merge counters reset themselves."""
+    torch.manual_seed(0)
+    max_kv = 2048
+    q = torch.randn(1, hq, hd, dtype=torch.bfloat16, device=gpu)
+    k = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    v = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    ctx = C.make_attention_ctx(hq, hkv, hd)
+    d_len = torch.tensor([kv_len], dtype=torch.int32, device=gpu)
+    ws_bytes = C.load().efm_attention_decode_workspace_bytes(ctx, max_kv)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=gpu)
+    outs = []
+    for _ in range(2):
+        o = torch.empty_like(q)
+        C.call("efm_attention_decode", ctx, ptr(q), ptr(k), ptr(v), ptr(o), 0, ptr(d_len), max_kv, ptr(ws),
+               ws.numel(), stream())
+        torch.cuda.synchronize()
+        outs.append(o)
+    plain, _ = _decode(ctx, q, k[:kv_len].contiguous(), v[:kv_len].contiguous(), kv_len)
+    assert_close_bf16(outs[0], plain)
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_attention_decode_no_rope_and_prerotated(gpu):
+    """pos_encoding NONE equals plain softmax attention; k_already_prerotated with
+    pre-rotated K equals RoPE-on-read (tests/operators/test_attention_prefill.py:118-164)."""
+    torch.manual_seed(3)
+    hq, hkv, hd, L = 12, 2, 128, 300
+    q = torch.randn(1, hq, hd, dtype=torch.bfloat16)
+    k = torch.randn(L, hkv, hd, dtype=torch.bfloat16)
+    v = torch.randn(L, hkv, hd, dtype=torch.bfloat16)
+    ref = O.attention_decode(q, k, v, L, O.AttnCtx(hq, hkv, hd, rope=False))
+    out, _ = _decode(C.make_attention_ctx(hq, hkv, hd, rope=False), q.to(gpu), k.to(gpu), v.to(gpu), L)
+    assert_close_bf16(out, ref, what="no-rope")
+    k_rot = O.rope_llama(k, torch.arange(L), 1.0e6).to(torch.bfloat16)
+    rot_ref = O.attention_decode(q, k, v, L, O.AttnCtx(hq, hkv, hd))
+    out2, _ = _decode(C.make_attention_ctx(hq, hkv, hd, k_already_prerotated=True), q.to(gpu), k_rot.to(gpu),
+                      v.to(gpu), L)
+    assert_close_bf16(out2, rot_ref, what="prerotated")
+
+
+def test_attention_decode_strided_views(gpu):
+    """q read from a fused QKV row and K/V from strided views equals contiguous inputs
+    (tests/operators/test_attention_prefill.py:167-300)."""
+    torch.manual_seed(4)
+    hq, hkv, hd, L = 12, 2, 128, 257
+    qkv = torch.randn(1, (hq + 2 * hkv) * hd, dtype=torch.bfloat16, device=gpu)
+    kv = torch.randn(L, 2, hkv, hd, dtype=torch.bfloat16, device=gpu)  # interleaved K/V rows
+    q = qkv[:, : hq * hd].reshape(1, hq, hd)
+    k = kv[:, 0]
+    v = kv[:, 1]
+    ctx = C.make_attention_ctx(hq, hkv, hd, q_stride_n=(hq + 2 * hkv) * hd, q_stride_h=hd,
+                               k_stride_n=2 * hkv * hd, k_stride_h=hd, kv_stride_n=2 * hkv * hd, kv_stride_h=hd)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, L), dtype=torch.uint8, device=gpu)
+    o = torch.empty(1, hq, hd, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_attention_decode", ctx, qkv.data_ptr(), kv.data_ptr(), kv[:, 1].data_ptr(), ptr(o), L, None, 0,
+           ptr(ws), ws.numel(), stream())
+    torch.cuda.synchronize()
+    ref, _ = _decode(C.make_attention_ctx(hq, hkv, hd), q.contiguous(), k.contiguous(), v.contiguous(), L)
+    assert_close_bf16(o, ref)
+
+
+def test_attention_decode_rejects_unsupported(gpu):
+    ctx = C.make_attention_ctx(10, 2, 128)  # group size 5
+    with pytest.raises(C.EfmError) as e:
+        C.call("efm_attention_decode", ctx, 1, 1, 1, 1, 1, None, 0, 1, 1 << 20, stream())
+    assert e.value.code == C.EFM_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("batch,hidden", [(1, 896), (1, 1536), (4, 2048), (7, 3584), (512, 1536)])
+def test_rms_norm_and_fused_add(gpu, batch, hidden):
+    torch.manual_seed(0)
+    x = torch.randn(batch, hidden, dtype=torch.bfloat16)
+    r = torch.randn(batch, hidden, dtype=torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(hidden)).to(torch.bfloat16)
+    eps = 1e-6
+    xg, rg, wg = x.to(gpu), r.to(gpu), w.to(gpu)
+    out = torch.empty_like(xg)
+    C.call("efm_rms_norm", batch, hidden, eps, ptr(xg), ptr(wg), ptr(out), stream())
+    torch.cuda.synchronize()
+    assert_close_bf16(out, O.rms_norm(x, w, eps), what="rms_norm")
+    C.call("efm_fused_add_rms_norm", batch, hidden, eps, ptr(xg), ptr(rg), ptr(wg), stream())
+    torch.cuda.synchronize()
+    ref_out, ref_res = O.fused_add_rms_norm(x, r, w, eps)
+    assert torch.equal(rg.cpu(), ref_res), "residual must be bf16(x + r) exactly"
+    assert_close_bf16(xg, ref_out, what="fused_add_rms_norm")
+
+
+@pytest.mark.parametrize("layout", [C.EFM_LAYOUT_UP_GATE, C.EFM_LAYOUT_GATE_UP])
+@pytest.mark.parametrize("batch,inter", [(1, 4864), (1, 8960), (5, 11008)])
+def test_act_and_mul(gpu, layout, batch, inter):
+    torch.manual_seed(0)
+    x = torch.randn(batch, 2 * inter, dtype=torch.bfloat16) * 3
+    out = torch.empty(batch, inter, dtype=torch.bfloat16, device=gpu)
+    xg = x.to(gpu)
+    C.call("efm_act_and_mul", batch, inter, layout, ptr(xg), ptr(out), stream())
+    torch.cuda.synchronize()
+    ref = O.act_and_mul(x, up_first=(layout == C.EFM_LAYOUT_UP_GATE))
+    # tests/operators/test_fused_gate_up_activation.py:75-79 (2e-2 / 6.25e-2)
+    assert_close_bf16(out, ref, rtol=2e-2, atol=6.25e-2)
+
+
+LINEAR_CASES = [
+    pytest.param(1536, 2048, True, id="1p5b_qkv"),
+    pytest.param(1536, 1536, False, id="1p5b_o"),
+    pytest.param(8960, 1536, False, id="1p5b_down"),
+    pytest.param(896, 1152, True, id="0p5b_qkv"),
+    pytest.param(4864, 896, False, id="0p5b_down"),
+    pytest.param(18944, 3584, False, id="7b_down"),
+    pytest.param(3584, 4608, True, id="7b_qkv"),
+]
+
+
+@pytest.mark.parametrize("k,n,bias", LINEAR_CASES)
+@pytest.mark.parametrize("m", [1, 3, 64, 512])
+def test_linear(gpu, k, n, bias, m):
+    torch.manual_seed(0)
+    x = torch.randn(m, k, dtype=torch.bfloat16)
+    w = (torch.randn(n, k) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(n) * 0.02).to(torch.bfloat16) if bias else None
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    xg, wg, bg = x.to(gpu), w.to(gpu), (b.to(gpu) if bias else None)
+    C.call("efm_linear", m, k, n, ptr(xg), ptr(wg), ptr(bg), ptr(y), C.EFM_DTYPE_BF16, stream())
+    torch.cuda.synchronize()
+    assert_close_bf16(y, O.linear(x, w, b), what=f"linear m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 17])
+def test_linear_fp32_logits(gpu, m):
+    torch.manual_seed(0)
+    k, n = 1536, 151936
+    x = torch.randn(m, k, dtype=torch.bfloat16)
+    w = (torch.randn(n, k) * 0.02).to(torch.bfloat16)
+    y = torch.empty(m, n, dtype=torch.float32, device=gpu)
+    xg, wg = x.to(gpu), w.to(gpu)
+    C.call("efm_linear", m, k, n, ptr(xg), ptr(wg), None, ptr(y), C.EFM_DTYPE_F32, stream())
+    torch.cuda.synchronize()
+    torch.testing.assert_close(y.cpu(), O.linear(x, w, out_f32=True), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("hidden,inter", [(896, 4864), (1536, 8960), (3584, 18944)])
+@pytest.mark.parametrize("m", [1, 5, 300])
+def test_fused_gate_up_swiglu(gpu, hidden, inter, m):
+    torch.manual_seed(0)
+    x = torch.randn(m, hidden, dtype=torch.bfloat16)
+    w = (torch.randn(2 * inter, hidden) * 0.05).to(torch.bfloat16)
+    out = torch.empty(m, inter, dtype=torch.bfloat16, device=gpu)
+    xg, wg = x.to(gpu), w.to(gpu)
+    C.call("efm_fused_gate_up_swiglu", m, hidden, inter, ptr(xg), ptr(wg), ptr(out), stream())
+    torch.cuda.synchronize()
+    assert_close_bf16(out, O.gate_up_swiglu(x, w), rtol=2e-2, atol=6.25e-2)
+
+
+def _top1_ref_ok(logits: torch.Tensor, tok: int) -> bool:
+    """GPU top-1 equals the oracle argmax, or the two differ by less than the fp32
+    accumulation-order noise (near tie)."""
+    ref = int(O.argmax_lowest(logits.unsqueeze(0))[0])
+    if tok == ref:
+        return True
+    return abs(float(logits[tok]) - float(logits[ref])) < 1e-4 * max(1.0, abs(float(logits[ref])))
+
+
+@pytest.mark.parametrize("hidden,vocab", [(896, 151936), (1536, 151936), (3584, 152064)])
+def test_lm_head_top1(gpu, hidden, vocab):
+    torch.manual_seed(0)
+    x = torch.randn(1, hidden, dtype=torch.bfloat16)
+    w = (torch.randn(vocab, hidden) * 0.02).to(torch.bfloat16)
+    ws = torch.zeros(C.load().efm_lm_head_top1_workspace_bytes(vocab), dtype=torch.uint8, device=gpu)
+    tok = torch.full((1,), -1, dtype=torch.int32, device=gpu)
+    xg, wg = x.to(gpu), w.to(gpu)
+    for _ in range(3):  # counter must reset itself between calls
+        C.call("efm_lm_head_top1", hidden, vocab, ptr(xg), ptr(wg), ptr(tok), ptr(ws), ws.numel(), stream())
+        torch.cuda.synchronize()
+        assert _top1_ref_ok(O.linear(x, w, out_f32=True)[0], int(tok.item()))
+
+
+def test_lm_head_top1_ties_pick_lowest_index(gpu):
+    """Duplicate the winning row at a higher and a lower index: the lowest wins
+    (src/layers/linear.cu:155-160)."""
+    torch.manual_seed(5)
+    hidden, vocab = 1536, 151936
+    x = torch.randn(1, hidden, dtype=torch.bfloat16)
+    w = (torch.randn(vocab, hidden) * 0.02).to(torch.bfloat16)
+    w[99_000] = x[0] * 0.1
+    w[150_000] = w[99_000]
+    w[1234] = w[99_000]
+    ws = torch.zeros(C.load().efm_lm_head_top1_workspace_bytes(vocab), dtype=torch.uint8, device=gpu)
+    tok = torch.full((1,), -1, dtype=torch.int32, device=gpu)
+    xg, wg = x.to(gpu), w.to(gpu)
+    C.call("efm_lm_head_top1", hidden, vocab, ptr(xg), ptr(wg), ptr(tok), ptr(ws), ws.numel(), stream())
+    torch.cuda.synchronize()
+    assert int(tok.item()) == 1234
+
+
+def test_sampler_greedy_ties(gpu):
+    torch.manual_seed(0)
+    rows, vocab = 4, 151936
+    logits = torch.randn(rows, vocab)
+    logits[0, 17] = logits[0, 9000] = 50.0
+    logits[1, vocab - 1] = 60.0
+    logits[2, :] = 1.0
+    logits[3, 123456] = 7.0
+    logits[3, 123455] = 7.0
+    ws = torch.zeros(C.load().efm_sampler_greedy_workspace_bytes(rows, vocab), dtype=torch.uint8, device=gpu)
+    out = torch.empty(rows, dtype=torch.int32, device=gpu)
+    lg = logits.to(gpu)
+    C.call("efm_sampler_greedy", rows, vocab, ptr(lg), ptr(out), ptr(ws), ws.numel(), stream())
+    torch.cuda.synchronize()
+    assert out.cpu().tolist() == O.argmax_lowest(logits).tolist() == [17, vocab - 1, 0, 123455]
+
+
+def test_embedding_lookup_with_insertion(gpu):
+    torch.manual_seed(0)
+    V, H = 1000, 1536
+    table = torch.randn(V, H).to(torch.bfloat16)
+    custom = torch.randn(5, H).to(torch.bfloat16)
+    ids = torch.tensor([3, 999, -1, 1000, 700, 701, 704, 705, 0], dtype=torch.int32)
+    out = torch.empty(ids.numel(), H, dtype=torch.bfloat16, device=gpu)
+    idg, tg, cg = ids.to(gpu), table.to(gpu), custom.to(gpu)
+    C.call("efm_embedding_lookup", ids.numel(), H, V, ptr(idg), ptr(tg), ptr(cg), 5, 700, ptr(out), stream())
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), O.embedding(ids, table, custom, 700))
+
+
+def test_decode_runtime_kernels(gpu):
+    kdim, vdim, rows = 256, 256, 10
+    kc = torch.zeros(rows, kdim, dtype=torch.bfloat16, device=gpu)
+    vc = torch.zeros(rows, vdim, dtype=torch.bfloat16, device=gpu)
+    ks = torch.randn(kdim).to(torch.bfloat16).to(gpu)
+    vs = torch.randn(vdim).to(torch.bfloat16).to(gpu)
+    d_len = torch.tensor([4], dtype=torch.int32, device=gpu)
+    C.call("efm_copy_decode_kv_cache_slots", ptr(ks), ptr(vs), ptr(kc), ptr(vc), kdim, vdim, ptr(d_len), stream())
+    sampled = torch.tensor([42], dtype=torch.int32, device=gpu)
+    resp = torch.zeros(3, dtype=torch.int32, device=gpu)
+    C.call("efm_finalize_decode_token", ptr(sampled), resp[1:].data_ptr(), ptr(d_len), stream())
+    trip = torch.tensor([5, 6, 7], dtype=torch.int32, device=gpu)
+    C.call("efm_increment_int32_triplet", ptr(trip), stream())
+    torch.cuda.synchronize()
+    assert torch.equal(kc[3], ks) and torch.equal(vc[3], vs)
+    assert kc[:3].abs().sum() == 0 and kc[4:].abs().sum() == 0
+    assert resp.cpu().tolist() == [0, 42, 0] and int(d_len.item()) == 5
+    assert trip.cpu().tolist() == [6, 7, 8]
+
+
+@pytest.mark.parametrize("hidden,hq,hkv,hd", [(1536, 12, 2, 128), (896, 14, 2, 64), (3584, 28, 4, 128)])
+@pytest.mark.parametrize("layer0", [True, False])
+def test_decode_norm_qkv_matches_unfused(gpu, hidden, hq, hkv, hd, layer0):
+    torch.manual_seed(0)
+    eps = 1e-6
+    qd, kvd = hq * hd, hkv * hd
+    h = torch.randn(1, hidden, dtype=torch.bfloat16)
+    r = torch.randn(1, hidden, dtype=torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(hidden)).to(torch.bfloat16)
+    W = (torch.randn(qd + 2 * kvd, hidden) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(qd + 2 * kvd) * 0.02).to(torch.bfloat16)
+    rows = 20
+    kc = torch.zeros(rows, kvd, dtype=torch.bfloat16, device=gpu)
+    vc = torch.zeros(rows, kvd, dtype=torch.bfloat16, device=gpu)
+    d_len = torch.tensor([13], dtype=torch.int32, device=gpu)
+    q_out = torch.empty(1, qd, dtype=torch.bfloat16, device=gpu)
+    r_out = torch.empty(1, hidden, dtype=torch.bfloat16, device=gpu)
+    hg, rg, nwg, Wg, bg = h.to(gpu), r.to(gpu), nw.to(gpu), W.to(gpu), b.to(gpu)
+    C.call("efm_decode_norm_qkv", hidden, qd, kvd, eps, ptr(hg), None if layer0 else ptr(rg), ptr(r_out), ptr(nwg),
+           ptr(Wg), ptr(bg), ptr(q_out), ptr(kc), ptr(vc), ptr(d_len), stream())
+    torch.cuda.synchronize()
+    if layer0:
+        n, res = O.rms_norm(h, nw, eps), h
+    else:
+        n, res = O.fused_add_rms_norm(h, r, nw, eps)
+    qkv = O.linear(n, W, b)
+    assert torch.equal(r_out.cpu(), res)
+    assert_close_bf16(q_out, qkv[:, :qd], what="q")
+    assert_close_bf16(kc[12:13], qkv[:, qd:qd + kvd], what="k slot")
+    assert_close_bf16(vc[12:13], qkv[:, qd + kvd:], what="v slot")
+    assert kc[:12].abs().sum() == 0 and kc[13:].abs().sum() == 0
+
+
+@pytest.mark.parametrize("hidden,inter", [(1536, 8960), (896, 4864), (3584, 18944)])
+def test_decode_norm_gate_up_swiglu_matches_unfused(gpu, hidden, inter):
+    torch.manual_seed(0)
+    eps = 1e-6
+    a = torch.randn(1, hidden, dtype=torch.bfloat16)
+    r = torch.randn(1, hidden, dtype=torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(hidden)).to(torch.bfloat16)
+    W = (torch.randn(2 * inter, hidden) * 0.05).to(torch.bfloat16)
+    out = torch.empty(1, inter, dtype=torch.bfloat16, device=gpu)
+    r_out = torch.empty(1, hidden, dtype=torch.bfloat16, device=gpu)
+    ag, rg, nwg, Wg = a.to(gpu), r.to(gpu), nw.to(gpu), W.to(gpu)
+    C.call("efm_decode_norm_gate_up_swiglu", hidden, inter, eps, ptr(ag), ptr(rg), ptr(r_out), ptr(nwg), ptr(Wg),
+           ptr(out), stream())
+    torch.cuda.synchronize()
+    n2, res = O.fused_add_rms_norm(a, r, nw, eps)
+    assert torch.equal(r_out.cpu(), res)
+    assert_close_bf16(out, O.gate_up_swiglu(n2, W), rtol=2e-2, atol=6.25e-2)
+
+
+@pytest.mark.parametrize("hidden,vocab", [(1536, 151936), (896, 151936)])
+def test_decode_norm_lm_head_top1_matches_unfused(gpu, hidden, vocab):
+    torch.manual_seed(2)
+    eps = 1e-6
+    h = torch.randn(1, hidden, dtype=torch.bfloat16)
+    r = torch.randn(1, hidden, dtype=torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(hidden)).to(torch.bfloat16)
+    W = (torch.randn(vocab, hidden) * 0.02).to(torch.bfloat16)
+    ws = torch.zeros(C.load().efm_lm_head_top1_workspace_bytes(vocab), dtype=torch.uint8, device=gpu)
+    tok = torch.full((1,), -1, dtype=torch.int32, device=gpu)
+    hg, rg, nwg, Wg = h.to(gpu), r.to(gpu), nw.to(gpu), W.to(gpu)
+    C.call("efm_decode_norm_lm_head_top1", hidden, vocab, eps, ptr(hg), ptr(rg), ptr(nwg), ptr(Wg), ptr(tok),
+           ptr(ws), ws.numel(), stream())
+    torch.cuda.synchronize()
+    x, _ = O.fused_add_rms_norm(h, r, nw, eps)
+    assert _top1_ref_ok(O.linear(x, W, out_f32=True)[0], int(tok.item()))
