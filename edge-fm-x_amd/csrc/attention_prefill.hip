@@ -1,0 +1,301 @@
+// Causal GQA prefill attention on the gfx950 matrix cores (bf16 in, fp32 softmax).
+//
+// Semantics (FlashInfer SinglePrefillWithKVCache with ROPE_LLAMA as called from
+// src/operators/attention_op.cu:1345-1426): query row i (position i + q_rope_pos_offset)
+// of head h attends keys j <= i + (L - S) of KV head h / (Hq/Hkv); with RoPE-Llama both
+// q and k (at position j + k_rope_pos_offset) are rotated in the kernel.
+//
+// Kernel design (one workgroup = 4 wave64s = 128 query rows of one head):
+//  * Scores are computed transposed, S^T = K . Q^T, with v_mfma_f32_32x32x16_bf16: the
+//    K tile is the A operand (read from LDS), the wave's 32 query rows are the B operand
+//    held in registers for the whole kernel. Each lane then owns one query row and 16
+//    of the 32 keys of a sub-tile, so the online-softmax max / sum are in-lane plus one
+//    cross-half exchange.
+//  * The output is accumulated transposed as well, O^T = V^T . P^T: P stays in the
+//    lanes that produced it (packed to bf16), V^T comes from LDS. The 16-key blocks of
+//    P are in the MFMA accumulator's row order; V^T is read with the same key
+//    permutation so the contraction is unchanged.
+//  * RoPE is applied while staging: q pairs (d, d+hd/2) sit in the same lane, K pairs
+//    are loaded together by one thread before the LDS store.
+//  * Causal tiles past the diagonal are skipped; late query tiles are scheduled first.
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace efm {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kPfThreads = 256;
+constexpr int kPfQ = 128;   // query rows per workgroup (32 per wave)
+constexpr int kPfKV = 64;   // keys per LDS tile
+
+struct PrefillArgs {
+    const bf16_t* q;
+    const bf16_t* k;
+    const bf16_t* v;
+    bf16_t* o;
+    int S, L, Hq, Hkv;
+    int q_sn, q_sh, k_sn, k_sh, v_sn, v_sh;
+    int o_sn, o_sh;
+    int causal;
+    int rope_q, rope_k;
+    int q_pos_off, k_pos_off;
+    float theta, rcp_scale;
+    float sm_scale_log2;
+};
+
+union Pack8 {
+    bf16x8_t v;
+    uint4 u;
+    uint32_t w[4];
+};
+
+template <int HD>
+__global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a) {
+    constexpr int HALF = HD / 2;
+    constexpr int KS = HD / 16;         // MFMA k-steps over head_dim
+    constexpr int DT = HD / 32;         // 32-row d tiles of O^T
+    constexpr int KP = HD + 8;          // LDS pitch of the K tile (bf16)
+    constexpr int VP = kPfKV + 8;       // LDS pitch of the V^T tile (bf16)
+    __shared__ __align__(16) bf16_t Ks[kPfKV * KP];
+    __shared__ __align__(16) bf16_t Vt[HD * VP];
+
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave, lane = tid % kWave;
+    const int ql = lane % 32, hh = lane / 32;
+    const int nqt = (a.S + kPfQ - 1) / kPfQ;
+    const int qt = nqt - 1 - (int)blockIdx.x;  // heavy (late) tiles first
+    const int head = blockIdx.y;
+    const int kvh = head / (a.Hq / a.Hkv);
+    const int q0 = qt * kPfQ + wave * 32;
+    const int qi = q0 + ql;                     // this lane's query row
+    const int diag = a.L - a.S;                 // key j visible to row i iff j <= i + diag
+
+    // ---- Q (B operand) for this lane's row: d = ks*16 + hh*8 + e, kept in registers.
+    Pack8 qf[KS];
+    {
+        float x[KS][8];
+        const bool qv = qi < a.S;
+        const bf16_t* qp = a.q + (size_t)(qv ? qi : 0) * a.q_sn + (size_t)head * a.q_sh;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            uint4 u = qv ? *reinterpret_cast<const uint4*>(qp + ks * 16 + hh * 8) : make_uint4(0, 0, 0, 0);
+            unpack8(u, x[ks]);
+        }
+        if (a.rope_q) {
+            const float pos = (float)(qi + a.q_pos_off);
+#pragma unroll
+            for (int ks = 0; ks < KS / 2; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int d = ks * 16 + hh * 8 + e;  // < HALF; partner at ks + KS/2
+                    float sn, cs;
+                    sincosf(pos * rope_inv_freq(d, HD, a.theta, a.rcp_scale), &sn, &cs);
+                    const float x0 = x[ks][e], x1 = x[ks + KS / 2][e];
+                    x[ks][e] = x0 * cs - x1 * sn;
+                    x[ks + KS / 2][e] = x1 * cs + x0 * sn;
+                }
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qf[ks].u = pack8(x[ks]);
+    }
+
+    f32x16_t oacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[t][e] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+    const int q_last = min(a.S - 1, qt * kPfQ + kPfQ - 1);
+    const int kv_end = a.causal ? min(a.L, q_last + diag + 1) : a.L;
+    const int ntiles = (kv_end + kPfKV - 1) / kPfKV;
+
+    const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
+    const bf16_t* vbase = a.v + (size_t)kvh * a.v_sh;
+    // K staging: thread -> (key, 8 rotation pairs starting at kd0); kd0 is fixed per
+    // thread because the thread count is a multiple of the pair-chunks per key.
+    constexpr int KCH = HALF / 8;
+    static_assert(kPfThreads % KCH == 0, "K staging assumes a fixed pair chunk per thread");
+    const int kd0 = (tid % KCH) * 8;
+    float kif[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kif[e] = rope_inv_freq(kd0 + e, HD, a.theta, a.rcp_scale);
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int k0 = t * kPfKV;
+        __syncthreads();
+        // ---- stage K (rotated)
+        for (int c = tid; c < kPfKV * KCH; c += kPfThreads) {
+            const int kr = c / KCH, d0 = kd0;
+            const int j = k0 + kr;
+            uint4 lo = make_uint4(0, 0, 0, 0), hi = make_uint4(0, 0, 0, 0);
+            if (j < kv_end) {
+                const bf16_t* kp = kbase + (size_t)j * a.k_sn;
+                lo = *reinterpret_cast<const uint4*>(kp + d0);
+                hi = *reinterpret_cast<const uint4*>(kp + d0 + HALF);
+                if (a.rope_k) {
+                    float x0[8], x1[8];
+                    unpack8(lo, x0);
+                    unpack8(hi, x1);
+                    const float pos = (float)(j + a.k_pos_off);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        float sn, cs;
+                        sincos_reduced(pos * kif[e], &sn, &cs);
+                        const float y0 = x0[e] * cs - x1[e] * sn;
+                        const float y1 = x1[e] * cs + x0[e] * sn;
+                        x0[e] = y0;
+                        x1[e] = y1;
+                    }
+                    lo = pack8(x0);
+                    hi = pack8(x1);
+                }
+            }
+            *reinterpret_cast<uint4*>(&Ks[kr * KP + d0]) = lo;
+            *reinterpret_cast<uint4*>(&Ks[kr * KP + d0 + HALF]) = hi;
+        }
+        // ---- stage V transposed: Vt[d][key]
+        constexpr int VCH = HD / 8;
+        for (int c = tid; c < kPfKV * VCH; c += kPfThreads) {
+            const int kr = c / VCH, d0 = (c % VCH) * 8;
+            const int j = k0 + kr;
+            uint4 u = (j < kv_end) ? *reinterpret_cast<const uint4*>(vbase + (size_t)j * a.v_sn + d0)
+                                   : make_uint4(0, 0, 0, 0);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                Vt[(d0 + 2 * e) * VP + kr] = (bf16_t)(w[e] & 0xffffu);
+                Vt[(d0 + 2 * e + 1) * VP + kr] = (bf16_t)(w[e] >> 16);
+            }
+        }
+        __syncthreads();
+
+        if (q0 >= a.S) continue;  // wave past the end of the sequence (still joins barriers)
+#pragma unroll
+        for (int sub = 0; sub < kPfKV / 32; ++sub) {
+            const int kb0 = k0 + sub * 32;
+            if (a.causal && kb0 > q0 + 31 + diag) break;   // whole sub-tile above the diagonal
+            if (kb0 >= kv_end) break;
+            f32x16_t s;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[e] = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const bf16x8_t ka =
+                    *reinterpret_cast<const bf16x8_t*>(&Ks[(sub * 32 + ql) * KP + ks * 16 + hh * 8]);
+                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[ks].v, s, 0, 0, 0);
+            }
+            // element e: key = kb0 + (e/4)*8 + hh*4 + e%4, query = qi
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int j = kb0 + (e / 4) * 8 + hh * 4 + (e % 4);
+                const bool ok = (j < kv_end) && (!a.causal || j <= qi + diag);
+                s[e] = ok ? s[e] * a.sm_scale_log2 : -INFINITY;
+                mloc = fmaxf(mloc, s[e]);
+            }
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+            float psum = 0.f;
+            float p[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                p[e] = (m_new == -INFINITY) ? 0.f : exp2f(s[e] - m_new);
+                psum += p[e];
+            }
+            psum += __shfl_xor(psum, 32, kWave);
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+            // P^T operand per 16-key block kb: slots i<8 -> elements e = 8*kb + i.
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                Pack8 pb;
+                pb.u = pack8(&p[8 * kb]);
+                const int kcol = sub * 32 + kb * 16 + hh * 4;
+#pragma unroll
+                for (int tt = 0; tt < DT; ++tt) {
+                    const bf16_t* vr = &Vt[(tt * 32 + ql) * VP + kcol];
+                    Pack8 va;
+                    const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
+                    const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 8);
+                    va.w[0] = v0.x;
+                    va.w[1] = v0.y;
+                    va.w[2] = v1.x;
+                    va.w[3] = v1.y;
+                    oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, pb.v, oacc[tt], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    if (qi >= a.S) return;
+    // O^T tile tt: element e -> d = tt*32 + (e/4)*8 + hh*4 + e%4, query = qi.
+    const float inv = (l_run > 0.f) ? 1.f / l_run : 0.f;
+    bf16_t* op = a.o + (size_t)qi * a.o_sn + (size_t)head * a.o_sh;
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = tt * 32 + g * 8 + hh * 4;
+            uint2 w;
+            w.x = pack_bf16x2(oacc[tt][g * 4 + 0] * inv, oacc[tt][g * 4 + 1] * inv);
+            w.y = pack_bf16x2(oacc[tt][g * 4 + 2] * inv, oacc[tt][g * 4 + 3] * inv);
+            *reinterpret_cast<uint2*>(op + d) = w;
+        }
+}
+
+int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
+
+}  // namespace efm
+
+using namespace efm;
+
+extern "C" int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v,
+                                     void* o, uint32_t qo_len, uint32_t kv_len, int32_t causal, hipStream_t stream) {
+    int rc = validate_attention_ctx(ctx, "attention_prefill");
+    if (rc) return rc;
+    if (!q || !k || !v || !o) return set_error(EFM_ERR_INVALID_ARGUMENT, "attention_prefill: null tensor pointer");
+    if (kv_len < qo_len)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "attention_prefill: kv_len %u < qo_len %u", kv_len, qo_len);
+    if (qo_len == 0) return EFM_OK;
+    if (qo_len > (1u << 20) || kv_len > (1u << 24))
+        return set_error(EFM_ERR_UNSUPPORTED, "attention_prefill: sequence too long");
+    const int hd = (int)ctx->head_dim;
+    PrefillArgs a;
+    a.q = static_cast<const bf16_t*>(q);
+    a.k = static_cast<const bf16_t*>(k);
+    a.v = static_cast<const bf16_t*>(v);
+    a.o = static_cast<bf16_t*>(o);
+    a.S = (int)qo_len;
+    a.L = (int)kv_len;
+    a.Hq = (int)ctx->num_qo_heads;
+    a.Hkv = (int)ctx->num_kv_heads;
+    a.q_sn = ctx->q_stride_n ? (int)ctx->q_stride_n : a.Hq * hd;
+    a.q_sh = ctx->q_stride_h ? (int)ctx->q_stride_h : hd;
+    a.k_sn = ctx->k_stride_n ? (int)ctx->k_stride_n : a.Hkv * hd;
+    a.k_sh = ctx->k_stride_h ? (int)ctx->k_stride_h : hd;
+    a.v_sn = ctx->kv_stride_n ? (int)ctx->kv_stride_n : a.Hkv * hd;
+    a.v_sh = ctx->kv_stride_h ? (int)ctx->kv_stride_h : hd;
+    a.o_sn = a.Hq * hd;
+    a.o_sh = hd;
+    a.causal = causal != 0;
+    a.rope_q = ctx->pos_encoding == EFM_POS_ROPE_LLAMA;
+    a.rope_k = a.rope_q && !ctx->k_already_prerotated;
+    a.q_pos_off = (int)ctx->q_rope_pos_offset;
+    a.k_pos_off = (int)ctx->k_rope_pos_offset;
+    a.theta = ctx->rope_theta;
+    a.rcp_scale = 1.0f / ctx->rope_scale;
+    a.sm_scale_log2 = 1.4426950408889634f / sqrtf((float)hd);
+    dim3 grid((qo_len + kPfQ - 1) / kPfQ, a.Hq), block(kPfThreads);
+    if (hd == 128) hipLaunchKernelGGL(prefill_attn_kernel<128>, grid, block, 0, stream, a);
+    else hipLaunchKernelGGL(prefill_attn_kernel<64>, grid, block, 0, stream, a);
+    return check_launch("attention_prefill");
+}

@@ -160,6 +160,18 @@ __device__ __forceinline__ float rope_inv_freq(int d, int head_dim, float theta,
     return (float)(exp(-e * log((double)theta)) * (double)rcp_scale);
 }
 
+// sin/cos of an fp32 angle (radians, |a| < 2^22): Cody-Waite reduction by 2*pi split
+// into an fp32 head and tail, then the hardware sin/cos on the reduced argument in
+// revolutions (|r| <= 0.5).
+__device__ __forceinline__ void sincos_reduced(float a, float* s, float* c) {
+    const float k = rintf(a * 0.15915494309189535f);
+    float r = fmaf(-k, 6.28318548202514648f, a);
+    r = fmaf(-k, -1.7484555314695172e-07f, r);
+    const float rev = r * 0.15915494309189535f;
+    *s = __builtin_amdgcn_sinf(rev);
+    *c = __builtin_amdgcn_cosf(rev);
+}
+
 }  // namespace efm
 
 // Error reporting shared by every entry point of the C ABI.

@@ -280,3 +280,167 @@ extern "C" int efm_sampler_greedy(int64_t rows, int64_t vocab, const float* logi
                        out);
     return check_launch("sampler_greedy stage2");
 }
+
+// ----------------------------------------------------------------------------------
+// M-RoPE (src/layers/attention.cu:17-118): rotation pair d of a head uses the position
+// row of its section (cumulative mrope_section boundaries; both halves of a pair share
+// the section of d). Rotated values are written back as bf16.
+// ----------------------------------------------------------------------------------
+namespace efm {
+
+struct MropeArgs {
+    bf16_t* q;
+    bf16_t* k;
+    const int32_t* pos;   // [3, pos_stride]
+    int pos_stride;       // tokens per position row
+    int S, Hq, Hkv, hd;
+    int q_sn, k_sn;       // token strides (elements); heads are contiguous hd apart
+    int cum0, cum1;
+    float theta, rcp_scale;
+};
+
+__device__ __forceinline__ void mrope_pair(bf16_t* row, int d, int half, int p, float inv) {
+    float sn, cs;
+    sincosf((float)p * inv, &sn, &cs);
+    const float x0 = bf16_to_f32(row[d]);
+    const float x1 = bf16_to_f32(row[d + half]);
+    row[d] = (bf16_t)f32_to_bf16(x0 * cs - x1 * sn);
+    row[d + half] = (bf16_t)f32_to_bf16(x1 * cs + x0 * sn);
+}
+
+// grid (S, Hq + Hkv), block >= hd/2 threads.
+__global__ void mrope_kernel(MropeArgs a) {
+    const int t = blockIdx.x;
+    const int h = blockIdx.y;
+    const int half = a.hd / 2;
+    const int d = threadIdx.x;
+    if (d >= half) return;
+    const int sec = (d < a.cum0) ? 0 : (d < a.cum1 ? 1 : 2);
+    const int p = a.pos[sec * a.pos_stride + t];
+    const float inv = rope_inv_freq(d, a.hd, a.theta, a.rcp_scale);
+    bf16_t* row = (h < a.Hq) ? a.q + (size_t)t * a.q_sn + (size_t)h * a.hd
+                             : a.k + (size_t)t * a.k_sn + (size_t)(h - a.Hq) * a.hd;
+    mrope_pair(row, d, half, p, inv);
+}
+
+// Decode: rotate q (src -> dst) and k, write rotated k and raw v to cache slot
+// (*d_kv_len - 1) (decode_runtime_kernels.cu:152-225). grid (1, Hq + 2*Hkv).
+__global__ void decode_mrope_write_kv_kernel(const bf16_t* q_src, const bf16_t* k_src, const bf16_t* v_src,
+                                             bf16_t* q_dst, bf16_t* k_cache, bf16_t* v_cache, int Hq, int Hkv,
+                                             int hd, const int32_t* pos, int cum0, int cum1, float theta,
+                                             float rcp_scale, const uint32_t* d_kv_len) {
+    const int h = blockIdx.y;
+    const int half = hd / 2;
+    const int d = threadIdx.x;
+    if (d >= half) return;
+    const uint32_t L = d_kv_len[0];
+    const size_t slot = (L > 0) ? (size_t)(L - 1) : 0;
+    const int kvd = Hkv * hd;
+    if (h >= Hq + Hkv) {  // V rows: plain copy
+        if (L == 0) return;
+        const int hv = h - Hq - Hkv;
+        v_cache[slot * kvd + hv * hd + d] = v_src[hv * hd + d];
+        v_cache[slot * kvd + hv * hd + d + half] = v_src[hv * hd + d + half];
+        return;
+    }
+    const int sec = (d < cum0) ? 0 : (d < cum1 ? 1 : 2);
+    const float inv = rope_inv_freq(d, hd, theta, rcp_scale);
+    float sn, cs;
+    sincosf((float)pos[sec] * inv, &sn, &cs);
+    const bf16_t* src = (h < Hq) ? q_src + (size_t)h * hd : k_src + (size_t)(h - Hq) * hd;
+    const float x0 = bf16_to_f32(src[d]);
+    const float x1 = bf16_to_f32(src[d + half]);
+    const bf16_t y0 = (bf16_t)f32_to_bf16(x0 * cs - x1 * sn);
+    const bf16_t y1 = (bf16_t)f32_to_bf16(x1 * cs + x0 * sn);
+    if (h < Hq) {
+        q_dst[(size_t)h * hd + d] = y0;
+        q_dst[(size_t)h * hd + d + half] = y1;
+    } else if (L > 0) {
+        const int hk = h - Hq;
+        k_cache[slot * kvd + hk * hd + d] = y0;
+        k_cache[slot * kvd + hk * hd + d + half] = y1;
+    }
+}
+
+static int mrope_check_sections(int hd, int s0, int s1, int s2) {
+    if (s0 < 0 || s1 < 0 || s2 < 0 || s0 + s1 + s2 != hd / 2)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "mrope: sections %d+%d+%d must sum to head_dim/2 = %d", s0, s1, s2,
+                         hd / 2);
+    return EFM_OK;
+}
+
+}  // namespace efm
+
+extern "C" int efm_mrope(void* q, void* k, const int32_t* position_ids, int32_t position_stride, int32_t seq_len,
+                         int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t q_stride_n,
+                         int32_t k_stride_n, int32_t section0, int32_t section1, int32_t section2, float rope_theta,
+                         float rope_scale, hipStream_t stream) {
+    if (!q || !k || !position_ids) return set_error(EFM_ERR_INVALID_ARGUMENT, "mrope: null pointer");
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 512) return set_error(EFM_ERR_UNSUPPORTED, "mrope: head_dim");
+    int rc = mrope_check_sections(head_dim, section0, section1, section2);
+    if (rc) return rc;
+    if (seq_len < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || position_stride < seq_len)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "mrope: bad sizes");
+    if (seq_len == 0) return EFM_OK;
+    MropeArgs a;
+    a.q = static_cast<bf16_t*>(q);
+    a.k = static_cast<bf16_t*>(k);
+    a.pos = position_ids;
+    a.pos_stride = position_stride;
+    a.S = seq_len;
+    a.Hq = num_qo_heads;
+    a.Hkv = num_kv_heads;
+    a.hd = head_dim;
+    a.q_sn = q_stride_n ? q_stride_n : num_qo_heads * head_dim;
+    a.k_sn = k_stride_n ? k_stride_n : num_kv_heads * head_dim;
+    a.cum0 = section0;
+    a.cum1 = section0 + section1;
+    a.theta = rope_theta;
+    a.rcp_scale = 1.0f / rope_scale;
+    hipLaunchKernelGGL(mrope_kernel, dim3(seq_len, num_qo_heads + num_kv_heads), dim3(((head_dim / 2) + 63) / 64 * 64),
+                       0, stream, a);
+    return check_launch("mrope");
+}
+
+extern "C" int efm_decode_mrope_write_kv(const void* q_src, const void* k_src, const void* v_src, void* q_dst,
+                                         void* k_cache, void* v_cache, int32_t num_qo_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, const int32_t* position_ids, int32_t section0,
+                                         int32_t section1, int32_t section2, float rope_theta, float rope_scale,
+                                         const uint32_t* d_kv_len, hipStream_t stream) {
+    if (!q_src || !k_src || !v_src || !q_dst || !k_cache || !v_cache || !position_ids || !d_kv_len)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "decode_mrope_write_kv: null pointer");
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 512)
+        return set_error(EFM_ERR_UNSUPPORTED, "decode_mrope_write_kv: head_dim");
+    int rc = mrope_check_sections(head_dim, section0, section1, section2);
+    if (rc) return rc;
+    hipLaunchKernelGGL(decode_mrope_write_kv_kernel, dim3(1, num_qo_heads + 2 * num_kv_heads),
+                       dim3(((head_dim / 2) + 63) / 64 * 64), 0, stream, static_cast<const bf16_t*>(q_src),
+                       static_cast<const bf16_t*>(k_src), static_cast<const bf16_t*>(v_src),
+                       static_cast<bf16_t*>(q_dst), static_cast<bf16_t*>(k_cache), static_cast<bf16_t*>(v_cache),
+                       num_qo_heads, num_kv_heads, head_dim, position_ids, section0, section0 + section1, rope_theta,
+                       1.0f / rope_scale, d_kv_len);
+    return check_launch("decode_mrope_write_kv");
+}
+
+// Device-side response write for graph-replayed decode: response[*step] = sampled[0],
+// *step += 1, *d_kv_len += 1 (replaces finalize_decode_token_kernel plus the per-step
+// retargeting of the response pointer in the captured graph, standard_engine.h:33-65).
+__global__ void finalize_indexed_kernel(const int32_t* sampled, int32_t* response, uint32_t* step,
+                                        uint32_t* d_kv_len, uint32_t capacity) {
+    if (threadIdx.x == 0) {
+        const uint32_t s = step[0];
+        if (s < capacity) response[s] = sampled[0];
+        step[0] = s + 1u;
+        if (d_kv_len != nullptr) d_kv_len[0] += 1u;
+    }
+}
+
+extern "C" int efm_finalize_decode_token_indexed(const int32_t* sampled_token, int32_t* response_base,
+                                                 uint32_t* d_step, uint32_t* d_kv_len, uint32_t capacity,
+                                                 hipStream_t stream) {
+    if (!sampled_token || !response_base || !d_step)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "finalize_decode_token_indexed: null pointer");
+    hipLaunchKernelGGL(finalize_indexed_kernel, dim3(1), dim3(kWave), 0, stream, sampled_token, response_base, d_step,
+                       d_kv_len, capacity);
+    return check_launch("finalize_decode_token_indexed");
+}

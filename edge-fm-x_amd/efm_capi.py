@@ -71,6 +71,14 @@ SIGNATURES = {
     "efm_attention_decode_workspace_bytes": (c_size_t, [POINTER(AttentionCtx), c_uint32]),
     "efm_attention_decode": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
                                        c_void_p, c_uint32, c_void_p, c_size_t, c_void_p]),
+    "efm_attention_prefill": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
+                                        c_uint32, c_int32, c_void_p]),
+    "efm_mrope": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                            c_int32, c_int32, c_int32, c_int32, c_float, c_float, c_void_p]),
+    "efm_decode_mrope_write_kv": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
+                                            c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32, c_float, c_float,
+                                            c_void_p, c_void_p]),
+    "efm_finalize_decode_token_indexed": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p]),
     "efm_rms_norm": (c_int32, [c_uint32, c_uint32, c_float, c_void_p, c_void_p, c_void_p, c_void_p]),
     "efm_fused_add_rms_norm": (c_int32, [c_uint32, c_uint32, c_float, c_void_p, c_void_p, c_void_p, c_void_p]),
     "efm_act_and_mul": (c_int32, [c_int64, c_int64, c_int32, c_void_p, c_void_p, c_void_p]),

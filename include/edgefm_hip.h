@@ -89,6 +89,26 @@ int efm_attention_decode(const efm_attention_ctx* ctx, const void* q, const void
                          void* o, uint32_t kv_len, const uint32_t* d_kv_len, uint32_t max_kv_len,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Causal / non-causal GQA prefill attention on the matrix cores. q [qo_len, Hq, hd]
+ * (q_stride_* may point into a fused QKV buffer), k, v [kv_len, Hkv, hd] with
+ * kv_len >= qo_len; o [qo_len, Hq * hd] contiguous. Query i has RoPE position
+ * i + q_rope_pos_offset and, when causal, sees keys j <= i + (kv_len - qo_len); key j is
+ * rotated at j + k_rope_pos_offset unless k_already_prerotated. fp32 online softmax,
+ * P rounded to bf16 for the PV product, sm_scale = 1/sqrt(hd).
+ * Replaces AttentionOp::forward_prefill (src/operators/attention_op.h:45-52,
+ * forward_prefill_impl, src/operators/attention_op.cu:1345-1426). */
+int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v, void* o,
+                          uint32_t qo_len, uint32_t kv_len, int32_t causal, hipStream_t stream);
+
+/* M-RoPE in place (src/layers/attention.cu:17-118, AttentionLayer::apply_mrope).
+ * q [seq_len, Hq, hd] and k [seq_len, Hkv, hd] with token strides q_stride_n /
+ * k_stride_n (0 = contiguous); position_ids [3, position_stride] int32 (rows t, h, w);
+ * sections (e.g. 16, 24, 24) sum to hd/2. Pair d uses the position row of its section. */
+int efm_mrope(void* q, void* k, const int32_t* position_ids, int32_t position_stride, int32_t seq_len,
+              int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t q_stride_n, int32_t k_stride_n,
+              int32_t section0, int32_t section1, int32_t section2, float rope_theta, float rope_scale,
+              hipStream_t stream);
+
 /* ------------------------------------------------------------------------------------
  * RMSNorm (src/operators/norm_op.h:14-55, FlashInfer norm::RMSNorm / FusedAddRMSNorm
  * called at src/operators/norm_op.cu:33-90).
@@ -166,6 +186,19 @@ int efm_finalize_decode_token(const int32_t* sampled_token, int32_t* response_to
                               hipStream_t stream);
 /* values[0..2] += 1 (decode M-RoPE positions). */
 int efm_increment_int32_triplet(int32_t* values, hipStream_t stream);
+/* Decode M-RoPE on q (q_src -> q_dst) and k, then rotated K and raw V rows into cache slot
+ * (*d_kv_len - 1); position_ids is the device [3] decode position
+ * (launch_decode_mrope_apply_q_write_kv, decode_runtime_kernels.cu:152-225, 406-472). */
+int efm_decode_mrope_write_kv(const void* q_src, const void* k_src, const void* v_src, void* q_dst, void* k_cache,
+                              void* v_cache, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                              const int32_t* position_ids, int32_t section0, int32_t section1, int32_t section2,
+                              float rope_theta, float rope_scale, const uint32_t* d_kv_len, hipStream_t stream);
+/* response_base[*d_step] = sampled_token[0] (if *d_step < capacity); *d_step += 1;
+ * *d_kv_len += 1. The device-side step index keeps one captured decode graph valid for
+ * every step; it replaces finalize_decode_token_kernel plus the per-replay retargeting
+ * of the response pointer (decode_runtime_kernels.cu:54-65, standard_engine.h:33-65). */
+int efm_finalize_decode_token_indexed(const int32_t* sampled_token, int32_t* response_base, uint32_t* d_step,
+                                      uint32_t* d_kv_len, uint32_t capacity, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------
  * Fused decode-step kernels. Each one replaces a short sequence of the reference's

@@ -373,3 +373,118 @@ def test_decode_norm_lm_head_top1_matches_unfused(gpu, hidden, vocab):
     torch.cuda.synchronize()
     x, _ = O.fused_add_rms_norm(h, r, nw, eps)
     assert _top1_ref_ok(O.linear(x, W, out_f32=True)[0], int(tok.item()))
+
+
+PREFILL_CASES = [
+    pytest.param(12, 2, 128, 512, 512, id="1p5b_s512"),
+    pytest.param(12, 2, 128, 37, 37, id="1p5b_s37"),
+    pytest.param(14, 2, 64, 200, 200, id="0p5b_s200"),
+    pytest.param(16, 2, 128, 300, 1100, id="3b_prefix800"),
+    pytest.param(28, 4, 128, 1, 65, id="7b_s1_prefix64"),
+    pytest.param(16, 2, 128, 1344, 1344, id="vl3b_s1344"),
+]
+
+
+@pytest.mark.parametrize("hq,hkv,hd,S,L", PREFILL_CASES)
+def test_attention_prefill_matches_oracle(gpu, hq, hkv, hd, S, L):
+    torch.manual_seed(0)
+    q = torch.randn(S, hq, hd, dtype=torch.bfloat16)
+    k = torch.randn(L, hkv, hd, dtype=torch.bfloat16)
+    v = torch.randn(L, hkv, hd, dtype=torch.bfloat16)
+    ref = O.attention_prefill(q, k, v, O.AttnCtx(hq, hkv, hd, q_rope_pos_offset=L - S), causal=True)
+    ctx = C.make_attention_ctx(hq, hkv, hd, q_rope_pos_offset=L - S)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    o = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_attention_prefill", ctx, ptr(qg), ptr(kg), ptr(vg), ptr(o), S, L, 1, stream())
+    torch.cuda.synchronize()
+    # P is rounded to bf16 before the PV product (as in FlashAttention-2 / FlashInfer)
+    assert_close_bf16(o.reshape(S, hq, hd), ref, rtol=2e-2, atol=2e-2, what=f"prefill S={S} L={L}")
+
+
+def test_attention_prefill_strided_qkv_no_rope_and_noncausal(gpu):
+    """q taken from a fused QKV buffer (q_stride_n = qkv_total), pos NONE (M-RoPE models),
+    and the non-causal mode."""
+    torch.manual_seed(1)
+    hq, hkv, hd, S = 16, 2, 128, 130
+    tot = (hq + 2 * hkv) * hd
+    qkv = torch.randn(S, tot, dtype=torch.bfloat16)
+    q = qkv[:, : hq * hd].reshape(S, hq, hd)
+    k = qkv[:, hq * hd: (hq + hkv) * hd].reshape(S, hkv, hd).contiguous()
+    v = qkv[:, (hq + hkv) * hd:].reshape(S, hkv, hd).contiguous()
+    for causal in (1, 0):
+        ref = O.attention(q, k, v, torch.arange(S), O.AttnCtx(hq, hkv, hd, rope=False),
+                          causal_offset=0 if causal else None)
+        ctx = C.make_attention_ctx(hq, hkv, hd, rope=False, q_stride_n=tot, q_stride_h=hd)
+        qkvg, kg, vg = qkv.to(gpu), k.to(gpu), v.to(gpu)
+        o = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
+        C.call("efm_attention_prefill", ctx, ptr(qkvg), ptr(kg), ptr(vg), ptr(o), S, S, causal, stream())
+        torch.cuda.synchronize()
+        assert_close_bf16(o.reshape(S, hq, hd), ref, rtol=2e-2, atol=2e-2, what=f"causal={causal}")
+
+
+def test_attention_prefill_last_row_equals_decode(gpu):
+    """The last prefill row equals single-query decode over the same cache (the
+    reference's prefill/decode consistency)."""
+    torch.manual_seed(2)
+    hq, hkv, hd, L = 12, 2, 128, 700
+    q = torch.randn(L, hq, hd, dtype=torch.bfloat16, device=gpu)
+    k = torch.randn(L, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    v = torch.randn(L, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    o = torch.empty(L, hq * hd, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_attention_prefill", C.make_attention_ctx(hq, hkv, hd), ptr(q), ptr(k), ptr(v), ptr(o), L, L, 1,
+           stream())
+    dec, _ = _decode(C.make_attention_ctx(hq, hkv, hd), q[-1:].contiguous(), k, v, L)
+    assert_close_bf16(o[-1].reshape(1, hq, hd), dec, rtol=2e-2, atol=2e-2)
+
+
+def test_mrope_matches_oracle(gpu):
+    torch.manual_seed(0)
+    S, hq, hkv, hd = 70, 16, 2, 128
+    sections = (16, 24, 24)
+    q = torch.randn(S, hq, hd, dtype=torch.bfloat16)
+    k = torch.randn(S, hkv, hd, dtype=torch.bfloat16)
+    pos = torch.stack([torch.zeros(S, dtype=torch.int32), torch.arange(S, dtype=torch.int32) // 7,
+                       torch.arange(S, dtype=torch.int32) % 7]) + 3
+    qg, kg, pg = q.to(gpu), k.to(gpu), pos.to(gpu)
+    C.call("efm_mrope", ptr(qg), ptr(kg), ptr(pg), S, S, hq, hkv, hd, 0, 0, *sections, 1.0e6, 1.0, stream())
+    torch.cuda.synchronize()
+    assert_close_bf16(qg, O.mrope(q, pos, sections, 1.0e6), what="mrope q")
+    assert_close_bf16(kg, O.mrope(k, pos, sections, 1.0e6), what="mrope k")
+
+
+def test_decode_mrope_write_kv(gpu):
+    torch.manual_seed(0)
+    hq, hkv, hd = 16, 2, 128
+    sections = (16, 24, 24)
+    qkv = torch.randn(1, (hq + 2 * hkv) * hd, dtype=torch.bfloat16)
+    pos = torch.tensor([40, 41, 45], dtype=torch.int32)
+    rows = 50
+    qkvg, pg = qkv.to(gpu), pos.to(gpu)
+    kc = torch.zeros(rows, hkv * hd, dtype=torch.bfloat16, device=gpu)
+    vc = torch.zeros(rows, hkv * hd, dtype=torch.bfloat16, device=gpu)
+    qd = torch.empty(1, hq * hd, dtype=torch.bfloat16, device=gpu)
+    d_len = torch.tensor([31], dtype=torch.int32, device=gpu)
+    base = qkvg.data_ptr()
+    C.call("efm_decode_mrope_write_kv", base, base + hq * hd * 2, base + (hq + hkv) * hd * 2, ptr(qd), ptr(kc),
+           ptr(vc), hq, hkv, hd, ptr(pg), *sections, 1.0e6, 1.0, ptr(d_len), stream())
+    torch.cuda.synchronize()
+    q = qkv[:, : hq * hd].reshape(1, hq, hd)
+    k = qkv[:, hq * hd: (hq + hkv) * hd].reshape(1, hkv, hd)
+    p3 = pos.reshape(3, 1)
+    assert_close_bf16(qd.reshape(1, hq, hd), O.mrope(q, p3, sections, 1.0e6))
+    assert_close_bf16(kc[30].reshape(1, hkv, hd), O.mrope(k, p3, sections, 1.0e6))
+    assert torch.equal(vc[30].cpu(), qkv[0, (hq + hkv) * hd:])
+    assert kc[:30].abs().sum() == 0 and kc[31:].abs().sum() == 0
+
+
+def test_finalize_indexed(gpu):
+    resp = torch.full((8,), -1, dtype=torch.int32, device=gpu)
+    step = torch.zeros(1, dtype=torch.int32, device=gpu)
+    d_len = torch.tensor([10], dtype=torch.int32, device=gpu)
+    tok = torch.zeros(1, dtype=torch.int32, device=gpu)
+    for i in range(10):
+        tok.fill_(100 + i)
+        C.call("efm_finalize_decode_token_indexed", ptr(tok), ptr(resp), ptr(step), ptr(d_len), 8, stream())
+    torch.cuda.synchronize()
+    assert resp.cpu().tolist() == [100 + i for i in range(8)]
+    assert int(step.item()) == 10 and int(d_len.item()) == 20
