@@ -29,6 +29,7 @@
 namespace efm {
 
 constexpr int kAttnThreads = 256;
+constexpr int kMaxSplits = 512;  // split_cap <= 512 / num_kv_heads
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeArgs {
@@ -41,13 +42,13 @@ struct DecodeArgs {
     uint32_t max_kv_len;
     int num_kv_heads;
     int q_sn, q_sh, k_sn, k_sh, v_sn, v_sh;   // element strides
-    float rope_rcp_scale, rope_theta;
     int q_pos_off, k_pos_off;
     int rope_q, rope_k;                       // apply rotation to q / to k
     int split_cap;                            // gridDim.x
     float* o_part;                            // [Hkv][split_cap][G][HD]
     float* ml_part;                           // [Hkv][split_cap][G][2]
     uint32_t* counter;                        // [Hkv]
+    RopeTable rope;
 };
 
 template <int HD, int G>
@@ -61,8 +62,11 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_kernel(DecodeArgs a)
     static_assert(VPT >= 1 && KP % KG == 0, "bad decode tiling");
 
     __shared__ float qs[G][HD];
+    __shared__ float sfreq[HALF];
     __shared__ float sc[G][KP];
     __shared__ float ored[kAttnThreads / kWave][G][HD];
+    __shared__ float sml[kMaxSplits * G];
+    __shared__ float sll[kMaxSplits * G];
     __shared__ bool is_last;
 
     const int tid = threadIdx.x;
@@ -79,6 +83,8 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_kernel(DecodeArgs a)
     const int start = b * chunk;
     const int end = min((int)L, start + chunk);
 
+    if (tid < HALF) sfreq[tid] = a.rope.inv_freq[tid];
+    __syncthreads();
     // Rotated, scaled queries -> LDS.
     const float qscale = kLog2e / sqrtf((float)HD);
     for (int t = tid; t < G * HALF; t += kAttnThreads) {
@@ -88,7 +94,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_kernel(DecodeArgs a)
         const float x1 = bf16_to_f32(qp[d + HALF]);
         float y0 = x0, y1 = x1;
         if (a.rope_q) {
-            const float ang = (float)((int)L - 1 + a.q_pos_off) * rope_inv_freq(d, HD, a.rope_theta, a.rope_rcp_scale);
+            const float ang = (float)((int)L - 1 + a.q_pos_off) * sfreq[d];
             float sn, cs;
             sincosf(ang, &sn, &cs);
             y0 = x0 * cs - x1 * sn;
@@ -112,7 +118,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_kernel(DecodeArgs a)
         }
     float ifreq[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ifreq[e] = rope_inv_freq(d0 + e, HD, a.rope_theta, a.rope_rcp_scale);
+    for (int e = 0; e < 8; ++e) ifreq[e] = sfreq[d0 + e];
 
     // PV role.
     const int dch = tid % DCH;
@@ -261,19 +267,33 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attn_kernel(DecodeArgs a)
     if (!is_last) return;
     __threadfence();
 
+    // Merge: stage every split's (m, l) in LDS with parallel loads, turn them into
+    // normalised weights w_s = exp2(m_s - M) / sum_s exp2(m_s - M) l_s (one wave per query
+    // head), then accumulate the partial outputs with independent, unrolled loads.
     const size_t head_base = (size_t)kvh * a.split_cap * G;
+    for (int i = tid; i < nsplit * G; i += kAttnThreads) {
+        sml[i] = a.ml_part[(head_base + i) * 2];
+        sll[i] = a.ml_part[(head_base + i) * 2 + 1];
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += kAttnThreads / kWave) {
+        float M = -INFINITY;
+        for (int s = lane; s < nsplit; s += kWave) M = fmaxf(M, sml[s * G + g]);
+        M = wave_max(M);
+        float den = 0.f;
+        for (int s = lane; s < nsplit; s += kWave) den += exp2f(sml[s * G + g] - M) * sll[s * G + g];
+        den = wave_sum(den);
+        const float inv = (den > 0.f) ? 1.f / den : 0.f;
+        for (int s = lane; s < nsplit; s += kWave) sml[s * G + g] = exp2f(sml[s * G + g] - M) * inv;
+    }
+    __syncthreads();
     for (int t = tid; t < G * HD; t += kAttnThreads) {
         const int g = t / HD, d = t % HD;
-        float M = -INFINITY;
-        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ml_part[(head_base + (size_t)s * G + g) * 2]);
-        float num = 0.f, den = 0.f;
-        for (int s = 0; s < nsplit; ++s) {
-            const size_t pg = head_base + (size_t)s * G + g;
-            const float w = exp2f(a.ml_part[pg * 2] - M);
-            den = fmaf(w, a.ml_part[pg * 2 + 1], den);
-            num = fmaf(w, a.o_part[pg * HD + d], num);
-        }
-        a.o[(size_t)(kvh * G + g) * HD + d] = (bf16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
+        const float* op = a.o_part + (head_base + g) * HD + d;
+        float num = 0.f;
+#pragma unroll 8
+        for (int s = 0; s < nsplit; ++s) num = fmaf(sml[s * G + g], op[(size_t)s * G * HD], num);
+        a.o[(size_t)(kvh * G + g) * HD + d] = (bf16_t)f32_to_bf16(num);
     }
     if (tid == 0) a.counter[kvh] = 0u;
 }
@@ -367,8 +387,7 @@ extern "C" int efm_attention_decode(const efm_attention_ctx* ctx, const void* q,
     a.k_sh = ctx->k_stride_h ? (int)ctx->k_stride_h : hd;
     a.v_sn = ctx->kv_stride_n ? (int)ctx->kv_stride_n : (int)(ctx->num_kv_heads * hd);
     a.v_sh = ctx->kv_stride_h ? (int)ctx->kv_stride_h : hd;
-    a.rope_rcp_scale = 1.0f / ctx->rope_scale;
-    a.rope_theta = ctx->rope_theta;
+    rope_table_fill(&a.rope, hd, ctx->rope_theta, ctx->rope_scale);
     a.q_pos_off = (int)ctx->q_rope_pos_offset;
     a.k_pos_off = (int)ctx->k_rope_pos_offset;
     a.rope_q = ctx->pos_encoding == EFM_POS_ROPE_LLAMA;

@@ -42,8 +42,8 @@ struct PrefillArgs {
     int causal;
     int rope_q, rope_k;
     int q_pos_off, k_pos_off;
-    float theta, rcp_scale;
     float sm_scale_log2;
+    RopeTable rope;
 };
 
 union Pack8 {
@@ -61,6 +61,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     constexpr int VP = kPfKV + 8;       // LDS pitch of the V^T tile (bf16)
     __shared__ __align__(16) bf16_t Ks[kPfKV * KP];
     __shared__ __align__(16) bf16_t Vt[HD * VP];
+    __shared__ float sfreq[HALF];
 
     const int tid = threadIdx.x;
     const int wave = tid / kWave, lane = tid % kWave;
@@ -72,6 +73,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     const int q0 = qt * kPfQ + wave * 32;
     const int qi = q0 + ql;                     // this lane's query row
     const int diag = a.L - a.S;                 // key j visible to row i iff j <= i + diag
+    if (tid < HALF) sfreq[tid] = a.rope.inv_freq[tid];
+    __syncthreads();
 
     // ---- Q (B operand) for this lane's row: d = ks*16 + hh*8 + e, kept in registers.
     Pack8 qf[KS];
@@ -92,7 +95,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
                 for (int e = 0; e < 8; ++e) {
                     const int d = ks * 16 + hh * 8 + e;  // < HALF; partner at ks + KS/2
                     float sn, cs;
-                    sincosf(pos * rope_inv_freq(d, HD, a.theta, a.rcp_scale), &sn, &cs);
+                    sincosf(pos * sfreq[d], &sn, &cs);
                     const float x0 = x[ks][e], x1 = x[ks + KS / 2][e];
                     x[ks][e] = x0 * cs - x1 * sn;
                     x[ks + KS / 2][e] = x1 * cs + x0 * sn;
@@ -122,7 +125,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
     const int kd0 = (tid % KCH) * 8;
     float kif[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) kif[e] = rope_inv_freq(kd0 + e, HD, a.theta, a.rcp_scale);
+    for (int e = 0; e < 8; ++e) kif[e] = sfreq[kd0 + e];
 
     for (int t = 0; t < ntiles; ++t) {
         const int k0 = t * kPfKV;
@@ -291,8 +294,7 @@ extern "C" int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q
     a.rope_k = a.rope_q && !ctx->k_already_prerotated;
     a.q_pos_off = (int)ctx->q_rope_pos_offset;
     a.k_pos_off = (int)ctx->k_rope_pos_offset;
-    a.theta = ctx->rope_theta;
-    a.rcp_scale = 1.0f / ctx->rope_scale;
+    rope_table_fill(&a.rope, hd, ctx->rope_theta, ctx->rope_scale);
     a.sm_scale_log2 = 1.4426950408889634f / sqrtf((float)hd);
     dim3 grid((qo_len + kPfQ - 1) / kPfQ, a.Hq), block(kPfThreads);
     if (hd == 128) hipLaunchKernelGGL(prefill_attn_kernel<128>, grid, block, 0, stream, a);

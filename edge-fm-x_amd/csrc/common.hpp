@@ -151,13 +151,20 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
     return t;
 }
 
-// RoPE inverse frequency for pair index d of a head of size head_dim:
-// (1/rope_scale) / theta^(2d/head_dim), evaluated in double and rounded once to
-// fp32. The rotation angle is then fp32(pos) * inv_freq in fp32.
+// RoPE inverse frequencies, computed on the host once per launch and passed in the
+// kernel arguments: inv_freq[d] = fp32((1/rope_scale) / theta^(2d/head_dim)), evaluated
+// in double and rounded once. The rotation angle is fp32(pos) * inv_freq[d] in fp32.
 // (src/operators/attention_op.cu:363-364, src/layers/attention.cu:57-60)
-__device__ __forceinline__ float rope_inv_freq(int d, int head_dim, float theta, float rcp_scale) {
-    const double e = (2.0 * (double)d) / (double)head_dim;
-    return (float)(exp(-e * log((double)theta)) * (double)rcp_scale);
+constexpr int kMaxHalfDim = 64;
+struct RopeTable {
+    float inv_freq[kMaxHalfDim];
+};
+
+static inline void rope_table_fill(RopeTable* t, int head_dim, float theta, float rope_scale) {
+    for (int d = 0; d < kMaxHalfDim; ++d) {
+        const double e = (2.0 * (double)d) / (double)head_dim;
+        t->inv_freq[d] = (d < head_dim / 2) ? (float)(exp(-e * log((double)theta)) / (double)rope_scale) : 0.f;
+    }
 }
 
 // sin/cos of an fp32 angle (radians, |a| < 2^22): Cody-Waite reduction by 2*pi split

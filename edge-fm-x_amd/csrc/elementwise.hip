@@ -296,7 +296,7 @@ struct MropeArgs {
     int S, Hq, Hkv, hd;
     int q_sn, k_sn;       // token strides (elements); heads are contiguous hd apart
     int cum0, cum1;
-    float theta, rcp_scale;
+    RopeTable rope;
 };
 
 __device__ __forceinline__ void mrope_pair(bf16_t* row, int d, int half, int p, float inv) {
@@ -317,7 +317,7 @@ __global__ void mrope_kernel(MropeArgs a) {
     if (d >= half) return;
     const int sec = (d < a.cum0) ? 0 : (d < a.cum1 ? 1 : 2);
     const int p = a.pos[sec * a.pos_stride + t];
-    const float inv = rope_inv_freq(d, a.hd, a.theta, a.rcp_scale);
+    const float inv = a.rope.inv_freq[d];
     bf16_t* row = (h < a.Hq) ? a.q + (size_t)t * a.q_sn + (size_t)h * a.hd
                              : a.k + (size_t)t * a.k_sn + (size_t)(h - a.Hq) * a.hd;
     mrope_pair(row, d, half, p, inv);
@@ -327,8 +327,8 @@ __global__ void mrope_kernel(MropeArgs a) {
 // (*d_kv_len - 1) (decode_runtime_kernels.cu:152-225). grid (1, Hq + 2*Hkv).
 __global__ void decode_mrope_write_kv_kernel(const bf16_t* q_src, const bf16_t* k_src, const bf16_t* v_src,
                                              bf16_t* q_dst, bf16_t* k_cache, bf16_t* v_cache, int Hq, int Hkv,
-                                             int hd, const int32_t* pos, int cum0, int cum1, float theta,
-                                             float rcp_scale, const uint32_t* d_kv_len) {
+                                             int hd, const int32_t* pos, int cum0, int cum1, RopeTable rope,
+                                             const uint32_t* d_kv_len) {
     const int h = blockIdx.y;
     const int half = hd / 2;
     const int d = threadIdx.x;
@@ -344,7 +344,7 @@ __global__ void decode_mrope_write_kv_kernel(const bf16_t* q_src, const bf16_t* 
         return;
     }
     const int sec = (d < cum0) ? 0 : (d < cum1 ? 1 : 2);
-    const float inv = rope_inv_freq(d, hd, theta, rcp_scale);
+    const float inv = rope.inv_freq[d];
     float sn, cs;
     sincosf((float)pos[sec] * inv, &sn, &cs);
     const bf16_t* src = (h < Hq) ? q_src + (size_t)h * hd : k_src + (size_t)(h - Hq) * hd;
@@ -376,7 +376,7 @@ extern "C" int efm_mrope(void* q, void* k, const int32_t* position_ids, int32_t 
                          int32_t k_stride_n, int32_t section0, int32_t section1, int32_t section2, float rope_theta,
                          float rope_scale, hipStream_t stream) {
     if (!q || !k || !position_ids) return set_error(EFM_ERR_INVALID_ARGUMENT, "mrope: null pointer");
-    if (head_dim <= 0 || head_dim % 2 || head_dim > 512) return set_error(EFM_ERR_UNSUPPORTED, "mrope: head_dim");
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 2 * kMaxHalfDim) return set_error(EFM_ERR_UNSUPPORTED, "mrope: head_dim");
     int rc = mrope_check_sections(head_dim, section0, section1, section2);
     if (rc) return rc;
     if (seq_len < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || position_stride < seq_len)
@@ -395,8 +395,7 @@ extern "C" int efm_mrope(void* q, void* k, const int32_t* position_ids, int32_t 
     a.k_sn = k_stride_n ? k_stride_n : num_kv_heads * head_dim;
     a.cum0 = section0;
     a.cum1 = section0 + section1;
-    a.theta = rope_theta;
-    a.rcp_scale = 1.0f / rope_scale;
+    rope_table_fill(&a.rope, head_dim, rope_theta, rope_scale);
     hipLaunchKernelGGL(mrope_kernel, dim3(seq_len, num_qo_heads + num_kv_heads), dim3(((head_dim / 2) + 63) / 64 * 64),
                        0, stream, a);
     return check_launch("mrope");
@@ -409,16 +408,18 @@ extern "C" int efm_decode_mrope_write_kv(const void* q_src, const void* k_src, c
                                          const uint32_t* d_kv_len, hipStream_t stream) {
     if (!q_src || !k_src || !v_src || !q_dst || !k_cache || !v_cache || !position_ids || !d_kv_len)
         return set_error(EFM_ERR_INVALID_ARGUMENT, "decode_mrope_write_kv: null pointer");
-    if (head_dim <= 0 || head_dim % 2 || head_dim > 512)
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 2 * kMaxHalfDim)
         return set_error(EFM_ERR_UNSUPPORTED, "decode_mrope_write_kv: head_dim");
     int rc = mrope_check_sections(head_dim, section0, section1, section2);
     if (rc) return rc;
+    RopeTable rope;
+    rope_table_fill(&rope, head_dim, rope_theta, rope_scale);
     hipLaunchKernelGGL(decode_mrope_write_kv_kernel, dim3(1, num_qo_heads + 2 * num_kv_heads),
                        dim3(((head_dim / 2) + 63) / 64 * 64), 0, stream, static_cast<const bf16_t*>(q_src),
                        static_cast<const bf16_t*>(k_src), static_cast<const bf16_t*>(v_src),
                        static_cast<bf16_t*>(q_dst), static_cast<bf16_t*>(k_cache), static_cast<bf16_t*>(v_cache),
-                       num_qo_heads, num_kv_heads, head_dim, position_ids, section0, section0 + section1, rope_theta,
-                       1.0f / rope_scale, d_kv_len);
+                       num_qo_heads, num_kv_heads, head_dim, position_ids, section0, section0 + section1, rope,
+                       d_kv_len);
     return check_launch("decode_mrope_write_kv");
 }
 

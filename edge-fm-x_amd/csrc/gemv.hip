@@ -27,8 +27,15 @@ namespace efm {
 enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ADD_NORM = 2 };
 enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_TOP1 = 4 };
 
+// Weight-stream load used by the GEMV main loop (non-temporal: weights are read once
+// per decode step and must not evict the activation working set).
+#ifndef EFM_WEIGHT_LOAD
+#define EFM_WEIGHT_LOAD load_stream16
+#endif
+
 constexpr int kGemvThreads = 256;
-constexpr int kNJMax = 6;        // max 16-byte chunks per lane per row per segment
+constexpr int kNJMax = 6;
+constexpr int kTop1MaxGridDev = 2048;  // max workgroups of a top-1 launch (partials slots)        // max 16-byte chunks per lane per row per segment
 constexpr int kProMax = 4;       // max prologue chunks per thread (K <= 8192)
 
 struct GemvArgs {
@@ -140,7 +147,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a, int nj, 
                 for (int j = 0; j < kNJMax; ++j) {
                     const int c = seg * segC + kw * kWave + lane + j * kWave * KS;
                     if (j < nj && n < a.N && c < C) {
-                        wr[r][p][j] = load_stream16(row + (size_t)c * 8);
+                        wr[r][p][j] = EFM_WEIGHT_LOAD(row + (size_t)c * 8);
                     } else {
                         wr[r][p][j] = make_uint4(0u, 0u, 0u, 0u);
                     }
@@ -260,15 +267,24 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a, int nj, 
         __syncthreads();
         if (is_last) {
             __threadfence();
-            ArgMax b;
-            b.v = -INFINITY;
-            b.i = 0x7fffffff;
-            for (int i = threadIdx.x; i < (int)gridDim.x; i += kGemvThreads) {
-                ArgMax o;
-                o.v = __builtin_nontemporal_load(&a.partials[i].v);
-                o.i = __builtin_nontemporal_load(&a.partials[i].i);
-                b = argmax_pick(b, o);
+            // The partials were written by other workgroups; load them all before
+            // reducing (independent loads, not a dependent chain).
+            constexpr int kPer = kTop1MaxGridDev / kGemvThreads;
+            ArgMax pv[kPer];
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int i = threadIdx.x + k * kGemvThreads;
+                if (i < (int)gridDim.x) {
+                    pv[k].v = __builtin_nontemporal_load(&a.partials[i].v);
+                    pv[k].i = __builtin_nontemporal_load(&a.partials[i].i);
+                } else {
+                    pv[k].v = -INFINITY;
+                    pv[k].i = 0x7fffffff;
+                }
             }
+            ArgMax b = pv[0];
+#pragma unroll
+            for (int k = 1; k < kPer; ++k) b = argmax_pick(b, pv[k]);
             b = wave_argmax(b);
             if (lane == 0) fin[wave] = b;
             __syncthreads();
@@ -294,8 +310,12 @@ struct GemvCfg {
     int R, KS, nj, nseg, grid, nrb;
 };
 
-// Launch geometry for K inputs and N logical rows (P physical rows each).
-static GemvCfg gemv_pick(int K, int N, int P, int max_grid, bool wide_rows) {
+// Launch geometry for K inputs and N logical rows (P physical rows each), chosen from
+// a sweep on MI355X: one row per wave (R = 1) except for very tall matrices (the LM
+// head, R = 4); the K split KS keeps each lane at <= 6 16-byte chunks per row;
+// about 4 workgroups per CU (2 for the top-1 reduction) walking row blocks grid-stride
+// amortise the per-workgroup prologue (the RMSNorm of the input vector).
+static GemvCfg gemv_pick(int K, int N, int P, int max_grid, bool tall) {
     GemvCfg g;
     const int C = K / 8;
     g.KS = (C <= 256) ? 1 : (C <= 512 ? 2 : 4);
@@ -304,13 +324,10 @@ static GemvCfg gemv_pick(int K, int N, int P, int max_grid, bool wide_rows) {
     g.nseg = (need + kNJMax - 1) / kNJMax;
     g.nj = (need + g.nseg - 1) / g.nseg;
     const int groups = 4 / g.KS;
-    // Prefer more rows per wave (more loads in flight per lane) while keeping at
-    // least ~2 workgroups per CU for the 256 CUs.
-    int R = 1;
-    const int rmax = wide_rows ? 4 : 2;
-    while (R < rmax && (N + groups * R * 2 - 1) / (groups * R * 2) >= 512 && R * 2 * P * g.nj <= 24) R *= 2;
-    g.R = R;
-    g.nrb = (N + groups * R - 1) / (groups * R);
+    g.R = 1;
+    if (tall && (int64_t)N >= 65536) g.R = 4;
+    else if (P == 1 && g.KS == 4 && (int64_t)N * K >= (64 << 20)) g.R = 2;  // very large K x N (7B down)
+    g.nrb = (N + groups * g.R - 1) / (groups * g.R);
     g.grid = std::min(g.nrb, max_grid);
     return g;
 }
@@ -358,7 +375,7 @@ static int gemv_check(int64_t K, int64_t N, const void* W, const void* x, const 
     return EFM_OK;
 }
 
-constexpr int kTop1MaxGrid = 2048;
+constexpr int kTop1MaxGrid = kTop1MaxGridDev;
 constexpr size_t kTop1CounterOffset = kTop1MaxGrid * sizeof(ArgMax);
 
 int gemv_plain(int64_t K, int64_t N, const void* x, const void* W, const void* bias, void* y, int32_t out_dtype,
@@ -369,10 +386,10 @@ int gemv_plain(int64_t K, int64_t N, const void* x, const void* W, const void* b
     a.bias = static_cast<const bf16_t*>(bias);
     a.y = y;
     if (out_dtype == EFM_DTYPE_BF16) {
-        return gemv_launch<PRO_PLAIN, EPI_BF16>(gemv_pick((int)K, (int)N, 1, 1 << 30, false), a, stream);
+        return gemv_launch<PRO_PLAIN, EPI_BF16>(gemv_pick((int)K, (int)N, 1, 1024, false), a, stream);
     }
     if (out_dtype == EFM_DTYPE_F32) {
-        return gemv_launch<PRO_PLAIN, EPI_F32>(gemv_pick((int)K, (int)N, 1, 4096, true), a, stream);
+        return gemv_launch<PRO_PLAIN, EPI_F32>(gemv_pick((int)K, (int)N, 1, 512, true), a, stream);
     }
     return set_error(EFM_ERR_UNSUPPORTED, "linear: output dtype %d not supported", out_dtype);
 }
@@ -382,7 +399,7 @@ int gemv_swiglu(int64_t K, int64_t inter, const void* x, const void* W, void* y,
     if (rc) return rc;
     GemvArgs a = gemv_args((int)K, (int)inter, W, x);
     a.y = y;
-    return gemv_launch<PRO_PLAIN, EPI_SWIGLU>(gemv_pick((int)K, (int)inter, 2, 1 << 30, false), a, stream);
+    return gemv_launch<PRO_PLAIN, EPI_SWIGLU>(gemv_pick((int)K, (int)inter, 2, 1024, false), a, stream);
 }
 
 }  // namespace efm
@@ -405,7 +422,7 @@ extern "C" int efm_lm_head_top1(int64_t hidden, int64_t vocab, const void* x, co
     a.partials = static_cast<ArgMax*>(workspace);
     a.counter = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kTop1CounterOffset);
     a.token_out = token_out;
-    return gemv_launch<PRO_PLAIN, EPI_TOP1>(gemv_pick((int)hidden, (int)vocab, 1, kTop1MaxGrid, true), a, stream);
+    return gemv_launch<PRO_PLAIN, EPI_TOP1>(gemv_pick((int)hidden, (int)vocab, 1, 512, true), a, stream);
 }
 
 extern "C" int efm_decode_norm_qkv(int32_t hidden, int32_t q_dim, int32_t kv_dim, float eps, const void* h,
@@ -432,7 +449,7 @@ extern "C" int efm_decode_norm_qkv(int32_t hidden, int32_t q_dim, int32_t kv_dim
     a.k_cache = static_cast<bf16_t*>(k_cache);
     a.v_cache = static_cast<bf16_t*>(v_cache);
     a.d_kv_len = d_kv_len;
-    const GemvCfg g = gemv_pick(hidden, N, 1, 1 << 30, false);
+    const GemvCfg g = gemv_pick(hidden, N, 1, 1024, false);
     if (residual_in == nullptr) return gemv_launch<PRO_NORM, EPI_QKV>(g, a, stream);
     return gemv_launch<PRO_ADD_NORM, EPI_QKV>(g, a, stream);
 }
@@ -452,7 +469,7 @@ extern "C" int efm_decode_norm_gate_up_swiglu(int32_t hidden, int32_t inter, flo
     a.norm_w = static_cast<const bf16_t*>(norm_w);
     a.eps = eps;
     a.y = out;
-    return gemv_launch<PRO_ADD_NORM, EPI_SWIGLU>(gemv_pick(hidden, inter, 2, 1 << 30, false), a, stream);
+    return gemv_launch<PRO_ADD_NORM, EPI_SWIGLU>(gemv_pick(hidden, inter, 2, 1024, false), a, stream);
 }
 
 extern "C" int efm_decode_norm_lm_head_top1(int32_t hidden, int64_t vocab, float eps, const void* h,
@@ -474,5 +491,5 @@ extern "C" int efm_decode_norm_lm_head_top1(int32_t hidden, int64_t vocab, float
     a.partials = static_cast<ArgMax*>(workspace);
     a.counter = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kTop1CounterOffset);
     a.token_out = token_out;
-    return gemv_launch<PRO_ADD_NORM, EPI_TOP1>(gemv_pick(hidden, (int)vocab, 1, kTop1MaxGrid, true), a, stream);
+    return gemv_launch<PRO_ADD_NORM, EPI_TOP1>(gemv_pick(hidden, (int)vocab, 1, 512, true), a, stream);
 }

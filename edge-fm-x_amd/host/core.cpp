@@ -130,4 +130,11 @@ Tensor Tensor::reshape(std::vector<int64_t> shape) const {
     return t;
 }
 
+Tensor Tensor::prefix_view(std::vector<int64_t> shape) const {
+    Tensor t = *this;
+    t.shape_ = std::move(shape);
+    check<InvalidArgumentError>(t.numel() <= numel(), "prefix_view: larger than the buffer");
+    return t;
+}
+
 }  // namespace edge_fm

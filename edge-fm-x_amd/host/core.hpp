@@ -73,6 +73,9 @@ public:
     size_t nbytes() const { return (size_t)numel() * dtype_size(dtype_); }
     // Same storage, new shape (element count must match).
     Tensor reshape(std::vector<int64_t> shape) const;
+    // View of the leading elements of this buffer with a new shape (element count must
+    // not exceed this tensor's).
+    Tensor prefix_view(std::vector<int64_t> shape) const;
 
 private:
     void* data_ = nullptr;

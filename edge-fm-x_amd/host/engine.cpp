@@ -1,0 +1,911 @@
+#include "engine.hpp"
+
+#include <dlfcn.h>
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <filesystem>
+#include <fstream>
+#include <set>
+#include <unordered_set>
+
+namespace fs = std::filesystem;
+
+namespace edge_fm {
+
+// =================================================================================
+// Safetensors + WeightLoader
+// =================================================================================
+std::map<std::string, SafetensorsEntry> read_safetensors_header(const std::string& path, size_t* data_offset) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) throw ModelNotLoadedError("cannot open safetensors file: " + path);
+    uint64_t n = 0;
+    f.read(reinterpret_cast<char*>(&n), 8);
+    if (!f || n == 0 || n > (1ull << 31)) throw ModelNotLoadedError("bad safetensors header size: " + path);
+    std::string hdr(n, '\0');
+    f.read(&hdr[0], (std::streamsize)n);
+    if (!f) throw ModelNotLoadedError("truncated safetensors header: " + path);
+    Json j = Json::parse(hdr);
+    std::map<std::string, SafetensorsEntry> out;
+    for (const auto& kv : j.as_object()) {
+        if (kv.first == "__metadata__") continue;
+        SafetensorsEntry e;
+        e.dtype = kv.second.at("dtype").as_string();
+        for (const auto& s : kv.second.at("shape").as_array()) e.shape.push_back(s.as_int());
+        const auto& off = kv.second.at("data_offsets").as_array();
+        e.begin = (size_t)off.at(0).as_int();
+        e.end = (size_t)off.at(1).as_int();
+        out[kv.first] = e;
+    }
+    *data_offset = 8 + n;
+    return out;
+}
+
+static DType st_dtype(const std::string& s) {
+    if (s == "BF16") return DType::BFloat16;
+    if (s == "F16") return DType::Float16;
+    if (s == "F32") return DType::Float32;
+    if (s == "I32") return DType::Int32;
+    if (s == "I64") return DType::Int64;
+    if (s == "I8") return DType::Int8;
+    if (s == "U8") return DType::UInt8;
+    throw ModelNotLoadedError("unsupported safetensors dtype " + s);
+}
+
+WeightLoader& WeightLoader::instance() {
+    static WeightLoader w;
+    return w;
+}
+
+void WeightLoader::load_weights_from_file(const std::string& model_dir, ModelStage stage, int32_t device_id) {
+    std::vector<std::string> files;
+    if (fs::is_regular_file(model_dir)) {
+        files.push_back(model_dir);
+    } else {
+        if (fs::exists(fs::path(model_dir) / "model.safetensors")) {
+            files.push_back((fs::path(model_dir) / "model.safetensors").string());
+        } else if (fs::is_directory(model_dir)) {
+            for (const auto& e : fs::directory_iterator(model_dir)) {
+                const std::string name = e.path().filename().string();
+                if (name.rfind("model-", 0) == 0 && e.path().extension() == ".safetensors") files.push_back(e.path());
+            }
+            std::sort(files.begin(), files.end());
+        }
+    }
+    if (files.empty()) throw ModelNotLoadedError("no safetensors weights found under " + model_dir);
+    hip_check(hipSetDevice(device_id), "hipSetDevice");
+    std::unordered_map<std::string, Tensor> loaded;
+    for (const auto& path : files) {
+        size_t data_off = 0;
+        auto entries = read_safetensors_header(path, &data_off);
+        int fd = ::open(path.c_str(), O_RDONLY);
+        if (fd < 0) throw ModelNotLoadedError("cannot open " + path);
+        struct stat st;
+        fstat(fd, &st);
+        void* map = ::mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+        ::close(fd);
+        if (map == MAP_FAILED) throw ModelNotLoadedError("mmap failed for " + path);
+        for (const auto& kv : entries) {
+            const auto& e = kv.second;
+            if (data_off + e.end > (size_t)st.st_size) {
+                ::munmap(map, (size_t)st.st_size);
+                throw ModelNotLoadedError("tensor " + kv.first + " out of file bounds in " + path);
+            }
+            Tensor t = Tensor::empty(e.shape, st_dtype(e.dtype), Device::GPU, device_id);
+            check<ModelNotLoadedError>(t.nbytes() == e.end - e.begin, "size mismatch for tensor " + kv.first);
+            hip_check(hipMemcpy(t.data_ptr(), static_cast<const char*>(map) + data_off + e.begin, t.nbytes(),
+                                hipMemcpyHostToDevice),
+                      "upload " + kv.first);
+            loaded[kv.first] = t;
+        }
+        ::munmap(map, (size_t)st.st_size);
+    }
+    std::lock_guard<std::mutex> lock(mu_);
+    auto& dst = stages_[(int)stage];
+    for (auto& kv : loaded) dst[kv.first] = kv.second;
+}
+
+void WeightLoader::register_tensor(ModelStage stage, const std::string& name, const Tensor& t) {
+    std::lock_guard<std::mutex> lock(mu_);
+    stages_[(int)stage][name] = t;
+}
+
+const std::unordered_map<std::string, Tensor>& WeightLoader::get(ModelStage stage) {
+    std::lock_guard<std::mutex> lock(mu_);
+    return stages_[(int)stage];
+}
+
+bool WeightLoader::has_stage(ModelStage stage) {
+    std::lock_guard<std::mutex> lock(mu_);
+    auto it = stages_.find((int)stage);
+    return it != stages_.end() && !it->second.empty();
+}
+
+void WeightLoader::clear_stage(ModelStage stage) {
+    std::lock_guard<std::mutex> lock(mu_);
+    stages_.erase((int)stage);
+}
+
+// =================================================================================
+// EngineConfig / ModelConfig
+// =================================================================================
+std::string EngineConfig::default_config_dir() {
+    if (const char* env = std::getenv("EDGE_FM_CONFIG_DIR")) return env;
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void*>(&EngineConfig::default_config_dir), &info) && info.dli_fname) {
+        return (fs::path(info.dli_fname).parent_path() / "configs").string();
+    }
+    return "configs";
+}
+
+EngineConfig::EngineConfig(const std::string& config_path) {
+    const fs::path def = fs::path(default_config_dir()) / "engine_default.json";
+    if (fs::exists(def)) json_ = Json::parse_file(def.string());
+    else json_ = Json::object();
+    Json user;
+    try {
+        user = Json::parse_file(config_path);
+    } catch (const std::exception& e) {
+        throw ConfigurationError(std::string("cannot load engine config: ") + e.what());
+    }
+    json_.update(user);
+    base_dir_ = fs::path(config_path).parent_path().string();
+    const std::string mp = prefill_model_path();
+    if (mp.empty()) throw ConfigurationError("prefill_model_path is required");
+    const fs::path cfgp = fs::path(mp) / "config.json";
+    if (!fs::exists(cfgp)) throw ConfigurationError("model config.json not found: " + cfgp.string());
+    model_json_ = Json::parse_file(cfgp.string());
+}
+
+std::string EngineConfig::model_name() const {
+    std::string n = json_.get_string("model_name");
+    if (n.empty()) n = model_json_.get_string("model_type", "qwen2_5");
+    return normalize_model_name(n);
+}
+int32_t EngineConfig::device_id() const { return json_.contains("runtime") ? (int32_t)json_.at("runtime").get_int("device_id", 0) : 0; }
+std::string EngineConfig::hw_profile() const {
+    std::string hw = json_.contains("runtime") ? json_.at("runtime").get_string("hw_profile") : "";
+    if (hw.empty() || hw == "auto") hw = "rocm_gfx950";
+    return normalize_identifier(hw);
+}
+bool EngineConfig::use_graph() const {
+    if (!json_.contains("runtime")) return true;
+    const Json& r = json_.at("runtime");
+    if (r.contains("use_hip_graph")) return r.get_bool("use_hip_graph", true);
+    return r.get_bool("use_cuda_graph", true);
+}
+bool EngineConfig::lm_head_top1() const {
+    return json_.contains("runtime") ? json_.at("runtime").get_bool("lm_head_top1", true) : true;
+}
+std::string EngineConfig::operator_table_path() const {
+    std::string p = json_.get_string("operator_impl_table_path");
+    if (!p.empty() && fs::path(p).is_relative() && !base_dir_.empty()) p = (fs::path(base_dir_) / p).string();
+    return p;
+}
+std::string EngineConfig::prefill_model_path() const {
+    std::string p = json_.get_string("prefill_model_path");
+    if (!p.empty() && fs::path(p).is_relative() && !base_dir_.empty()) p = (fs::path(base_dir_) / p).string();
+    return p;
+}
+std::vector<KVSlotConfig> EngineConfig::kv_slots() const {
+    std::vector<KVSlotConfig> out;
+    if (json_.contains("kvcache") && json_.at("kvcache").contains("requests")) {
+        for (const auto& r : json_.at("kvcache").at("requests").as_array()) {
+            KVSlotConfig s;
+            s.request_id = (int32_t)r.get_int("request_id", 0);
+            s.max_tokens = (int32_t)r.get_int("max_tokens", 4096);
+            if (r.contains("prefix_token_ids"))
+                for (const auto& t : r.at("prefix_token_ids").as_array()) s.prefix_token_ids.push_back((int32_t)t.as_int());
+            out.push_back(s);
+        }
+    }
+    if (out.empty()) out.push_back(KVSlotConfig{});
+    return out;
+}
+int32_t EngineConfig::max_new_tokens() const {
+    return json_.contains("sampling") ? (int32_t)json_.at("sampling").get_int("max_new_tokens", 256) : 256;
+}
+float EngineConfig::temperature() const {
+    return json_.contains("sampling") ? (float)json_.at("sampling").get_double("temperature", 1.0) : 1.0f;
+}
+float EngineConfig::top_p() const {
+    return json_.contains("sampling") ? (float)json_.at("sampling").get_double("top_p", 1.0) : 1.0f;
+}
+uint64_t EngineConfig::seed() const {
+    return json_.contains("sampling") ? (uint64_t)json_.at("sampling").get_int("seed", 0) : 0;
+}
+std::vector<int32_t> EngineConfig::stop_token_ids() const {
+    std::vector<int32_t> out;
+    if (json_.contains("sampling") && json_.at("sampling").contains("stop_token_ids"))
+        for (const auto& t : json_.at("sampling").at("stop_token_ids").as_array()) out.push_back((int32_t)t.as_int());
+    return out;
+}
+std::vector<int32_t> EngineConfig::eos_token_ids() const {
+    std::vector<int32_t> out;
+    auto add = [&](const Json& j) {
+        if (!j.contains("eos_token_id")) return;
+        const Json& e = j.at("eos_token_id");
+        if (e.is_number()) out.push_back((int32_t)e.as_int());
+        else if (e.is_array())
+            for (const auto& t : e.as_array()) out.push_back((int32_t)t.as_int());
+    };
+    add(model_json_);
+    const fs::path gen = fs::path(prefill_model_path()) / "generation_config.json";
+    if (fs::exists(gen)) add(Json::parse_file(gen.string()));
+    return out;
+}
+
+ModelConfig ModelConfig::from_json(const Json& j0) {
+    // Qwen2.5-VL keeps the language model hyper-parameters under text_config.
+    const Json& j = j0.contains("text_config") ? j0.at("text_config") : j0;
+    ModelConfig m;
+    m.hidden = (int32_t)j.get_int("hidden_size", 0);
+    m.inter = (int32_t)j.get_int("intermediate_size", 0);
+    m.layers = (int32_t)j.get_int("num_hidden_layers", 0);
+    m.heads = (int32_t)j.get_int("num_attention_heads", 0);
+    m.kv_heads = (int32_t)j.get_int("num_key_value_heads", m.heads);
+    m.head_dim = (int32_t)j.get_int("head_dim", m.heads ? m.hidden / m.heads : 0);
+    m.vocab = j.get_int("vocab_size", j0.get_int("vocab_size", 0));
+    m.eps = (float)j.get_double("rms_norm_eps", 1e-6);
+    double theta = j.get_double("rope_theta", 0.0);
+    if (theta == 0.0 && j.contains("rope_parameters")) theta = j.at("rope_parameters").get_double("rope_theta", 0.0);
+    m.theta = (float)(theta > 0.0 ? theta : 1.0e6);
+    m.tied = j0.get_bool("tie_word_embeddings", j.get_bool("tie_word_embeddings", true));
+    const Json* rs = nullptr;
+    if (j.contains("rope_scaling") && j.at("rope_scaling").is_object()) rs = &j.at("rope_scaling");
+    else if (j0.contains("rope_scaling") && j0.at("rope_scaling").is_object()) rs = &j0.at("rope_scaling");
+    if (rs && rs->contains("mrope_section")) {
+        const auto& s = rs->at("mrope_section").as_array();
+        check<ConfigurationError>(s.size() == 3, "mrope_section must have 3 entries");
+        for (int i = 0; i < 3; ++i) m.mrope_section[i] = (int32_t)s[i].as_int();
+        m.mrope = true;
+    }
+    check<ConfigurationError>(m.hidden > 0 && m.layers > 0 && m.heads > 0 && m.kv_heads > 0 && m.vocab > 0 &&
+                                  m.inter > 0,
+                              "incomplete model config.json");
+    const std::string td = j0.get_string("torch_dtype", j.get_string("torch_dtype", "bfloat16"));
+    check<ConfigurationError>(td == "bfloat16" || td == "bf16",
+                              "the gfx950 kernels run bf16 models (torch_dtype " + td + ")");
+    return m;
+}
+
+// =================================================================================
+// KVManager
+// =================================================================================
+KVManager::KVManager(const std::vector<KVSlotConfig>& slots, const ModelConfig& m, int32_t device_id) : m_(m) {
+    std::set<int32_t> seen;
+    for (const auto& s : slots) {
+        check<ConfigurationError>(seen.insert(s.request_id).second, "duplicate kvcache request_id");
+        check<ConfigurationError>(s.max_tokens > 0, "kvcache max_tokens must be positive");
+        check<ConfigurationError>((int32_t)s.prefix_token_ids.size() < s.max_tokens, "prefix longer than max_tokens");
+        KVSlot slot;
+        slot.cfg = s;
+        slot.prefix_size = (int32_t)s.prefix_token_ids.size();
+        slot.buffer = Tensor::zeros({(int64_t)m.layers, 2, (int64_t)s.max_tokens, (int64_t)m.kv_dim()},
+                                    DType::BFloat16, Device::GPU, device_id);
+        slots_.push_back(std::move(slot));
+    }
+}
+
+KVSlot& KVManager::slot(int32_t request_id) {
+    for (auto& s : slots_)
+        if (s.cfg.request_id == request_id) return s;
+    throw InvalidRequestError("Invalid request_id: " + std::to_string(request_id));
+}
+bool KVManager::is_request_valid(int32_t request_id) const {
+    for (const auto& s : slots_)
+        if (s.cfg.request_id == request_id) return true;
+    return false;
+}
+void* KVManager::k_cache(int32_t request_id, int layer) {
+    KVSlot& s = slot(request_id);
+    const size_t per = (size_t)s.cfg.max_tokens * m_.kv_dim() * 2;
+    return static_cast<char*>(s.buffer.data_ptr()) + (size_t)layer * 2 * per;
+}
+void* KVManager::v_cache(int32_t request_id, int layer) {
+    KVSlot& s = slot(request_id);
+    const size_t per = (size_t)s.cfg.max_tokens * m_.kv_dim() * 2;
+    return static_cast<char*>(s.buffer.data_ptr()) + ((size_t)layer * 2 + 1) * per;
+}
+std::vector<int32_t> KVManager::request_ids() const {
+    std::vector<int32_t> out;
+    for (const auto& s : slots_) out.push_back(s.cfg.request_id);
+    return out;
+}
+
+// =================================================================================
+// Qwen2_5
+// =================================================================================
+const Tensor& Qwen2_5::w(const std::unordered_map<std::string, Tensor>& ws, const std::string& name) const {
+    // Qwen2.5-VL checkpoints prefix the language model (engine_factory.cpp:73-98).
+    for (const std::string& p : {std::string(""), std::string("model.language_model."), std::string("language_model.")}) {
+        std::string key = name;
+        if (!p.empty()) {
+            if (name.rfind("model.", 0) != 0) continue;
+            key = p + name.substr(6);
+        }
+        auto it = ws.find(key);
+        if (it != ws.end()) return it->second;
+    }
+    throw ModelNotLoadedError("missing weight tensor: " + name);
+}
+
+static Tensor concat_rows(const std::vector<const Tensor*>& parts, int32_t device_id, hipStream_t s) {
+    int64_t rows = 0, cols = -1;
+    for (auto* p : parts) {
+        check<ModelNotLoadedError>(p->dtype() == DType::BFloat16, "weights must be bf16");
+        const int64_t c = p->shape().size() == 2 ? p->shape()[1] : 1;
+        check<ModelNotLoadedError>(cols < 0 || c == cols, "fused weight column mismatch");
+        cols = c;
+        rows += p->shape()[0];
+    }
+    Tensor out = parts[0]->shape().size() == 2 ? Tensor::empty({rows, cols}, DType::BFloat16, Device::GPU, device_id)
+                                               : Tensor::empty({rows}, DType::BFloat16, Device::GPU, device_id);
+    size_t off = 0;
+    for (auto* p : parts) {
+        hip_check(hipMemcpyAsync(static_cast<char*>(out.data_ptr()) + off, p->data_ptr(), p->nbytes(),
+                                 hipMemcpyDeviceToDevice, s),
+                  "fuse weights");
+        off += p->nbytes();
+    }
+    return out;
+}
+
+Qwen2_5::Qwen2_5(const EngineConfig& cfg, const ModelConfig& m, const std::unordered_map<std::string, Tensor>& ws,
+                 int32_t device_id)
+    : m_(m), device_id_(device_id) {
+    model_name_ = cfg.model_name();
+    hw_profile_ = cfg.hw_profile();
+    table_path_ = cfg.operator_table_path();
+    hip_check(hipSetDevice(device_id), "hipSetDevice");
+    check<ConfigurationError>(m.hidden % 8 == 0 && m.inter % 8 == 0 && m.q_dim() % 8 == 0,
+                              "hidden / intermediate sizes must be multiples of 8");
+
+    // ---- operator resolution (attention.cu:211-276, linear_impl.cu:866-915) ----
+    auto resolve = [&](const char* kind, const char* stage) {
+        OperatorQuery q;
+        q.op_kind = kind;
+        q.stage = stage;
+        return resolve_impl_id(model_name_, hw_profile_, table_path_, q);
+    };
+    AttentionOpContext actx = attn_ctx();
+    attn_ = AttentionOpRegistry::instance().find_impl_by_id(resolve("attention", "prefill"));
+    if (attn_ == nullptr || !attn_->supports(actx)) attn_ = AttentionOpRegistry::instance().default_impl(actx);
+    const std::string lin_id = resolve("linear", "prefill");
+    linear_ = LinearOpRegistry::instance().find_impl_by_id(lin_id);
+    if (linear_ == nullptr) throw ConfigurationError("operator table selects unknown linear impl '" + lin_id + "'");
+    RMSNormOpContext nctx;
+    nctx.hidden_size = (uint32_t)m.hidden;
+    norm_ = NormOpRegistry::instance().find_impl_by_id(resolve("norm", "prefill"));
+    if (norm_ == nullptr || !norm_->supports(nctx)) norm_ = NormOpRegistry::instance().default_impl(nctx);
+    ActivationOpContext act;
+    act.hidden_size = m.inter;
+    act.input_layout = ActivationInputLayout::kUpGate;
+    act_ = ActivationOpRegistry::instance().find_impl_by_id(resolve("activation", "prefill"));
+    if (act_ == nullptr || !act_->supports(act)) act_ = ActivationOpRegistry::instance().default_impl(act);
+    FusedGateUpActivationContext gctx;
+    gctx.stage = ModelStage::Prefill;
+    gctx.m = 2;
+    gctx.hidden = m.hidden;
+    gctx.intermediate = m.inter;
+    swiglu_ = FusedGateUpActivationRegistry::instance().find_impl_by_id(resolve("fused_gate_up_activation", "prefill"));
+    if (swiglu_ == nullptr) swiglu_ = FusedGateUpActivationRegistry::instance().default_impl(gctx);
+
+    // ---- weights: fused layouts (linear.cu:1629-1785, 1923-1943, 2239-2286) ----
+    hipStream_t s = nullptr;
+    embed_ = w(ws, "model.embed_tokens.weight");
+    check<ModelNotLoadedError>(embed_.shape().size() == 2 && embed_.shape()[0] == m.vocab &&
+                                   embed_.shape()[1] == m.hidden,
+                               "embed_tokens shape mismatch");
+    final_norm_ = w(ws, "model.norm.weight");
+    auto lm = ws.find("lm_head.weight");
+    lm_head_ = (!m.tied && lm != ws.end()) ? lm->second : embed_;
+    if (lm != ws.end() && !m.tied) lm_head_ = lm->second;
+    for (int l = 0; l < m.layers; ++l) {
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        Layer L;
+        L.qkv_w = concat_rows({&w(ws, p + "self_attn.q_proj.weight"), &w(ws, p + "self_attn.k_proj.weight"),
+                               &w(ws, p + "self_attn.v_proj.weight")},
+                              device_id, s);
+        check<ModelNotLoadedError>(L.qkv_w.shape()[0] == m.q_dim() + 2 * m.kv_dim() && L.qkv_w.shape()[1] == m.hidden,
+                                   "qkv weight shape mismatch");
+        L.qkv_b = concat_rows({&w(ws, p + "self_attn.q_proj.bias"), &w(ws, p + "self_attn.k_proj.bias"),
+                               &w(ws, p + "self_attn.v_proj.bias")},
+                              device_id, s);
+        L.o_w = w(ws, p + "self_attn.o_proj.weight");
+        L.gu_w = concat_rows({&w(ws, p + "mlp.up_proj.weight"), &w(ws, p + "mlp.gate_proj.weight")}, device_id, s);
+        L.down_w = w(ws, p + "mlp.down_proj.weight");
+        L.in_norm = w(ws, p + "input_layernorm.weight");
+        L.post_norm = w(ws, p + "post_attention_layernorm.weight");
+        layers_.push_back(std::move(L));
+    }
+    hip_check(hipDeviceSynchronize(), "fuse weights");
+
+    // ---- decode scratch ----
+    const int64_t H = m.hidden;
+    dec_h_ = Tensor::zeros({1, H}, DType::BFloat16, Device::GPU, device_id);
+    dec_res_[0] = Tensor::zeros({1, H}, DType::BFloat16, Device::GPU, device_id);
+    dec_res_[1] = Tensor::zeros({1, H}, DType::BFloat16, Device::GPU, device_id);
+    dec_q_ = Tensor::zeros({1, (int64_t)m.q_dim()}, DType::BFloat16, Device::GPU, device_id);
+    dec_attn_ = Tensor::zeros({1, (int64_t)m.q_dim()}, DType::BFloat16, Device::GPU, device_id);
+    dec_a_ = Tensor::zeros({1, H}, DType::BFloat16, Device::GPU, device_id);
+    dec_mid_ = Tensor::zeros({1, (int64_t)m.inter}, DType::BFloat16, Device::GPU, device_id);
+    dec_kvtmp_ = Tensor::zeros({2, (int64_t)m.kv_dim()}, DType::BFloat16, Device::GPU, device_id);
+    dec_one_ = Tensor::empty({1}, DType::Int32, Device::GPU, device_id);
+    const uint32_t one = 1;
+    hip_check(hipMemcpy(dec_one_.data_ptr(), &one, 4, hipMemcpyHostToDevice), "init");
+    top1_ws_ = Tensor::zeros({(int64_t)efm_lm_head_top1_workspace_bytes(m.vocab)}, DType::UInt8, Device::GPU, device_id);
+}
+
+void Qwen2_5::reserve_decode(uint32_t max_kv_len) {
+    const efm_attention_ctx c = to_c_ctx(attn_ctx());
+    const size_t bytes = efm_attention_decode_workspace_bytes(&c, max_kv_len);
+    if (attn_ws_.empty() || attn_ws_.nbytes() < bytes)
+        attn_ws_ = Tensor::zeros({(int64_t)bytes}, DType::UInt8, Device::GPU, device_id_);
+}
+
+AttentionOpContext Qwen2_5::attn_ctx() const {
+    AttentionOpContext c;
+    c.num_qo_heads = (uint32_t)m_.heads;
+    c.num_kv_heads = (uint32_t)m_.kv_heads;
+    c.head_dim = (uint32_t)m_.head_dim;
+    c.rope_theta = m_.theta;
+    c.rope_scale = 1.0f;
+    c.dtype = DType::BFloat16;
+    // Text models rotate inside attention; M-RoPE models rotate before the cache write
+    // (src/layers/attention.cu:135-139).
+    c.pos_encoding = m_.mrope ? AttentionPosEncoding::kNone : AttentionPosEncoding::kRoPELlama;
+    c.device_id = device_id_;
+    return c;
+}
+
+void Qwen2_5::ensure_prefill_capacity(int32_t S) {
+    if (S <= pf_cap_) return;
+    const int64_t n = std::max<int64_t>(S, 64);
+    const int64_t H = m_.hidden;
+    pf_hidden_ = Tensor::empty({n, H}, DType::BFloat16, Device::GPU, device_id_);
+    pf_res_ = Tensor::empty({n, H}, DType::BFloat16, Device::GPU, device_id_);
+    pf_norm_ = Tensor::empty({n, H}, DType::BFloat16, Device::GPU, device_id_);
+    pf_qkv_ = Tensor::empty({n, (int64_t)(m_.q_dim() + 2 * m_.kv_dim())}, DType::BFloat16, Device::GPU, device_id_);
+    pf_attn_ = Tensor::empty({n, (int64_t)m_.q_dim()}, DType::BFloat16, Device::GPU, device_id_);
+    pf_mid_ = Tensor::empty({n, (int64_t)m_.inter}, DType::BFloat16, Device::GPU, device_id_);
+    pf_cap_ = (int32_t)n;
+}
+
+void Qwen2_5::prefill(int32_t S, int32_t base, const int32_t* ids, const Tensor* emb, int32_t embed_token_id,
+                      const int32_t* position_ids, void** k_caches, void** v_caches, int32_t* token_out, float* logits,
+                      hipStream_t stream) {
+    ensure_prefill_capacity(S);
+    const int64_t H = m_.hidden, QD = m_.q_dim(), KVD = m_.kv_dim(), TOT = QD + 2 * KVD;
+    const int32_t L = base + S;
+    // 1. embedding (embed_head.cu:135-164)
+    efm_check(efm_embedding_lookup(S, H, m_.vocab, ids, embed_.data_ptr(), emb ? emb->data_ptr() : nullptr,
+                                   emb ? emb->shape()[0] : 0, embed_token_id, pf_hidden_.data_ptr(), stream),
+              "prefill embedding");
+    RMSNormOpContext nctx;
+    nctx.batch_size = (uint32_t)S;
+    nctx.hidden_size = (uint32_t)H;
+    nctx.eps = m_.eps;
+    AttentionOpContext actx = attn_ctx();
+    actx.q_stride_n = (uint32_t)TOT;
+    actx.q_stride_h = (uint32_t)m_.head_dim;
+    if (!m_.mrope) actx.q_rope_pos_offset = (uint32_t)base;  // qwen2_5.cpp:807-830
+    const size_t row = (size_t)KVD * 2;
+    for (int l = 0; l < m_.layers; ++l) {
+        const Layer& Ly = layers_[l];
+        Tensor hid = pf_hidden_.prefix_view({S, H}), nrm = pf_norm_.prefix_view({S, H}), res = pf_res_.prefix_view({S, H});
+        // 2a. input norm (qwen2_5.cpp:564-576)
+        if (l == 0) {
+            norm_->rms_norm_forward_fn()(nctx, hid, Ly.in_norm, nrm, stream);
+            hip_check(hipMemcpyAsync(res.data_ptr(), hid.data_ptr(), (size_t)S * H * 2, hipMemcpyDeviceToDevice,
+                                     stream),
+                      "save residual");
+        } else {
+            norm_->fused_add_rms_norm_forward_fn()(nctx, nrm, res, Ly.in_norm, stream);
+        }
+        // 2b. fused QKV projection + bias
+        LinearOpContext lctx;
+        lctx.layer_role = "fused_qkv";
+        lctx.stage = ModelStage::Prefill;
+        lctx.shape = {S, DType::BFloat16, DType::BFloat16, DType::BFloat16, H, TOT};
+        lctx.has_bias = true;
+        Tensor qkv = pf_qkv_.prefix_view({S, TOT});
+        linear_->forward(lctx, Ly.qkv_w, &Ly.qkv_b, nrm, qkv, stream);
+        // 2c. K / V rows into cache rows [base, base + S) (qwen2_5.cpp:743-746)
+        char* kc = static_cast<char*>(k_caches[l]);
+        char* vc = static_cast<char*>(v_caches[l]);
+        const char* qkvp = static_cast<const char*>(qkv.data_ptr());
+        hip_check(hipMemcpy2DAsync(kc + (size_t)base * row, row, qkvp + (size_t)QD * 2, (size_t)TOT * 2, row, S,
+                                   hipMemcpyDeviceToDevice, stream),
+                  "copy K to cache");
+        hip_check(hipMemcpy2DAsync(vc + (size_t)base * row, row, qkvp + (size_t)(QD + KVD) * 2, (size_t)TOT * 2, row,
+                                   S, hipMemcpyDeviceToDevice, stream),
+                  "copy V to cache");
+        if (m_.mrope) {
+            // rotate q in the fused buffer and the freshly written K rows (attention.cu:17-118)
+            efm_check(efm_mrope(qkv.data_ptr(), kc + (size_t)base * row, position_ids, S, S, m_.heads, m_.kv_heads,
+                                m_.head_dim, (int32_t)TOT, (int32_t)KVD, m_.mrope_section[0], m_.mrope_section[1],
+                                m_.mrope_section[2], m_.theta, 1.0f, stream),
+                      "prefill mrope");
+        }
+        // 2d. attention over cache rows [0, L)
+        Tensor qv = Tensor::view(qkv.data_ptr(), {S, m_.heads, m_.head_dim}, DType::BFloat16, Device::GPU, device_id_);
+        Tensor kv_k = Tensor::view(kc, {L, m_.kv_heads, m_.head_dim}, DType::BFloat16, Device::GPU, device_id_);
+        Tensor kv_v = Tensor::view(vc, {L, m_.kv_heads, m_.head_dim}, DType::BFloat16, Device::GPU, device_id_);
+        Tensor ao = pf_attn_.prefix_view({S, QD});
+        attn_->forward_prefill(actx, qv, kv_k, kv_v, ao, true, stream);
+        // 2e. o_proj -> hidden, post-attention fused add + norm
+        lctx.layer_role = "attention_output";
+        lctx.shape = {S, DType::BFloat16, DType::BFloat16, DType::BFloat16, QD, H};
+        lctx.has_bias = false;
+        linear_->forward(lctx, Ly.o_w, nullptr, ao, hid, stream);
+        norm_->fused_add_rms_norm_forward_fn()(nctx, hid, res, Ly.post_norm, stream);
+        // 2f. MLP: gate/up GEMM with SwiGLU epilogue, down projection into the next
+        // layer's norm input (or hidden for the last layer), qwen2_5.cpp:855-875
+        Tensor mid = pf_mid_.prefix_view({S, (int64_t)m_.inter});
+        FusedGateUpActivationContext gctx;
+        gctx.stage = ModelStage::Prefill;
+        gctx.m = S;
+        gctx.hidden = H;
+        gctx.intermediate = m_.inter;
+        if (swiglu_ == nullptr || !swiglu_->run(gctx, Ly.gu_w, hid, mid, stream)) {
+            throw ConfigurationError("fused gate/up + SwiGLU unavailable for this shape");
+        }
+        lctx.layer_role = "mlp_down";
+        lctx.shape = {S, DType::BFloat16, DType::BFloat16, DType::BFloat16, (int64_t)m_.inter, H};
+        Tensor dst = (l < m_.layers - 1) ? nrm : hid;
+        linear_->forward(lctx, Ly.down_w, nullptr, mid, dst, stream);
+    }
+    // 3-4. final norm + LM head on the last row (qwen2_5.cpp:883-929)
+    const size_t last = (size_t)(S - 1) * H * 2;
+    const char* h_last = static_cast<const char*>(pf_hidden_.data_ptr()) + last;
+    const char* r_last = static_cast<const char*>(pf_res_.data_ptr()) + last;
+    if (logits == nullptr) {
+        efm_check(efm_decode_norm_lm_head_top1(m_.hidden, m_.vocab, m_.eps, h_last, r_last, final_norm_.data_ptr(),
+                                               lm_head_.data_ptr(), token_out, top1_ws_.data_ptr(), top1_ws_.nbytes(),
+                                               stream),
+                  "prefill lm head top1");
+    } else {
+        // final fused add + norm on the last row, then fp32 logits
+        hip_check(hipMemcpyAsync(dec_h_.data_ptr(), h_last, H * 2, hipMemcpyDeviceToDevice, stream), "copy");
+        hip_check(hipMemcpyAsync(dec_res_[1].data_ptr(), r_last, H * 2, hipMemcpyDeviceToDevice, stream), "copy");
+        efm_check(efm_fused_add_rms_norm(1, (uint32_t)H, m_.eps, dec_h_.data_ptr(), dec_res_[1].data_ptr(),
+                                         final_norm_.data_ptr(), stream),
+                  "prefill final norm");
+        efm_check(efm_linear(1, H, m_.vocab, dec_h_.data_ptr(), lm_head_.data_ptr(), nullptr, logits, EFM_DTYPE_F32,
+                             stream),
+                  "prefill lm head");
+    }
+}
+
+void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t max_kv_len, const int32_t* d_pos3,
+                          void** k_caches, void** v_caches, float* logits, hipStream_t stream) {
+    const int32_t H = m_.hidden, QD = m_.q_dim(), KVD = m_.kv_dim();
+    // embedding of the previous token (qwen2_5.cpp:541-549)
+    efm_check(efm_embedding_lookup(1, H, m_.vocab, token_buf, embed_.data_ptr(), nullptr, 0, -1, dec_h_.data_ptr(),
+                                   stream),
+              "decode embedding");
+    const efm_attention_ctx c = to_c_ctx(attn_ctx());
+    check<InternalError>(!attn_ws_.empty() && attn_ws_.nbytes() >= efm_attention_decode_workspace_bytes(&c, max_kv_len),
+                         "decode workspace not reserved for this cache length");
+    for (int l = 0; l < m_.layers; ++l) {
+        const Layer& Ly = layers_[l];
+        // input norm (+ residual) + QKV + bias, K/V straight into the cache slot
+        void* kdst = k_caches[l];
+        void* vdst = v_caches[l];
+        const uint32_t* slot_len = d_kv_len;
+        if (m_.mrope) {  // M-RoPE rotates K before the cache write: stage through kvtmp
+            kdst = dec_kvtmp_.data_ptr();
+            vdst = static_cast<char*>(dec_kvtmp_.data_ptr()) + (size_t)KVD * 2;
+            slot_len = static_cast<const uint32_t*>(dec_one_.data_ptr());
+        }
+        efm_check(efm_decode_norm_qkv(H, QD, KVD, m_.eps, (l == 0) ? dec_h_.data_ptr() : dec_h_.data_ptr(),
+                                      (l == 0) ? nullptr : dec_res_[1].data_ptr(), dec_res_[0].data_ptr(),
+                                      Ly.in_norm.data_ptr(), Ly.qkv_w.data_ptr(), Ly.qkv_b.data_ptr(),
+                                      dec_q_.data_ptr(), kdst, vdst, slot_len, stream),
+                  "decode norm+qkv");
+        if (m_.mrope) {
+            efm_check(efm_decode_mrope_write_kv(dec_q_.data_ptr(), kdst, vdst, dec_q_.data_ptr(), k_caches[l],
+                                                v_caches[l], m_.heads, m_.kv_heads, m_.head_dim, d_pos3,
+                                                m_.mrope_section[0], m_.mrope_section[1], m_.mrope_section[2],
+                                                m_.theta, 1.0f, d_kv_len, stream),
+                      "decode mrope + kv write");
+        }
+        efm_check(efm_attention_decode(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], dec_attn_.data_ptr(), 0,
+                                       d_kv_len, max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(), stream),
+                  "decode attention");
+        efm_check(efm_linear(1, QD, H, dec_attn_.data_ptr(), Ly.o_w.data_ptr(), nullptr, dec_a_.data_ptr(),
+                             EFM_DTYPE_BF16, stream),
+                  "decode o_proj");
+        efm_check(efm_decode_norm_gate_up_swiglu(H, m_.inter, m_.eps, dec_a_.data_ptr(), dec_res_[0].data_ptr(),
+                                                 dec_res_[1].data_ptr(), Ly.post_norm.data_ptr(),
+                                                 Ly.gu_w.data_ptr(), dec_mid_.data_ptr(), stream),
+                  "decode norm+gate_up+swiglu");
+        efm_check(efm_linear(1, m_.inter, H, dec_mid_.data_ptr(), Ly.down_w.data_ptr(), nullptr, dec_h_.data_ptr(),
+                             EFM_DTYPE_BF16, stream),
+                  "decode down_proj");
+    }
+    if (logits == nullptr) {
+        efm_check(efm_decode_norm_lm_head_top1(H, m_.vocab, m_.eps, dec_h_.data_ptr(), dec_res_[1].data_ptr(),
+                                               final_norm_.data_ptr(), lm_head_.data_ptr(), token_buf,
+                                               top1_ws_.data_ptr(), top1_ws_.nbytes(), stream),
+                  "decode lm head top1");
+    } else {
+        efm_check(efm_fused_add_rms_norm(1, (uint32_t)H, m_.eps, dec_h_.data_ptr(), dec_res_[1].data_ptr(),
+                                         final_norm_.data_ptr(), stream),
+                  "decode final norm");
+        efm_check(efm_linear(1, H, m_.vocab, dec_h_.data_ptr(), lm_head_.data_ptr(), nullptr, logits, EFM_DTYPE_F32,
+                             stream),
+                  "decode lm head");
+    }
+}
+
+// =================================================================================
+// StandardEngine
+// =================================================================================
+namespace {
+struct EventTimer {
+    hipEvent_t a = nullptr, b = nullptr;
+    EventTimer() {
+        hip_check(hipEventCreate(&a), "event");
+        hip_check(hipEventCreate(&b), "event");
+    }
+    ~EventTimer() {
+        hipEventDestroy(a);
+        hipEventDestroy(b);
+    }
+    double ms() {
+        float t = 0.f;
+        hip_check(hipEventElapsedTime(&t, a, b), "event elapsed");
+        return t;
+    }
+};
+}  // namespace
+
+StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_path) {
+    device_id_ = cfg_.device_id();
+    hip_check(hipSetDevice(device_id_), "hipSetDevice");
+    hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+    const ModelConfig m = ModelConfig::from_json(cfg_.model_config());
+    auto& loader = WeightLoader::instance();
+    if (!loader.has_stage(ModelStage::Prefill)) {
+        loader.load_weights_from_file(cfg_.prefill_model_path(), ModelStage::Prefill, device_id_);
+    }
+    model_ = std::make_unique<Qwen2_5>(cfg_, m, loader.get(ModelStage::Prefill), device_id_);
+    kv_ = std::make_unique<KVManager>(cfg_.kv_slots(), m, device_id_);
+    state_ = Tensor::zeros({16}, DType::Int32, Device::GPU, device_id_);
+    int32_t max_resp = 1;
+    for (const auto& s : cfg_.kv_slots()) {
+        max_resp = std::max(max_resp, s.max_tokens + 1);
+        model_->reserve_decode((uint32_t)s.max_tokens);
+    }
+    response_dev_ = Tensor::zeros({(int64_t)max_resp}, DType::Int32, Device::GPU, device_id_);
+    logits_ = Tensor::zeros({m.vocab}, DType::Float32, Device::GPU, device_id_);
+    sample_ws_ = Tensor::zeros({(int64_t)efm_sampler_greedy_workspace_bytes(1, m.vocab)}, DType::UInt8, Device::GPU,
+                               device_id_);
+    warmup();
+}
+
+StandardEngine::~StandardEngine() {
+    for (auto& kv : graphs_) {
+        if (kv.second.exec) hipGraphExecDestroy(kv.second.exec);
+        if (kv.second.graph) hipGraphDestroy(kv.second.graph);
+    }
+    if (stream_) hipStreamDestroy(stream_);
+}
+
+std::vector<void*> StandardEngine::caches(int32_t request_id, bool k) {
+    std::vector<void*> out;
+    for (int l = 0; l < model_->config().layers; ++l)
+        out.push_back(k ? kv_->k_cache(request_id, l) : kv_->v_cache(request_id, l));
+    return out;
+}
+
+// Fixed-prefix KV: prefill every slot's prefix once (standard_engine.cpp:515-556).
+void StandardEngine::warmup() {
+    for (int32_t rid : kv_->request_ids()) {
+        KVSlot& s = kv_->slot(rid);
+        if (s.prefix_size == 0 || s.prefix_ready) continue;
+        const int32_t n = s.prefix_size;
+        if (ids_dev_.empty() || ids_dev_.numel() < n) ids_dev_ = Tensor::empty({n}, DType::Int32, Device::GPU, device_id_);
+        hip_check(hipMemcpyAsync(ids_dev_.data_ptr(), s.cfg.prefix_token_ids.data(), (size_t)n * 4,
+                                 hipMemcpyHostToDevice, stream_),
+                  "prefix ids");
+        auto kc = caches(rid, true), vc = caches(rid, false);
+        int32_t* tok = static_cast<int32_t*>(state_.data_ptr()) + 2;
+        model_->prefill(n, 0, static_cast<int32_t*>(ids_dev_.data_ptr()), nullptr, -1, nullptr, kc.data(), vc.data(),
+                        tok, nullptr, stream_);
+        hip_check(hipStreamSynchronize(stream_), "prefix warmup");
+        s.prefix_ready = true;
+    }
+}
+
+void StandardEngine::sample_logits(uint32_t) {
+    int32_t* tok = static_cast<int32_t*>(state_.data_ptr()) + 2;
+    const float T = cfg_.temperature();
+    if (T < 1e-6f) {
+        efm_check(efm_sampler_greedy(1, model_->config().vocab, static_cast<float*>(logits_.data_ptr()), tok,
+                                     sample_ws_.data_ptr(), sample_ws_.nbytes(), stream_),
+                  "greedy sampler");
+        return;
+    }
+    throw ConfigurationError("temperature sampling is not available in this build");
+}
+
+void StandardEngine::run_decode_step(int32_t request_id, bool) {
+    int32_t* st = static_cast<int32_t*>(state_.data_ptr());
+    uint32_t* d_kv_len = reinterpret_cast<uint32_t*>(st + 0);
+    uint32_t* d_step = reinterpret_cast<uint32_t*>(st + 1);
+    int32_t* tok = st + 2;
+    const int32_t* pos3 = st + 3;
+    KVSlot& slot = kv_->slot(request_id);
+    auto kc = caches(request_id, true), vc = caches(request_id, false);
+    const bool greedy_fused = cfg_.temperature() < 1e-6f && cfg_.lm_head_top1();
+    model_->decode_step(tok, d_kv_len, (uint32_t)slot.cfg.max_tokens, pos3, kc.data(), vc.data(),
+                        greedy_fused ? nullptr : static_cast<float*>(logits_.data_ptr()), stream_);
+    if (!greedy_fused) sample_logits(0);
+    efm_check(efm_finalize_decode_token_indexed(tok, static_cast<int32_t*>(response_dev_.data_ptr()), d_step, d_kv_len,
+                                                (uint32_t)response_dev_.numel(), stream_),
+              "finalize decode token");
+    if (model_->config().mrope) efm_check(efm_increment_int32_triplet(st + 3, stream_), "advance mrope position");
+}
+
+Response StandardEngine::generate(const Request& req) {
+    hip_check(hipSetDevice(device_id_), "hipSetDevice");
+    check<InvalidRequestError>(!req.token_ids.empty(), "Request must contain at least one token id");
+    KVSlot& slot = kv_->slot(req.request_id);
+    const ModelConfig& m = model_->config();
+    const int32_t n_ids = (int32_t)req.token_ids.size();
+    check<InvalidRequestError>(n_ids <= slot.cfg.max_tokens, "Request sequence length exceeds kvcache max_tokens");
+    for (int32_t id : req.token_ids) {
+        const bool custom = req.has_embedding() && req.embed_token_id >= 0 && id >= req.embed_token_id &&
+                            id < req.embed_token_id + req.embedding.shape()[0];
+        check<InvalidRequestError>(custom || (id >= 0 && id < m.vocab), "token id out of vocabulary range");
+    }
+    if (m.mrope) check<InvalidRequestError>(req.has_position_ids(), "Qwen2.5-VL requests need position_ids [3, S]");
+
+    // prefix handling: ids starting with the slot prefix only prefill the suffix
+    // (standard_engine.cpp:1213-1235)
+    int32_t base = 0;
+    if (slot.prefix_size > 0 && n_ids > slot.prefix_size &&
+        std::equal(slot.cfg.prefix_token_ids.begin(), slot.cfg.prefix_token_ids.end(), req.token_ids.begin())) {
+        base = slot.prefix_size;
+    }
+    const int32_t S = n_ids - base;
+    // max_generated = min(max_new_tokens, max_tokens - len(ids) + 1) (scheduler.cpp:123-134)
+    const int32_t n_gen = std::max(1, std::min(cfg_.max_new_tokens(), slot.cfg.max_tokens - n_ids + 1));
+
+    if (ids_dev_.empty() || ids_dev_.numel() < S) ids_dev_ = Tensor::empty({S}, DType::Int32, Device::GPU, device_id_);
+    hip_check(hipMemcpyAsync(ids_dev_.data_ptr(), req.token_ids.data() + base, (size_t)S * 4, hipMemcpyHostToDevice,
+                             stream_),
+              "token ids H2D");
+    Tensor emb, pos;
+    if (req.has_embedding()) {
+        auto [dev, did] = req.embedding.device();
+        emb = (dev == Device::GPU) ? req.embedding
+                                   : Tensor::clone_from(req.embedding.data_ptr(), req.embedding.shape(),
+                                                        req.embedding.dtype(), Device::CPU, 0, Device::GPU, device_id_,
+                                                        stream_);
+        check<InvalidRequestError>(emb.dtype() == DType::BFloat16 && emb.shape().size() == 2 &&
+                                       emb.shape()[1] == m.hidden,
+                                   "embedding must be bf16 [rows, hidden]");
+    }
+    std::vector<int32_t> last_pos(3, 0);
+    if (m.mrope) {
+        const auto& ps = req.position_ids.shape();
+        check<InvalidRequestError>(ps.size() == 2 && ps[0] == 3 && ps[1] == n_ids && req.position_ids.dtype() == DType::Int32,
+                                   "position_ids must be int32 [3, len(token_ids)]");
+        std::vector<int32_t> host(3 * (size_t)n_ids);
+        auto [dev, did] = req.position_ids.device();
+        hip_check(hipMemcpy(host.data(), req.position_ids.data_ptr(), host.size() * 4,
+                            dev == Device::GPU ? hipMemcpyDeviceToHost : hipMemcpyHostToHost),
+                  "position ids");
+        // positions of the prefilled rows [base, n_ids)
+        std::vector<int32_t> sub(3 * (size_t)S);
+        for (int r = 0; r < 3; ++r)
+            std::copy(host.begin() + (size_t)r * n_ids + base, host.begin() + (size_t)(r + 1) * n_ids,
+                      sub.begin() + (size_t)r * S);
+        pos = Tensor::clone_from(sub.data(), {3, S}, DType::Int32, Device::CPU, 0, Device::GPU, device_id_, stream_);
+        // decode positions continue from the request's last position triplet, or the
+        // global max replicated (src/models/model.cpp:34-45; +1 for hidden >= 3584,
+        // qwen2_5.cpp:974-978)
+        if (req.mrope_last_pos.size() == 3) {
+            last_pos = req.mrope_last_pos;
+        } else {
+            const int32_t mx = *std::max_element(host.begin(), host.end());
+            last_pos = {mx, mx, mx};
+            if (m.hidden >= 3584)
+                for (auto& p : last_pos) p += 1;
+        }
+    }
+
+    metrics_.clear();
+    EventTimer pf, dc;
+    auto kc = caches(req.request_id, true), vc = caches(req.request_id, false);
+    int32_t* st = static_cast<int32_t*>(state_.data_ptr());
+    // decode state: d_kv_len = rows after prefill, step = 0, positions = last + 1
+    int32_t init[6] = {base + S, 0, 0, last_pos[0] + 1, last_pos[1] + 1, last_pos[2] + 1};
+    hip_check(hipMemcpyAsync(st, init, sizeof(init), hipMemcpyHostToDevice, stream_), "decode state H2D");
+
+    hip_check(hipEventRecord(pf.a, stream_), "event");
+    const bool greedy_fused = cfg_.temperature() < 1e-6f && cfg_.lm_head_top1();
+    model_->prefill(S, base, static_cast<int32_t*>(ids_dev_.data_ptr()), emb.empty() ? nullptr : &emb,
+                    req.embed_token_id, pos.empty() ? nullptr : static_cast<int32_t*>(pos.data_ptr()), kc.data(),
+                    vc.data(), st + 2, greedy_fused ? nullptr : static_cast<float*>(logits_.data_ptr()), stream_);
+    if (!greedy_fused) sample_logits(0);
+    efm_check(efm_finalize_decode_token_indexed(st + 2, static_cast<int32_t*>(response_dev_.data_ptr()),
+                                                reinterpret_cast<uint32_t*>(st + 1), reinterpret_cast<uint32_t*>(st),
+                                                (uint32_t)response_dev_.numel(), stream_),
+              "finalize prefill token");
+    hip_check(hipEventRecord(pf.b, stream_), "event");
+
+    hip_check(hipEventRecord(dc.a, stream_), "event");
+    const int32_t steps = n_gen - 1;
+    if (steps > 0) {
+        if (cfg_.use_graph()) {
+            GraphEntry& g = graphs_[req.request_id];
+            if (g.exec == nullptr) {
+                hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
+                try {
+                    run_decode_step(req.request_id, true);
+                } catch (...) {
+                    hipGraph_t tmp = nullptr;
+                    hipStreamEndCapture(stream_, &tmp);
+                    if (tmp) hipGraphDestroy(tmp);
+                    throw;
+                }
+                hip_check(hipStreamEndCapture(stream_, &g.graph), "end capture");
+                hip_check(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0), "graph instantiate");
+            }
+            for (int32_t i = 0; i < steps; ++i) hip_check(hipGraphLaunch(g.exec, stream_), "graph launch");
+        } else {
+            for (int32_t i = 0; i < steps; ++i) run_decode_step(req.request_id, false);
+        }
+    }
+    hip_check(hipEventRecord(dc.b, stream_), "event");
+
+    std::vector<int32_t> host((size_t)n_gen);
+    hip_check(hipMemcpyAsync(host.data(), response_dev_.data_ptr(), (size_t)n_gen * 4, hipMemcpyDeviceToHost, stream_),
+              "response D2H");
+    hip_check(hipStreamSynchronize(stream_), "generate sync");
+
+    // stop tokens truncate after the first hit, inclusive (standard_engine.cpp:1060-1068)
+    if (!req.ignore_stop_tokens) {
+        std::unordered_set<int32_t> stop;
+        for (int32_t t : cfg_.eos_token_ids()) stop.insert(t);
+        for (int32_t t : cfg_.stop_token_ids()) stop.insert(t);
+        for (int32_t t : req.stop_token_ids) stop.insert(t);
+        for (size_t i = 0; i < host.size(); ++i)
+            if (stop.count(host[i])) {
+                host.resize(i + 1);
+                break;
+            }
+    }
+    const double prefill_ms = pf.ms(), decode_ms = dc.ms();
+    metrics_["prefill_ms"] = prefill_ms;
+    metrics_["decode_ms"] = decode_ms;
+    metrics_["total_stage_ms"] = prefill_ms + decode_ms;
+    metrics_["decode_steps"] = steps;
+    metrics_["decode_step_avg_ms"] = steps > 0 ? decode_ms / steps : 0.0;
+    metrics_["generated_tokens_total"] = n_gen;
+    metrics_["returned_tokens"] = (double)host.size();
+    metrics_["prefill_tokens"] = S;
+    metrics_["prefill_tokens_per_second"] = prefill_ms > 0 ? S * 1000.0 / prefill_ms : 0.0;
+    metrics_["decode_tokens_per_second"] = decode_ms > 0 ? steps * 1000.0 / decode_ms : 0.0;
+    metrics_["tokens_per_second"] = (prefill_ms + decode_ms) > 0 ? n_gen * 1000.0 / (prefill_ms + decode_ms) : 0.0;
+    metrics_["use_hip_graph"] = cfg_.use_graph() ? 1.0 : 0.0;
+    Response r;
+    r.token_ids = std::move(host);
+    return r;
+}
+
+EdgeFM::EdgeFM(const std::string& config_path) : engine_(std::make_unique<StandardEngine>(config_path)) {}
+Response EdgeFM::generate(const Request& request) const { return engine_->generate(request); }
+std::unordered_map<std::string, double> EdgeFM::last_generate_metrics() const { return engine_->last_generate_metrics(); }
+
+}  // namespace edge_fm

@@ -1,0 +1,228 @@
+// Token-generation runtime of the MI355X EdgeFM engine: weight loading, engine
+// configuration, fixed-prefix KV slots, the Qwen2.5 / Qwen2.5-VL model and the
+// single-request generate loop with a HIP-graph-replayed decode step.
+//
+// Mirrors, in C++17 over HIP, the reference's src/engine (EngineConfig,
+// engine_factory, StandardEngine, KVManager, Scheduler), src/models/qwen2_5 and
+// src/utils/device/weight_loader.
+#pragma once
+
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "core.hpp"
+#include "json.hpp"
+#include "operators.hpp"
+
+namespace edge_fm {
+
+// ---------------------------------------------------------------------------------
+// WeightLoader (src/utils/device/weight_loader.h:20-120): per-stage name -> device
+// tensor cache. Tensors come from safetensors files or are registered by the caller
+// (device views, no copy).
+// ---------------------------------------------------------------------------------
+class WeightLoader {
+public:
+    static WeightLoader& instance();
+    void load_weights_from_file(const std::string& model_dir, ModelStage stage, int32_t device_id);
+    void register_tensor(ModelStage stage, const std::string& name, const Tensor& t);
+    const std::unordered_map<std::string, Tensor>& get(ModelStage stage);
+    bool has_stage(ModelStage stage);
+    void clear_stage(ModelStage stage);
+
+private:
+    std::mutex mu_;
+    std::map<int, std::unordered_map<std::string, Tensor>> stages_;
+};
+
+// Parse one safetensors file into host-side descriptors (tests and tools use it).
+struct SafetensorsEntry {
+    std::string dtype;
+    std::vector<int64_t> shape;
+    size_t begin = 0, end = 0;
+};
+std::map<std::string, SafetensorsEntry> read_safetensors_header(const std::string& path, size_t* data_offset);
+
+// ---------------------------------------------------------------------------------
+// EngineConfig (src/engine/engine.h:29-89): engine_default.json merged with the user
+// JSON (src/engine/engine.cpp:207-212).
+// ---------------------------------------------------------------------------------
+struct KVSlotConfig {
+    int32_t request_id = 0;
+    std::vector<int32_t> prefix_token_ids;
+    int32_t max_tokens = 4096;
+};
+
+class EngineConfig {
+public:
+    explicit EngineConfig(const std::string& config_path);
+    static std::string default_config_dir();
+
+    const Json& json() const { return json_; }
+    std::string model_name() const;
+    int32_t device_id() const;
+    std::string hw_profile() const;
+    bool use_graph() const;
+    bool lm_head_top1() const;
+    std::string operator_table_path() const;
+    std::string prefill_model_path() const;
+    std::vector<KVSlotConfig> kv_slots() const;
+    int32_t max_new_tokens() const;
+    float temperature() const;
+    float top_p() const;
+    uint64_t seed() const;
+    std::vector<int32_t> stop_token_ids() const;
+    const Json& model_config() const { return model_json_; }
+    std::vector<int32_t> eos_token_ids() const;
+
+private:
+    Json json_;
+    Json model_json_;
+    std::string base_dir_;
+};
+
+// Hyper-parameters read from the model's config.json (HF Qwen2 / Qwen2.5-VL format).
+struct ModelConfig {
+    int32_t hidden = 0, inter = 0, layers = 0, heads = 0, kv_heads = 0, head_dim = 0;
+    int64_t vocab = 0;
+    float eps = 1e-6f, theta = 1.0e6f;
+    bool tied = true;
+    bool mrope = false;
+    int32_t mrope_section[3] = {0, 0, 0};
+    static ModelConfig from_json(const Json& j);
+    int32_t q_dim() const { return heads * head_dim; }
+    int32_t kv_dim() const { return kv_heads * head_dim; }
+};
+
+// ---------------------------------------------------------------------------------
+// KVManager (src/engine/tasks/token_generation/kv_manager.h:58-106): one contiguous
+// buffer per request slot, laid out [layer][K | V][max_tokens][Hkv * hd] bf16.
+// ---------------------------------------------------------------------------------
+struct KVSlot {
+    KVSlotConfig cfg;
+    Tensor buffer;
+    int32_t prefix_size = 0;
+    bool prefix_ready = false;
+};
+
+class KVManager {
+public:
+    KVManager(const std::vector<KVSlotConfig>& slots, const ModelConfig& m, int32_t device_id);
+    KVSlot& slot(int32_t request_id);
+    bool is_request_valid(int32_t request_id) const;
+    void* k_cache(int32_t request_id, int layer);
+    void* v_cache(int32_t request_id, int layer);
+    std::vector<int32_t> request_ids() const;
+
+private:
+    ModelConfig m_;
+    std::vector<KVSlot> slots_;
+};
+
+// ---------------------------------------------------------------------------------
+// Qwen2.5 model (src/models/qwen2_5/qwen2_5.cpp:84-980)
+// ---------------------------------------------------------------------------------
+class Qwen2_5 {
+public:
+    Qwen2_5(const EngineConfig& cfg, const ModelConfig& m, const std::unordered_map<std::string, Tensor>& weights,
+            int32_t device_id);
+
+    const ModelConfig& config() const { return m_; }
+
+    // Prefill S tokens into cache rows [base, base + S) of (k_caches, v_caches).
+    // ids: device int32 [S]; embeddings (optional) device bf16 [n_custom, H];
+    // position_ids (M-RoPE) device int32 [3, S]. Writes the greedy token of the last
+    // row into token_out (device int32[1]) or, if logits != nullptr, fp32 logits.
+    void prefill(int32_t S, int32_t base, const int32_t* ids, const Tensor* embeddings, int32_t embed_token_id,
+                 const int32_t* position_ids, void** k_caches, void** v_caches, int32_t* token_out, float* logits,
+                 hipStream_t stream);
+
+    // One decode step for the token in token_buf (device int32[1]) at cache length
+    // *d_kv_len (device). Graph-capturable: no allocation, no host reads.
+    void decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t max_kv_len, const int32_t* d_pos3,
+                     void** k_caches, void** v_caches, float* logits, hipStream_t stream);
+
+    // Allocate the decode scratch for caches of up to max_kv_len rows (must run before
+    // a decode step is captured into a graph: capture cannot allocate).
+    void reserve_decode(uint32_t max_kv_len);
+
+private:
+    struct Layer {
+        Tensor qkv_w, qkv_b, o_w, gu_w, down_w, in_norm, post_norm;
+    };
+    ModelConfig m_;
+    int32_t device_id_;
+    std::string model_name_, hw_profile_, table_path_;
+    Tensor embed_, lm_head_, final_norm_;
+    std::vector<Layer> layers_;
+    // operator instances resolved from the implementation table
+    AttentionOp* attn_ = nullptr;
+    LinearImpl* linear_ = nullptr;
+    NormOp* norm_ = nullptr;
+    FusedGateUpActivationOp* swiglu_ = nullptr;
+    ActivationOp* act_ = nullptr;
+    // decode scratch
+    Tensor dec_h_, dec_res_[2], dec_q_, dec_attn_, dec_a_, dec_mid_, dec_kvtmp_, dec_one_, top1_ws_;
+    Tensor attn_ws_;
+    // prefill scratch (grow-only)
+    int32_t pf_cap_ = 0;
+    Tensor pf_hidden_, pf_res_, pf_norm_, pf_qkv_, pf_attn_, pf_mid_;
+
+    const Tensor& w(const std::unordered_map<std::string, Tensor>& ws, const std::string& name) const;
+    void ensure_prefill_capacity(int32_t S);
+    AttentionOpContext attn_ctx() const;
+};
+
+// ---------------------------------------------------------------------------------
+// StandardEngine + EdgeFM facade (include/edge-fm/edge-fm.h:10-111)
+// ---------------------------------------------------------------------------------
+class StandardEngine {
+public:
+    explicit StandardEngine(const std::string& config_path);
+    ~StandardEngine();
+    Response generate(const Request& request);
+    std::unordered_map<std::string, double> last_generate_metrics() const { return metrics_; }
+    const ModelConfig& model_config() const { return model_->config(); }
+    const EngineConfig& engine_config() const { return cfg_; }
+    void warmup();
+
+private:
+    EngineConfig cfg_;
+    int32_t device_id_;
+    hipStream_t stream_ = nullptr;
+    std::unique_ptr<Qwen2_5> model_;
+    std::unique_ptr<KVManager> kv_;
+    std::unordered_map<std::string, double> metrics_;
+    // device decode state: [0] d_kv_len, [1] d_step, [2] token, [3..5] M-RoPE position
+    Tensor state_;
+    Tensor response_dev_;
+    Tensor ids_dev_;
+    Tensor logits_;
+    Tensor sample_ws_;
+    struct GraphEntry {
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+    };
+    std::map<int32_t, GraphEntry> graphs_;  // per request slot
+
+    void run_decode_step(int32_t request_id, bool capture);
+    void sample_logits(uint32_t step_index);
+    std::vector<void*> caches(int32_t request_id, bool k);
+};
+
+class EdgeFM {
+public:
+    explicit EdgeFM(const std::string& config_path);
+    Response generate(const Request& request) const;
+    std::unordered_map<std::string, double> last_generate_metrics() const;
+    const StandardEngine& engine() const { return *engine_; }
+
+private:
+    std::unique_ptr<StandardEngine> engine_;
+};
+
+}  // namespace edge_fm

@@ -1,0 +1,192 @@
+// Python module `edge_fm`: the reference's pybind surface (src/python/pybind_debug.cpp:
+// 313-1735) for the MI355X runtime — DType / Device / ModelStage, Tensor (zero-copy
+// views of device memory, DLPack export as kDLROCM), Request / Response, EdgeFM with
+// generate() and last_generate_metrics(), the WeightLoader singleton and apply_mrope.
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <ATen/dlpack.h>
+
+#include "engine.hpp"
+
+namespace py = pybind11;
+using namespace edge_fm;
+
+namespace {
+
+DLDataType to_dl(DType d) {
+    switch (d) {
+        case DType::Float32: return {kDLFloat, 32, 1};
+        case DType::Float16: return {kDLFloat, 16, 1};
+        case DType::BFloat16: return {kDLBfloat, 16, 1};
+        case DType::Int32: return {kDLInt, 32, 1};
+        case DType::Int64: return {kDLInt, 64, 1};
+        case DType::UInt8: return {kDLUInt, 8, 1};
+        case DType::Int8: return {kDLInt, 8, 1};
+    }
+    return {kDLFloat, 32, 1};
+}
+
+struct DLHolder {
+    Tensor t;  // keeps the storage alive
+    std::vector<int64_t> shape, strides;
+    DLManagedTensor managed{};
+};
+
+py::capsule to_dlpack(const Tensor& t) {
+    auto* h = new DLHolder();
+    h->t = t;
+    h->shape = t.shape();
+    h->strides.resize(h->shape.size());
+    int64_t s = 1;
+    for (int i = (int)h->shape.size() - 1; i >= 0; --i) {
+        h->strides[i] = s;
+        s *= h->shape[i];
+    }
+    auto [dev, did] = t.device();
+    DLTensor& d = h->managed.dl_tensor;
+    d.data = t.data_ptr();
+    d.device = {dev == Device::GPU ? kDLROCM : kDLCPU, did};  // ROCm export (reference: kDLCUDA, tensor.cpp:40)
+    d.ndim = (int32_t)h->shape.size();
+    d.dtype = to_dl(t.dtype());
+    d.shape = h->shape.data();
+    d.strides = h->strides.data();
+    d.byte_offset = 0;
+    h->managed.manager_ctx = h;
+    h->managed.deleter = [](DLManagedTensor* m) { delete static_cast<DLHolder*>(m->manager_ctx); };
+    return py::capsule(&h->managed, "dltensor", [](PyObject* cap) {
+        if (PyCapsule_IsValid(cap, "dltensor")) {
+            auto* m = static_cast<DLManagedTensor*>(PyCapsule_GetPointer(cap, "dltensor"));
+            if (m && m->deleter) m->deleter(m);
+        }
+    });
+}
+
+}  // namespace
+
+PYBIND11_MODULE(edge_fm, m) {
+    m.doc() = "EdgeFM single-request transformer runtime for AMD Instinct MI355X (gfx950)";
+
+    // exceptions -> Python (core.h:219-407); more specific types registered last so
+    // they are matched first.
+    auto base = py::register_exception<Error>(m, "Error", PyExc_RuntimeError);
+    py::register_exception<InvalidRequestError>(m, "InvalidRequestError", base.ptr());
+    py::register_exception<DeviceError>(m, "DeviceError", base.ptr());
+    py::register_exception<ConfigurationError>(m, "ConfigurationError", base.ptr());
+    py::register_exception<ModelNotLoadedError>(m, "ModelNotLoadedError", base.ptr());
+    py::register_exception<OutOfMemoryError>(m, "OutOfMemoryError", base.ptr());
+    py::register_exception<InternalError>(m, "InternalError", base.ptr());
+    py::register_exception<InvalidArgumentError>(m, "InvalidArgumentError", base.ptr());
+
+    py::enum_<DType>(m, "DType")
+        .value("Float32", DType::Float32)
+        .value("Float16", DType::Float16)
+        .value("BFloat16", DType::BFloat16)
+        .value("Int32", DType::Int32)
+        .value("Int64", DType::Int64)
+        .value("UInt8", DType::UInt8)
+        .value("Int8", DType::Int8);
+    py::enum_<Device>(m, "Device").value("CPU", Device::CPU).value("GPU", Device::GPU);
+    py::enum_<ModelStage>(m, "ModelStage").value("Prefill", ModelStage::Prefill).value("Decode", ModelStage::Decode);
+
+    py::class_<Tensor>(m, "Tensor")
+        .def(py::init<>())
+        .def(py::init([](uintptr_t ptr, std::vector<int64_t> shape, DType dtype, Device device, int32_t device_id,
+                         bool owned) {
+                 if (owned) throw InvalidArgumentError("Tensor(ptr, ...) creates views only; pass owned=False");
+                 return Tensor::view(reinterpret_cast<void*>(ptr), std::move(shape), dtype, device, device_id);
+             }),
+             py::arg("data_ptr"), py::arg("shape"), py::arg("dtype"), py::arg("device") = Device::GPU,
+             py::arg("device_id") = 0, py::arg("owned") = false)
+        .def("to_dlpack", &to_dlpack)
+        .def("empty", [](const Tensor& t) { return t.empty(); })
+        .def("dtype", &Tensor::dtype)
+        .def("shape", &Tensor::shape)
+        .def("device", &Tensor::device)
+        .def("nbytes", &Tensor::nbytes)
+        .def("data_ptr", [](const Tensor& t) { return reinterpret_cast<uintptr_t>(t.data_ptr()); });
+
+    py::class_<Request>(m, "Request")
+        .def(py::init<int32_t, std::vector<int32_t>>(), py::arg("request_id"), py::arg("token_ids"))
+        .def(py::init([](int32_t rid, std::vector<int32_t> ids, const Tensor& emb, int32_t embed_token_id) {
+                 Request r(rid, std::move(ids));
+                 r.embedding = emb;
+                 r.embed_token_id = embed_token_id;
+                 return r;
+             }),
+             py::arg("request_id"), py::arg("token_ids"), py::arg("embedding"), py::arg("embed_token_id") = -1)
+        .def(py::init([](int32_t rid, std::vector<int32_t> ids, const Tensor& emb, int32_t embed_token_id,
+                         const Tensor& pos, std::vector<int32_t> last) {
+                 Request r(rid, std::move(ids));
+                 r.embedding = emb;
+                 r.embed_token_id = embed_token_id;
+                 r.position_ids = pos;
+                 r.mrope_last_pos = std::move(last);
+                 return r;
+             }),
+             py::arg("request_id"), py::arg("token_ids"), py::arg("embedding"), py::arg("embed_token_id"),
+             py::arg("position_ids"), py::arg("mrope_last_pos") = std::vector<int32_t>{})
+        .def("request_id", [](const Request& r) { return r.request_id; })
+        .def("token_ids", [](const Request& r) { return r.token_ids; })
+        .def("embedding", [](const Request& r) { return r.embedding; })
+        .def("embed_token_id", [](const Request& r) { return r.embed_token_id; })
+        .def("has_embedding", &Request::has_embedding)
+        .def("position_ids", [](const Request& r) { return r.position_ids; })
+        .def("has_position_ids", &Request::has_position_ids)
+        .def("mrope_last_pos", [](const Request& r) { return r.mrope_last_pos; })
+        .def("has_mrope_last_pos", [](const Request& r) { return !r.mrope_last_pos.empty(); })
+        .def("set_stop_token_ids", [](Request& r, std::vector<int32_t> v) { r.stop_token_ids = std::move(v); })
+        .def("stop_token_ids", [](const Request& r) { return r.stop_token_ids; })
+        .def("set_ignore_stop_tokens", [](Request& r, bool v) { r.ignore_stop_tokens = v; })
+        .def("ignore_stop_tokens", [](const Request& r) { return r.ignore_stop_tokens; });
+
+    py::class_<Response>(m, "Response").def("token_ids", [](const Response& r) { return r.token_ids; });
+
+    py::class_<EdgeFM>(m, "EdgeFM")
+        .def(py::init<const std::string&>(), py::arg("config_path"), py::call_guard<py::gil_scoped_release>())
+        .def("generate", &EdgeFM::generate, py::arg("request"), py::call_guard<py::gil_scoped_release>())
+        .def("last_generate_metrics", &EdgeFM::last_generate_metrics)
+        .def("model_config", [](const EdgeFM& e) {
+            const ModelConfig& c = e.engine().model_config();
+            py::dict d;
+            d["hidden_size"] = c.hidden;
+            d["intermediate_size"] = c.inter;
+            d["num_hidden_layers"] = c.layers;
+            d["num_attention_heads"] = c.heads;
+            d["num_key_value_heads"] = c.kv_heads;
+            d["head_dim"] = c.head_dim;
+            d["vocab_size"] = c.vocab;
+            d["mrope"] = c.mrope;
+            return d;
+        });
+
+    py::class_<WeightLoader, std::unique_ptr<WeightLoader, py::nodelete>>(m, "WeightLoader")
+        .def_static("instance", &WeightLoader::instance, py::return_value_policy::reference)
+        .def("load_weights_from_file", &WeightLoader::load_weights_from_file, py::arg("model_path"),
+             py::arg("stage"), py::arg("device_id") = 0, py::call_guard<py::gil_scoped_release>())
+        .def("register_tensor", &WeightLoader::register_tensor, py::arg("stage"), py::arg("name"), py::arg("tensor"))
+        .def("get", [](WeightLoader& w, ModelStage s) {
+            py::dict d;
+            for (const auto& kv : w.get(s)) d[py::str(kv.first)] = kv.second;
+            return d;
+        })
+        .def("clear_stage", &WeightLoader::clear_stage);
+
+    m.def("apply_mrope",
+          [](Tensor& q, Tensor& k, const Tensor& position_ids, std::vector<int32_t> mrope_section, float rope_theta,
+             float rope_scale) {
+              check<InvalidArgumentError>(mrope_section.size() == 3, "mrope_section must have 3 entries");
+              check<InvalidArgumentError>(q.shape().size() == 3 && k.shape().size() == 3, "q, k must be [S, H, hd]");
+              const int32_t S = (int32_t)q.shape()[0];
+              efm_check(efm_mrope(q.data_ptr(), k.data_ptr(), static_cast<const int32_t*>(position_ids.data_ptr()),
+                                  (int32_t)position_ids.shape().back(), S, (int32_t)q.shape()[1], (int32_t)k.shape()[1],
+                                  (int32_t)q.shape()[2], 0, 0, mrope_section[0], mrope_section[1], mrope_section[2],
+                                  rope_theta, rope_scale, nullptr),
+                        "apply_mrope");
+              hip_check(hipStreamSynchronize(nullptr), "apply_mrope sync");
+          },
+          py::arg("q"), py::arg("k"), py::arg("position_ids"), py::arg("mrope_section"), py::arg("rope_theta"),
+          py::arg("rope_scale") = 1.0f);
+
+    m.attr("__version__") = efm_version();
+}

@@ -333,9 +333,11 @@ class QwenState:
 class Qwen2Oracle:
     """Qwen2_5::forward_impl (qwen2_5.cpp:534-930) on the CPU with Appendix-A rounding."""
 
-    def __init__(self, cfg: QwenConfig, fused: dict, max_tokens: int):
+    def __init__(self, cfg: QwenConfig, fused: dict, max_tokens: int, cache_f32: bool = False):
+        """cache_f32 keeps an fp32 copy of every weight matrix so repeated steps do not
+        re-convert bf16 -> fp32 (same values, faster on large models)."""
         self.cfg = cfg
-        self.w = fused
+        self.w = {k: v.to(F32) for k, v in fused.items()} if cache_f32 else fused
         self.max_tokens = max_tokens
 
     def new_state(self) -> QwenState:

@@ -1,0 +1,187 @@
+"""End-to-end GPU tests of the C++ engine (pybind `edge_fm.EdgeFM.generate`) against
+the CPU oracle: greedy token ids are compared step by step with the oracle
+teacher-forced on the GPU's own tokens, so a mismatch is accepted only where the
+oracle's top-1 / chosen-token logit gap is below the bf16 accumulation noise
+(SURVEY "near-tie flip" rule). Mirrors tests/engine/test_qwen2_generate.py of the
+reference (HF transformers dumps there; the oracle here is pinned to HF in
+tests/test_oracle.py)."""
+import os
+import tempfile
+
+import pytest
+import torch
+
+import edge_fm
+import efm_setup as S
+from oracle import efm_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TINY = S.ModelShape(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=64, inter=512, vocab=1000)
+TINY_VL = S.ModelShape(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=64, inter=512, vocab=1000,
+                       mrope_section=(8, 12, 12))
+
+
+def _oracle_cfg(shape: S.ModelShape) -> O.QwenConfig:
+    return O.QwenConfig(hidden=shape.hidden, layers=shape.layers, heads=shape.heads, kv_heads=shape.kv_heads,
+                        head_dim=shape.head_dim, inter=shape.inter, vocab=shape.vocab, eps=shape.eps,
+                        theta=shape.theta, tied=shape.tied, mrope_section=shape.mrope_section)
+
+
+def _engine(tmp, shape, weights_cpu, **cfg):
+    wdev = {k: v.to("cuda:0").contiguous() for k, v in weights_cpu.items()}
+    S.register_weights(wdev)
+    mdir = S.write_model_dir(os.path.join(tmp, "model"), shape)
+    ecfg = S.write_engine_config(os.path.join(tmp, "engine.json"), mdir, **cfg)
+    return edge_fm.EdgeFM(ecfg), wdev
+
+
+def _check_against_oracle(tokens, steps, tol):
+    assert len(tokens) == len(steps)
+    exact = 0
+    for i, (tok, (ref, margin, gap)) in enumerate(zip(tokens, steps)):
+        if tok == ref:
+            exact += 1
+        else:
+            assert gap < tol, f"step {i}: gpu {tok} vs oracle {ref}, logit gap {gap:.4f} (margin {margin:.4f})"
+    return exact
+
+
+def _teacher_forced(orc, prompt, gpu_tokens, embeds=None, pos=None, decode_pos=None):
+    """Oracle logits for every step given the GPU's own token sequence; returns
+    (argmax, top1-top2 margin, top1 - logit[gpu token]) per step."""
+    st = orc.new_state()
+    logits = orc.forward(st, prompt, embeds=embeds, position_ids=pos)
+    out = []
+    for i, tok in enumerate(gpu_tokens):
+        ref = int(O.argmax_lowest(logits.unsqueeze(0))[0])
+        top2 = torch.topk(logits.double(), 2).values
+        out.append((ref, float(top2[0] - top2[1]), float(logits[ref] - logits[tok])))
+        if i + 1 == len(gpu_tokens):
+            break
+        p = None if decode_pos is None else decode_pos(i)
+        logits = orc.forward(st, torch.tensor([tok], dtype=torch.int32), position_ids=p)
+    return out
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_tiny_greedy_matches_oracle(gpu, use_graph):
+    w = O.random_weights(_oracle_cfg(TINY), seed=11, std=0.2)
+    prompt = torch.randint(0, TINY.vocab, (40,), generator=torch.Generator().manual_seed(3)).to(torch.int32)
+    with tempfile.TemporaryDirectory() as tmp:
+        eng, keep = _engine(tmp, TINY, w, max_tokens=128, max_new_tokens=24, use_graph=use_graph)
+        req = edge_fm.Request(0, prompt.tolist())
+        req.set_ignore_stop_tokens(True)
+        toks = eng.generate(req).token_ids()
+        m = eng.last_generate_metrics()
+    assert len(toks) == 24 and m["decode_steps"] == 23
+    orc = O.Qwen2Oracle(_oracle_cfg(TINY), O.fuse_weights(_oracle_cfg(TINY), w), max_tokens=128)
+    exact = _check_against_oracle(toks, _teacher_forced(orc, prompt, toks), tol=0.05)
+    assert exact >= 22
+
+
+def test_graph_and_eager_agree_and_repeat(gpu):
+    w = O.random_weights(_oracle_cfg(TINY), seed=12, std=0.2)
+    prompt = list(range(5, 45))
+    outs = []
+    with tempfile.TemporaryDirectory() as tmp:
+        for g in (True, False):
+            eng, keep = _engine(tmp, TINY, w, max_tokens=128, max_new_tokens=30, use_graph=g)
+            req = edge_fm.Request(0, prompt)
+            req.set_ignore_stop_tokens(True)
+            outs.append(eng.generate(req).token_ids())
+            outs.append(eng.generate(req).token_ids())  # second call reuses the captured graph
+            del eng
+    assert outs[0] == outs[1] == outs[2] == outs[3]
+
+
+def test_prefix_slot_and_stop_tokens_and_cap(gpu):
+    w = O.random_weights(_oracle_cfg(TINY), seed=13, std=0.2)
+    prompt = list(range(100, 150))
+    with tempfile.TemporaryDirectory() as tmp:
+        eng, keep = _engine(tmp, TINY, w, max_tokens=128, max_new_tokens=16)
+        req = edge_fm.Request(0, prompt)
+        req.set_ignore_stop_tokens(True)
+        base = eng.generate(req).token_ids()
+        del eng
+        # fixed-prefix slot: the prefix is prefilled at warmup, generate prefills the suffix
+        eng, keep = _engine(tmp, TINY, w, max_tokens=128, max_new_tokens=16, prefix_token_ids=prompt[:20])
+        req = edge_fm.Request(0, prompt)
+        req.set_ignore_stop_tokens(True)
+        assert eng.generate(req).token_ids() == base
+        # stop tokens truncate after the first hit, inclusive
+        req2 = edge_fm.Request(0, prompt)
+        req2.set_stop_token_ids([base[3]])
+        got = eng.generate(req2).token_ids()
+        assert got == base[: base.index(base[3]) + 1]
+        del eng
+        # generated-token cap: min(max_new_tokens, max_tokens - len + 1)
+        eng, keep = _engine(tmp, TINY, w, max_tokens=55, max_new_tokens=16)
+        req = edge_fm.Request(0, prompt)
+        req.set_ignore_stop_tokens(True)
+        got = eng.generate(req).token_ids()
+        assert got == base[: 55 - 50 + 1]
+        # invalid request id / empty request / out-of-vocab ids raise InvalidRequestError
+        with pytest.raises(edge_fm.InvalidRequestError):
+            eng.generate(edge_fm.Request(7, prompt))
+        with pytest.raises(edge_fm.InvalidRequestError):
+            eng.generate(edge_fm.Request(0, []))
+        with pytest.raises(edge_fm.InvalidRequestError):
+            eng.generate(edge_fm.Request(0, [1, 2, TINY.vocab]))
+
+
+def test_tiny_vl_mrope_with_custom_embeddings(gpu):
+    shape = TINY_VL
+    cfg = _oracle_cfg(shape)
+    w = O.random_weights(cfg, seed=14, std=0.2)
+    n_vis, n_txt = 24, 8
+    embed_token_id = 900
+    ids = [embed_token_id + i for i in range(n_vis)] + list(range(10, 10 + n_txt))
+    vis = (torch.randn(n_vis, shape.hidden, generator=torch.Generator().manual_seed(5))).to(torch.bfloat16)
+    # (t, h, w) grid 1 x 4 x 6 for the vision rows, then text positions continue
+    t = torch.zeros(n_vis, dtype=torch.int32)
+    hh = torch.arange(n_vis, dtype=torch.int32) // 6
+    ww = torch.arange(n_vis, dtype=torch.int32) % 6
+    start = int(max(hh.max(), ww.max())) + 1
+    txt = torch.arange(start, start + n_txt, dtype=torch.int32)
+    pos = torch.stack([torch.cat([t, txt]), torch.cat([hh, txt]), torch.cat([ww, txt])]).contiguous()
+    with tempfile.TemporaryDirectory() as tmp:
+        eng, keep = _engine(tmp, shape, w, max_tokens=96, max_new_tokens=12, model_name="qwen2_5_vl")
+        vis_g = vis.to("cuda:0")
+        pos_g = pos.to("cuda:0")
+        req = edge_fm.Request(0, ids, edge_fm.Tensor(vis_g.data_ptr(), list(vis_g.shape), edge_fm.DType.BFloat16,
+                                                     edge_fm.Device.GPU, 0, False), embed_token_id,
+                              edge_fm.Tensor(pos_g.data_ptr(), [3, len(ids)], edge_fm.DType.Int32,
+                                             edge_fm.Device.GPU, 0, False))
+        req.set_ignore_stop_tokens(True)
+        toks = eng.generate(req).token_ids()
+    assert len(toks) == 12
+    orc = O.Qwen2Oracle(cfg, O.fuse_weights(cfg, w), max_tokens=96)
+    emb = O.embedding(torch.tensor(ids, dtype=torch.int32), w["model.embed_tokens.weight"], vis, embed_token_id)
+    last = int(pos.max())
+
+    def dpos(i):  # decode step i+1 position: last + 1 + i (qwen2_5.cpp:932-955)
+        return torch.full((3, 1), last + 1 + i, dtype=torch.int32)
+
+    steps = _teacher_forced(orc, torch.tensor(ids, dtype=torch.int32), toks, embeds=emb, pos=pos, decode_pos=dpos)
+    exact = _check_against_oracle(toks, steps, tol=0.05)
+    assert exact >= 10
+
+
+def test_qwen25_1p5b_shape_greedy_matches_oracle(gpu):
+    """Full Qwen2.5-1.5B shape (28 layers, vocab 151936, tied head), random-init
+    N(0, 0.02): 64-token prompt, 10 greedy tokens checked against the oracle."""
+    shape = S.QWEN25_1P5B
+    cfg = _oracle_cfg(shape)
+    w = O.random_weights(cfg, seed=21, std=0.02)
+    prompt = torch.randint(0, shape.vocab, (64,), generator=torch.Generator().manual_seed(4)).to(torch.int32)
+    with tempfile.TemporaryDirectory() as tmp:
+        eng, keep = _engine(tmp, shape, w, max_tokens=256, max_new_tokens=10)
+        req = edge_fm.Request(0, prompt.tolist())
+        req.set_ignore_stop_tokens(True)
+        toks = eng.generate(req).token_ids()
+        del eng, keep
+    torch.cuda.empty_cache()
+    orc = O.Qwen2Oracle(cfg, O.fuse_weights(cfg, w), max_tokens=256, cache_f32=True)
+    exact = _check_against_oracle(toks, _teacher_forced(orc, prompt, toks), tol=0.05)
+    assert exact >= 8
