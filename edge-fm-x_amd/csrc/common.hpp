@@ -1,8 +1,8 @@
 // Shared device helpers for the gfx950 kernels of the EdgeFM hot path.
 //
 // Activations and weights are stored as raw bf16 bit patterns (uint16_t) and all
-// arithmetic is fp32. Conversions are written out here so the rounding rule
-// (round-to-nearest-even, quiet NaN) is explicit and identical in every kernel.
+// arithmetic is fp32. Every fp32 -> bf16 rounding goes through the helpers below
+// (round-to-nearest-even, quiet NaN), so the rule is identical in every kernel.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -20,14 +20,10 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
     return __uint_as_float(bits16 << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16; NaN inputs map to a quiet NaN.
+// fp32 -> bf16 with round-to-nearest-even (NaN -> quiet NaN), using the gfx950
+// conversion instruction v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) {
-        return (u >> 16) | 0x40u;
-    }
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+    return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)f);
 }
 
 __device__ __forceinline__ float round_bf16(float f) {
@@ -38,8 +34,13 @@ __device__ __forceinline__ float round_bf16(float f) {
 __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+    bf16x2_t v;
+    v.x = (__bf16)lo;
+    v.y = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 // Unpack 8 bf16 (one 16-byte vector) into fp32.

@@ -24,7 +24,7 @@
 
 namespace efm {
 
-enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ADD_NORM = 2 };
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ADD_NORM = 2, PRO_ATTN_MERGE = 3 };
 enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_TOP1 = 4 };
 
 // Weight-stream load used by the GEMV main loop (non-temporal: weights are read once
@@ -56,7 +56,16 @@ struct GemvArgs {
     ArgMax* partials;           // TOP1: one per workgroup
     uint32_t* counter;          // TOP1: arrival counter (zero between launches)
     int32_t* token_out;
+    // ATTN_MERGE: decode-attention split partials (efm_decode_attention_partials)
+    const float* o_part;        // [Hkv][split_cap][G][hd]
+    const float* ml_part;       // [Hkv][split_cap][G][2]
+    int split_cap, keys_per_split, head_dim, group;
+    const uint32_t* attn_len;   // *attn_len = attended rows (clamped to attn_max_len)
+    uint32_t attn_max_len;
 };
+
+constexpr int kMergeMaxSplits = 8;
+constexpr int kMergeMaxHeads = 64;
 
 template <int PRO>
 __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, bf16_t* xs, float* red) {
@@ -65,6 +74,55 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, bf16_t* xs, flo
     uint4* xs4 = reinterpret_cast<uint4*>(xs);
     if (PRO == PRO_PLAIN) {
         for (int c = threadIdx.x; c < C; c += kGemvThreads) xs4[c] = x4[c];
+        return;
+    }
+    if (PRO == PRO_ATTN_MERGE) {
+        // x[h*hd + d] = bf16( sum_s w[h][s] * o_part[kvh][s][g][d] ),
+        // w[h][s] = exp2(m_s - M) / sum_s exp2(m_s - M) l_s  (log-sum-exp merge of the splits)
+        __shared__ float sw[kMergeMaxHeads * kMergeMaxSplits];
+        const uint32_t L = min(a.attn_len[0], a.attn_max_len);
+        const int kps = a.keys_per_split;
+        const int nsplit = (L == 0) ? 1 : (int)min((uint32_t)a.split_cap, (L + kps - 1) / kps);
+        const int hd = a.head_dim, G = a.group;
+        const int Hq = a.K / hd;
+        for (int i = threadIdx.x; i < Hq * nsplit; i += kGemvThreads) {
+            const int h = i / nsplit, sidx = i % nsplit;
+            const size_t idx = ((size_t)(h / G) * a.split_cap + sidx) * G + (h % G);
+            sw[i] = a.ml_part[idx * 2];
+        }
+        __syncthreads();
+        if (threadIdx.x < Hq) {
+            const int h = threadIdx.x;
+            float M = -INFINITY;
+            for (int j = 0; j < nsplit; ++j) M = fmaxf(M, sw[h * nsplit + j]);
+            float den = 0.f, w[kMergeMaxSplits];
+            for (int j = 0; j < nsplit; ++j) {
+                const size_t idx = ((size_t)(h / G) * a.split_cap + j) * G + (h % G);
+                const float m = sw[h * nsplit + j];
+                w[j] = (m == -INFINITY) ? 0.f : exp2f(m - M);
+                den = fmaf(w[j], a.ml_part[idx * 2 + 1], den);
+            }
+            const float inv = (den > 0.f) ? 1.f / den : 0.f;
+            for (int j = 0; j < nsplit; ++j) sw[h * nsplit + j] = w[j] * inv;
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < (a.K >> 2); c += kGemvThreads) {
+            const int n0 = c * 4, h = n0 / hd, d0 = n0 % hd;
+            const float* op = a.o_part + ((size_t)(h / G) * a.split_cap * G + (h % G)) * hd + d0;
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < nsplit; ++j) {
+                const float4 v = *reinterpret_cast<const float4*>(op + (size_t)j * G * hd);
+                const float wj = sw[h * nsplit + j];
+                acc[0] = fmaf(wj, v.x, acc[0]);
+                acc[1] = fmaf(wj, v.y, acc[1]);
+                acc[2] = fmaf(wj, v.z, acc[2]);
+                acc[3] = fmaf(wj, v.w, acc[3]);
+            }
+            uint2 pk;
+            pk.x = pack_bf16x2(acc[0], acc[1]);
+            pk.y = pack_bf16x2(acc[2], acc[3]);
+            reinterpret_cast<uint2*>(xs)[c] = pk;
+        }
         return;
     }
     float s[kProMax][8];
@@ -470,6 +528,44 @@ extern "C" int efm_decode_norm_gate_up_swiglu(int32_t hidden, int32_t inter, flo
     a.eps = eps;
     a.y = out;
     return gemv_launch<PRO_ADD_NORM, EPI_SWIGLU>(gemv_pick(hidden, inter, 2, 1024, false), a, stream);
+}
+
+namespace efm {
+int decode_split_cap(int num_kv_heads, uint32_t max_kv_len);
+int decode_keys_per_split();
+size_t decode_workspace_bytes(const efm_attention_ctx* ctx, uint32_t max_kv_len);
+size_t decode_ml_offset(const efm_attention_ctx* ctx, uint32_t max_kv_len);
+int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
+}  // namespace efm
+
+extern "C" int efm_decode_attention_merge_o_proj(const efm_attention_ctx* ctx, const uint32_t* d_kv_len,
+                                                 uint32_t max_kv_len, const void* workspace,
+                                                 size_t workspace_bytes, const void* w_o, int32_t hidden, void* out,
+                                                 hipStream_t stream) {
+    int rc = validate_attention_ctx(ctx, "attention_merge_o_proj");
+    if (rc) return rc;
+    if (d_kv_len == nullptr || workspace == nullptr || w_o == nullptr || out == nullptr)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "attention_merge_o_proj: null pointer");
+    const int q_dim = (int)(ctx->num_qo_heads * ctx->head_dim);
+    rc = gemv_check(q_dim, hidden, w_o, workspace, out, false);
+    if (rc) return rc;
+    const int cap = decode_split_cap((int)ctx->num_kv_heads, max_kv_len);
+    if ((int64_t)cap > kMergeMaxSplits || (int)ctx->num_qo_heads > kMergeMaxHeads)
+        return set_error(EFM_ERR_UNSUPPORTED, "attention_merge_o_proj: %d splits / %u heads exceed the fused merge",
+                         cap, ctx->num_qo_heads);
+    if (workspace_bytes < decode_workspace_bytes(ctx, max_kv_len))
+        return set_error(EFM_ERR_WORKSPACE, "attention_merge_o_proj: workspace too small");
+    GemvArgs a = gemv_args(q_dim, hidden, w_o, workspace);
+    a.y = out;
+    a.o_part = static_cast<const float*>(workspace);
+    a.ml_part = reinterpret_cast<const float*>(static_cast<const char*>(workspace) + decode_ml_offset(ctx, max_kv_len));
+    a.split_cap = cap;
+    a.keys_per_split = decode_keys_per_split();
+    a.head_dim = (int)ctx->head_dim;
+    a.group = (int)(ctx->num_qo_heads / ctx->num_kv_heads);
+    a.attn_len = d_kv_len;
+    a.attn_max_len = max_kv_len;
+    return gemv_launch<PRO_ATTN_MERGE, EPI_BF16>(gemv_pick(q_dim, hidden, 1, 1024, false), a, stream);
 }
 
 extern "C" int efm_decode_norm_lm_head_top1(int32_t hidden, int64_t vocab, float eps, const void* h,

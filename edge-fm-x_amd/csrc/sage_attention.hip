@@ -1,0 +1,388 @@
+// SageAttention-style prefill attention for gfx950: K smoothing, per-128-token-block
+// symmetric int8 quantisation of Q and K, QK^T on the int8 matrix cores
+// (v_mfma_i32_32x32x32_i8) with exact int32 accumulation, fp32 online softmax, and
+// P.V on the bf16 matrix cores with fp32 accumulation (the EdgeFM
+// reference names the feature, README.md:23, but has no implementation).
+//
+// Definition (Zhang et al., SageAttention, 2024, with the choices fixed here):
+//   kmean[h][d] = fp32( sum_j K[j][h][d] (float64) / L )       (softmax-invariant shift)
+//   per (128-token block b, head h): scale = max|x| / 127 (1 for an all-zero block),
+//   x8 = clamp(round_half_even(x / scale), -127, 127), with x = Q or K - kmean
+//   score_log2(i, j) = float(int32(Q8_i . K8_j)) * ((sq * sk) * (log2(e) / sqrt(hd)))
+//   causal: query i sees keys j <= i + (L - S); P rounded to bf16 for the PV product.
+//
+// Three launches: K mean (one workgroup per KV head, float64 accumulation), block
+// quantisation of Q and K (one workgroup per block x head), attention (one workgroup =
+// 128 query rows of one head, 64-key tiles staged in LDS as int8 K and transposed V).
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace efm {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef int int32x4_t __attribute__((ext_vector_type(4)));
+typedef int int32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kSageBlock = 128;
+constexpr int kSageThreads = 256;
+constexpr int kSageQ = 128;   // query rows per attention workgroup
+constexpr int kSageKV = 64;   // keys per LDS tile
+
+// ---- K mean over tokens: grid (Hkv), 256 threads --------------------------------
+__global__ __launch_bounds__(kSageThreads) void sage_kmean_kernel(const bf16_t* k, int L, int k_sn, int k_sh, int hd,
+                                                                  float* kmean) {
+    __shared__ double part[kSageThreads];
+    const int h = blockIdx.x;
+    const int P = kSageThreads / hd;
+    const int d = threadIdx.x % hd, p = threadIdx.x / hd;
+    double s = 0.0;
+    if (p < P) {
+        for (int j = p; j < L; j += P) s += (double)bf16_to_f32(k[(size_t)j * k_sn + (size_t)h * k_sh + d]);
+    }
+    part[threadIdx.x] = s;
+    __syncthreads();
+    if (threadIdx.x < hd) {
+        double t = 0.0;
+        for (int q = 0; q < P; ++q) t += part[q * hd + threadIdx.x];
+        kmean[h * hd + threadIdx.x] = (float)(t / (double)L);
+    }
+}
+
+// ---- block quantisation: grid (blocks, H), 256 threads --------------------------
+// dst [T][H][hd] int8 (contiguous), scales [blocks][H].
+__global__ __launch_bounds__(kSageThreads) void sage_quant_kernel(const bf16_t* src, int T, int H, int sn, int sh,
+                                                                  int hd, const float* kmean, int8_t* dst,
+                                                                  float* scales) {
+    __shared__ float red[kSageThreads / kWave];
+    const int b = blockIdx.x, h = blockIdx.y;
+    const int t0 = b * kSageBlock;
+    const int rows = min(kSageBlock, T - t0);
+    const int cpr = hd / 8;  // 16-byte chunks per row
+    const int nch = rows * cpr;
+    constexpr int kMaxPer = kSageBlock * 128 / 8 / kSageThreads;  // 8
+    float x[kMaxPer][8];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxPer; ++i) {
+        const int c = threadIdx.x + i * kSageThreads;
+        if (c < nch) {
+            const int r = c / cpr, d0 = (c % cpr) * 8;
+            unpack8(*reinterpret_cast<const uint4*>(src + (size_t)(t0 + r) * sn + (size_t)h * sh + d0), x[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                if (kmean != nullptr) x[i][e] -= kmean[h * hd + d0 + e];
+                amax = fmaxf(amax, fabsf(x[i][e]));
+            }
+        }
+    }
+    amax = wave_max(amax);
+    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = amax;
+    __syncthreads();
+    float m = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSageThreads / kWave; ++w) m = fmaxf(m, red[w]);
+    const float scale = (m > 0.f) ? m / 127.0f : 1.0f;
+    if (threadIdx.x == 0) scales[b * H + h] = scale;
+#pragma unroll
+    for (int i = 0; i < kMaxPer; ++i) {
+        const int c = threadIdx.x + i * kSageThreads;
+        if (c < nch) {
+            const int r = c / cpr, d0 = (c % cpr) * 8;
+            uint32_t w[2] = {0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float qv = rintf(x[i][e] / scale);
+                qv = fminf(fmaxf(qv, -127.f), 127.f);
+                w[e / 4] |= ((uint32_t)((int)qv & 0xff)) << (8 * (e % 4));
+            }
+            *reinterpret_cast<uint2*>(dst + ((size_t)(t0 + r) * H + h) * hd + d0) = make_uint2(w[0], w[1]);
+        }
+    }
+}
+
+// ---- attention -----------------------------------------------------------------
+struct SageArgs {
+    const int8_t* q8;    // [S][Hq][hd]
+    const int8_t* k8;    // [L][Hkv][hd]
+    const float* sq;     // [ceil(S/128)][Hq]
+    const float* sk;     // [ceil(L/128)][Hkv]
+    const bf16_t* v;
+    bf16_t* o;
+    int S, L, Hq, Hkv;
+    int v_sn, v_sh;
+    int causal;
+    float scale_log2;
+};
+
+union Pack8 {
+    bf16x8_t v;
+    uint4 u;
+    uint32_t w[4];
+};
+
+template <int HD>
+__global__ __launch_bounds__(kSageThreads) void sage_attn_kernel(SageArgs a) {
+    constexpr int KS8 = HD / 32;       // int8 MFMA k-steps
+    constexpr int DT = HD / 32;        // d tiles of O^T
+    constexpr int KP = HD + 16;        // LDS pitch of the int8 K tile (bytes)
+    constexpr int VP = kSageKV + 8;    // LDS pitch of the V^T tile (bf16)
+    __shared__ __align__(16) int8_t Ks[kSageKV * KP];
+    __shared__ __align__(16) bf16_t Vt[HD * VP];
+
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave, lane = tid % kWave;
+    const int ql = lane % 32, hh = lane / 32;
+    const int nqt = (a.S + kSageQ - 1) / kSageQ;
+    const int qt = nqt - 1 - (int)blockIdx.x;  // heavy (late) tiles first
+    const int head = blockIdx.y;
+    const int kvh = head / (a.Hq / a.Hkv);
+    const int q0 = qt * kSageQ + wave * 32;
+    const int qi = q0 + ql;
+    const int diag = a.L - a.S;
+
+    // Q8 B operand: lane row qi, k = ks*32 + hh*16 + byte
+    int32x4_t qf[KS8];
+    {
+        const bool qv = qi < a.S;
+        const int8_t* qp = a.q8 + ((size_t)(qv ? qi : 0) * a.Hq + head) * HD + hh * 16;
+#pragma unroll
+        for (int ks = 0; ks < KS8; ++ks) {
+            const uint4 u = qv ? *reinterpret_cast<const uint4*>(qp + ks * 32) : make_uint4(0, 0, 0, 0);
+            qf[ks] = int32x4_t{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+        }
+    }
+    const float qscale = (qi < a.S) ? a.sq[(qi / kSageBlock) * a.Hq + head] * 1.0f : 0.f;
+
+    f32x16_t oacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[t][e] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+    const int q_last = min(a.S - 1, qt * kSageQ + kSageQ - 1);
+    const int kv_end = a.causal ? min(a.L, q_last + diag + 1) : a.L;
+    const int ntiles = (kv_end + kSageKV - 1) / kSageKV;
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int k0 = t * kSageKV;
+        __syncthreads();
+        constexpr int KCH = HD / 16;  // 16-byte chunks per int8 K row
+        for (int c = tid; c < kSageKV * KCH; c += kSageThreads) {
+            const int kr = c / KCH, off = (c % KCH) * 16;
+            const int j = k0 + kr;
+            const uint4 u = (j < kv_end) ? *reinterpret_cast<const uint4*>(a.k8 + ((size_t)j * a.Hkv + kvh) * HD + off)
+                                         : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4*>(&Ks[kr * KP + off]) = u;
+        }
+        constexpr int VCH = HD / 8;
+        for (int c = tid; c < kSageKV * VCH; c += kSageThreads) {
+            const int kr = c / VCH, d0 = (c % VCH) * 8;
+            const int j = k0 + kr;
+            const uint4 u = (j < kv_end)
+                                ? *reinterpret_cast<const uint4*>(a.v + (size_t)j * a.v_sn + (size_t)kvh * a.v_sh + d0)
+                                : make_uint4(0, 0, 0, 0);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                Vt[(d0 + 2 * e) * VP + kr] = (bf16_t)(w[e] & 0xffffu);
+                Vt[(d0 + 2 * e + 1) * VP + kr] = (bf16_t)(w[e] >> 16);
+            }
+        }
+        __syncthreads();
+        if (q0 >= a.S) continue;
+        // sk is per 128-key block; a 64-key tile lies inside one block
+        const float coef_k = a.sk[(k0 / kSageBlock) * a.Hkv + kvh];
+        const float coef = (qscale * coef_k) * a.scale_log2;
+#pragma unroll
+        for (int sub = 0; sub < kSageKV / 32; ++sub) {
+            const int kb0 = k0 + sub * 32;
+            if (a.causal && kb0 > q0 + 31 + diag) break;
+            if (kb0 >= kv_end) break;
+            int32x16_t acc;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[e] = 0;
+#pragma unroll
+            for (int ks = 0; ks < KS8; ++ks) {
+                const uint4 u = *reinterpret_cast<const uint4*>(&Ks[(sub * 32 + ql) * KP + ks * 32 + hh * 16]);
+                const int32x4_t ka = int32x4_t{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka, qf[ks], acc, 0, 0, 0);
+            }
+            float s[16];
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int j = kb0 + (e / 4) * 8 + hh * 4 + (e % 4);
+                const bool ok = (j < kv_end) && (!a.causal || j <= qi + diag);
+                s[e] = ok ? (float)acc[e] * coef : -INFINITY;
+                mloc = fmaxf(mloc, s[e]);
+            }
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+            float p[16], psum = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                p[e] = (m_new == -INFINITY) ? 0.f : exp2f(s[e] - m_new);
+                psum += p[e];
+            }
+            psum += __shfl_xor(psum, 32, kWave);
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                Pack8 pb;
+                pb.u = pack8(&p[8 * kb]);
+                const int kcol = sub * 32 + kb * 16 + hh * 4;
+#pragma unroll
+                for (int tt = 0; tt < DT; ++tt) {
+                    const bf16_t* vr = &Vt[(tt * 32 + ql) * VP + kcol];
+                    Pack8 va;
+                    const uint2 v0 = *reinterpret_cast<const uint2*>(vr);
+                    const uint2 v1 = *reinterpret_cast<const uint2*>(vr + 8);
+                    va.w[0] = v0.x;
+                    va.w[1] = v0.y;
+                    va.w[2] = v1.x;
+                    va.w[3] = v1.y;
+                    oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, pb.v, oacc[tt], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    if (qi >= a.S) return;
+    const float inv = (l_run > 0.f) ? 1.f / l_run : 0.f;
+    bf16_t* op = a.o + ((size_t)qi * a.Hq + head) * HD;
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = tt * 32 + g * 8 + hh * 4;
+            uint2 w;
+            w.x = pack_bf16x2(oacc[tt][g * 4 + 0] * inv, oacc[tt][g * 4 + 1] * inv);
+            w.y = pack_bf16x2(oacc[tt][g * 4 + 2] * inv, oacc[tt][g * 4 + 3] * inv);
+            *reinterpret_cast<uint2*>(op + d) = w;
+        }
+}
+
+int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
+
+static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct SageWs {
+    size_t q8, k8, sq, sk, km;
+    size_t total() const { return q8 + k8 + sq + sk + km; }
+};
+
+static SageWs sage_ws(const efm_attention_ctx* c, uint32_t S, uint32_t L) {
+    SageWs w;
+    const size_t hd = c->head_dim;
+    w.q8 = al256((size_t)S * c->num_qo_heads * hd);
+    w.k8 = al256((size_t)L * c->num_kv_heads * hd);
+    w.sq = al256((size_t)((S + kSageBlock - 1) / kSageBlock) * c->num_qo_heads * 4);
+    w.sk = al256((size_t)((L + kSageBlock - 1) / kSageBlock) * c->num_kv_heads * 4);
+    w.km = al256((size_t)c->num_kv_heads * hd * 4);
+    return w;
+}
+
+static int sage_quantize_impl(const efm_attention_ctx* c, const void* q, const void* k, uint32_t S, uint32_t L,
+                              int8_t* q8, float* sq, int8_t* k8, float* sk, float* kmean, hipStream_t stream) {
+    const int hd = (int)c->head_dim;
+    const int q_sn = c->q_stride_n ? (int)c->q_stride_n : (int)(c->num_qo_heads * hd);
+    const int q_sh = c->q_stride_h ? (int)c->q_stride_h : hd;
+    const int k_sn = c->k_stride_n ? (int)c->k_stride_n : (int)(c->num_kv_heads * hd);
+    const int k_sh = c->k_stride_h ? (int)c->k_stride_h : hd;
+    hipLaunchKernelGGL(sage_kmean_kernel, dim3(c->num_kv_heads), dim3(kSageThreads), 0, stream,
+                       static_cast<const bf16_t*>(k), (int)L, k_sn, k_sh, hd, kmean);
+    int rc = check_launch("sage kmean");
+    if (rc) return rc;
+    hipLaunchKernelGGL(sage_quant_kernel, dim3((S + kSageBlock - 1) / kSageBlock, c->num_qo_heads),
+                       dim3(kSageThreads), 0, stream, static_cast<const bf16_t*>(q), (int)S, (int)c->num_qo_heads,
+                       q_sn, q_sh, hd, (const float*)nullptr, q8, sq);
+    rc = check_launch("sage quant q");
+    if (rc) return rc;
+    hipLaunchKernelGGL(sage_quant_kernel, dim3((L + kSageBlock - 1) / kSageBlock, c->num_kv_heads),
+                       dim3(kSageThreads), 0, stream, static_cast<const bf16_t*>(k), (int)L, (int)c->num_kv_heads,
+                       k_sn, k_sh, hd, (const float*)kmean, k8, sk);
+    return check_launch("sage quant k");
+}
+
+static int sage_validate(const efm_attention_ctx* c, uint32_t S, uint32_t L) {
+    int rc = validate_attention_ctx(c, "sage_attention");
+    if (rc) return rc;
+    if (c->pos_encoding != EFM_POS_NONE)
+        return set_error(EFM_ERR_UNSUPPORTED,
+                         "sage_attention: rotate q/k before quantisation (pos_encoding must be NONE)");
+    if (L < S) return set_error(EFM_ERR_INVALID_ARGUMENT, "sage_attention: kv_len %u < qo_len %u", L, S);
+    if (L == 0 || S > (1u << 20) || L > (1u << 24))
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "sage_attention: bad sequence lengths");
+    return EFM_OK;
+}
+
+}  // namespace efm
+
+using namespace efm;
+
+extern "C" size_t efm_attention_prefill_sage_int8_workspace_bytes(const efm_attention_ctx* ctx, uint32_t qo_len,
+                                                                   uint32_t kv_len) {
+    if (validate_attention_ctx(ctx, "sage_attention") != EFM_OK) return 0;
+    return sage_ws(ctx, qo_len, kv_len).total();
+}
+
+extern "C" int efm_sage_quantize(const efm_attention_ctx* ctx, const void* q, const void* k, uint32_t qo_len,
+                                 uint32_t kv_len, int8_t* q8, float* q_scales, int8_t* k8, float* k_scales,
+                                 float* k_mean, hipStream_t stream) {
+    int rc = sage_validate(ctx, qo_len, kv_len);
+    if (rc) return rc;
+    if (!q || !k || !q8 || !q_scales || !k8 || !k_scales || !k_mean)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "sage_quantize: null pointer");
+    if (qo_len == 0) return EFM_OK;
+    return sage_quantize_impl(ctx, q, k, qo_len, kv_len, q8, q_scales, k8, k_scales, k_mean, stream);
+}
+
+extern "C" int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, const void* q, const void* k,
+                                               const void* v, void* o, uint32_t qo_len, uint32_t kv_len,
+                                               int32_t causal, void* workspace, size_t workspace_bytes,
+                                               hipStream_t stream) {
+    int rc = sage_validate(ctx, qo_len, kv_len);
+    if (rc) return rc;
+    if (!q || !k || !v || !o) return set_error(EFM_ERR_INVALID_ARGUMENT, "sage_attention: null tensor pointer");
+    if (qo_len == 0) return EFM_OK;
+    const SageWs w = sage_ws(ctx, qo_len, kv_len);
+    if (workspace == nullptr || workspace_bytes < w.total())
+        return set_error(EFM_ERR_WORKSPACE, "sage_attention: workspace of %zu bytes required", w.total());
+    char* p = static_cast<char*>(workspace);
+    int8_t* q8 = reinterpret_cast<int8_t*>(p);
+    int8_t* k8 = reinterpret_cast<int8_t*>(p + w.q8);
+    float* sq = reinterpret_cast<float*>(p + w.q8 + w.k8);
+    float* sk = reinterpret_cast<float*>(p + w.q8 + w.k8 + w.sq);
+    float* km = reinterpret_cast<float*>(p + w.q8 + w.k8 + w.sq + w.sk);
+    rc = sage_quantize_impl(ctx, q, k, qo_len, kv_len, q8, sq, k8, sk, km, stream);
+    if (rc) return rc;
+    const int hd = (int)ctx->head_dim;
+    SageArgs a;
+    a.q8 = q8;
+    a.k8 = k8;
+    a.sq = sq;
+    a.sk = sk;
+    a.v = static_cast<const bf16_t*>(v);
+    a.o = static_cast<bf16_t*>(o);
+    a.S = (int)qo_len;
+    a.L = (int)kv_len;
+    a.Hq = (int)ctx->num_qo_heads;
+    a.Hkv = (int)ctx->num_kv_heads;
+    a.v_sn = ctx->kv_stride_n ? (int)ctx->kv_stride_n : a.Hkv * hd;
+    a.v_sh = ctx->kv_stride_h ? (int)ctx->kv_stride_h : hd;
+    a.causal = causal != 0;
+    a.scale_log2 = (float)(1.4426950408889634 / sqrt((double)hd));
+    dim3 grid((qo_len + kSageQ - 1) / kSageQ, a.Hq), block(kSageThreads);
+    if (hd == 128) hipLaunchKernelGGL(sage_attn_kernel<128>, grid, block, 0, stream, a);
+    else hipLaunchKernelGGL(sage_attn_kernel<64>, grid, block, 0, stream, a);
+    return check_launch("sage_attention");
+}

@@ -71,8 +71,17 @@ SIGNATURES = {
     "efm_attention_decode_workspace_bytes": (c_size_t, [POINTER(AttentionCtx), c_uint32]),
     "efm_attention_decode": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
                                        c_void_p, c_uint32, c_void_p, c_size_t, c_void_p]),
+    "efm_decode_attention_partials": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p,
+                                                c_uint32, c_void_p, c_size_t, c_void_p]),
+    "efm_decode_attention_merge_o_proj": (c_int32, [POINTER(AttentionCtx), c_void_p, c_uint32, c_void_p, c_size_t,
+                                                    c_void_p, c_int32, c_void_p, c_void_p]),
     "efm_attention_prefill": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
                                         c_uint32, c_int32, c_void_p]),
+    "efm_attention_prefill_sage_int8_workspace_bytes": (c_size_t, [POINTER(AttentionCtx), c_uint32, c_uint32]),
+    "efm_attention_prefill_sage_int8": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p,
+                                                  c_uint32, c_uint32, c_int32, c_void_p, c_size_t, c_void_p]),
+    "efm_sage_quantize": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_uint32, c_uint32, c_void_p, c_void_p,
+                                    c_void_p, c_void_p, c_void_p, c_void_p]),
     "efm_mrope": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
                             c_int32, c_int32, c_int32, c_int32, c_float, c_float, c_void_p]),
     "efm_decode_mrope_write_kv": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32,

@@ -593,6 +593,9 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
     const efm_attention_ctx c = to_c_ctx(attn_ctx());
     check<InternalError>(!attn_ws_.empty() && attn_ws_.nbytes() >= efm_attention_decode_workspace_bytes(&c, max_kv_len),
                          "decode workspace not reserved for this cache length");
+    // The merge folds into the o_proj prologue when the cache needs at most 8 splits of
+    // 128 keys (max_kv_len <= 1024) and the model has at most 64 query heads.
+    fused_attn_merge_ = max_kv_len <= 1024 && m_.heads <= 64;
     for (int l = 0; l < m_.layers; ++l) {
         const Layer& Ly = layers_[l];
         // input norm (+ residual) + QKV + bias, K/V straight into the cache slot
@@ -616,12 +619,24 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
                                                 m_.theta, 1.0f, d_kv_len, stream),
                       "decode mrope + kv write");
         }
-        efm_check(efm_attention_decode(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], dec_attn_.data_ptr(), 0,
-                                       d_kv_len, max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(), stream),
-                  "decode attention");
-        efm_check(efm_linear(1, QD, H, dec_attn_.data_ptr(), Ly.o_w.data_ptr(), nullptr, dec_a_.data_ptr(),
-                             EFM_DTYPE_BF16, stream),
-                  "decode o_proj");
+        if (fused_attn_merge_) {
+            // split partials, merged in the o_proj prologue (two launches instead of an
+            // attention kernel with an in-kernel merge plus the o_proj)
+            efm_check(efm_decode_attention_partials(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], d_kv_len,
+                                                    max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(), stream),
+                      "decode attention partials");
+            efm_check(efm_decode_attention_merge_o_proj(&c, d_kv_len, max_kv_len, attn_ws_.data_ptr(),
+                                                        attn_ws_.nbytes(), Ly.o_w.data_ptr(), H, dec_a_.data_ptr(),
+                                                        stream),
+                      "decode attention merge + o_proj");
+        } else {
+            efm_check(efm_attention_decode(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], dec_attn_.data_ptr(), 0,
+                                           d_kv_len, max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(), stream),
+                      "decode attention");
+            efm_check(efm_linear(1, QD, H, dec_attn_.data_ptr(), Ly.o_w.data_ptr(), nullptr, dec_a_.data_ptr(),
+                                 EFM_DTYPE_BF16, stream),
+                      "decode o_proj");
+        }
         efm_check(efm_decode_norm_gate_up_swiglu(H, m_.inter, m_.eps, dec_a_.data_ptr(), dec_res_[0].data_ptr(),
                                                  dec_res_[1].data_ptr(), Ly.post_norm.data_ptr(),
                                                  Ly.gu_w.data_ptr(), dec_mid_.data_ptr(), stream),

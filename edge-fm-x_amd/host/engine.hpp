@@ -168,6 +168,7 @@ private:
     // decode scratch
     Tensor dec_h_, dec_res_[2], dec_q_, dec_attn_, dec_a_, dec_mid_, dec_kvtmp_, dec_one_, top1_ws_;
     Tensor attn_ws_;
+    bool fused_attn_merge_ = false;
     // prefill scratch (grow-only)
     int32_t pf_cap_ = 0;
     Tensor pf_hidden_, pf_res_, pf_norm_, pf_qkv_, pf_attn_, pf_mid_;

@@ -89,6 +89,29 @@ int efm_attention_decode(const efm_attention_ctx* ctx, const void* q, const void
                          void* o, uint32_t kv_len, const uint32_t* d_kv_len, uint32_t max_kv_len,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Decode attention split partials only (no in-kernel merge): every split writes its
+ * unnormalised fp32 output and (max, sum) of exp2-domain scores into `workspace`
+ * (efm_attention_decode_workspace_bytes(ctx, max_kv_len) bytes); the partials are
+ * consumed by efm_decode_attention_merge_o_proj. Same semantics and length handling
+ * as efm_attention_decode with d_kv_len (required). Part of the split of
+ * AttentionOp::forward_decode + the o_proj LinearImpl::forward
+ * (src/models/qwen2_5/qwen2_5.cpp:831-847) into two launches with the merge folded
+ * into the projection. */
+int efm_decode_attention_partials(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v,
+                                  const uint32_t* d_kv_len, uint32_t max_kv_len, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream);
+
+/* o_proj over the merged attention output: out[hidden] = bf16(merge(partials)) . W_o^T,
+ * where merge is the log-sum-exp combination of the splits written by
+ * efm_decode_attention_partials with the same ctx, d_kv_len, max_kv_len and workspace;
+ * the merged vector is rounded to bf16 before the projection, as the unfused
+ * attention output would be. Supports up to 8 splits (max_kv_len <= 1024) and 64 query
+ * heads. Replaces the o_proj LinearImpl::forward (role attention_output,
+ * src/layers/linear.cu:41-58). */
+int efm_decode_attention_merge_o_proj(const efm_attention_ctx* ctx, const uint32_t* d_kv_len, uint32_t max_kv_len,
+                                      const void* workspace, size_t workspace_bytes, const void* w_o, int32_t hidden,
+                                      void* out, hipStream_t stream);
+
 /* Causal / non-causal GQA prefill attention on the matrix cores. q [qo_len, Hq, hd]
  * (q_stride_* may point into a fused QKV buffer), k, v [kv_len, Hkv, hd] with
  * kv_len >= qo_len; o [qo_len, Hq * hd] contiguous. Query i has RoPE position
@@ -99,6 +122,25 @@ int efm_attention_decode(const efm_attention_ctx* ctx, const void* q, const void
  * forward_prefill_impl, src/operators/attention_op.cu:1345-1426). */
 int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v, void* o,
                           uint32_t qo_len, uint32_t kv_len, int32_t causal, hipStream_t stream);
+
+/* SageAttention-style prefill attention (named but not implemented by
+ * the reference, README.md:23). K is smoothed by its per-(KV head, channel) mean over
+ * tokens (float64 sum, rounded to fp32); Q and the smoothed K are quantised to int8 per
+ * (128-token block, head) with scale = max|x| / 127 (1 for an all-zero block) and
+ * round-half-even; QK^T runs on the int8 matrix cores with exact int32 accumulation,
+ * score_log2 = float(acc) * ((sq * sk) * (log2(e) / sqrt(hd))); fp32 online softmax;
+ * P (bf16) . V with fp32 accumulation. Layouts as efm_attention_prefill; pos_encoding
+ * must be EFM_POS_NONE (rotate before quantising). workspace: see the size query. */
+size_t efm_attention_prefill_sage_int8_workspace_bytes(const efm_attention_ctx* ctx, uint32_t qo_len,
+                                                       uint32_t kv_len);
+int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v,
+                                    void* o, uint32_t qo_len, uint32_t kv_len, int32_t causal, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream);
+/* The quantisation step alone (exposed so the integer path can be checked bit-exactly):
+ * q8 [qo_len, Hq, hd] int8, q_scales [ceil(qo_len/128), Hq], k8 [kv_len, Hkv, hd] int8,
+ * k_scales [ceil(kv_len/128), Hkv], k_mean [Hkv, hd]. */
+int efm_sage_quantize(const efm_attention_ctx* ctx, const void* q, const void* k, uint32_t qo_len, uint32_t kv_len,
+                      int8_t* q8, float* q_scales, int8_t* k8, float* k_scales, float* k_mean, hipStream_t stream);
 
 /* M-RoPE in place (src/layers/attention.cu:17-118, AttentionLayer::apply_mrope).
  * q [seq_len, Hq, hd] and k [seq_len, Hkv, hd] with token strides q_stride_n /

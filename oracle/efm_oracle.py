@@ -409,3 +409,87 @@ class Qwen2Oracle:
             nxt = forced[i] if forced is not None else tok
             logits = self.forward(st, torch.tensor([nxt], dtype=torch.int32))
         return out
+
+
+# ---------------------------------------------------------------------------------
+# SageAttention-style int8 QK^T prefill attention. The reference
+# has no implementation (README.md:23 only names it), so this restates the published
+# method (Zhang et al., "SageAttention: Accurate 8-Bit Attention for Plug-and-play
+# Inference Acceleration", 2024) with the choices fixed here:
+#   * K smoothing: K_s = K - mean_over_tokens(K) per (KV head, channel); the mean is
+#     accumulated in float64 and rounded once to fp32. Softmax is invariant to it.
+#   * symmetric int8 per (128-token block, head) for Q and for K_s:
+#     scale = max|x| / 127 (fp32; 1.0 for an all-zero block), x8 = round-half-even(x /
+#     scale) clamped to [-127, 127].
+#   * S = int32(Q8 . K8^T); score_log2 = float(S) * ((sq * sk) * (log2(e) / sqrt(hd)))
+#     in fp32, in that order.
+#   * causal online softmax in fp32 (base 2), P rounded to bf16, O = P . V with fp32
+#     accumulation, normalised, rounded to bf16.
+# The integer part (Q8, K8, scales, S) is bit-exact by construction and is compared
+# exactly; the output is compared with the bf16 attention within tolerance.
+# ---------------------------------------------------------------------------------
+SAGE_BLOCK = 128
+
+
+def sage_kmean(k: torch.Tensor) -> torch.Tensor:
+    """Per (KV head, channel) mean over tokens: float64 sum / L, rounded to fp32. k [L, Hkv, hd]."""
+    return (k.to(torch.float64).sum(0) / k.shape[0]).to(F32)
+
+
+def sage_quant_blocks(x: torch.Tensor, block: int = SAGE_BLOCK):
+    """Symmetric int8 per (block of tokens, head). x fp32 [T, H, hd] -> (int8 [T, H, hd],
+    scales fp32 [ceil(T/block), H])."""
+    T, H, hd = x.shape
+    nb = (T + block - 1) // block
+    q8 = torch.empty(T, H, hd, dtype=torch.int8)
+    scales = torch.empty(nb, H, dtype=F32)
+    for b in range(nb):
+        xb = x[b * block:(b + 1) * block]                       # [t, H, hd]
+        amax = xb.abs().amax(dim=(0, 2))                        # [H] fp32
+        sc = torch.where(amax > 0, amax / torch.tensor(127.0, dtype=F32), torch.ones_like(amax))
+        scales[b] = sc
+        q8[b * block:(b + 1) * block] = torch.clamp(torch.round(xb / sc[None, :, None]), -127, 127).to(torch.int8)
+    return q8, scales
+
+
+def sage_quantize(q: torch.Tensor, k: torch.Tensor, block: int = SAGE_BLOCK):
+    """(q8, sq, k8, sk, kmean) for q [S, Hq, hd], k [L, Hkv, hd] (bf16)."""
+    kmean = sage_kmean(k)
+    ks = k.to(F32) - kmean[None]
+    q8, sq = sage_quant_blocks(q.to(F32), block)
+    k8, sk = sage_quant_blocks(ks, block)
+    return q8, sq, k8, sk, kmean
+
+
+def sage_scores_int32(q8: torch.Tensor, k8: torch.Tensor, num_kv_heads: int) -> torch.Tensor:
+    """Exact int32 Q8 . K8^T per query head: [Hq, S, L] (int64 matmul, no overflow)."""
+    G = q8.shape[1] // num_kv_heads
+    kk = k8.to(torch.int64).repeat_interleave(G, dim=1)          # [L, Hq, hd]
+    return torch.einsum("shd,lhd->hsl", q8.to(torch.int64), kk).to(torch.int32)
+
+
+def sage_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_kv_heads: int, causal: bool = True,
+                   block: int = SAGE_BLOCK) -> torch.Tensor:
+    """SageAttention-style prefill attention, q [S, Hq, hd], k/v [L, Hkv, hd] bf16 -> bf16
+    [S, Hq, hd]. Query i sees keys j <= i + (L - S) when causal."""
+    S, Hq, hd = q.shape
+    L = k.shape[0]
+    G = Hq // num_kv_heads
+    q8, sq, k8, sk, _ = sage_quantize(q, k, block)
+    acc = sage_scores_int32(q8, k8, num_kv_heads).to(F32)        # [Hq, S, L]
+    scale_log2 = torch.tensor(1.4426950408889634 / math.sqrt(hd), dtype=F32)
+    sq_row = sq.repeat_interleave(block, 0)[:S].t()               # [Hq, S]
+    sk_col = sk.repeat_interleave(block, 0)[:L].t().repeat_interleave(G, 0)  # [Hq, L]
+    coef = (sq_row[:, :, None] * sk_col[:, None, :]) * scale_log2
+    s2 = acc * coef                                              # base-2 scores
+    if causal:
+        i = torch.arange(S).unsqueeze(1)
+        j = torch.arange(L).unsqueeze(0)
+        s2 = s2.masked_fill((j > i + (L - S)).unsqueeze(0), float("-inf"))
+    m = s2.amax(-1, keepdim=True)
+    p = torch.exp2(s2 - m)
+    den = p.sum(-1, keepdim=True)
+    pb = p.to(BF16).to(F32)                                      # P rounded to bf16 for PV
+    vf = v.to(F32).repeat_interleave(G, dim=1)                    # [L, Hq, hd]
+    o = torch.einsum("hsl,lhd->shd", pb, vf) / den.permute(1, 0, 2)
+    return o.to(BF16)

@@ -488,3 +488,102 @@ def test_finalize_indexed(gpu):
     torch.cuda.synchronize()
     assert resp.cpu().tolist() == [100 + i for i in range(8)]
     assert int(step.item()) == 10 and int(d_len.item()) == 20
+
+
+@pytest.mark.parametrize("hq,hkv,hd,hidden", [pytest.param(12, 2, 128, 1536, id="1p5b"),
+                                               pytest.param(14, 2, 64, 896, id="0p5b"),
+                                               pytest.param(16, 2, 128, 2048, id="vl3b")])
+@pytest.mark.parametrize("kv_len", [1, 100, 640, 767])
+def test_decode_attention_partials_merge_o_proj(gpu, hq, hkv, hd, hidden, kv_len):
+    """Split partials + merge folded into the o_proj GEMV == attention then o_proj."""
+    torch.manual_seed(0)
+    max_kv = 768
+    q = torch.randn(1, hq, hd, dtype=torch.bfloat16)
+    k = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16)
+    v = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16)
+    wo = (torch.randn(hidden, hq * hd) * 0.02).to(torch.bfloat16)
+    ctx = C.make_attention_ctx(hq, hkv, hd)
+    qg, kg, vg, wg = q.to(gpu), k.to(gpu), v.to(gpu), wo.to(gpu)
+    d_len = torch.tensor([kv_len], dtype=torch.int32, device=gpu)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=gpu)
+    out = torch.empty(1, hidden, dtype=torch.bfloat16, device=gpu)
+    for _ in range(2):
+        C.call("efm_decode_attention_partials", ctx, ptr(qg), ptr(kg), ptr(vg), ptr(d_len), max_kv, ptr(ws),
+               ws.numel(), stream())
+        C.call("efm_decode_attention_merge_o_proj", ctx, ptr(d_len), max_kv, ptr(ws), ws.numel(), ptr(wg), hidden,
+               ptr(out), stream())
+    torch.cuda.synchronize()
+    att = O.attention_decode(q, k, v, kv_len, O.AttnCtx(hq, hkv, hd))
+    ref = O.linear(att.reshape(1, hq * hd), wo)
+    assert_close_bf16(out, ref, what=f"partials+merge kv={kv_len}")
+
+
+def _sage_inputs(S, L, hq, hkv, hd, seed=0, gpu=None):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(S, hq, hd, generator=g).to(torch.bfloat16)
+    k = (torch.randn(L, hkv, hd, generator=g) + 0.5).to(torch.bfloat16)  # non-zero channel means
+    v = torch.randn(L, hkv, hd, generator=g).to(torch.bfloat16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("S,L,hq,hkv,hd", [(300, 300, 28, 4, 128), (129, 257, 4, 2, 64), (1, 40, 8, 1, 128)])
+def test_sage_quantize_bit_exact(gpu, S, L, hq, hkv, hd):
+    """The int8 path is exact: Q8 / K8 / scales equal the oracle bit for bit (K8 and its
+    scales recomputed from the GPU's float64-accumulated K mean)."""
+    q, k, v = _sage_inputs(S, L, hq, hkv, hd)
+    ctx = C.make_attention_ctx(hq, hkv, hd, rope=False)
+    qg, kg = q.to(gpu), k.to(gpu)
+    nbq, nbk = (S + 127) // 128, (L + 127) // 128
+    q8 = torch.empty(S, hq, hd, dtype=torch.int8, device=gpu)
+    k8 = torch.empty(L, hkv, hd, dtype=torch.int8, device=gpu)
+    sq = torch.empty(nbq, hq, dtype=torch.float32, device=gpu)
+    sk = torch.empty(nbk, hkv, dtype=torch.float32, device=gpu)
+    km = torch.empty(hkv, hd, dtype=torch.float32, device=gpu)
+    C.call("efm_sage_quantize", ctx, ptr(qg), ptr(kg), S, L, ptr(q8), ptr(sq), ptr(k8), ptr(sk), ptr(km), stream())
+    torch.cuda.synchronize()
+    ref_km = O.sage_kmean(k)
+    torch.testing.assert_close(km.cpu(), ref_km, rtol=2e-7, atol=1e-7)
+    rq8, rsq = O.sage_quant_blocks(q.float())
+    rk8, rsk = O.sage_quant_blocks(k.float() - km.cpu()[None])
+    assert torch.equal(q8.cpu(), rq8) and torch.equal(sq.cpu(), rsq)
+    assert torch.equal(k8.cpu(), rk8) and torch.equal(sk.cpu(), rsk)
+
+
+@pytest.mark.parametrize("S,L,hq,hkv,hd", [(512, 512, 28, 4, 128), (300, 700, 8, 2, 128), (200, 200, 14, 2, 64)])
+def test_sage_attention_matches_oracle(gpu, S, L, hq, hkv, hd):
+    q, k, v = _sage_inputs(S, L, hq, hkv, hd, seed=1)
+    ctx = C.make_attention_ctx(hq, hkv, hd, rope=False)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    o = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
+    ws = torch.zeros(C.load().efm_attention_prefill_sage_int8_workspace_bytes(ctx, S, L), dtype=torch.uint8,
+                     device=gpu)
+    C.call("efm_attention_prefill_sage_int8", ctx, ptr(qg), ptr(kg), ptr(vg), ptr(o), S, L, 1, ptr(ws), ws.numel(),
+           stream())
+    torch.cuda.synchronize()
+    ref = O.sage_attention(q, k, v, hkv, causal=True)
+    assert_close_bf16(o.reshape(S, hq, hd), ref, rtol=2e-2, atol=2e-2, what="sage vs int8 oracle")
+    bf = O.attention_prefill(q, k, v, O.AttnCtx(hq, hkv, hd, rope=False), causal=True)
+    err = (o.reshape(S, hq, hd).float().cpu() - bf.float()).abs()
+    assert float(err.mean()) < 5e-3 and float(err.max()) < 0.1, (float(err.mean()), float(err.max()))
+
+
+def test_sage_attention_c4_shape_vs_bf16_kernel(gpu):
+    """BASELINE config 4 at full size (28/4 heads, hd 128, S 4096, causal): int8 path vs
+    the bf16 MFMA prefill kernel on the same inputs (size-independent error bounds)."""
+    S, hq, hkv, hd = 4096, 28, 4, 128
+    g = torch.Generator(device=gpu).manual_seed(7)
+    q = torch.randn(S, hq, hd, generator=g, device=gpu).to(torch.bfloat16)
+    k = torch.randn(S, hkv, hd, generator=g, device=gpu).to(torch.bfloat16)
+    v = torch.randn(S, hkv, hd, generator=g, device=gpu).to(torch.bfloat16)
+    ctx = C.make_attention_ctx(hq, hkv, hd, rope=False)
+    o8 = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
+    ob = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
+    ws = torch.zeros(C.load().efm_attention_prefill_sage_int8_workspace_bytes(ctx, S, S), dtype=torch.uint8,
+                     device=gpu)
+    C.call("efm_attention_prefill_sage_int8", ctx, ptr(q), ptr(k), ptr(v), ptr(o8), S, S, 1, ptr(ws), ws.numel(),
+           stream())
+    C.call("efm_attention_prefill", ctx, ptr(q), ptr(k), ptr(v), ptr(ob), S, S, 1, stream())
+    torch.cuda.synchronize()
+    err = (o8.float() - ob.float()).abs()
+    cos = torch.nn.functional.cosine_similarity(o8.float().flatten(), ob.float().flatten(), dim=0)
+    assert float(err.mean()) < 5e-3 and float(cos) > 0.999, (float(err.mean()), float(cos))

@@ -298,3 +298,63 @@ def test_generate_token_cap():
     orc = O.Qwen2Oracle(TINY, O.fuse_weights(TINY, w), max_tokens=12)
     steps = orc.generate_greedy(torch.arange(8, dtype=torch.int32), 100)
     assert len(steps) == 12 - 8 + 1
+
+
+# ----------------------------------------------------------------------------------
+# SageAttention-style int8 path (no reference implementation: pinned by exact integer
+# brute force, quantisation error bounds, the softmax shift invariance K smoothing
+# relies on, and agreement with the bf16 attention).
+def test_sage_int32_scores_brute_force():
+    g = torch.Generator().manual_seed(0)
+    q8 = torch.randint(-127, 128, (3, 4, 8), generator=g).to(torch.int8)
+    k8 = torch.randint(-127, 128, (5, 2, 8), generator=g).to(torch.int8)
+    s = O.sage_scores_int32(q8, k8, 2)
+    for h in range(4):
+        for i in range(3):
+            for j in range(5):
+                ref = sum(int(q8[i, h, d]) * int(k8[j, h // 2, d]) for d in range(8))
+                assert int(s[h, i, j]) == ref
+
+
+def test_sage_quant_blocks_bounds_and_rounding():
+    x = torch.randn(300, 3, 16) * 3
+    x[128:256, 1] = 0.0  # an all-zero (block, head)
+    q8, sc = O.sage_quant_blocks(x)
+    assert sc.shape == (3, 3) and float(sc[1, 1]) == 1.0 and q8[128:256, 1].abs().sum() == 0
+    for b in range(3):
+        xb = x[b * 128:(b + 1) * 128]
+        amax = xb.abs().amax(dim=(0, 2))
+        for h in range(3):
+            if float(amax[h]) > 0:
+                assert float(sc[b, h]) == float(np.float32(amax[h]) / np.float32(127.0))
+        deq = q8[b * 128:(b + 1) * 128].float() * sc[b][None, :, None]
+        assert float((deq - xb).abs().max()) <= float(sc[b].max()) * 0.5 + 1e-6
+    assert int(q8.abs().max()) <= 127
+    # round half to even at exact ties
+    t = torch.tensor([[[127.0, 0.5, 1.5, -2.5, 2.5]]])
+    q, s = O.sage_quant_blocks(t)
+    assert float(s[0, 0]) == 1.0 and q.flatten().tolist() == [127, 0, 2, -2, 2]
+
+
+def test_sage_k_smoothing_is_softmax_invariant():
+    """Adding a per-channel constant to K does not change the (exact) attention, which is
+    what makes subtracting the K mean legal; the oracle's result barely moves."""
+    torch.manual_seed(1)
+    q = torch.randn(64, 4, 64).to(torch.bfloat16)
+    k = torch.randn(64, 2, 64).to(torch.bfloat16)
+    v = torch.randn(64, 2, 64).to(torch.bfloat16)
+    shift = (torch.randn(1, 2, 64) * 4).to(torch.bfloat16).float()
+    k2 = (k.float() + shift).to(torch.bfloat16)
+    o1 = O.sage_attention(q, k, v, 2).float()
+    o2 = O.sage_attention(q, k2, v, 2).float()
+    assert float((o1 - o2).abs().mean()) < 5e-3
+
+
+def test_sage_attention_close_to_bf16_attention():
+    torch.manual_seed(2)
+    q = torch.randn(200, 4, 128).to(torch.bfloat16)
+    k = torch.randn(260, 2, 128).to(torch.bfloat16)
+    v = torch.randn(260, 2, 128).to(torch.bfloat16)
+    o = O.sage_attention(q, k, v, 2).float()
+    r = O.attention_prefill(q, k, v, O.AttnCtx(4, 2, 128, rope=False)).float()
+    assert float((o - r).abs().mean()) < 5e-3 and float((o - r).abs().max()) < 0.1
