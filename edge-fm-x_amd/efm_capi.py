@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_size_t, c_uint32, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libedgefm_hip.so")
@@ -97,6 +97,8 @@ SIGNATURES = {
     "efm_lm_head_top1": (c_int32, [c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "efm_sampler_greedy_workspace_bytes": (c_size_t, [c_int64, c_int64]),
     "efm_sampler_greedy": (c_int32, [c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "efm_sampler_top_p": (c_int32, [c_int64, c_void_p, c_float, c_float, c_uint64, c_uint64, c_void_p, c_void_p,
+                                    c_void_p]),
     "efm_embedding_lookup": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int32,
                                        c_void_p, c_void_p]),
     "efm_copy_decode_kv_cache_slots": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,

@@ -683,6 +683,10 @@ struct EventTimer {
 }  // namespace
 
 StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_path) {
+    // sampling parameters are validated before any device work (src/layers/sampler.cu:130-132)
+    check<ConfigurationError>(cfg_.temperature() >= 0.0f,
+                              "temperature must be non-negative. Got: " + std::to_string(cfg_.temperature()));
+    check<ConfigurationError>(cfg_.top_p() > 0.0f, "top_p must be positive. Got: " + std::to_string(cfg_.top_p()));
     device_id_ = cfg_.device_id();
     hip_check(hipSetDevice(device_id_), "hipSetDevice");
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
@@ -749,7 +753,12 @@ void StandardEngine::sample_logits(uint32_t) {
                   "greedy sampler");
         return;
     }
-    throw ConfigurationError("temperature sampling is not available in this build");
+    // temperature / top-p: the draw's counter is the response index of the token being
+    // sampled (device-resident step counter), so graph replays draw fresh numbers
+    const int32_t* d_step = static_cast<const int32_t*>(state_.data_ptr()) + 1;
+    efm_check(efm_sampler_top_p(model_->config().vocab, static_cast<const float*>(logits_.data_ptr()), T,
+                                cfg_.top_p(), cfg_.seed(), 0, d_step, tok, stream_),
+              "top-p sampler");
 }
 
 void StandardEngine::run_decode_step(int32_t request_id, bool) {

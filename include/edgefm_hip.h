@@ -206,6 +206,21 @@ int efm_sampler_greedy(int64_t rows, int64_t vocab, const float* logits, int32_t
                        size_t workspace_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------
+ * Temperature / top-p sampler of one fp32 logits row (the non-greedy branch of
+ * SamplerLayer::forward_sampling, src/layers/sampler.cu:251-298, which samples
+ * softmax(logits / T) by inverse CDF; top-p is an addition). Exact integer-mass
+ * definition: e_i = expf((l_i - max l) / T), w_i = rint(e_i * 2^44); nucleus = all ids
+ * when top_p >= 1, else the ids with e_i >= tau, tau the largest value whose upper set
+ * holds >= ceil(top_p * sum w) of the mass; the 24-bit draw x = Philox4x32-10(counter =
+ * offset (+ *d_offset when d_offset is not NULL), key = seed).x >> 8 picks the smallest
+ * nucleus id whose prefix mass exceeds floor(N * x / 2^24). No workspace.
+ * temperature >= 1e-6 (smaller means greedy: use efm_sampler_greedy), top_p > 0,
+ * 1 <= vocab <= 2^20.
+ * ---------------------------------------------------------------------------------- */
+int efm_sampler_top_p(int64_t vocab, const float* logits, float temperature, float top_p, uint64_t seed,
+                      uint64_t offset, const int32_t* d_offset, int32_t* token_out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------
  * Embedding lookup (src/layers/embed_head.cu:23-164). out[t,:] = table[ids[t],:];
  * ids in [embed_token_id, embed_token_id + n_custom) take custom_embeddings rows when
  * custom_embeddings != NULL and embed_token_id >= 0; ids outside the vocabulary give

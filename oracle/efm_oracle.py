@@ -493,3 +493,114 @@ def sage_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_kv_hea
     vf = v.to(F32).repeat_interleave(G, dim=1)                    # [L, Hq, hd]
     o = torch.einsum("hsl,lhd->shd", pb, vf) / den.permute(1, 0, 2)
     return o.to(BF16)
+
+
+# ---------------------------------------------------------------------------------
+# Temperature / top-p sampling. The reference samples with
+# FlashInfer OnlineSoftmax + SamplingFromProb(seed, offset 0) and has no top-p
+# (src/layers/sampler.cu:251-298); its RNG is cuRAND inside un-vendored FlashInfer, so
+# index parity with it is unpinned. This build defines the sampler exactly, with all
+# mass arithmetic in integers so that it is reproducible bit for bit:
+#   m      = max_i l_i                                   (fp32 logits)
+#   e_i    = expf((l_i - m) / T)                         (fp32 subtract, divide, exp)
+#   w_i    = rint(e_i * 2^44)                            (uint64; sum fits for V <= 2^20)
+#   W      = sum_i w_i
+#   nucleus: all i when top_p >= 1, else { i : e_i >= tau } with tau the largest fp32
+#            value such that sum_{e_j >= tau} w_j >= ceil(top_p * W) (top_p as float64)
+#   x      = philox4x32_10(counter = (off_lo, off_hi, 0, 0), key = (seed_lo, seed_hi))[0]
+#   r      = floor(N * (x >> 8) / 2^24), N = nucleus mass  (0 <= r < N)
+#   token  = the smallest nucleus index i with sum_{j <= i, j in nucleus} w_j > r
+# offset = the index of the token in the response, so every step draws a fresh number.
+# Philox4x32-10 is pinned by its published known-answer vectors.
+# ---------------------------------------------------------------------------------
+_PHILOX_M0, _PHILOX_M1 = 0xD2511F53, 0xCD9E8D57
+_PHILOX_W0, _PHILOX_W1 = 0x9E3779B9, 0xBB67AE85
+SAMPLE_MASS_BITS = 44
+
+
+def philox4x32_10(counter, key):
+    """Philox4x32 with 10 rounds (Salmon, Moraes, Dror, Shaw, SC'11). counter: 4 uint32,
+    key: 2 uint32 -> 4 uint32."""
+    c = [int(x) & 0xFFFFFFFF for x in counter]
+    k0, k1 = int(key[0]) & 0xFFFFFFFF, int(key[1]) & 0xFFFFFFFF
+    for r in range(10):
+        p0 = _PHILOX_M0 * c[0]
+        p1 = _PHILOX_M1 * c[2]
+        hi0, lo0 = p0 >> 32, p0 & 0xFFFFFFFF
+        hi1, lo1 = p1 >> 32, p1 & 0xFFFFFFFF
+        c = [hi1 ^ c[1] ^ k0, lo1, hi0 ^ c[3] ^ k1, lo0]
+        if r < 9:
+            k0 = (k0 + _PHILOX_W0) & 0xFFFFFFFF
+            k1 = (k1 + _PHILOX_W1) & 0xFFFFFFFF
+    return c
+
+
+def sampling_bits(seed: int, offset: int) -> int:
+    """The 24 random bits one sampling call consumes."""
+    x = philox4x32_10((offset & 0xFFFFFFFF, (offset >> 32) & 0xFFFFFFFF, 0, 0),
+                      (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF))[0]
+    return x >> 8
+
+
+def sample_masses(logits, temperature: float):
+    """fp32 e_i and uint64 w_i of one logits row (numpy float32 arithmetic)."""
+    l = np.asarray(logits, dtype=np.float32)
+    x = (l - l.max()) / np.float32(temperature)
+    e = np.exp(x.astype(np.float32)).astype(np.float32)
+    w = np.rint(e.astype(np.float64) * float(2 ** SAMPLE_MASS_BITS)).astype(np.uint64)
+    return e, w
+
+
+def nucleus_threshold(e, w, top_p: float):
+    """Smallest kept e (tau) of the top-p nucleus; brute force over the distinct values."""
+    total = int(w.sum(dtype=np.uint64))
+    need = math.ceil(float(top_p) * total)
+    order = np.argsort(-e, kind="stable")
+    vals = e[order]
+    cum = np.cumsum(w[order], dtype=np.uint64)
+    # first position whose cumulative mass reaches `need`, then widen to all ties
+    pos = int(np.searchsorted(cum, np.uint64(need), side="left"))
+    pos = min(pos, len(vals) - 1)
+    return np.float32(vals[pos])
+
+
+def sample_top_p(logits, temperature: float, top_p: float, seed: int, offset: int):
+    """Returns (token, info) for one fp32 logits row. info: nucleus size, tau, masses and
+    the relative distance of the random target to the nearest CDF boundary."""
+    top_p = float(np.float32(top_p))
+    e, w = sample_masses(logits, temperature)
+    if top_p >= 1.0:
+        keep = np.ones(e.shape, dtype=bool)
+        tau = np.float32(0.0)
+    else:
+        tau = nucleus_threshold(e, w, top_p)
+        keep = e >= tau
+    wk = np.where(keep, w, np.uint64(0))
+    n_mass = int(wk.sum(dtype=np.uint64))
+    bits = sampling_bits(seed, offset)
+    r = (n_mass * bits) >> 24
+    cdf = np.cumsum(wk, dtype=np.uint64)
+    token = int(np.searchsorted(cdf, np.uint64(r), side="right"))
+    return token, {"nucleus": int(keep.sum()), "tau": float(tau), "total": int(w.sum(dtype=np.uint64)),
+                   "mass": n_mass, "r": r}
+
+
+def sample_margin(logits, temperature: float, top_p: float, seed: int, offset: int) -> float:
+    """Smallest relative distance of a sampling decision to its boundary: the random
+    target r to any CDF step (/ N) and ceil(top_p * W) to any cumulative sorted mass
+    (/ W). Below ~1e-6 a one-ulp difference in some e_i may change the token."""
+    top_p = float(np.float32(top_p))
+    e, w = sample_masses(logits, temperature)
+    total = int(w.sum(dtype=np.uint64))
+    margin = 1.0
+    keep = np.ones(e.shape, dtype=bool)
+    if top_p < 1.0:
+        need = math.ceil(float(top_p) * total)
+        cum = np.cumsum(w[np.argsort(-e, kind="stable")], dtype=np.uint64).astype(np.float64)
+        margin = min(margin, float(np.min(np.abs(cum - need))) / total)
+        keep = e >= nucleus_threshold(e, w, top_p)
+    wk = np.where(keep, w, np.uint64(0))
+    n_mass = int(wk.sum(dtype=np.uint64))
+    r = (n_mass * sampling_bits(seed, offset)) >> 24
+    cdf = np.cumsum(wk, dtype=np.uint64).astype(np.float64)
+    return min(margin, float(np.min(np.abs(cdf - r))) / max(n_mass, 1))

@@ -185,3 +185,58 @@ def test_qwen25_1p5b_shape_greedy_matches_oracle(gpu):
     orc = O.Qwen2Oracle(cfg, O.fuse_weights(cfg, w), max_tokens=256, cache_f32=True)
     exact = _check_against_oracle(toks, _teacher_forced(orc, prompt, toks), tol=0.05)
     assert exact >= 8
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_tiny_top_p_sampling_matches_oracle(gpu, use_graph):
+    """temperature 0.8 / top-p 0.9: every token is the oracle sampler's choice on the
+    oracle's logits (teacher-forced on the GPU's tokens) with the draw counter = the
+    token's response index; a mismatch is accepted only where the decision lies within
+    10 % (relative mass) of a boundary, the reach of bf16 logit noise at T = 0.8."""
+    T, P, SEED = 0.8, 0.9, 5
+    w = O.random_weights(_oracle_cfg(TINY), seed=31, std=0.2)
+    prompt = torch.randint(0, TINY.vocab, (32,), generator=torch.Generator().manual_seed(8)).to(torch.int32)
+    with tempfile.TemporaryDirectory() as tmp:
+        eng, keep = _engine(tmp, TINY, w, max_tokens=128, max_new_tokens=32, use_graph=use_graph, temperature=T,
+                            top_p=P, seed=SEED)
+        req = edge_fm.Request(0, prompt.tolist())
+        req.set_ignore_stop_tokens(True)
+        toks = eng.generate(req).token_ids()
+        again = eng.generate(req).token_ids()
+        del eng
+    assert toks == again, "same seed must give the same tokens"
+    assert len(toks) == 32
+    orc = O.Qwen2Oracle(_oracle_cfg(TINY), O.fuse_weights(_oracle_cfg(TINY), w), max_tokens=128)
+    st = orc.new_state()
+    logits = orc.forward(st, prompt)
+    exact = 0
+    for i, tok in enumerate(toks):
+        lg = logits.numpy().astype("float32")
+        ref, _ = O.sample_top_p(lg, T, P, SEED, i)
+        if tok == ref:
+            exact += 1
+        else:
+            margin = O.sample_margin(lg, T, P, SEED, i)
+            assert margin < 0.1, f"step {i}: gpu {tok} vs oracle {ref}, margin {margin:.4f}"
+        logits = orc.forward(st, torch.tensor([tok], dtype=torch.int32))
+    assert exact >= 24
+
+
+def test_top_p_sampling_seeds_differ_and_config_checks(gpu):
+    w = O.random_weights(_oracle_cfg(TINY), seed=32, std=0.2)
+    prompt = list(range(10, 40))
+    outs = []
+    with tempfile.TemporaryDirectory() as tmp:
+        for seed in (1, 2):
+            eng, keep = _engine(tmp, TINY, w, max_tokens=128, max_new_tokens=24, temperature=1.0, top_p=0.95,
+                                seed=seed)
+            req = edge_fm.Request(0, prompt)
+            req.set_ignore_stop_tokens(True)
+            outs.append(eng.generate(req).token_ids())
+            del eng
+        assert outs[0] != outs[1]
+        mdir = S.write_model_dir(os.path.join(tmp, "model"), TINY)
+        for bad in (dict(temperature=-0.5), dict(temperature=0.7, top_p=0.0)):
+            ecfg = S.write_engine_config(os.path.join(tmp, "bad.json"), mdir, max_tokens=128, **bad)
+            with pytest.raises(edge_fm.ConfigurationError):
+                edge_fm.EdgeFM(ecfg)

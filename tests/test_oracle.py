@@ -358,3 +358,79 @@ def test_sage_attention_close_to_bf16_attention():
     o = O.sage_attention(q, k, v, 2).float()
     r = O.attention_prefill(q, k, v, O.AttnCtx(4, 2, 128, rope=False)).float()
     assert float((o - r).abs().mean()) < 5e-3 and float((o - r).abs().max()) < 0.1
+
+
+# ----------------------------------------------------------------------------------
+# Temperature / top-p sampler. The reference's RNG (cuRAND inside un-vendored
+# FlashInfer) is not reproducible here, so the oracle is pinned by the published
+# Philox4x32-10 known-answer vectors, brute force of the nucleus on tiny rows, and the
+# sampled distribution itself (chi-square against softmax(l / T) over the nucleus).
+@pytest.mark.parametrize("ctr,key,expect", [
+    ((0, 0, 0, 0), (0, 0), (0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8)),
+    ((0xffffffff,) * 4, (0xffffffff,) * 2, (0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd)),
+    ((0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344), (0xa4093822, 0x299f31d0),
+     (0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1)),
+])
+def test_philox4x32_10_known_answers(ctr, key, expect):
+    # Random123 kat_vectors, philox4x32_10 (Salmon et al., SC'11)
+    assert tuple(O.philox4x32_10(ctr, key)) == expect
+
+
+def _brute_nucleus(l, T, p):
+    """float64 probabilities, sorted descending, smallest prefix with mass >= p (all ties
+    of the last value included)."""
+    pr = np.exp((l.astype(np.float64) - l.max()) / T)
+    pr /= pr.sum()
+    order = sorted(range(len(l)), key=lambda i: -pr[i])
+    acc, kept = 0.0, []
+    for i in order:
+        if acc >= p * (1 - 1e-12):
+            if pr[i] < pr[kept[-1]]:
+                break
+        kept.append(i)
+        acc += pr[i]
+    return set(kept), pr
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_sampler_nucleus_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    for T, p in [(0.7, 0.9), (1.0, 0.5), (1.3, 0.95), (0.5, 0.3)]:
+        l = (rng.standard_normal(12) * 2).astype(np.float32)
+        want, _ = _brute_nucleus(l, T, p)
+        e, w = O.sample_masses(l, T)
+        tau = O.nucleus_threshold(e, w, p)
+        got = set(np.nonzero(e >= tau)[0].tolist())
+        assert got == want, (T, p, sorted(got), sorted(want))
+    # ties on the boundary value are all kept
+    l = np.array([3.0, 1.0, 1.0, 1.0, -2.0], dtype=np.float32)
+    e, w = O.sample_masses(l, 1.0)
+    assert set(np.nonzero(e >= O.nucleus_threshold(e, w, 0.8))[0].tolist()) == {0, 1, 2, 3}
+
+
+@pytest.mark.parametrize("T,p", [(0.7, 1.0), (0.7, 0.9), (1.5, 0.6)])
+def test_sampler_distribution_chi_square(T, p):
+    from scipy.stats import chisquare
+    l = np.array([2.0, 1.5, 1.0, 0.4, 0.0, -0.5, -1.0, -3.0], dtype=np.float32)
+    keep, pr = _brute_nucleus(l, T, p) if p < 1 else (set(range(len(l))), None)
+    if pr is None:
+        pr = np.exp((l.astype(np.float64) - l.max()) / T)
+        pr /= pr.sum()
+    n = 20000
+    counts = np.zeros(len(l))
+    for off in range(n):
+        tok, _ = O.sample_top_p(l, T, p, seed=1234, offset=off)
+        counts[tok] += 1
+    ids = sorted(keep)
+    assert counts[[i for i in range(len(l)) if i not in keep]].sum() == 0
+    expect = pr[ids] / pr[ids].sum() * n
+    assert chisquare(counts[ids], expect).pvalue > 1e-4
+
+
+def test_sampler_offsets_and_seeds_draw_fresh_numbers():
+    bits = [O.sampling_bits(7, off) for off in range(4096)]
+    assert len(set(bits)) > 4000
+    assert abs(np.mean(bits) / 2 ** 24 - 0.5) < 0.02
+    assert O.sampling_bits(7, 3) != O.sampling_bits(8, 3)
+    assert O.sampling_bits(1 << 40, 3) != O.sampling_bits(0, 3)   # high seed word is used
+    assert O.sampling_bits(7, 1 << 33) != O.sampling_bits(7, 0)   # high offset word is used
