@@ -61,15 +61,19 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 }
 
 // 8-wide bf16 dot product accumulated in fp32.
+// acc + a . b over 8 bf16 pairs in fp32, as four v_dot2c_f32_bf16 (each adds two exact
+// bf16 x bf16 products to the accumulator); no unpacking, a quarter of the VALU work of
+// scalar FMAs. Every GEMV shares this helper, so fused and unfused kernels agree bit for
+// bit.
 __device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float acc) {
-    acc = fmaf(lo_f32(a.x), lo_f32(b.x), acc);
-    acc = fmaf(hi_f32(a.x), hi_f32(b.x), acc);
-    acc = fmaf(lo_f32(a.y), lo_f32(b.y), acc);
-    acc = fmaf(hi_f32(a.y), hi_f32(b.y), acc);
-    acc = fmaf(lo_f32(a.z), lo_f32(b.z), acc);
-    acc = fmaf(hi_f32(a.z), hi_f32(b.z), acc);
-    acc = fmaf(lo_f32(a.w), lo_f32(b.w), acc);
-    acc = fmaf(hi_f32(a.w), hi_f32(b.w), acc);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.x), __builtin_bit_cast(bf16x2_t, b.x), acc,
+                                          false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.y), __builtin_bit_cast(bf16x2_t, b.y), acc,
+                                          false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.z), __builtin_bit_cast(bf16x2_t, b.z), acc,
+                                          false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.w), __builtin_bit_cast(bf16x2_t, b.w), acc,
+                                          false);
     return acc;
 }
 

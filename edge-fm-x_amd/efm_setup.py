@@ -76,13 +76,14 @@ def write_model_dir(path: str, shape: ModelShape, eos_token_id=None) -> str:
 def write_engine_config(path: str, model_dir: str, *, max_tokens: int = 4096, max_new_tokens: int = 256,
                         prefix_token_ids=None, use_graph: bool = True, temperature: float = 0.0,
                         top_p: float = 1.0, seed: int = 0, lm_head_top1: bool = True, model_name: str = "",
-                        operator_impl_table_path: str = "", extra_slots=None) -> str:
+                        operator_impl_table_path: str = "", extra_slots=None, decode_chain: bool = False) -> str:
     slots = [{"request_id": 0, "prefix_token_ids": list(prefix_token_ids or []), "max_tokens": max_tokens}]
     for s in extra_slots or []:
         slots.append(s)
     cfg = {
         "model_name": model_name,
-        "runtime": {"device": "gpu", "device_id": 0, "use_cuda_graph": use_graph, "lm_head_top1": lm_head_top1},
+        "runtime": {"device": "gpu", "device_id": 0, "use_cuda_graph": use_graph, "lm_head_top1": lm_head_top1,
+                    "decode_chain": decode_chain},
         "prefill_model_path": model_dir,
         "operator_impl_table_path": operator_impl_table_path,
         "kvcache": {"dtype": "bf16", "requests": slots},

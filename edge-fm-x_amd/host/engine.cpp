@@ -7,6 +7,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <chrono>
 #include <cstring>
 #include <filesystem>
@@ -181,6 +182,11 @@ bool EngineConfig::use_graph() const {
 }
 bool EngineConfig::lm_head_top1() const {
     return json_.contains("runtime") ? json_.at("runtime").get_bool("lm_head_top1", true) : true;
+}
+bool EngineConfig::decode_chain() const {
+    const char* env = std::getenv("EDGE_FM_DECODE_CHAIN");
+    if (env != nullptr && env[0] != '\0') return std::string(env) != "0";
+    return json_.contains("runtime") ? json_.at("runtime").get_bool("decode_chain", false) : false;
 }
 std::string EngineConfig::operator_table_path() const {
     std::string p = json_.get_string("operator_impl_table_path");
@@ -361,6 +367,7 @@ Qwen2_5::Qwen2_5(const EngineConfig& cfg, const ModelConfig& m, const std::unord
     : m_(m), device_id_(device_id) {
     model_name_ = cfg.model_name();
     hw_profile_ = cfg.hw_profile();
+    chain_enabled_ = cfg.decode_chain() && !m.mrope;
     table_path_ = cfg.operator_table_path();
     hip_check(hipSetDevice(device_id), "hipSetDevice");
     check<ConfigurationError>(m.hidden % 8 == 0 && m.inter % 8 == 0 && m.q_dim() % 8 == 0,
@@ -447,6 +454,21 @@ void Qwen2_5::reserve_decode(uint32_t max_kv_len) {
     const size_t bytes = efm_attention_decode_workspace_bytes(&c, max_kv_len);
     if (attn_ws_.empty() || attn_ws_.nbytes() < bytes)
         attn_ws_ = Tensor::zeros({(int64_t)bytes}, DType::UInt8, Device::GPU, device_id_);
+    if (uses_decode_chain(max_kv_len) && chain_ws_.empty()) {
+        const size_t cb = efm_decode_chain_workspace_bytes(m_.hidden, m_.inter);
+        chain_ws_ = Tensor::zeros({(int64_t)cb}, DType::UInt8, Device::GPU, device_id_);
+    }
+}
+
+bool Qwen2_5::uses_decode_chain(uint32_t max_kv_len) const {
+    if (!chain_enabled_) return false;
+    const efm_attention_ctx c = to_c_ctx(attn_ctx());
+    return efm_decode_chain_supported(&c, m_.hidden, m_.inter, max_kv_len) == EFM_OK;
+}
+
+void Qwen2_5::check_decode_status(hipStream_t stream) {
+    if (chain_ws_.empty()) return;
+    efm_check(efm_decode_chain_status(chain_ws_.data_ptr(), m_.hidden, m_.inter, stream), "decode chain");
 }
 
 AttentionOpContext Qwen2_5::attn_ctx() const {
@@ -593,6 +615,57 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
     const efm_attention_ctx c = to_c_ctx(attn_ctx());
     check<InternalError>(!attn_ws_.empty() && attn_ws_.nbytes() >= efm_attention_decode_workspace_bytes(&c, max_kv_len),
                          "decode workspace not reserved for this cache length");
+    if (!chain_ws_.empty() && uses_decode_chain(max_kv_len)) {
+        // layer 0: input RMSNorm + QKV; then per layer the attention partials and one
+        // persistent launch for o_proj .. next layer's QKV (the residual stream
+        // alternates between dec_res_[0] and dec_res_[1])
+        const Layer& L0 = layers_[0];
+        efm_check(efm_decode_norm_qkv(H, QD, KVD, m_.eps, dec_h_.data_ptr(), nullptr, dec_res_[0].data_ptr(),
+                                      L0.in_norm.data_ptr(), L0.qkv_w.data_ptr(), L0.qkv_b.data_ptr(),
+                                      dec_q_.data_ptr(), k_caches[0], v_caches[0], d_kv_len, stream),
+                  "decode norm+qkv");
+        for (int l = 0; l < m_.layers; ++l) {
+            const Layer& Ly = layers_[l];
+            const bool last = (l + 1 == m_.layers);
+            efm_check(efm_decode_attention_partials(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], d_kv_len,
+                                                    max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(), stream),
+                      "decode attention partials");
+            efm_decode_chain_layer d{};
+            d.w_o = Ly.o_w.data_ptr();
+            d.post_norm = Ly.post_norm.data_ptr();
+            d.w_up_gate = Ly.gu_w.data_ptr();
+            d.w_down = Ly.down_w.data_ptr();
+            if (!last) {
+                const Layer& Nx = layers_[l + 1];
+                d.in_norm_next = Nx.in_norm.data_ptr();
+                d.w_qkv_next = Nx.qkv_w.data_ptr();
+                d.b_qkv_next = Nx.qkv_b.data_ptr();
+                d.q_next = dec_q_.data_ptr();
+                d.k_cache_next = k_caches[l + 1];
+                d.v_cache_next = v_caches[l + 1];
+            }
+            efm_check(efm_decode_layer_chain(&c, H, m_.inter, m_.eps, &d, d_kv_len, max_kv_len, attn_ws_.data_ptr(),
+                                             attn_ws_.nbytes(), dec_res_[l % 2].data_ptr(),
+                                             dec_res_[(l + 1) % 2].data_ptr(), last ? dec_h_.data_ptr() : nullptr,
+                                             chain_ws_.data_ptr(), chain_ws_.nbytes(), stream),
+                      "decode layer chain");
+        }
+        void* res = dec_res_[m_.layers % 2].data_ptr();
+        if (logits == nullptr) {
+            efm_check(efm_decode_norm_lm_head_top1(H, m_.vocab, m_.eps, dec_h_.data_ptr(), res, final_norm_.data_ptr(),
+                                                   lm_head_.data_ptr(), token_buf, top1_ws_.data_ptr(),
+                                                   top1_ws_.nbytes(), stream),
+                      "decode lm head top1");
+        } else {
+            efm_check(efm_fused_add_rms_norm(1, (uint32_t)H, m_.eps, dec_h_.data_ptr(), res, final_norm_.data_ptr(),
+                                             stream),
+                      "decode final norm");
+            efm_check(efm_linear(1, H, m_.vocab, dec_h_.data_ptr(), lm_head_.data_ptr(), nullptr, logits,
+                                 EFM_DTYPE_F32, stream),
+                      "decode lm head");
+        }
+        return;
+    }
     // The merge folds into the o_proj prologue when the cache needs at most 8 splits of
     // 128 keys (max_kv_len <= 1024) and the model has at most 64 query heads.
     fused_attn_merge_ = max_kv_len <= 1024 && m_.heads <= 64;
@@ -897,6 +970,7 @@ Response StandardEngine::generate(const Request& req) {
     hip_check(hipMemcpyAsync(host.data(), response_dev_.data_ptr(), (size_t)n_gen * 4, hipMemcpyDeviceToHost, stream_),
               "response D2H");
     hip_check(hipStreamSynchronize(stream_), "generate sync");
+    model_->check_decode_status(stream_);
 
     // stop tokens truncate after the first hit, inclusive (standard_engine.cpp:1060-1068)
     if (!req.ignore_stop_tokens) {
@@ -923,6 +997,7 @@ Response StandardEngine::generate(const Request& req) {
     metrics_["decode_tokens_per_second"] = decode_ms > 0 ? steps * 1000.0 / decode_ms : 0.0;
     metrics_["tokens_per_second"] = (prefill_ms + decode_ms) > 0 ? n_gen * 1000.0 / (prefill_ms + decode_ms) : 0.0;
     metrics_["use_hip_graph"] = cfg_.use_graph() ? 1.0 : 0.0;
+    metrics_["decode_chain"] = model_->uses_decode_chain((uint32_t)slot.cfg.max_tokens) ? 1.0 : 0.0;
     Response r;
     r.token_ids = std::move(host);
     return r;

@@ -68,6 +68,10 @@ public:
     std::string hw_profile() const;
     bool use_graph() const;
     bool lm_head_top1() const;
+    // Persistent post-attention decode chain (runtime.decode_chain, default off: on
+    // MI355X its cross-workgroup exchanges cost more than the kernel boundaries they
+    // remove; EDGE_FM_DECODE_CHAIN=1 / 0 overrides the config).
+    bool decode_chain() const;
     std::string operator_table_path() const;
     std::string prefill_model_path() const;
     std::vector<KVSlotConfig> kv_slots() const;
@@ -150,6 +154,13 @@ public:
     // a decode step is captured into a graph: capture cannot allocate).
     void reserve_decode(uint32_t max_kv_len);
 
+    // Whether decode steps with caches of max_kv_len rows run the persistent
+    // post-attention chain (efm_decode_layer_chain) instead of the per-operator kernels.
+    bool uses_decode_chain(uint32_t max_kv_len) const;
+    // Throws DeviceError if a chain launch since the last check could not exchange its
+    // vectors in time (synchronises the stream).
+    void check_decode_status(hipStream_t stream);
+
 private:
     struct Layer {
         Tensor qkv_w, qkv_b, o_w, gu_w, down_w, in_norm, post_norm;
@@ -169,6 +180,8 @@ private:
     Tensor dec_h_, dec_res_[2], dec_q_, dec_attn_, dec_a_, dec_mid_, dec_kvtmp_, dec_one_, top1_ws_;
     Tensor attn_ws_;
     bool fused_attn_merge_ = false;
+    bool chain_enabled_ = false;   // config switch (text models only)
+    Tensor chain_ws_;
     // prefill scratch (grow-only)
     int32_t pf_cap_ = 0;
     Tensor pf_hidden_, pf_res_, pf_norm_, pf_qkv_, pf_attn_, pf_mid_;

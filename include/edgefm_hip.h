@@ -206,6 +206,49 @@ int efm_sampler_greedy(int64_t rows, int64_t vocab, const float* logits, int32_t
                        size_t workspace_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------
+ * Post-attention decode chain of one layer in one persistent launch: o_proj over the
+ * merged attention splits (written by efm_decode_attention_partials with the same ctx,
+ * d_kv_len, max_kv_len and workspace), residual add + RMSNorm(post_norm), gate/up +
+ * SwiGLU, down_proj, then, unless this is the last layer, the next layer's residual add
+ * + RMSNorm(in_norm_next) + QKV + bias with q to q_next and K / V into slot
+ * *d_kv_len - 1 of the next layer's cache. residual_in is r_l (the residual after the
+ * layer's input add); residual_out receives r_{l+1} = bf16(h + r'), or r' on the last
+ * layer, where hidden_out also receives h = bf16(down_proj output) for the final norm +
+ * LM head. Results are bit-identical to efm_decode_attention_merge_o_proj,
+ * efm_decode_norm_gate_up_swiglu, efm_linear and efm_decode_norm_qkv run in sequence.
+ * Replaces the operator sequence of the Qwen2.5 decode layer from the o_proj through the
+ * next layer's FusedQKVLinearLayer (src/models/qwen2_5/qwen2_5.cpp:600-929).
+ * The launch uses one workgroup per CU, all co-resident; workgroups exchange vectors
+ * through the workspace (zero-filled once, then reused by every launch; launches that
+ * share a workspace must be stream-ordered). A workgroup that does not receive its
+ * inputs within about a second gives up and flags the workspace:
+ * efm_decode_chain_status reports and clears the flag (it synchronises the stream).
+ * Limits (efm_decode_chain_supported): hidden and q_dim <= 1536, inter <= 10240, at most
+ * 8 attention splits (max_kv_len <= 1024 with 128 keys per split), 64 query heads.
+ * ---------------------------------------------------------------------------------- */
+typedef struct efm_decode_chain_layer {
+    const void* w_o;          /* [hidden, q_dim] */
+    const void* post_norm;    /* [hidden] */
+    const void* w_up_gate;    /* [2 * inter, hidden], rows [up; gate] */
+    const void* w_down;       /* [hidden, inter] */
+    const void* in_norm_next; /* [hidden]; NULL marks the last layer */
+    const void* w_qkv_next;   /* [q_dim + 2 * kv_dim, hidden] */
+    const void* b_qkv_next;   /* [q_dim + 2 * kv_dim] */
+    void* q_next;             /* [q_dim] */
+    void* k_cache_next;       /* [max tokens, kv_dim] */
+    void* v_cache_next;
+} efm_decode_chain_layer;
+
+size_t efm_decode_chain_workspace_bytes(int32_t hidden, int32_t inter);
+int efm_decode_chain_supported(const efm_attention_ctx* ctx, int32_t hidden, int32_t inter, uint32_t max_kv_len);
+int efm_decode_layer_chain(const efm_attention_ctx* ctx, int32_t hidden, int32_t inter, float eps,
+                           const efm_decode_chain_layer* layer, const uint32_t* d_kv_len, uint32_t max_kv_len,
+                           const void* attn_workspace, size_t attn_workspace_bytes, const void* residual_in,
+                           void* residual_out, void* hidden_out, void* chain_workspace, size_t chain_workspace_bytes,
+                           hipStream_t stream);
+int efm_decode_chain_status(void* chain_workspace, int32_t hidden, int32_t inter, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------
  * Temperature / top-p sampler of one fp32 logits row (the non-greedy branch of
  * SamplerLayer::forward_sampling, src/layers/sampler.cu:251-298, which samples
  * softmax(logits / T) by inverse CDF; top-p is an addition). Exact integer-mass

@@ -240,3 +240,27 @@ def test_top_p_sampling_seeds_differ_and_config_checks(gpu):
             ecfg = S.write_engine_config(os.path.join(tmp, "bad.json"), mdir, max_tokens=128, **bad)
             with pytest.raises(edge_fm.ConfigurationError):
                 edge_fm.EdgeFM(ecfg)
+
+
+@pytest.mark.parametrize("shape_id", ["tiny", "1p5b"])
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_decode_chain_matches_per_operator_path(gpu, shape_id, use_graph):
+    """The persistent post-attention chain is bit-identical to the per-operator decode
+    kernels, so both engines must produce the same tokens; the metric says which ran."""
+    if shape_id == "tiny":
+        shape, seed, n_prompt, n_gen = TINY, 41, 40, 24
+    else:
+        shape, seed, n_prompt, n_gen = S.QWEN25_1P5B, 42, 64, 16
+    w = O.random_weights(_oracle_cfg(shape), seed=seed, std=0.02 if shape_id == "1p5b" else 0.2)
+    prompt = torch.randint(0, shape.vocab, (n_prompt,), generator=torch.Generator().manual_seed(6)).tolist()
+    toks = {}
+    with tempfile.TemporaryDirectory() as tmp:
+        for chain in (True, False):
+            eng, keep = _engine(tmp, shape, w, max_tokens=256, max_new_tokens=n_gen, use_graph=use_graph,
+                                decode_chain=chain)
+            req = edge_fm.Request(0, prompt)
+            req.set_ignore_stop_tokens(True)
+            toks[chain] = [eng.generate(req).token_ids() for _ in range(2)]
+            assert eng.last_generate_metrics()["decode_chain"] == (1.0 if chain else 0.0)
+            del eng, keep
+    assert toks[True][0] == toks[True][1] == toks[False][0] == toks[False][1]
