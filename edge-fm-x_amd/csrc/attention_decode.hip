@@ -17,7 +17,9 @@
 //    staged per wave in LDS with the same key permutation as the accumulator rows.
 //  * RoPE on read by angle addition: cos/sin(k * f_d) for the 32 key offsets of a tile
 //    are tabulated once per workgroup, cos/sin(base * f_d) once per tile (one sincos
-//    per thread), so rotating a key pair costs FMAs, not transcendentals.
+//    per thread), so rotating a key pair costs FMAs, not transcendentals. The tables
+//    use sincos_reduced (Cody-Waite reduction + the hardware sin/cos, ~1e-6 absolute),
+//    as the reference's decode kernel uses the fast sin/cos intrinsics.
 //  * Each wave walks 32-key tiles of the workgroup's chunk; the next tile's K/V loads
 //    are issued before the current tile's matrix work. Waves merge their (m, l, O)
 //    through LDS.
@@ -129,14 +131,14 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
     __syncthreads();
     if (a.rope_q && tid < HALF) {
         float sn, cs;
-        sincosf((float)((int)L - 1 + a.q_pos_off) * sfreq[tid], &sn, &cs);
+        sincos_reduced((float)((int)L - 1 + a.q_pos_off) * sfreq[tid], &sn, &cs);
         cs_q[tid] = make_float2(cs, sn);
     }
     if (a.rope_k) {
         for (int i = tid; i < kTileKeys * HALF; i += kAttnThreads) {
             const int kk = i / HALF, d = i % HALF;
             float sn, cs;
-            sincosf((float)kk * sfreq[d], &sn, &cs);
+            sincos_reduced((float)kk * sfreq[d], &sn, &cs);
             cs_off[kk][d] = make_float2(cs, sn);
         }
     }
@@ -191,7 +193,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
             const int w = tid / HALF, d = tid % HALF;
             const int base = start + (r * kAttnWaves + w) * kTileKeys + a.k_pos_off;
             float sn, cs;
-            sincosf((float)base * sfreq[d], &sn, &cs);
+            sincos_reduced((float)base * sfreq[d], &sn, &cs);
             cs_base[w][d] = make_float2(cs, sn);
         }
         // V^T into this wave's LDS tile: Vt[d][key]

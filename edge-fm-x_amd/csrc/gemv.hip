@@ -76,6 +76,82 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, bf16_t* xs, flo
         for (int c = threadIdx.x; c < C; c += kGemvThreads) xs4[c] = x4[c];
         return;
     }
+    if (PRO == PRO_ATTN_MERGE && a.K <= 2 * 4 * kGemvThreads && a.split_cap <= kMergeMaxSplits) {
+        // Same merge as below with every load issued up front (the cache length, each head's
+        // split statistics and this thread's partial outputs for every split slot; slots
+        // beyond the live split count get weight 0): one memory round trip instead of two.
+        __shared__ float swf[kMergeMaxHeads * kMergeMaxSplits];
+        const int hd = a.head_dim, G = a.group, cap = a.split_cap;
+        const int Hq = a.K / hd;
+        const uint32_t L = min(a.attn_len[0], a.attn_max_len);
+        float2 ml[kMergeMaxSplits];
+        if ((int)threadIdx.x < Hq) {
+            const int h = threadIdx.x;
+#pragma unroll
+            for (int j = 0; j < kMergeMaxSplits; ++j) {
+                const size_t idx = ((size_t)(h / G) * cap + j) * G + (h % G);
+                ml[j] = (j < cap) ? *reinterpret_cast<const float2*>(a.ml_part + idx * 2) : make_float2(0.f, 0.f);
+            }
+        }
+        float4 op[2][kMergeMaxSplits];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int c = threadIdx.x + q * kGemvThreads;
+            if (c < (a.K >> 2)) {
+                const int n0 = c * 4, h = n0 / hd, d0 = n0 % hd;
+                const float* base = a.o_part + ((size_t)(h / G) * cap * G + (h % G)) * hd + d0;
+#pragma unroll
+                for (int j = 0; j < kMergeMaxSplits; ++j)
+                    op[q][j] = (j < cap) ? *reinterpret_cast<const float4*>(base + (size_t)j * G * hd)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+        const int kps = a.keys_per_split;
+        const int nsplit = (L == 0) ? 1 : (int)min((uint32_t)cap, (L + kps - 1) / kps);
+        if ((int)threadIdx.x < Hq) {
+            const int h = threadIdx.x;
+            float M = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kMergeMaxSplits; ++j)
+                if (j < nsplit) M = fmaxf(M, ml[j].x);
+            float den = 0.f, w[kMergeMaxSplits];
+#pragma unroll
+            for (int j = 0; j < kMergeMaxSplits; ++j) {
+                if (j < nsplit) {
+                    w[j] = (ml[j].x == -INFINITY) ? 0.f : exp2f(ml[j].x - M);
+                    den = fmaf(w[j], ml[j].y, den);
+                }
+            }
+            const float inv = (den > 0.f) ? 1.f / den : 0.f;
+#pragma unroll
+            for (int j = 0; j < kMergeMaxSplits; ++j)
+                if (j < nsplit) swf[h * nsplit + j] = w[j] * inv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int c = threadIdx.x + q * kGemvThreads;
+            if (c < (a.K >> 2)) {
+                const int h = (c * 4) / hd;
+                float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < kMergeMaxSplits; ++j) {
+                    if (j < nsplit) {
+                        const float wj = swf[h * nsplit + j];
+                        acc[0] = fmaf(wj, op[q][j].x, acc[0]);
+                        acc[1] = fmaf(wj, op[q][j].y, acc[1]);
+                        acc[2] = fmaf(wj, op[q][j].z, acc[2]);
+                        acc[3] = fmaf(wj, op[q][j].w, acc[3]);
+                    }
+                }
+                uint2 pk;
+                pk.x = pack_bf16x2(acc[0], acc[1]);
+                pk.y = pack_bf16x2(acc[2], acc[3]);
+                reinterpret_cast<uint2*>(xs)[c] = pk;
+            }
+        }
+        return;
+    }
     if (PRO == PRO_ATTN_MERGE) {
         // x[h*hd + d] = bf16( sum_s w[h][s] * o_part[kvh][s][g][d] ),
         // w[h][s] = exp2(m_s - M) / sum_s exp2(m_s - M) l_s  (log-sum-exp merge of the splits)
