@@ -171,6 +171,206 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(const bf16_t* _
     }
 }
 
+// ---------------------------------------------------------------------------------
+// Pipelined variant for K % 64 == 0: K slabs of 64 stream global -> LDS with
+// global_load_lds (no staging registers) into an S-deep ring, so S - 1 slabs are in
+// flight while the matrix cores work on one. Each wave's 1 KB DMA load covers 8 rows x 128
+// bytes; lane l fetches chunk (l % 8) ^ (row % 8) of its row, so the ring holds an
+// XOR-swizzled layout and the 32-row MFMA operand reads spread over the LDS banks. The
+// operand reads are issued as ds_read_b128 with explicit waits: each wave waits for its
+// own DMA loads of the slab (vmcnt, counted exactly: every wave issues LPW loads per slab)
+// and a workgroup barrier makes all waves' loads visible. Tiles are assigned XCD by XCD
+// (dispatch is round-robin over the 8 XCDs), so workgroups that share weight columns
+// share an L2.
+// ---------------------------------------------------------------------------------
+constexpr int kPBK = 64;            // K per slab
+constexpr int kPRow = kPBK * 2;     // bytes per operand row in LDS
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int LPW>
+__device__ __forceinline__ void vm_wait_slabs(int slabs) {
+    switch (slabs) {
+        case 0: vm_wait<0>(); break;
+        case 1: vm_wait<1 * LPW>(); break;
+        case 2: vm_wait<2 * LPW>(); break;
+        case 3: vm_wait<3 * LPW>(); break;
+        case 4: vm_wait<4 * LPW>(); break;
+        case 5: vm_wait<5 * LPW>(); break;
+        default: vm_wait<6 * LPW>(); break;
+    }
+}
+
+template <int BM, int BN, int S, int EPI>
+__global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* __restrict__ A,
+                                                                 const bf16_t* __restrict__ B,
+                                                                 const bf16_t* __restrict__ bias,
+                                                                 void* __restrict__ Cout, int M, int N, int K, int ldc,
+                                                                 int mt, int nt) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int STAGE = (BM + BN) * kPRow;
+    constexpr int QA = BM / 8, QB = BN / 8;  // 1 KB wave loads per operand per slab
+    constexpr int LPW = (QA + QB) / 4;       // wave loads per wave per slab
+    static_assert((QA + QB) % 4 == 0 && S >= 2 && S <= 8 && (S - 2) * LPW <= 63, "bad pipeline shape");
+    static_assert(EPI != GEPI_SWIGLU || TN % 2 == 0, "SwiGLU needs paired N tiles");
+    __shared__ __align__(1024) unsigned char smem[S * STAGE];
+
+    const int T = mt * nt;
+    const int per = (T + 7) / 8;
+    const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    if (t >= T) return;
+    const int tm = t % mt, tn = t / mt;
+    const int m0 = tm * BM;
+    const int n0 = (EPI == GEPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
+
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave, lane = tid % kWave;
+    const int wm = wave / 2, wn = wave % 2;
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
+
+    auto b_row = [&](int r) -> int {
+        if (EPI == GEPI_SWIGLU) {
+            const int blk = r / 32;
+            const int col = n0 + (blk / 2) * 32 + (r % 32);
+            return (col < N) ? ((blk % 2 == 0) ? col : N + col) : -1;
+        }
+        const int n = n0 + r;
+        return (n < N) ? n : -1;
+    };
+
+    auto issue = [&](int kk, int slot) {
+        const int k0 = kk * kPBK;
+        const int rr = lane >> 3, cs = lane & 7;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int q = wave + i * 4;
+            const bf16_t* src;
+            if (q < QA) {
+                const int row = min(m0 + q * 8 + rr, M - 1);
+                src = A + (size_t)row * K + k0 + ((cs ^ rr) << 3);
+            } else {
+                int br = b_row((q - QA) * 8 + rr);
+                if (br < 0) br = 0;
+                src = B + (size_t)br * K + k0 + ((cs ^ rr) << 3);
+            }
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(src),
+                (__attribute__((address_space(3))) void*)(smem + slot * STAGE + q * 1024), 16, 0, 0);
+        }
+    };
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+    auto compute = [&](int slot) {
+        const uint32_t base = lds0 + (uint32_t)(slot * STAGE);
+        constexpr int KSN = kPBK / 16;
+        bf16x8_t af[KSN][TM], bfr[KSN][TN];
+        // all operand reads of the slab first (one LDS latency per slab), then the MFMAs
+#pragma unroll
+        for (int ks = 0; ks < KSN; ++ks) {
+            const int c = ks * 2 + (lane >> 5);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int r = wm * WM + i * 32 + (lane & 31);
+                const uint32_t addr = base + (uint32_t)(r * kPRow + ((c ^ (r & 7)) << 4));
+                asm volatile("ds_read_b128 %0, %1" : "=v"(af[ks][i]) : "v"(addr) : "memory");
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int r = wn * WN + j * 32 + (lane & 31);
+                const uint32_t addr = base + (uint32_t)(BM * kPRow + r * kPRow + ((c ^ (r & 7)) << 4));
+                asm volatile("ds_read_b128 %0, %1" : "=v"(bfr[ks][j]) : "v"(addr) : "memory");
+            }
+        }
+        // The fragments come from inline-asm reads the compiler cannot track: wait for
+        // them, then pass every fragment through an asm "write" so that no MFMA can be
+        // scheduled above the wait.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int ks = 0; ks < KSN; ++ks) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[ks][i]));
+#pragma unroll
+            for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bfr[ks][j]));
+        }
+#pragma unroll
+        for (int ks = 0; ks < KSN; ++ks)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][i], bfr[ks][j], acc[i][j], 0, 0, 0);
+    };
+
+    const int nk = K / kPBK;
+    const int pre = min(S - 1, nk);
+    for (int p = 0; p < pre; ++p) issue(p, p);
+    for (int kt = 0; kt < nk; ++kt) {
+        // Own DMA loads of slab kt have landed in LDS; the bare barrier (no fence, which
+        // would drain every slab in flight) then orders them before all waves' reads, and
+        // all waves' reads of slot (kt - 1) % S before it is refilled below.
+        vm_wait_slabs<LPW>(min(S - 2, nk - 1 - kt));
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+        compute(kt % S);
+    }
+
+    // Epilogue. Accumulator element e of tile (i, j): row = (e/4)*8 + (lane/32)*4 + e%4,
+    // column = lane % 32 within the 32 x 32 tile.
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + wm * WM + i * 32 + (e / 4) * 8 + (lane / 32) * 4 + (e % 4);
+            if (row >= M) continue;
+            if (EPI == GEPI_SWIGLU) {
+#pragma unroll
+                for (int j = 0; j < TN; j += 2) {
+                    const int col = n0 + ((wn * WN + j * 32) / 64) * 32 + (lane % 32);
+                    if (col < N) {
+                        const float u = round_bf16(acc[i][j][e]);
+                        const float g = round_bf16(acc[i][j + 1][e]);
+                        const float o = (g / (1.0f + expf(-g))) * u;
+                        reinterpret_cast<bf16_t*>(Cout)[(size_t)row * ldc + col] = (bf16_t)f32_to_bf16(o);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int col = n0 + wn * WN + j * 32 + (lane % 32);
+                    if (col >= N) continue;
+                    float v = acc[i][j][e];
+                    if (bias != nullptr) v += bf16_to_f32(bias[col]);
+                    if (EPI == GEPI_F32) reinterpret_cast<float*>(Cout)[(size_t)row * ldc + col] = v;
+                    else reinterpret_cast<bf16_t*>(Cout)[(size_t)row * ldc + col] = (bf16_t)f32_to_bf16(v);
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int S, int EPI>
+static void gemm_pipe_launch(int M, int N, int K, const bf16_t* A, const bf16_t* B, const bf16_t* bias, void* C,
+                             int ldc, hipStream_t stream) {
+    const int ocols = (EPI == GEPI_SWIGLU) ? BN / 2 : BN;
+    const int mt = (M + BM - 1) / BM, nt = (N + ocols - 1) / ocols;
+    const int grid = 8 * ((mt * nt + 7) / 8);
+    hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, S, EPI>), dim3(grid), dim3(kGemmThreads), 0, stream, A, B, bias, C,
+                       M, N, K, ldc, mt, nt);
+}
+
 template <int EPI>
 static int gemm_dispatch(int M, int N, int K, const bf16_t* A, const bf16_t* B, const bf16_t* bias, void* C, int ldc,
                          hipStream_t stream) {
@@ -180,6 +380,16 @@ static int gemm_dispatch(int M, int N, int K, const bf16_t* A, const bf16_t* B, 
         return (long)((M + bm - 1) / bm) * ((N + ocols - 1) / ocols);
     };
     const dim3 block(kGemmThreads);
+    if (K % kPBK == 0) {
+        if (tiles(128, 128) >= 256) {
+            gemm_pipe_launch<128, 128, 4, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+        } else if constexpr (EPI == GEPI_SWIGLU) {
+            gemm_pipe_launch<64, 128, 5, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+        } else {
+            gemm_pipe_launch<64, 64, 8, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+        }
+        return check_launch("gemm_bf16");
+    }
     if (tiles(128, 128) >= 256) {
         const int oc = (EPI == GEPI_SWIGLU) ? 64 : 128;
         dim3 grid((M + 127) / 128, (N + oc - 1) / oc);
