@@ -132,6 +132,315 @@ def kernel_only(torch, C, S, shape, seed):
                       "bytes_per_launch": gate_up_bytes(shape), "copy_calibration_bytes": 256 << 20}))
 
 
+
+# ---------------------------------------------------------------------------------
+# Other BASELINE configurations (bench.py --config c1|c3|c4|c5). The default run (c2) is
+# the headline line above; these print one JSON line each for their own workload.
+# ---------------------------------------------------------------------------------
+def _graph_time_us(torch, fn, reps, stream):
+    """Average µs of fn() over a graph of `reps` calls, replayed between HIP events on
+    the capture/replay stream."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream, capture_error_mode="thread_local"):
+        for _ in range(reps):
+            fn(stream.cuda_stream)
+    with torch.cuda.stream(stream):
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def run_c4(args):
+    """C4: SageAttention-style int8 prefill attention operator alone at the Qwen2.5-VL-7B
+    head shape (28/4, hd 128), S = 4096, causal, Q/K/V N(0,1); the bf16 MFMA attention on
+    the same inputs beside it."""
+    import torch
+    import efm_capi as C
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    S, Hq, Hkv, hd = 4096, 28, 4, 128
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    q = torch.randn(S, Hq, hd, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(S, Hkv, hd, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(S, Hkv, hd, device=dev, generator=g).to(torch.bfloat16)
+    o8 = torch.empty_like(q)
+    o16 = torch.empty_like(q)
+    ctx = C.make_attention_ctx(Hq, Hkv, hd, rope=False)
+    ws = torch.zeros(C.load().efm_attention_prefill_sage_int8_workspace_bytes(ctx, S, S), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.Stream()
+
+    def sage(sh):
+        C.call("efm_attention_prefill_sage_int8", ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), o8.data_ptr(), S, S,
+               1, ws.data_ptr(), ws.numel(), sh)
+
+    def bf16(sh):
+        C.call("efm_attention_prefill", ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), o16.data_ptr(), S, S, 1, sh)
+
+    t8 = _graph_time_us(torch, sage, args.steps, stream)
+    t16 = _graph_time_us(torch, bf16, args.steps, stream)
+    pairs = S * (S + 1) // 2
+    qk_ops = 2.0 * Hq * hd * pairs          # int8 ops
+    pv_flop = 2.0 * Hq * hd * pairs         # bf16 FLOP
+    t_peak = qk_ops / 5.0e15 + pv_flop / 2.5e15
+    diff = (o8.float() - o16.float()).abs()
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import efm_oracle as O
+        Sc = 512
+        qc, kc, vc = q[:Sc].cpu(), k[:Sc].cpu(), v[:Sc].cpu()
+        c0 = time.perf_counter()
+        O.sage_attention(qc, kc, vc, Hkv, causal=True)
+        cs = time.perf_counter() - c0
+        cpu = {"value": round(cs * 1e3, 2), "unit": "ms", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"CPU oracle of the int8 path at S = {Sc} (all 28 heads), ms per call; the GPU line is S = {S}"}
+    print(json.dumps({
+        "metric": "SageAttention int8 prefill attention op, ms per call (C4: 28/4 heads, hd 128, S 4096, causal)",
+        "value": round(t8 / 1e3, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": 1,
+        "higher_is_better": False, "dtype": "int8 QK^T / bf16 PV", "data": "synthetic N(0,1) q/k/v",
+        "config": {"workload": "C4: Sage int8 attention op, Qwen2.5-VL-7B head shape", "S": S, "heads": "28/4",
+                   "head_dim": hd, "causal": True},
+        "bf16_attention_ms": round(t16 / 1e3, 4),
+        "max_abs_diff_int8_vs_bf16": round(float(diff.max()), 4),
+        "mean_abs_diff_int8_vs_bf16": round(float(diff.mean()), 5),
+        "roofline": {"bound": "mfma", "achieved": round((qk_ops + pv_flop) / (t8 * 1e-6) / 1e12, 1),
+                     "peak": round((qk_ops + pv_flop) / t_peak / 1e12, 1), "unit": "TFLOP/s",
+                     "frac": round(t_peak / (t8 * 1e-6), 4), "traffic": None,
+                     "note": "int8 QK^T (6.01e10 ops) at 5.0 POP/s + bf16 PV (6.01e10 FLOP) at 2.5 PFLOP/s"},
+        "bf16_roofline_frac": round((2 * pv_flop / 2.5e15) / (t16 * 1e-6), 4),
+        "cpu_baseline": cpu,
+    }))
+
+
+def run_c1(args):
+    """C1: one decode step of a single Qwen2.5-0.5B-shaped layer (hidden 896, 14/2 heads,
+    hd 64, inter 4864), KV cache of 1024 N(0,1) positions, input hidden N(0,1). 16 copies
+    of the layer (weights + cache, 485 MB) are rotated so the 256 MB Infinity Cache does
+    not serve the weights."""
+    import torch
+    import efm_capi as C
+    import efm_setup as S
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    sh = S.QWEN25_0P5B
+    H, QD, KVD, I, hd = sh.hidden, sh.q_dim, sh.kv_dim, sh.inter, sh.head_dim
+    prefix, max_kv = 1024, 1025
+    ncopy = 16
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+
+    def n(*s, std=0.02):
+        return (torch.randn(*s, device=dev, generator=g) * std).to(torch.bfloat16)
+
+    layers = []
+    for _ in range(ncopy):
+        L = {"in_norm": torch.ones(H, device=dev, dtype=torch.bfloat16), "w_qkv": n(QD + 2 * KVD, H),
+             "b_qkv": n(QD + 2 * KVD), "w_o": n(H, QD), "post": torch.ones(H, device=dev, dtype=torch.bfloat16),
+             "w_gu": n(2 * I, H), "w_down": n(H, I),
+             "k": torch.randn(max_kv, KVD, device=dev, generator=g).to(torch.bfloat16),
+             "v": torch.randn(max_kv, KVD, device=dev, generator=g).to(torch.bfloat16)}
+        layers.append(L)
+    h = torch.randn(1, H, device=dev, generator=g).to(torch.bfloat16)
+    res_in = torch.randn(1, H, device=dev, generator=g).to(torch.bfloat16)
+    d_len = torch.tensor([max_kv], dtype=torch.int32, device=dev)
+    ctx = C.make_attention_ctx(sh.heads, sh.kv_heads, hd)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=dev)
+    r0 = torch.empty(1, H, device=dev, dtype=torch.bfloat16)
+    r1 = torch.empty_like(r0)
+    q = torch.empty(1, QD, device=dev, dtype=torch.bfloat16)
+    att = torch.empty_like(q)
+    a = torch.empty(1, H, device=dev, dtype=torch.bfloat16)
+    mid = torch.empty(1, I, device=dev, dtype=torch.bfloat16)
+    out = torch.empty(1, H, device=dev, dtype=torch.bfloat16)
+    state = {"i": 0}
+    # as the engine: the split merge folds into o_proj when the cache needs <= 8 splits of
+    # 128 keys (1024 rows); 1025 rows take the attention kernel's own merge + o_proj GEMV
+    fused_merge = max_kv <= 1024
+
+    def step(stream_handle):
+        # the engine's per-layer decode sequence (Qwen2_5::decode_step): norm + QKV + KV
+        # write, attention split partials, merge + o_proj, norm + gate/up + SwiGLU, down
+        L = layers[state["i"] % ncopy]
+        state["i"] += 1
+        C.call("efm_decode_norm_qkv", H, QD, KVD, sh.eps, h.data_ptr(), res_in.data_ptr(), r0.data_ptr(),
+               L["in_norm"].data_ptr(), L["w_qkv"].data_ptr(), L["b_qkv"].data_ptr(), q.data_ptr(), L["k"].data_ptr(),
+               L["v"].data_ptr(), d_len.data_ptr(), stream_handle)
+        if fused_merge:
+            C.call("efm_decode_attention_partials", ctx, q.data_ptr(), L["k"].data_ptr(), L["v"].data_ptr(),
+                   d_len.data_ptr(), max_kv, ws.data_ptr(), ws.numel(), stream_handle)
+            C.call("efm_decode_attention_merge_o_proj", ctx, d_len.data_ptr(), max_kv, ws.data_ptr(), ws.numel(),
+                   L["w_o"].data_ptr(), H, a.data_ptr(), stream_handle)
+        else:
+            C.call("efm_attention_decode", ctx, q.data_ptr(), L["k"].data_ptr(), L["v"].data_ptr(), att.data_ptr(), 0,
+                   d_len.data_ptr(), max_kv, ws.data_ptr(), ws.numel(), stream_handle)
+            C.call("efm_linear", 1, QD, H, att.data_ptr(), L["w_o"].data_ptr(), None, a.data_ptr(), C.EFM_DTYPE_BF16,
+                   stream_handle)
+        C.call("efm_decode_norm_gate_up_swiglu", H, I, sh.eps, a.data_ptr(), r0.data_ptr(), r1.data_ptr(),
+               L["post"].data_ptr(), L["w_gu"].data_ptr(), mid.data_ptr(), stream_handle)
+        C.call("efm_linear", 1, I, H, mid.data_ptr(), L["w_down"].data_ptr(), None, out.data_ptr(), C.EFM_DTYPE_BF16,
+               stream_handle)
+
+    stream = torch.cuda.Stream()
+    us = _graph_time_us(torch, step, ncopy * max(1, args.steps), stream)
+    wbytes = ((QD + 2 * KVD) * (H + 1) + H * QD + 2 * I * H + I * H + 2 * H) * 2
+    kvbytes = 2 * max_kv * KVD * 2
+    nbytes = wbytes + kvbytes
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import efm_oracle as O
+        cfg = O.QwenConfig(hidden=H, layers=1, heads=sh.heads, kv_heads=sh.kv_heads, head_dim=hd, inter=I, vocab=8)
+        w = O.random_weights(cfg, seed=args.seed)
+        orc = O.Qwen2Oracle(cfg, O.fuse_weights(cfg, w), max_tokens=max_kv + 1, cache_f32=True)
+        ts = []
+        for _ in range(23):
+            st = orc.new_state()
+            st.k[0][:prefix] = torch.randn(prefix, sh.kv_heads, hd).to(torch.bfloat16)
+            st.v[0][:prefix] = torch.randn(prefix, sh.kv_heads, hd).to(torch.bfloat16)
+            st.length = prefix
+            emb = torch.randn(1, H).to(torch.bfloat16)
+            c0 = time.perf_counter()
+            orc.forward(st, torch.zeros(1, dtype=torch.int32), embeds=emb)
+            ts.append(time.perf_counter() - c0)
+        ts = sorted(ts[3:])
+        cpu = {"value": round(ts[len(ts) // 2] * 1e6, 1), "unit": "us/step", "cores": torch.get_num_threads(),
+               "kind": "port", "sample": "CPU oracle layer (one decode step at position 1024, vocab-8 head), "
+                                         "median of 20 after 3 warmup"}
+    print(json.dumps({
+        "metric": "single Qwen2.5-0.5B-shaped layer decode step, us/step (C1)", "value": round(us, 3),
+        "unit": "us/step", "n_gpus": 1, "steps": ncopy * max(1, args.steps), "warmup": ncopy,
+        "higher_is_better": False, "dtype": "bf16", "data": "synthetic N(0,0.02) weights, N(0,1) KV and hidden",
+        "config": {"workload": "C1: 0.5B layer, kv 1024, one decode step", "hidden": H, "heads": "14/2",
+                   "head_dim": hd, "intermediate": I, "copies_rotated": ncopy},
+        "roofline": {"bound": "hbm", "achieved": round(nbytes / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_step": nbytes, "note": "launches: norm+qkv+kv write, attention (+ merge), o_proj, norm+gate/up+swiglu, down"},
+        "cpu_baseline": cpu,
+    }))
+
+
+def _engine_generate(args, shape, prompt, max_new, temperature=0.0, top_p=1.0, seed=0, emb=None, embed_id=-1,
+                     pos=None, last_pos=None, model_name=""):
+    """Build an engine for `shape` with synthetic weights, run `warmup` + up to 2 timed
+    generate() calls of `prompt`, return (per-call metrics, last tokens, weights)."""
+    import torch
+    import edge_fm
+    import efm_setup as S
+
+    weights = S.synthetic_weights_gpu(shape, seed=args.seed)
+    S.register_weights(weights)
+    tmp = tempfile.mkdtemp(prefix="efm_bench_")
+    mdir = S.write_model_dir(os.path.join(tmp, "model"), shape)
+    ecfg = S.write_engine_config(os.path.join(tmp, "engine.json"), mdir, max_tokens=len(prompt) + max_new + 1,
+                                 max_new_tokens=max_new, use_graph=True, temperature=temperature, top_p=top_p,
+                                 seed=seed, model_name=model_name)
+    eng = edge_fm.EdgeFM(ecfg)
+    if emb is not None:
+        et = edge_fm.Tensor(emb.data_ptr(), list(emb.shape), edge_fm.DType.BFloat16, edge_fm.Device.GPU, 0, False)
+        pt = edge_fm.Tensor(pos.data_ptr(), list(pos.shape), edge_fm.DType.Int32, edge_fm.Device.GPU, 0, False)
+    mets, toks = [], None
+    for it in range(args.warmup + max(1, min(args.steps, 2))):
+        if emb is not None:
+            req = edge_fm.Request(0, prompt, et, embed_id, pt, last_pos)
+        else:
+            req = edge_fm.Request(0, prompt)
+        req.set_ignore_stop_tokens(True)
+        toks = eng.generate(req).token_ids()
+        if it >= args.warmup:
+            mets.append(eng.last_generate_metrics())
+    torch.cuda.synchronize()
+    del eng
+    return mets, toks, weights
+
+
+def run_c5(args):
+    """C5: Qwen2.5-7B-shaped long-context decode with top-p 0.9 / temperature 0.7 sampling
+    (fixed seed). The 16384-position prefix is prefilled through the engine from random
+    prompt ids (the engine has no interface to inject N(0,1) cache rows, so the cache holds
+    the model's own K/V); 128 tokens are then sampled."""
+    import torch
+    import efm_setup as S
+
+    torch.cuda.set_device(0)
+    shape = S.QWEN25_7B
+    P, G = 16384, 128
+    g = torch.Generator().manual_seed(args.seed)
+    prompt = torch.randint(0, shape.vocab, (P,), generator=g).tolist()
+    mets, toks, w = _engine_generate(args, shape, prompt, G, temperature=0.7, top_p=0.9, seed=1234)
+    dec_steps = sum(m["decode_steps"] for m in mets)
+    dec_ms = sum(m["decode_ms"] for m in mets)
+    pf_ms = sum(m["prefill_ms"] for m in mets) / len(mets)
+    tps = dec_steps * 1000.0 / dec_ms
+    H, I, L, V = shape.hidden, shape.inter, shape.layers, shape.vocab
+    per_layer = ((shape.q_dim + 2 * shape.kv_dim) * (H + 1) + shape.q_dim * H + 3 * I * H + 2 * H) * 2
+    mean_ctx = P + (G + 1) / 2.0
+    nbytes = L * per_layer + V * H * 2 * 2 + H * 2 + 2 * mean_ctx * shape.kv_dim * 2 * L
+    gbs = nbytes * tps / 1e9
+    print(json.dumps({
+        "metric": "bs=1 decode tokens/s, Qwen2.5-7B shape at 16k context, top-p 0.9 / T 0.7 sampling (C5)",
+        "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1, "steps": len(mets), "warmup": args.warmup,
+        "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) bf16 weights; 16384-token random prompt prefilled through the engine)",
+        "config": {"workload": "C5: 7B shape, 28 layers, hidden 3584, 28/4 heads, inter 18944, vocab 152064 untied",
+                   "prefix": P, "generated": G, "temperature": 0.7, "top_p": 0.9, "seed": 1234},
+        "prefill_ms_16k": round(pf_ms, 1), "prefill_tokens_per_s": round(P * 1000.0 / pf_ms, 1),
+        "decode_loop": {"bytes_per_token": int(nbytes), "achieved_GBs": round(gbs, 1),
+                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)},
+        "tokens_head": toks[:8], "cpu_baseline": None,
+    }))
+
+
+def run_c3(args):
+    """C3: Qwen2.5-VL-3B-shaped multimodal prefill (1280 N(0,1) vision embeddings on a
+    1 x 32 x 40 grid with 3-D M-RoPE positions, sections 16/24/24, plus 64 random text
+    tokens), then 128 greedy tokens."""
+    import torch
+    import efm_setup as S
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    shape = S.QWEN25_VL_3B
+    nv, nt, G = 1280, 64, 128
+    g = torch.Generator().manual_seed(args.seed)
+    embed_id = shape.vocab + 1000
+    text = torch.randint(0, shape.vocab, (nt,), generator=g).tolist()
+    prompt = [embed_id + i for i in range(nv)] + text
+    emb = torch.randn(nv, shape.hidden, generator=g).to(torch.bfloat16).to(dev)
+    pos = torch.empty(3, nv + nt, dtype=torch.int32)
+    idx = torch.arange(nv)
+    pos[0, :nv] = 0
+    pos[1, :nv] = idx // 40
+    pos[2, :nv] = idx % 40
+    pos[:, nv:] = (40 + torch.arange(nt)).to(torch.int32)
+    pos = pos.to(dev)
+    last = int(pos.max().item())
+    mets, toks, w = _engine_generate(args, shape, prompt, G, emb=emb, embed_id=embed_id, pos=pos,
+                                     last_pos=[last, last, last], model_name="qwen2_5_vl")
+    S_ = nv + nt
+    pf_ms = sum(m["prefill_ms"] for m in mets) / len(mets)
+    dec_tps = sum(m["decode_steps"] for m in mets) * 1000.0 / sum(m["decode_ms"] for m in mets)
+    H, I, L = shape.hidden, shape.inter, shape.layers
+    lin = 2.0 * S_ * L * ((shape.q_dim + 2 * shape.kv_dim) * H + shape.q_dim * H + 3 * I * H)
+    attn = 2.0 * 2 * L * shape.heads * shape.head_dim * (S_ * (S_ + 1) / 2)
+    tf = (lin + attn) / (pf_ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "multimodal prefill tokens/s, Qwen2.5-VL-3B shape, 1344 tokens (C3)",
+        "value": round(S_ * 1000.0 / pf_ms, 1), "unit": "tokens/s", "n_gpus": 1, "steps": len(mets),
+        "warmup": args.warmup, "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic (random-init bf16 weights, N(0,1) vision embeddings, random text ids)",
+        "config": {"workload": "C3: VL-3B, 36 layers, hidden 2048, 16/2 heads, inter 11008, M-RoPE 16/24/24",
+                   "vision_tokens": nv, "text_tokens": nt, "generated": G},
+        "prefill_ms": round(pf_ms, 2), "decode_tokens_per_s": round(dec_tps, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tf / 2500.0, 4), "traffic": None,
+                     "note": "whole prefill: linear %.3g + attention %.3g FLOP over the engine's prefill time" % (lin, attn)},
+        "tokens_head": toks[:8], "cpu_baseline": None,
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -141,6 +450,8 @@ def main():
     ap.add_argument("--gen", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+                    help="BASELINE configuration (default c2, the headline decode benchmark)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the copy calibration and the roofline kernel (for rocprofv3 --pmc passes)")
     args = ap.parse_args()
@@ -155,6 +466,9 @@ def main():
     import efm_capi as C
     import efm_setup as S
 
+    if args.config != "c2":
+        {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config](args)
+        return
     shape = S.QWEN25_1P5B
     if args.kernel_only:
         kernel_only(torch, C, S, shape, args.seed)
