@@ -11,7 +11,7 @@
 //   score_log2(i, j) = float(int32(Q8_i . K8_j)) * ((sq * sk) * (log2(e) / sqrt(hd)))
 //   causal: query i sees keys j <= i + (L - S); P rounded to bf16 for the PV product.
 //
-// Three launches: K mean (one workgroup per KV head, float64 accumulation), block
+// Three launches: K mean (one workgroup per KV head and 8 channels, float64), block
 // quantisation of Q and K (one workgroup per block x head), attention (one workgroup =
 // 128 query rows of one head, 64-key tiles staged in LDS as int8 K and transposed V).
 #include "common.hpp"
@@ -30,24 +30,50 @@ constexpr int kSageThreads = 256;
 constexpr int kSageQ = 128;   // query rows per attention workgroup
 constexpr int kSageKV = 64;   // keys per LDS tile
 
-// ---- K mean over tokens: grid (Hkv), 256 threads --------------------------------
+// ---- K mean over tokens: grid (Hkv, hd / 8), 256 threads ------------------------
+// Workgroup (h, c) owns channels [8c, 8c + 8) of KV head h; thread t adds rows
+// j = t (mod 256) with 16-byte loads (four rows in flight per step), then a fixed
+// LDS tree sums the 256 per-thread float64 partials. Sums of bf16 values in float64
+// are exact while their binary range fits the 53-bit significand, as it does for
+// cache contents, so the result matches any summation order.
 __global__ __launch_bounds__(kSageThreads) void sage_kmean_kernel(const bf16_t* k, int L, int k_sn, int k_sh, int hd,
                                                                   float* kmean) {
-    __shared__ double part[kSageThreads];
-    const int h = blockIdx.x;
-    const int P = kSageThreads / hd;
-    const int d = threadIdx.x % hd, p = threadIdx.x / hd;
-    double s = 0.0;
-    if (p < P) {
-        for (int j = p; j < L; j += P) s += (double)bf16_to_f32(k[(size_t)j * k_sn + (size_t)h * k_sh + d]);
+    __shared__ double part[8][kSageThreads];
+    const int h = blockIdx.x, d0 = blockIdx.y * 8, t = threadIdx.x;
+    const bf16_t* base = k + (size_t)h * k_sh + d0;
+    double s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = 0.0;
+    int j = t;
+    for (; j + 3 * kSageThreads < L; j += 4 * kSageThreads) {
+        uint4 u[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) u[r] = *reinterpret_cast<const uint4*>(base + (size_t)(j + r * kSageThreads) * k_sn);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float x[8];
+            unpack8(u[r], x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[e] += (double)x[e];
+        }
     }
-    part[threadIdx.x] = s;
+    for (; j < L; j += kSageThreads) {
+        float x[8];
+        unpack8(*reinterpret_cast<const uint4*>(base + (size_t)j * k_sn), x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] += (double)x[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[e][t] = s[e];
     __syncthreads();
-    if (threadIdx.x < hd) {
-        double t = 0.0;
-        for (int q = 0; q < P; ++q) t += part[q * hd + threadIdx.x];
-        kmean[h * hd + threadIdx.x] = (float)(t / (double)L);
+    for (int stride = kSageThreads / 2; stride > 0; stride >>= 1) {
+        if (t < stride) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) part[e][t] += part[e][t + stride];
+        }
+        __syncthreads();
     }
+    if (t < 8) kmean[h * hd + d0 + t] = (float)(part[t][0] / (double)L);
 }
 
 // ---- block quantisation: grid (blocks, H), 256 threads --------------------------
@@ -298,7 +324,7 @@ static int sage_quantize_impl(const efm_attention_ctx* c, const void* q, const v
     const int q_sh = c->q_stride_h ? (int)c->q_stride_h : hd;
     const int k_sn = c->k_stride_n ? (int)c->k_stride_n : (int)(c->num_kv_heads * hd);
     const int k_sh = c->k_stride_h ? (int)c->k_stride_h : hd;
-    hipLaunchKernelGGL(sage_kmean_kernel, dim3(c->num_kv_heads), dim3(kSageThreads), 0, stream,
+    hipLaunchKernelGGL(sage_kmean_kernel, dim3(c->num_kv_heads, hd / 8), dim3(kSageThreads), 0, stream,
                        static_cast<const bf16_t*>(k), (int)L, k_sn, k_sh, hd, kmean);
     int rc = check_launch("sage kmean");
     if (rc) return rc;

@@ -119,8 +119,9 @@ SIGNATURES = {
                                          c_void_p, c_uint32, c_void_p, c_size_t, c_void_p, c_void_p, c_void_p,
                                          c_void_p, c_size_t, c_void_p]),
     "efm_decode_chain_status": (c_int32, [c_void_p, c_int32, c_int32, c_void_p]),
+    "efm_sampler_top_p_workspace_bytes": (c_size_t, [c_int64]),
     "efm_sampler_top_p": (c_int32, [c_int64, c_void_p, c_float, c_float, c_uint64, c_uint64, c_void_p, c_void_p,
-                                    c_void_p]),
+                                    c_void_p, c_size_t, c_void_p]),
     "efm_embedding_lookup": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int32,
                                        c_void_p, c_void_p]),
     "efm_copy_decode_kv_cache_slots": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,

@@ -778,8 +778,9 @@ StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_pat
     }
     response_dev_ = Tensor::zeros({(int64_t)max_resp}, DType::Int32, Device::GPU, device_id_);
     logits_ = Tensor::zeros({m.vocab}, DType::Float32, Device::GPU, device_id_);
-    sample_ws_ = Tensor::zeros({(int64_t)efm_sampler_greedy_workspace_bytes(1, m.vocab)}, DType::UInt8, Device::GPU,
-                               device_id_);
+    sample_ws_ = Tensor::zeros({(int64_t)std::max(efm_sampler_greedy_workspace_bytes(1, m.vocab),
+                                                   efm_sampler_top_p_workspace_bytes(m.vocab))},
+                               DType::UInt8, Device::GPU, device_id_);
     warmup();
 }
 
@@ -830,7 +831,8 @@ void StandardEngine::sample_logits(uint32_t) {
     // sampled (device-resident step counter), so graph replays draw fresh numbers
     const int32_t* d_step = static_cast<const int32_t*>(state_.data_ptr()) + 1;
     efm_check(efm_sampler_top_p(model_->config().vocab, static_cast<const float*>(logits_.data_ptr()), T,
-                                cfg_.top_p(), cfg_.seed(), 0, d_step, tok, stream_),
+                                cfg_.top_p(), cfg_.seed(), 0, d_step, tok, sample_ws_.data_ptr(), sample_ws_.nbytes(),
+                                stream_),
               "top-p sampler");
 }
 

@@ -256,12 +256,16 @@ int efm_decode_chain_status(void* chain_workspace, int32_t hidden, int32_t inter
  * when top_p >= 1, else the ids with e_i >= tau, tau the largest value whose upper set
  * holds >= ceil(top_p * sum w) of the mass; the 24-bit draw x = Philox4x32-10(counter =
  * offset (+ *d_offset when d_offset is not NULL), key = seed).x >> 8 picks the smallest
- * nucleus id whose prefix mass exceeds floor(N * x / 2^24). No workspace.
+ * nucleus id whose prefix mass exceeds floor(N * x / 2^24).
  * temperature >= 1e-6 (smaller means greedy: use efm_sampler_greedy), top_p > 0,
- * 1 <= vocab <= 2^20.
+ * 1 <= vocab < 2^20. workspace: efm_sampler_top_p_workspace_bytes(vocab) bytes of
+ * device memory, no initial contents required; calls that share a workspace must be
+ * ordered on one stream. 3 launches when top_p >= 1, 6 otherwise.
  * ---------------------------------------------------------------------------------- */
+size_t efm_sampler_top_p_workspace_bytes(int64_t vocab);
 int efm_sampler_top_p(int64_t vocab, const float* logits, float temperature, float top_p, uint64_t seed,
-                      uint64_t offset, const int32_t* d_offset, int32_t* token_out, hipStream_t stream);
+                      uint64_t offset, const int32_t* d_offset, int32_t* token_out, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------
  * Embedding lookup (src/layers/embed_head.cu:23-164). out[t,:] = table[ids[t],:];

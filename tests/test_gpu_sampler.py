@@ -17,11 +17,18 @@ pytestmark = pytest.mark.gpu
 MARGIN = 1e-5
 
 
+def _ws(gpu, vocab):
+    # garbage-filled on purpose: the sampler needs no initial workspace contents
+    n = C.load().efm_sampler_top_p_workspace_bytes(vocab)
+    return torch.full((n,), 0xA5, dtype=torch.uint8, device=gpu)
+
+
 def _gpu_sample(gpu, logits, T, p, seed, offset, d_offset=None):
     lg = torch.from_numpy(np.ascontiguousarray(logits, dtype=np.float32)).to(gpu)
     out = torch.full((1,), -1, dtype=torch.int32, device=gpu)
+    ws = _ws(gpu, lg.numel())
     C.call("efm_sampler_top_p", lg.numel(), ptr(lg), float(T), float(p), seed, offset, ptr(d_offset), ptr(out),
-           stream())
+           ptr(ws), ws.numel(), stream())
     torch.cuda.synchronize()
     return int(out.item())
 
@@ -54,6 +61,34 @@ def test_sampler_top_p_llm_like_logits(gpu):
     logits[rng.integers(0, 151936, 20)] += rng.uniform(8, 14, 20).astype(np.float32)
     for off in range(16):
         _check(gpu, logits, 0.7, 0.9, seed=42, offset=off)
+
+
+def test_sampler_top_p_flat_logits_large_nucleus(gpu):
+    """Nearly uniform logits (a random-init LM head): the nucleus holds ~90 % of the
+    vocabulary, so the located token can sit in any of the 149 logit blocks."""
+    rng = np.random.default_rng(8)
+    logits = (rng.standard_normal(152064) * 0.05).astype(np.float32)
+    seen = set()
+    for off in range(24):
+        got, want, info = _check(gpu, logits, 0.7, 0.9, seed=1234, offset=off)
+        assert info["nucleus"] > 100000
+        seen.add(got // 1024)
+    assert len(seen) > 12
+
+
+def test_sampler_top_p_workspace_reuse(gpu):
+    """One workspace across calls of different vocabulary sizes and top-p modes."""
+    ws = _ws(gpu, 152064)
+    rng = np.random.default_rng(21)
+    for i, (V, p) in enumerate([(152064, 0.9), (1000, 1.0), (32000, 0.5), (7, 0.9), (151936, 1.0)]):
+        logits = (rng.standard_normal(V) * 3).astype(np.float32)
+        lg = torch.from_numpy(logits).to(gpu)
+        out = torch.full((1,), -1, dtype=torch.int32, device=gpu)
+        C.call("efm_sampler_top_p", V, ptr(lg), 0.8, p, 99, i, None, ptr(out), ptr(ws), ws.numel(), stream())
+        torch.cuda.synchronize()
+        want, _ = O.sample_top_p(logits, 0.8, p, 99, i)
+        got = int(out.item())
+        assert got == want or O.sample_margin(logits, 0.8, p, 99, i) < MARGIN, (V, p)
 
 
 def test_sampler_top_p_ties_and_dominant(gpu):
@@ -99,14 +134,16 @@ def test_sampler_top_p_distribution(gpu):
     lg = torch.from_numpy(logits).to(gpu)
     n = 4000
     outs = torch.empty(n, dtype=torch.int32, device=gpu)
+    ws = _ws(gpu, 8)
     for off in range(n):
-        C.call("efm_sampler_top_p", 8, ptr(lg), T, 1.0, 2024, off, None, outs.data_ptr() + 4 * off, stream())
+        C.call("efm_sampler_top_p", 8, ptr(lg), T, 1.0, 2024, off, None, outs.data_ptr() + 4 * off, ptr(ws),
+               ws.numel(), stream())
     torch.cuda.synchronize()
     counts = np.bincount(outs.cpu().numpy(), minlength=8)
     assert chisquare(counts, pr * n).pvalue > 1e-4
 
 
-@pytest.mark.parametrize("bad", ["vocab0", "vocab_big", "temp0", "temp_nan", "top_p0"])
+@pytest.mark.parametrize("bad", ["vocab0", "vocab_big", "temp0", "temp_nan", "top_p0", "small_ws"])
 def test_sampler_top_p_rejects_bad_arguments(gpu, bad):
     lg = torch.zeros(16, dtype=torch.float32, device=gpu)
     out = torch.zeros(1, dtype=torch.int32, device=gpu)
@@ -119,7 +156,11 @@ def test_sampler_top_p_rejects_bad_arguments(gpu, bad):
         args["T"] = 0.0
     elif bad == "temp_nan":
         args["T"] = float("nan")
-    else:
+    elif bad == "top_p0":
         args["p"] = 0.0
+    ws = _ws(gpu, 16)
+    if bad == "small_ws":
+        ws = ws[:64]
     with pytest.raises(C.EfmError):
-        C.call("efm_sampler_top_p", args["vocab"], ptr(lg), args["T"], args["p"], 1, 0, None, ptr(out), stream())
+        C.call("efm_sampler_top_p", args["vocab"], ptr(lg), args["T"], args["p"], 1, 0, None, ptr(out), ptr(ws),
+               ws.numel(), stream())
