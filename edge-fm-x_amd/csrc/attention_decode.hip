@@ -15,19 +15,24 @@
 //    so each lane owns one head column and 16 keys; the online softmax is in-lane plus
 //    one cross-half exchange. O^T = V^T . P^T reuses P from the score registers; V^T is
 //    staged per wave in LDS with the same key permutation as the accumulator rows.
-//  * RoPE on read by angle addition: cos/sin(k * f_d) for the 32 key offsets of a tile
-//    are tabulated once per workgroup, cos/sin(base * f_d) once per tile (one sincos
-//    per thread), so rotating a key pair costs FMAs, not transcendentals. The tables
-//    use sincos_reduced (Cody-Waite reduction + the hardware sin/cos, ~1e-6 absolute),
-//    as the reference's decode kernel uses the fast sin/cos intrinsics.
-//  * Each wave walks 32-key tiles of the workgroup's chunk; the next tile's K/V loads
+//  * Keys are either rotated on read (cache of un-rotated K, the reference's layout) by
+//    angle addition: cos/sin(k * f_d) for the 32 key offsets of a tile are tabulated
+//    once per workgroup, cos/sin(base * f_d) once per tile (one sincos per thread); or
+//    the cache already holds rotated keys and only this step's newest row is rotated
+//    (and stored back) by the two lanes that hold it. The tables use sincos_reduced
+//    (Cody-Waite reduction + the hardware sin/cos, ~1e-6 absolute), as the reference's
+//    decode kernel uses the fast sin/cos intrinsics.
+//  * Latency first: the query, the first tile of every wave and the RoPE frequencies
+//    are requested before *d_kv_len is read. Split b always covers keys
+//    [b * kps, (b + 1) * kps) (kps fixed per launch from max_kv_len), so those loads do
+//    not wait for the length; rows past it are masked afterwards.
+//  * Each wave walks 32-key tiles of the workgroup's split; the next tile's K/V loads
 //    are issued before the current tile's matrix work. Waves merge their (m, l, O)
 //    through LDS.
-//  * The split count is derived on the device from L = *d_kv_len and a host-chosen
-//    keys-per-split target, so one launch geometry (sized by max_kv_len) serves every
-//    step of a captured HIP graph. Short contexts run one workgroup per KV head (no
-//    merge); long ones write fp32 (o, m, l) partials and the last workgroup of a KV head
-//    (device-scope fence + atomic counter) merges them and resets the counter.
+//  * One launch geometry (sized by max_kv_len) serves every step of a captured HIP
+//    graph. A single split writes the output itself; otherwise every split writes fp32
+//    (o, m, l) partials that a second kernel (one workgroup per query head) merges, or
+//    that the o_proj GEMV merges in its prologue (efm_decode_attention_merge_o_proj).
 #include "common.hpp"
 
 #include <algorithm>
@@ -54,12 +59,14 @@ struct DecodeArgs {
     int num_kv_heads;
     int q_sn, q_sh, k_sn, k_sh, v_sn, v_sh;   // element strides
     int q_pos_off, k_pos_off;
-    int rope_q, rope_k;                       // apply rotation to q / to k
+    int rope_q;                               // rotate q (and, by ROTK / fix_last, keys)
+    int fix_last;                             // rotate + store back row L - 1 (ROTK = false)
+    int row_bound;                            // rows that may be read (allocation bound)
     int split_cap;                            // gridDim.x
-    int keys_per_split;                       // target chunk length
+    int keys_per_split;                       // keys of split b: [b * kps, (b + 1) * kps)
     float* o_part;                            // [Hkv][split_cap][G][HD]
     float* ml_part;                           // [Hkv][split_cap][G][2]
-    uint32_t* counter;                        // [Hkv]
+    uint32_t* counter;                        // [Hkv] (reserved in the workspace, unused)
     RopeTable rope;
 };
 
@@ -69,10 +76,14 @@ union BfPack {
     uint32_t w[4];
 };
 
-// MERGE = true: self-contained operator (the last workgroup of a KV head merges the
-// splits). MERGE = false: every split only writes its (o, m, l) partial; the consumer
-// (the o_proj GEMV prologue, efm_decode_attention_merge_o_proj) merges them.
-template <int HD, int G, bool MERGE>
+// MERGE = true: a single split (split_cap == 1) writes the normalised output directly.
+// MERGE = false: every split writes its (o, m, l) partial; a consumer merges them
+// (decode_merge_kernel, or the o_proj GEMV prologue of efm_decode_attention_merge_o_proj).
+// ROTK = true: every key is rotated on read (the cache holds un-rotated K). ROTK = false:
+// the cache holds rotated K; with a.fix_last its newest row L - 1 is still un-rotated
+// (written by the QKV projection of this step): the two lanes holding it rotate it,
+// use it and store it back rotated, so the cache is fully rotated after the call.
+template <int HD, int G, bool MERGE, bool ROTK>
 __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs a) {
     constexpr int HALF = HD / 2;
     constexpr int KS = HD / 16;        // MFMA k-steps over head_dim
@@ -80,42 +91,39 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
     constexpr int VP = kTileKeys + 8;  // V^T row pitch (bf16)
     static_assert(G <= 32, "group too large");
 
-    __shared__ float sfreq[HALF];
-    __shared__ float2 cs_off[kTileKeys][HALF + 1];      // cos/sin(k * f_d), k < 32 (padded rows)
-    __shared__ float2 cs_q[HALF];                       // cos/sin(qpos * f_d)
-    __shared__ float2 cs_base[kAttnWaves][HALF];        // cos/sin(base * f_d) of each wave's tile
+    __shared__ float2 cs_qk[2][HALF];                                 // cos/sin at q's / key L-1's position
+    __shared__ float sfreq[ROTK ? HALF : 1];
+    __shared__ float2 cs_off[ROTK ? kTileKeys : 1][HALF + 1];         // cos/sin(k * f_d), k < 32
+    __shared__ float2 cs_base[ROTK ? kAttnWaves : 1][HALF];           // cos/sin(tile base * f_d)
     __shared__ __align__(16) bf16_t Vt[kAttnWaves][HD * VP];
     __shared__ float om[kAttnWaves][32], ol[kAttnWaves][32];
     __shared__ float ob[kAttnWaves][G][HD];
-    __shared__ float sml[kMaxSplits * G];
-    __shared__ float sll[kMaxSplits * G];
-    __shared__ bool is_last;
 
     const int tid = threadIdx.x;
     const int wave = tid / kWave, lane = tid % kWave;
     const int ql = lane % 32, hh = lane / 32;
     const int kvh = blockIdx.y;
     const int b = blockIdx.x;
-
-    uint32_t L = a.kv_len;
-    if (a.d_kv_len != nullptr) L = min(a.d_kv_len[0], a.max_kv_len);
-    const int kps = max(a.keys_per_split, kTileKeys);
-    const int nsplit = (L == 0) ? 1 : (int)min((uint32_t)a.split_cap, (L + kps - 1) / kps);
-    if (b >= nsplit) return;
-    const int chunk = (L == 0) ? 0 : (int)((L + nsplit - 1) / nsplit);
-    const int start = b * chunk;
-    const int end = min((int)L, start + chunk);
-    const int ntiles = (end > start) ? (end - start + kTileKeys - 1) / kTileKeys : 0;
-    const int rounds = (ntiles + kAttnWaves - 1) / kAttnWaves;
+    const int kps = a.keys_per_split;   // a multiple of 4 x 32 keys, fixed per launch
+    const int start = b * kps;
 
     const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
     const bf16_t* vbase = a.v + (size_t)kvh * a.v_sh;
 
-    // ---- issue the first tile's K / V loads before anything else
+    // ---- 1. every load that does not depend on L goes out first: the query, each
+    //         wave's first tile (rows below the allocation bound; rows >= L are masked
+    //         once L is known) and the RoPE frequencies
+    uint4 qraw[KS];
+    {
+        const bool qv = ql < G;
+        const bf16_t* qp = a.q + (size_t)(kvh * G + (qv ? ql : 0)) * a.q_sh + hh * 8;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qraw[ks] = qv ? *reinterpret_cast<const uint4*>(qp + ks * 16) : make_uint4(0, 0, 0, 0);
+    }
     uint4 kr[KS], vr[KS];
-    auto load_tile = [&](int t) {
+    auto load_tile = [&](int t, int lim) {
         const int j = start + t * kTileKeys + ql;
-        const bool ok = (t < ntiles) && (j < end);
+        const bool ok = j < lim;
         const bf16_t* kp = kbase + (size_t)(ok ? j : 0) * a.k_sn + hh * 8;
         const bf16_t* vp = vbase + (size_t)(ok ? j : 0) * a.v_sn + hh * 8;
 #pragma unroll
@@ -124,17 +132,29 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
             vr[ks] = ok ? load_stream16(vp + ks * 16) : make_uint4(0, 0, 0, 0);
         }
     };
-    load_tile(wave);
+    load_tile(wave, min(a.row_bound, start + kps));
+    const float freq = (a.rope_q && tid < 2 * HALF) ? a.rope.inv_freq[tid % HALF] : 0.f;
 
-    // ---- RoPE tables
-    if (tid < HALF) sfreq[tid] = a.rope.inv_freq[tid];
-    __syncthreads();
-    if (a.rope_q && tid < HALF) {
+    // ---- 2. the context length and this split's key range [start, end)
+    uint32_t L = a.kv_len;
+    if (a.d_kv_len != nullptr) L = min(a.d_kv_len[0], a.max_kv_len);
+    const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
+    if (b >= nsplit) return;
+    const int end = min((int)L, start + kps);
+    const int ntiles = (end > start) ? (end - start + kTileKeys - 1) / kTileKeys : 0;
+    const int rounds = (ntiles + kAttnWaves - 1) / kAttnWaves;
+
+    // ---- 3. RoPE: cos/sin at the query position (threads < HALF) and at the newest
+    //         key's position (threads HALF .. 2 HALF - 1), one sincos per thread
+    if (a.rope_q && tid < 2 * HALF) {
+        const int pos = (int)L - 1 + (tid < HALF ? a.q_pos_off : a.k_pos_off);
         float sn, cs;
-        sincos_reduced((float)((int)L - 1 + a.q_pos_off) * sfreq[tid], &sn, &cs);
-        cs_q[tid] = make_float2(cs, sn);
+        sincos_reduced((float)pos * freq, &sn, &cs);
+        cs_qk[tid / HALF][tid % HALF] = make_float2(cs, sn);
+        if (ROTK && tid < HALF) sfreq[tid] = freq;
     }
-    if (a.rope_k) {
+    if (ROTK) {
+        __syncthreads();
         for (int i = tid; i < kTileKeys * HALF; i += kAttnThreads) {
             const int kk = i / HALF, d = i % HALF;
             float sn, cs;
@@ -142,25 +162,20 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
             cs_off[kk][d] = make_float2(cs, sn);
         }
     }
-
     __syncthreads();
+
     // ---- queries: B operand, lane = head column ql (zero for ql >= G), d = ks*16 + hh*8 + e
     BfPack qf[KS];
     {
         float x[KS][8];
-        const bool qv = ql < G;
-        const bf16_t* qp = a.q + (size_t)(kvh * G + (qv ? ql : 0)) * a.q_sh + hh * 8;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            uint4 u = qv ? *reinterpret_cast<const uint4*>(qp + ks * 16) : make_uint4(0, 0, 0, 0);
-            unpack8(u, x[ks]);
-        }
+        for (int ks = 0; ks < KS; ++ks) unpack8(qraw[ks], x[ks]);
         if (a.rope_q) {
 #pragma unroll
             for (int ks = 0; ks < KS / 2; ++ks)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float2 c2 = cs_q[ks * 16 + hh * 8 + e];
+                    const float2 c2 = cs_qk[0][ks * 16 + hh * 8 + e];
                     const float cs = c2.x, sn = c2.y;
                     const float x0 = x[ks][e], x1 = x[ks + KS / 2][e];
                     x[ks][e] = x0 * cs - x1 * sn;
@@ -183,18 +198,25 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
         for (int e = 0; e < 16; ++e) oacc[t][e] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
     bf16_t* vt = Vt[wave];
+    const int fix_row = (!ROTK && a.rope_q && a.fix_last && L > 0) ? (int)L - 1 : -1;
 
     for (int r = 0; r < rounds; ++r) {
         const int t = r * kAttnWaves + wave;
         const bool active = t < ntiles;
         const int t0 = start + t * kTileKeys;
-        // base-angle table for the 4 tiles of this round: one sincos per thread
-        if (a.rope_k && tid < kAttnWaves * HALF) {
+        if (ROTK && tid < kAttnWaves * HALF) {
+            // base-angle table for the 4 tiles of this round: one sincos per thread
             const int w = tid / HALF, d = tid % HALF;
             const int base = start + (r * kAttnWaves + w) * kTileKeys + a.k_pos_off;
             float sn, cs;
             sincos_reduced((float)base * sfreq[d], &sn, &cs);
             cs_base[w][d] = make_float2(cs, sn);
+        }
+        // the first tile was loaded before L was known: rows >= end carry P = 0 but
+        // may hold any bits (NaN / Inf), so their V is zeroed
+        if (r == 0 && t0 + ql >= end) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) vr[ks] = make_uint4(0, 0, 0, 0);
         }
         // V^T into this wave's LDS tile: Vt[d][key]
 #pragma unroll
@@ -209,9 +231,9 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
         }
         __syncthreads();
 
-        // rotate K in registers (angle addition) and pack the A operand
+        // the A operand: keys rotated in registers (angle addition), or as stored
         BfPack kp[KS];
-        if (a.rope_k) {
+        if (ROTK) {
 #pragma unroll
             for (int ks = 0; ks < KS / 2; ++ks) {
                 float x0[8], x1[8];
@@ -233,11 +255,33 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
                 kp[ks + KS / 2].u = pack8(x1);
             }
         } else {
+            if (t0 + ql == fix_row) {
+                // the newest key: rotate at its position and store it back rotated
+                bf16_t* kw = const_cast<bf16_t*>(kbase) + (size_t)fix_row * a.k_sn + hh * 8;
+#pragma unroll
+                for (int ks = 0; ks < KS / 2; ++ks) {
+                    float x0[8], x1[8];
+                    unpack8(kr[ks], x0);
+                    unpack8(kr[ks + KS / 2], x1);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float2 c2 = cs_qk[1][ks * 16 + hh * 8 + e];
+                        const float y0 = x0[e] * c2.x - x1[e] * c2.y;
+                        const float y1 = x1[e] * c2.x + x0[e] * c2.y;
+                        x0[e] = y0;
+                        x1[e] = y1;
+                    }
+                    kr[ks] = pack8(x0);
+                    kr[ks + KS / 2] = pack8(x1);
+                    *reinterpret_cast<uint4*>(kw + ks * 16) = kr[ks];
+                    *reinterpret_cast<uint4*>(kw + (ks + KS / 2) * 16) = kr[ks + KS / 2];
+                }
+            }
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) kp[ks].u = kr[ks];
         }
         // prefetch the next round's tile while this one is multiplied
-        load_tile(t + kAttnWaves);
+        load_tile(t + kAttnWaves, end);
 
         if (active) {
             f32x16_t s;
@@ -255,7 +299,6 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
             }
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
             const float m_new = fmaxf(m_run, mloc);  // finite: the tile holds a valid key
-            const float alpha = exp2f(m_run - m_new);
             float p[16], psum = 0.f;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
@@ -263,12 +306,17 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
                 psum += p[e];
             }
             psum += __shfl_xor(psum, 32, kWave);
-            l_run = l_run * alpha + psum;
+            if (r == 0) {
+                l_run = psum;   // first tile: nothing accumulated yet to rescale
+            } else {
+                const float alpha = exp2f(m_run - m_new);
+                l_run = l_run * alpha + psum;
+#pragma unroll
+                for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+            }
             m_run = m_new;
-#pragma unroll
-            for (int tt = 0; tt < DT; ++tt)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 BfPack pb;
@@ -327,66 +375,120 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
             }
         }
     }
-    if (!MERGE || nsplit == 1) return;
+}
 
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&a.counter[kvh], 1u);
-        is_last = (prev == (uint32_t)nsplit - 1);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-
-    // Merge: stage every split's (m, l) in LDS with parallel loads, turn them into
-    // normalised weights w_s = exp2(m_s - M) / sum_s exp2(m_s - M) l_s (one wave per query
-    // head), then accumulate the partial outputs with independent, unrolled loads.
-    const size_t head_base = (size_t)kvh * a.split_cap * G;
-    for (int i = tid; i < nsplit * G; i += kAttnThreads) {
-        sml[i] = a.ml_part[(head_base + i) * 2];
-        sll[i] = a.ml_part[(head_base + i) * 2 + 1];
-    }
-    __syncthreads();
-    for (int g = wave; g < G; g += kAttnWaves) {
+// Split merge of efm_attention_decode: one workgroup per query head, 256 threads =
+// HD/4 float4 columns x NPART split lanes. The partial loads of the first chunk are
+// issued before the (m, l) pairs are reduced into the normalised split weights
+// w_s = exp2(m_s - M) / sum_s exp2(m_s - M) l_s; each lane accumulates its splits in
+// order and the lanes are summed in a fixed order.
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void decode_merge_kernel(DecodeArgs a, int G) {
+    constexpr int NCOL = HD / 4;
+    constexpr int NPART = kAttnThreads / NCOL;
+    constexpr int CH = 8;   // loads in flight per thread
+    __shared__ float sw[kMaxSplits];
+    __shared__ float4 red[NPART][NCOL];
+    const int tid = threadIdx.x;
+    const int h = blockIdx.x, kvh = h / G, g = h % G;
+    const int col = tid % NCOL, part = tid / NCOL;
+    uint32_t L = a.kv_len;
+    if (a.d_kv_len != nullptr) L = min(a.d_kv_len[0], a.max_kv_len);
+    const int kps = a.keys_per_split;
+    const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
+    const size_t row0 = (size_t)kvh * a.split_cap * G + g;   // (kvh, split 0, g) in units of rows
+    const float* op = a.o_part + row0 * HD + col * 4;
+    float4 v[CH];
+    auto load_chunk = [&](int s0) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int sp = s0 + k * NPART;
+            v[k] = (sp < nsplit) ? *reinterpret_cast<const float4*>(op + (size_t)sp * G * HD)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    load_chunk(part);
+    if (tid < kWave) {
+        constexpr int kPerLane = kMaxSplits / kWave;
+        float ms[kPerLane], ls[kPerLane];
         float M = -INFINITY;
-        for (int s = lane; s < nsplit; s += kWave) M = fmaxf(M, sml[s * G + g]);
+#pragma unroll
+        for (int k = 0; k < kPerLane; ++k) {
+            const int sp = tid + k * kWave;
+            ms[k] = -INFINITY;
+            ls[k] = 0.f;
+            if (sp < nsplit) {
+                const float2 ml = *reinterpret_cast<const float2*>(a.ml_part + (row0 + (size_t)sp * G) * 2);
+                ms[k] = ml.x;
+                ls[k] = ml.y;
+            }
+            M = fmaxf(M, ms[k]);
+        }
         M = wave_max(M);
         float den = 0.f;
-        for (int s = lane; s < nsplit; s += kWave) {
-            const float m = sml[s * G + g];
-            den += (m == -INFINITY) ? 0.f : exp2f(m - M) * sll[s * G + g];
-        }
+#pragma unroll
+        for (int k = 0; k < kPerLane; ++k) den += (ms[k] == -INFINITY) ? 0.f : exp2f(ms[k] - M) * ls[k];
         den = wave_sum(den);
         const float inv = (den > 0.f) ? 1.f / den : 0.f;
-        for (int s = lane; s < nsplit; s += kWave) {
-            const float m = sml[s * G + g];
-            sml[s * G + g] = (m == -INFINITY) ? 0.f : exp2f(m - M) * inv;
+#pragma unroll
+        for (int k = 0; k < kPerLane; ++k) {
+            const int sp = tid + k * kWave;
+            if (sp < nsplit) sw[sp] = (ms[k] == -INFINITY) ? 0.f : exp2f(ms[k] - M) * inv;
         }
     }
     __syncthreads();
-    for (int t = tid; t < G * HD; t += kAttnThreads) {
-        const int g = t / HD, d = t % HD;
-        const float* op = a.o_part + (head_base + g) * HD + d;
-        float num = 0.f;
-#pragma unroll 8
-        for (int s = 0; s < nsplit; ++s) num = fmaf(sml[s * G + g], op[(size_t)s * G * HD], num);
-        a.o[(size_t)(kvh * G + g) * HD + d] = (bf16_t)f32_to_bf16(num);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = part; s0 < nsplit; s0 += CH * NPART) {
+        if (s0 != part) load_chunk(s0);
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int sp = s0 + k * NPART;
+            if (sp < nsplit) {
+                const float wk = sw[sp];
+                acc.x = fmaf(wk, v[k].x, acc.x);
+                acc.y = fmaf(wk, v[k].y, acc.y);
+                acc.z = fmaf(wk, v[k].z, acc.z);
+                acc.w = fmaf(wk, v[k].w, acc.w);
+            }
+        }
     }
-    if (tid == 0) a.counter[kvh] = 0u;
+    red[part][col] = acc;
+    __syncthreads();
+    if (part == 0) {
+        float4 t = red[0][col];
+#pragma unroll
+        for (int p = 1; p < NPART; ++p) {
+            t.x += red[p][col].x;
+            t.y += red[p][col].y;
+            t.z += red[p][col].z;
+            t.w += red[p][col].w;
+        }
+        bf16_t* o = a.o + (size_t)h * HD + col * 4;
+        o[0] = (bf16_t)f32_to_bf16(t.x);
+        o[1] = (bf16_t)f32_to_bf16(t.y);
+        o[2] = (bf16_t)f32_to_bf16(t.z);
+        o[3] = (bf16_t)f32_to_bf16(t.w);
+    }
 }
 
-// Keys per split: one 32-key tile per wave (128 keys per workgroup) so that every K/V
-// load of a workgroup is in flight at once; the split count is capped at 256 workgroups.
+// Split geometry: 128 keys (one 32-key tile per wave) per workgroup, so that every K/V
+// load of a workgroup is in flight at once, until the grid reaches 256 workgroups; past
+// that the keys per split grow in steps of 128. Split b covers keys [b * kps, (b+1) * kps)
+// whatever the current length, so its first loads need not wait for *d_kv_len.
 constexpr int kKeysPerSplit = 128;
 
-int decode_split_cap(int num_kv_heads, uint32_t max_kv_len) {
-    const int by_len = (int)std::max<uint32_t>(1u, (max_kv_len + kKeysPerSplit - 1) / kKeysPerSplit);
-    const int by_chip = std::max(1, kMaxSplits / std::max(1, num_kv_heads));
-    return std::min(by_len, by_chip);
+int decode_keys_per_split(int num_kv_heads, uint32_t max_kv_len) {
+    const uint32_t bound = std::max<uint32_t>(max_kv_len, 1u);
+    const uint32_t by_chip = (uint32_t)std::max(1, kMaxSplits / std::max(1, num_kv_heads));
+    const uint32_t steps = (bound + kKeysPerSplit * by_chip - 1) / (kKeysPerSplit * by_chip);
+    return (int)(steps * kKeysPerSplit);
 }
 
-int decode_keys_per_split() { return kKeysPerSplit; }
+int decode_split_cap(int num_kv_heads, uint32_t max_kv_len) {
+    const uint32_t bound = std::max<uint32_t>(max_kv_len, 1u);
+    const int kps = decode_keys_per_split(num_kv_heads, bound);
+    return (int)((bound + kps - 1) / kps);
+}
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -419,6 +521,8 @@ int validate_attention_ctx(const efm_attention_ctx* c, const char* who) {
         return set_error(EFM_ERR_UNSUPPORTED, "%s: GQA group size %u not supported", who, G);
     if (c->pos_encoding != EFM_POS_NONE && c->pos_encoding != EFM_POS_ROPE_LLAMA)
         return set_error(EFM_ERR_UNSUPPORTED, "%s: pos_encoding %d", who, c->pos_encoding);
+    if (c->k_already_prerotated < 0 || c->k_already_prerotated > EFM_K_PREROTATED_EXCEPT_NEWEST)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "%s: k_already_prerotated %d", who, c->k_already_prerotated);
     if (c->pos_encoding == EFM_POS_ROPE_LLAMA && (c->rope_theta <= 0.f || c->rope_scale <= 0.f))
         return set_error(EFM_ERR_INVALID_ARGUMENT, "%s: rope_theta/rope_scale must be positive", who);
     const uint32_t strides[6] = {c->q_stride_n, c->q_stride_h, c->k_stride_n, c->k_stride_h, c->kv_stride_n,
@@ -474,20 +578,28 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
     a.q_pos_off = (int)ctx->q_rope_pos_offset;
     a.k_pos_off = (int)ctx->k_rope_pos_offset;
     a.rope_q = ctx->pos_encoding == EFM_POS_ROPE_LLAMA;
-    a.rope_k = a.rope_q && !ctx->k_already_prerotated;
-    a.split_cap = decode_split_cap((int)ctx->num_kv_heads, std::max<uint32_t>(bound, 1u));
-    a.keys_per_split = kKeysPerSplit;
+    const bool rotk = a.rope_q && ctx->k_already_prerotated == 0;
+    a.fix_last = a.rope_q && ctx->k_already_prerotated == EFM_K_PREROTATED_EXCEPT_NEWEST;
+    a.row_bound = (int)std::max<uint32_t>(bound, 1u);
+    a.split_cap = decode_split_cap((int)ctx->num_kv_heads, bound);
+    a.keys_per_split = decode_keys_per_split((int)ctx->num_kv_heads, bound);
     char* wsb = static_cast<char*>(workspace);
     a.o_part = reinterpret_cast<float*>(wsb);
     a.ml_part = reinterpret_cast<float*>(wsb + ws.o_bytes);
     a.counter = reinterpret_cast<uint32_t*>(wsb + ws.o_bytes + ws.ml_bytes);
 
     dim3 grid(a.split_cap, ctx->num_kv_heads), block(kAttnThreads);
-#define EFM_DEC_CASE(HDV, GV)                                                                             \
-    if (hd == HDV && G == GV) {                                                                           \
-        if (merge) hipLaunchKernelGGL((decode_attn_kernel<HDV, GV, true>), grid, block, 0, stream, a);    \
-        else hipLaunchKernelGGL((decode_attn_kernel<HDV, GV, false>), grid, block, 0, stream, a);         \
-        return check_launch("attention_decode");                                                          \
+    // one split: that workgroup writes the output; more: partials, then the merge kernel
+    const bool direct = merge && a.split_cap == 1;
+#define EFM_DEC_CASE(HDV, GV)                                                                                  \
+    if (hd == HDV && G == GV) {                                                                                \
+        if (direct && rotk) hipLaunchKernelGGL((decode_attn_kernel<HDV, GV, true, true>), grid, block, 0, stream, a); \
+        else if (direct) hipLaunchKernelGGL((decode_attn_kernel<HDV, GV, true, false>), grid, block, 0, stream, a);   \
+        else if (rotk) hipLaunchKernelGGL((decode_attn_kernel<HDV, GV, false, true>), grid, block, 0, stream, a);     \
+        else hipLaunchKernelGGL((decode_attn_kernel<HDV, GV, false, false>), grid, block, 0, stream, a);              \
+        if (merge && !direct)                                                                                  \
+            hipLaunchKernelGGL((decode_merge_kernel<HDV>), dim3(ctx->num_qo_heads), block, 0, stream, a, G);    \
+        return check_launch("attention_decode");                                                               \
     }
     EFM_DEC_CASE(128, 1) EFM_DEC_CASE(128, 2) EFM_DEC_CASE(128, 3) EFM_DEC_CASE(128, 4)
     EFM_DEC_CASE(128, 6) EFM_DEC_CASE(128, 7) EFM_DEC_CASE(128, 8)

@@ -265,6 +265,8 @@ extern "C" int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q
                                      void* o, uint32_t qo_len, uint32_t kv_len, int32_t causal, hipStream_t stream) {
     int rc = validate_attention_ctx(ctx, "attention_prefill");
     if (rc) return rc;
+    if (ctx->k_already_prerotated == EFM_K_PREROTATED_EXCEPT_NEWEST)
+        return set_error(EFM_ERR_UNSUPPORTED, "attention_prefill: k_already_prerotated = 2 is a decode-only mode");
     if (!q || !k || !v || !o) return set_error(EFM_ERR_INVALID_ARGUMENT, "attention_prefill: null tensor pointer");
     if (kv_len < qo_len)
         return set_error(EFM_ERR_INVALID_ARGUMENT, "attention_prefill: kv_len %u < qo_len %u", kv_len, qo_len);

@@ -239,7 +239,7 @@ __global__ __launch_bounds__(kChainThreads, 1) void decode_chain_kernel(ChainArg
         if (lane == 0) s_epoch = coherent_load(a.epoch);
         const uint32_t L = min(a.d_kv_len[0], a.max_kv_len);
         const int kps = a.keys_per_split;
-        const int nsplit = (L == 0) ? 1 : (int)min((uint32_t)a.split_cap, (L + kps - 1) / kps);
+        const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
         uint4 rv[4], pv[4], iv[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(kChainThreads, 1) void decode_chain_kernel(ChainArg
 namespace efm {
 
 int decode_split_cap(int num_kv_heads, uint32_t max_kv_len);
-int decode_keys_per_split();
+int decode_keys_per_split(int num_kv_heads, uint32_t max_kv_len);
 size_t decode_workspace_bytes(const efm_attention_ctx* ctx, uint32_t max_kv_len);
 size_t decode_ml_offset(const efm_attention_ctx* ctx, uint32_t max_kv_len);
 int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
@@ -652,7 +652,7 @@ extern "C" int efm_decode_layer_chain(const efm_attention_ctx* ctx, int32_t hidd
     a.ml_part = reinterpret_cast<const float*>(static_cast<const char*>(attn_workspace) +
                                                decode_ml_offset(ctx, max_kv_len));
     a.split_cap = decode_split_cap(Hkv, max_kv_len);
-    a.keys_per_split = decode_keys_per_split();
+    a.keys_per_split = decode_keys_per_split(Hkv, max_kv_len);
     a.d_kv_len = d_kv_len;
     a.max_kv_len = max_kv_len;
     a.r_in = static_cast<const bf16_t*>(residual_in);

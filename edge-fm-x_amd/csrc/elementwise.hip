@@ -291,8 +291,9 @@ namespace efm {
 struct MropeArgs {
     bf16_t* q;
     bf16_t* k;
-    const int32_t* pos;   // [3, pos_stride]
+    const int32_t* pos;   // [3, pos_stride]; NULL: every section uses pos_offset + token
     int pos_stride;       // tokens per position row
+    int pos_offset;
     int S, Hq, Hkv, hd;
     int q_sn, k_sn;       // token strides (elements); heads are contiguous hd apart
     int cum0, cum1;
@@ -316,7 +317,7 @@ __global__ void mrope_kernel(MropeArgs a) {
     const int d = threadIdx.x;
     if (d >= half) return;
     const int sec = (d < a.cum0) ? 0 : (d < a.cum1 ? 1 : 2);
-    const int p = a.pos[sec * a.pos_stride + t];
+    const int p = (a.pos != nullptr) ? a.pos[sec * a.pos_stride + t] : a.pos_offset + t;
     const float inv = a.rope.inv_freq[d];
     bf16_t* row = (h < a.Hq) ? a.q + (size_t)t * a.q_sn + (size_t)h * a.hd
                              : a.k + (size_t)t * a.k_sn + (size_t)(h - a.Hq) * a.hd;
@@ -387,6 +388,7 @@ extern "C" int efm_mrope(void* q, void* k, const int32_t* position_ids, int32_t 
     a.k = static_cast<bf16_t*>(k);
     a.pos = position_ids;
     a.pos_stride = position_stride;
+    a.pos_offset = 0;
     a.S = seq_len;
     a.Hq = num_qo_heads;
     a.Hkv = num_kv_heads;
@@ -399,6 +401,35 @@ extern "C" int efm_mrope(void* q, void* k, const int32_t* position_ids, int32_t 
     hipLaunchKernelGGL(mrope_kernel, dim3(seq_len, num_qo_heads + num_kv_heads), dim3(((head_dim / 2) + 63) / 64 * 64),
                        0, stream, a);
     return check_launch("mrope");
+}
+
+extern "C" int efm_rope_llama_inplace(void* q, void* k, int32_t seq_len, int32_t num_qo_heads, int32_t num_kv_heads,
+                                      int32_t head_dim, int32_t q_stride_n, int32_t k_stride_n, int32_t pos_offset,
+                                      float rope_theta, float rope_scale, hipStream_t stream) {
+    if (!q || !k) return set_error(EFM_ERR_INVALID_ARGUMENT, "rope_llama_inplace: null pointer");
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 2 * kMaxHalfDim)
+        return set_error(EFM_ERR_UNSUPPORTED, "rope_llama_inplace: head_dim");
+    if (seq_len < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || pos_offset < 0)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "rope_llama_inplace: bad sizes");
+    if (seq_len == 0) return EFM_OK;
+    MropeArgs a;
+    a.q = static_cast<bf16_t*>(q);
+    a.k = static_cast<bf16_t*>(k);
+    a.pos = nullptr;
+    a.pos_stride = 0;
+    a.pos_offset = pos_offset;
+    a.S = seq_len;
+    a.Hq = num_qo_heads;
+    a.Hkv = num_kv_heads;
+    a.hd = head_dim;
+    a.q_sn = q_stride_n ? q_stride_n : num_qo_heads * head_dim;
+    a.k_sn = k_stride_n ? k_stride_n : num_kv_heads * head_dim;
+    a.cum0 = head_dim / 2;
+    a.cum1 = head_dim / 2;
+    rope_table_fill(&a.rope, head_dim, rope_theta, rope_scale);
+    hipLaunchKernelGGL(mrope_kernel, dim3(seq_len, num_qo_heads + num_kv_heads), dim3(((head_dim / 2) + 63) / 64 * 64),
+                       0, stream, a);
+    return check_launch("rope_llama_inplace");
 }
 
 extern "C" int efm_decode_mrope_write_kv(const void* q_src, const void* k_src, const void* v_src, void* q_dst,

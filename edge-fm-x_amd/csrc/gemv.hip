@@ -107,7 +107,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, bf16_t* xs, flo
             }
         }
         const int kps = a.keys_per_split;
-        const int nsplit = (L == 0) ? 1 : (int)min((uint32_t)cap, (L + kps - 1) / kps);
+        const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
         if ((int)threadIdx.x < Hq) {
             const int h = threadIdx.x;
             float M = -INFINITY;
@@ -158,7 +158,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, bf16_t* xs, flo
         __shared__ float sw[kMergeMaxHeads * kMergeMaxSplits];
         const uint32_t L = min(a.attn_len[0], a.attn_max_len);
         const int kps = a.keys_per_split;
-        const int nsplit = (L == 0) ? 1 : (int)min((uint32_t)a.split_cap, (L + kps - 1) / kps);
+        const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
         const int hd = a.head_dim, G = a.group;
         const int Hq = a.K / hd;
         for (int i = threadIdx.x; i < Hq * nsplit; i += kGemvThreads) {
@@ -608,7 +608,7 @@ extern "C" int efm_decode_norm_gate_up_swiglu(int32_t hidden, int32_t inter, flo
 
 namespace efm {
 int decode_split_cap(int num_kv_heads, uint32_t max_kv_len);
-int decode_keys_per_split();
+int decode_keys_per_split(int num_kv_heads, uint32_t max_kv_len);
 size_t decode_workspace_bytes(const efm_attention_ctx* ctx, uint32_t max_kv_len);
 size_t decode_ml_offset(const efm_attention_ctx* ctx, uint32_t max_kv_len);
 int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
@@ -636,7 +636,7 @@ extern "C" int efm_decode_attention_merge_o_proj(const efm_attention_ctx* ctx, c
     a.o_part = static_cast<const float*>(workspace);
     a.ml_part = reinterpret_cast<const float*>(static_cast<const char*>(workspace) + decode_ml_offset(ctx, max_kv_len));
     a.split_cap = cap;
-    a.keys_per_split = decode_keys_per_split();
+    a.keys_per_split = decode_keys_per_split((int)ctx->num_kv_heads, max_kv_len);
     a.head_dim = (int)ctx->head_dim;
     a.group = (int)(ctx->num_qo_heads / ctx->num_kv_heads);
     a.attn_len = d_kv_len;

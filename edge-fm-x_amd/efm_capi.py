@@ -29,6 +29,7 @@ EFM_DTYPE_I32 = 3
 
 EFM_POS_NONE = 0
 EFM_POS_ROPE_LLAMA = 1
+EFM_K_PREROTATED_EXCEPT_NEWEST = 2
 
 EFM_LAYOUT_GATE_UP = 0
 EFM_LAYOUT_UP_GATE = 1
@@ -98,6 +99,8 @@ SIGNATURES = {
                                                   c_uint32, c_uint32, c_int32, c_void_p, c_size_t, c_void_p]),
     "efm_sage_quantize": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_uint32, c_uint32, c_void_p, c_void_p,
                                     c_void_p, c_void_p, c_void_p, c_void_p]),
+    "efm_rope_llama_inplace": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                         c_int32, c_float, c_float, c_void_p]),
     "efm_mrope": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
                             c_int32, c_int32, c_int32, c_int32, c_float, c_float, c_void_p]),
     "efm_decode_mrope_write_kv": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32,

@@ -450,7 +450,7 @@ Qwen2_5::Qwen2_5(const EngineConfig& cfg, const ModelConfig& m, const std::unord
 }
 
 void Qwen2_5::reserve_decode(uint32_t max_kv_len) {
-    const efm_attention_ctx c = to_c_ctx(attn_ctx());
+    const efm_attention_ctx c = decode_ctx();
     const size_t bytes = efm_attention_decode_workspace_bytes(&c, max_kv_len);
     if (attn_ws_.empty() || attn_ws_.nbytes() < bytes)
         attn_ws_ = Tensor::zeros({(int64_t)bytes}, DType::UInt8, Device::GPU, device_id_);
@@ -462,7 +462,7 @@ void Qwen2_5::reserve_decode(uint32_t max_kv_len) {
 
 bool Qwen2_5::uses_decode_chain(uint32_t max_kv_len) const {
     if (!chain_enabled_) return false;
-    const efm_attention_ctx c = to_c_ctx(attn_ctx());
+    const efm_attention_ctx c = decode_ctx();
     return efm_decode_chain_supported(&c, m_.hidden, m_.inter, max_kv_len) == EFM_OK;
 }
 
@@ -483,6 +483,15 @@ AttentionOpContext Qwen2_5::attn_ctx() const {
     // (src/layers/attention.cu:135-139).
     c.pos_encoding = m_.mrope ? AttentionPosEncoding::kNone : AttentionPosEncoding::kRoPELlama;
     c.device_id = device_id_;
+    return c;
+}
+
+efm_attention_ctx Qwen2_5::decode_ctx() const {
+    efm_attention_ctx c = to_c_ctx(attn_ctx());
+    // text models: the cache holds keys rotated at their positions (prefill rotates
+    // them before the cache write); this step's key, written un-rotated by the QKV
+    // projection, is rotated by the attention call that first reads it
+    if (!m_.mrope) c.k_already_prerotated = EFM_K_PREROTATED_EXCEPT_NEWEST;
     return c;
 }
 
@@ -513,10 +522,13 @@ void Qwen2_5::prefill(int32_t S, int32_t base, const int32_t* ids, const Tensor*
     nctx.batch_size = (uint32_t)S;
     nctx.hidden_size = (uint32_t)H;
     nctx.eps = m_.eps;
+    // Q and K are rotated before attention (M-RoPE, or RoPE at positions base + i for
+    // text models, qwen2_5.cpp:807-830), so the cache holds rotated keys and the
+    // attention kernels apply no rotation.
     AttentionOpContext actx = attn_ctx();
     actx.q_stride_n = (uint32_t)TOT;
     actx.q_stride_h = (uint32_t)m_.head_dim;
-    if (!m_.mrope) actx.q_rope_pos_offset = (uint32_t)base;  // qwen2_5.cpp:807-830
+    actx.pos_encoding = AttentionPosEncoding::kNone;
     const size_t row = (size_t)KVD * 2;
     for (int l = 0; l < m_.layers; ++l) {
         const Layer& Ly = layers_[l];
@@ -554,6 +566,10 @@ void Qwen2_5::prefill(int32_t S, int32_t base, const int32_t* ids, const Tensor*
                                 m_.head_dim, (int32_t)TOT, (int32_t)KVD, m_.mrope_section[0], m_.mrope_section[1],
                                 m_.mrope_section[2], m_.theta, 1.0f, stream),
                       "prefill mrope");
+        } else {
+            efm_check(efm_rope_llama_inplace(qkv.data_ptr(), kc + (size_t)base * row, S, m_.heads, m_.kv_heads,
+                                             m_.head_dim, (int32_t)TOT, (int32_t)KVD, base, m_.theta, 1.0f, stream),
+                      "prefill rope");
         }
         // 2d. attention over cache rows [0, L)
         Tensor qv = Tensor::view(qkv.data_ptr(), {S, m_.heads, m_.head_dim}, DType::BFloat16, Device::GPU, device_id_);
@@ -612,7 +628,7 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
     efm_check(efm_embedding_lookup(1, H, m_.vocab, token_buf, embed_.data_ptr(), nullptr, 0, -1, dec_h_.data_ptr(),
                                    stream),
               "decode embedding");
-    const efm_attention_ctx c = to_c_ctx(attn_ctx());
+    const efm_attention_ctx c = decode_ctx();
     check<InternalError>(!attn_ws_.empty() && attn_ws_.nbytes() >= efm_attention_decode_workspace_bytes(&c, max_kv_len),
                          "decode workspace not reserved for this cache length");
     if (!chain_ws_.empty() && uses_decode_chain(max_kv_len)) {

@@ -188,6 +188,7 @@ private:
 
     const Tensor& w(const std::unordered_map<std::string, Tensor>& ws, const std::string& name) const;
     void ensure_prefill_capacity(int32_t S);
+    efm_attention_ctx decode_ctx() const;
     AttentionOpContext attn_ctx() const;
 };
 

@@ -71,8 +71,15 @@ typedef struct efm_attention_ctx {
     uint32_t k_rope_pos_offset;
     int32_t dtype;        /* EFM_DTYPE_BF16 only */
     int32_t pos_encoding; /* EFM_POS_NONE | EFM_POS_ROPE_LLAMA */
-    int32_t k_already_prerotated;
+    int32_t k_already_prerotated; /* 0, 1, or EFM_K_PREROTATED_EXCEPT_NEWEST (decode only) */
 } efm_attention_ctx;
+
+/* k_already_prerotated value for the decode entry points (no counterpart in the
+ * reference, which rotates every key on read): cache rows [0, L-1) hold keys already
+ * rotated at their positions; row L-1 (this step's key, written un-rotated by the QKV
+ * projection) is rotated by the call at L-1 + k_rope_pos_offset, used, and stored back
+ * rotated. Running the same call twice on one cache state is therefore not idempotent. */
+#define EFM_K_PREROTATED_EXCEPT_NEWEST 2
 
 /* Bytes of workspace efm_attention_decode needs for caches of up to max_kv_len rows. */
 size_t efm_attention_decode_workspace_bytes(const efm_attention_ctx* ctx, uint32_t max_kv_len);
@@ -80,7 +87,8 @@ size_t efm_attention_decode_workspace_bytes(const efm_attention_ctx* ctx, uint32
 /* Single-query GQA decode attention, split-KV with an in-kernel log-sum-exp merge.
  * q [1, Hq, hd]; k, v [>= kv rows, Hkv, hd]; o [1, Hq, hd].
  * The number of attended rows is *d_kv_len when d_kv_len != NULL (device-resident,
- * graph-stable; then max_kv_len bounds it), else kv_len. With EFM_POS_ROPE_LLAMA, q is
+ * graph-stable; then max_kv_len bounds it and k, v must hold max_kv_len rows, which the
+ * kernel may read before *d_kv_len is known), else kv_len. With EFM_POS_ROPE_LLAMA, q is
  * rotated at position (L - 1 + q_rope_pos_offset) and key j at (j + k_rope_pos_offset)
  * on read; the cache holds un-rotated K. sm_scale = 1/sqrt(hd).
  * Replaces AttentionOp::forward_decode (src/operators/attention_op.h:53-61,
@@ -150,6 +158,15 @@ int efm_mrope(void* q, void* k, const int32_t* position_ids, int32_t position_st
               int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t q_stride_n, int32_t k_stride_n,
               int32_t section0, int32_t section1, int32_t section2, float rope_theta, float rope_scale,
               hipStream_t stream);
+
+/* Rotate-half RoPE in place (the ROPE_LLAMA rotation that the reference applies inside
+ * attention, src/operators/attention_op.cu:1345-1426, moved to the cache write so that
+ * the cache holds rotated keys): token t of q [seq_len, Hq, hd] and k [seq_len, Hkv, hd]
+ * (token strides q_stride_n / k_stride_n, 0 = contiguous) is rotated at position
+ * pos_offset + t; pair (d, d + hd/2) by angle pos * theta^(-2d/hd) / rope_scale. */
+int efm_rope_llama_inplace(void* q, void* k, int32_t seq_len, int32_t num_qo_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int32_t q_stride_n, int32_t k_stride_n, int32_t pos_offset,
+                           float rope_theta, float rope_scale, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------
  * RMSNorm (src/operators/norm_op.h:14-55, FlashInfer norm::RMSNorm / FusedAddRMSNorm

@@ -183,8 +183,13 @@ def test_qwen25_1p5b_shape_greedy_matches_oracle(gpu):
         del eng, keep
     torch.cuda.empty_cache()
     orc = O.Qwen2Oracle(cfg, O.fuse_weights(cfg, w), max_tokens=256, cache_f32=True)
-    exact = _check_against_oracle(toks, _teacher_forced(orc, prompt, toks), tol=0.05)
-    assert exact >= 8
+    steps = _teacher_forced(orc, prompt, toks)
+    exact = _check_against_oracle(toks, steps, tol=0.05)
+    # Every step whose oracle top-2 margin is >= 0.05 logits must match (the gap check
+    # enforces it); with N(0, 0.02) weights the logits are nearly flat (spread ~0.8), so
+    # near-ties below that margin may resolve either way under bf16 rounding.
+    clear = sum(1 for _, margin, _ in steps if margin >= 0.05)
+    assert clear >= 5 and exact >= clear
 
 
 @pytest.mark.parametrize("use_graph", [True, False])

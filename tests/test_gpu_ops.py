@@ -102,6 +102,93 @@ def test_attention_decode_no_rope_and_prerotated(gpu):
     assert_close_bf16(out2, rot_ref, what="prerotated")
 
 
+@pytest.mark.parametrize("hq,hkv,hd", HEAD_CASES)
+@pytest.mark.parametrize("kv_len", [1, 129, 767, 1025, 4099])
+@pytest.mark.parametrize("merge", [True, False])
+def test_attention_decode_prerotated_except_newest(gpu, hq, hkv, hd, kv_len, merge):
+    """EFM_K_PREROTATED_EXCEPT_NEWEST: rows [0, L-1) hold rotated keys, row L-1 the
+    un-rotated key of this step. The output equals RoPE-on-read over the un-rotated cache
+    (and the oracle), row L-1 is stored back rotated (within one bf16 rounding of the
+    oracle's rotation) and no other row changes. Rows >= L of the max_kv_len allocation
+    hold NaN: the split loads issued before the length is read must not leak them."""
+    torch.manual_seed(kv_len)
+    max_kv = kv_len + 77
+    q = torch.randn(1, hq, hd, dtype=torch.bfloat16)
+    k = torch.randn(kv_len, hkv, hd, dtype=torch.bfloat16)
+    v = torch.randn(kv_len, hkv, hd, dtype=torch.bfloat16)
+    ref = O.attention_decode(q, k, v, kv_len, O.AttnCtx(hq, hkv, hd))
+    k_rot = O.rope_llama(k, torch.arange(kv_len), 1.0e6).to(torch.bfloat16)
+    kc = torch.full((max_kv, hkv, hd), float("nan"), dtype=torch.bfloat16)
+    vc = torch.full((max_kv, hkv, hd), float("nan"), dtype=torch.bfloat16)
+    kc[: kv_len - 1] = k_rot[: kv_len - 1]
+    kc[kv_len - 1] = k[kv_len - 1]
+    vc[:kv_len] = v
+    kc, vc, qg = kc.to(gpu), vc.to(gpu), q.to(gpu)
+    ctx = C.make_attention_ctx(hq, hkv, hd)
+    ctx.k_already_prerotated = C.EFM_K_PREROTATED_EXCEPT_NEWEST
+    d_len = torch.tensor([kv_len], dtype=torch.int32, device=gpu)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=gpu)
+    if merge:
+        o = torch.empty_like(qg)
+        C.call("efm_attention_decode", ctx, ptr(qg), ptr(kc), ptr(vc), ptr(o), 0, ptr(d_len), max_kv, ptr(ws),
+               ws.numel(), stream())
+        torch.cuda.synchronize()
+        assert_close_bf16(o, ref, what=f"prerotated-except-newest L={kv_len}")
+        plain, _ = _decode(C.make_attention_ctx(hq, hkv, hd), qg, k.to(gpu), v.to(gpu), kv_len)
+        assert_close_bf16(o, plain, what="vs rope-on-read")
+    else:
+        C.call("efm_decode_attention_partials", ctx, ptr(qg), ptr(kc), ptr(vc), ptr(d_len), max_kv, ptr(ws),
+               ws.numel(), stream())
+        torch.cuda.synchronize()
+    got = kc.cpu()
+    assert torch.equal(got[: kv_len - 1], k_rot[: kv_len - 1]), "rows before the newest must not change"
+    assert torch.isnan(got[kv_len:].float()).all(), "rows past L must not be written"
+    assert_close_bf16(got[kv_len - 1], k_rot[kv_len - 1], rtol=1e-2, atol=1e-2, what="newest row stored rotated")
+
+
+def test_attention_decode_partials_ignore_stale_rows(gpu):
+    """Rows >= L of the cache hold NaN / Inf; the partials + merge path must give the
+    same result as a cache that ends at L."""
+    torch.manual_seed(9)
+    hq, hkv, hd, L, max_kv = 12, 2, 128, 300, 1024
+    q = torch.randn(1, hq, hd, dtype=torch.bfloat16, device=gpu)
+    k = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    v = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    k[L:] = float("inf")
+    v[L:] = float("nan")
+    ctx = C.make_attention_ctx(hq, hkv, hd)
+    d_len = torch.tensor([L], dtype=torch.int32, device=gpu)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=gpu)
+    o = torch.empty_like(q)
+    C.call("efm_attention_decode", ctx, ptr(q), ptr(k), ptr(v), ptr(o), 0, ptr(d_len), max_kv, ptr(ws), ws.numel(),
+           stream())
+    torch.cuda.synchronize()
+    ref = O.attention_decode(q.cpu(), k[:L].cpu(), v[:L].cpu(), L, O.AttnCtx(hq, hkv, hd))
+    assert torch.isfinite(o.float()).all()
+    assert_close_bf16(o, ref)
+
+
+@pytest.mark.parametrize("S,base,hq,hkv,hd", [(37, 0, 12, 2, 128), (5, 1000, 14, 2, 64), (300, 16000, 28, 4, 128)])
+def test_rope_llama_inplace_matches_oracle(gpu, S, base, hq, hkv, hd):
+    """Q in a fused QKV buffer (token stride) and K rows rotated in place at positions
+    base + t; one bf16 rounding of the oracle's fp32 rotation."""
+    torch.manual_seed(S)
+    tot = (hq + 2 * hkv) * hd
+    qkv = torch.randn(S, tot, dtype=torch.bfloat16)
+    kc = torch.randn(S, hkv, hd, dtype=torch.bfloat16)
+    pos = base + torch.arange(S)
+    want_q = O.rope_llama(qkv[:, : hq * hd].reshape(S, hq, hd), pos, 1.0e6).to(torch.bfloat16)
+    want_k = O.rope_llama(kc, pos, 1.0e6).to(torch.bfloat16)
+    qkv_g, kc_g = qkv.to(gpu), kc.to(gpu)
+    C.call("efm_rope_llama_inplace", ptr(qkv_g), ptr(kc_g), S, hq, hkv, hd, tot, hkv * hd, base, 1.0e6, 1.0,
+           stream())
+    torch.cuda.synchronize()
+    got = qkv_g.cpu()
+    assert_close_bf16(got[:, : hq * hd].reshape(S, hq, hd), want_q, rtol=1e-2, atol=1e-2, what="q")
+    assert torch.equal(got[:, hq * hd:], qkv[:, hq * hd:]), "K/V columns of the QKV buffer untouched"
+    assert_close_bf16(kc_g, want_k, rtol=1e-2, atol=1e-2, what="k")
+
+
 def test_attention_decode_strided_views(gpu):
     """q read from a fused QKV row and K/V from strided views equals contiguous inputs
     (tests/operators/test_attention_prefill.py:167-300)."""
