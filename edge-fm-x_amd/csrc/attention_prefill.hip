@@ -21,6 +21,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace efm {
 
@@ -255,7 +256,265 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
         }
 }
 
+// ---------------------------------------------------------------------------------
+// Pipelined variant (head_dim 128, keys already rotated): one workgroup = 8 wave64s =
+// 256 query rows of one head, 32 per wave. 64-key K and V tiles stream global -> LDS
+// with global_load_lds into a 4-deep ring (no staging registers), so three tiles are
+// in flight while the matrix cores work on one; both tiles keep the row-major layout
+// with 16-byte chunks XOR-swizzled by ((row & 7) << 1). The K operand of S^T = K . Q^T
+// is read with ds_read_b128; the V^T operand of O^T = V^T . P^T is read from the
+// row-major V tile with ds_read_b64_tr_b16, whose 16-lane groups return the transpose
+// of four 4-element rows: lane i of a group receives element i % 4 of the rows read by
+// lanes i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4. The scale is applied in the exponent
+// (exp2(s * scale - m)); the running max is only raised when a row's tile max exceeds
+// it by more than 2^8 (p <= 256 otherwise), which skips most rescales of O; tiles that
+// neither cross the diagonal nor the end are not masked.
+// ---------------------------------------------------------------------------------
+constexpr int kP2Threads = 512;
+constexpr int kP2Q = 256;          // query rows per workgroup
+constexpr int kP2KV = 64;          // keys per tile
+constexpr int kP2S = 4;            // ring depth
+constexpr int kP2HD = 128;
+constexpr int kP2Row = kP2HD * 2;  // bytes per K / V row in LDS
+constexpr int kP2Tile = kP2KV * kP2Row;
+constexpr int kP2Stage = 2 * kP2Tile;
+constexpr int kP2LPW = kP2Stage / 1024 / (kP2Threads / kWave);   // 1 KB wave loads per wave per tile
+constexpr float kP2Lazy = 8.0f;
+
+template <int N>
+__device__ __forceinline__ void p2_vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void p2_vm_wait_tiles(int tiles) {
+    switch (tiles) {
+        case 0: p2_vm_wait<0>(); break;
+        case 1: p2_vm_wait<1 * kP2LPW>(); break;
+        default: p2_vm_wait<2 * kP2LPW>(); break;
+    }
+}
+
+__device__ __forceinline__ uint32_t p2_off(int row, int chunk) {
+    return (uint32_t)(row * kP2Row + ((chunk ^ ((row & 7) << 1)) << 4));
+}
+
+__global__ __launch_bounds__(kP2Threads) void prefill_attn_pipe_kernel(PrefillArgs a, int nqt) {
+    constexpr int KS = kP2HD / 16;     // 8 k-steps
+    constexpr int DT = kP2HD / 32;     // 4 d tiles
+    static_assert(kP2LPW * (kP2Threads / kWave) * 1024 == kP2Stage, "tile not a whole number of wave loads");
+    __shared__ __align__(1024) unsigned char smem[kP2S * kP2Stage];
+
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave, lane = tid % kWave;
+    const int ql = lane % 32, hh = lane / 32;
+    const int t = (int)blockIdx.x;
+    const int qt = nqt - 1 - t / a.Hq;       // heavy (late) query tiles first
+    const int head = t % a.Hq;
+    const int kvh = head / (a.Hq / a.Hkv);
+    const int q0 = qt * kP2Q + wave * 32;
+    const int qi = q0 + ql;
+    const int diag = a.L - a.S;
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
+
+    const int q_last = min(a.S - 1, qt * kP2Q + kP2Q - 1);
+    const int kv_end = a.causal ? min(a.L, q_last + diag + 1) : a.L;
+    const int ntiles = (kv_end + kP2KV - 1) / kP2KV;
+    const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
+    const bf16_t* vbase = a.v + (size_t)kvh * a.v_sh;
+
+    // wave load i of a tile: 4 rows x 16 chunks; lane -> (row l / 16, physical chunk l % 16)
+    auto issue = [&](int tile, int slot) {
+        const int k0 = tile * kP2KV;
+        const int pr = lane >> 4, pc = lane & 15;
+#pragma unroll
+        for (int i = 0; i < kP2LPW; ++i) {
+            const int q = wave + i * (kP2Threads / kWave);   // wave-load index in the stage
+            const bool isv = q >= kP2Tile / 1024;
+            const int row = (q % (kP2Tile / 1024)) * 4 + pr;
+            const int c = pc ^ ((row & 7) << 1);
+            const int j = min(k0 + row, a.L - 1);
+            const bf16_t* src = (isv ? vbase + (size_t)j * a.v_sn : kbase + (size_t)j * a.k_sn) + c * 8;
+            __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                             (__attribute__((address_space(3))) void*)(smem + slot * kP2Stage + q * 1024),
+                                             16, 0, 0);
+        }
+    };
+    // ---- Q (B operand) of this lane's row, d = ks*16 + hh*8 + e; requested before the
+    //      first tiles so that its wait does not include them
+    uint4 qraw[KS];
+    {
+        const bool qv = qi < a.S;
+        const bf16_t* qp = a.q + (size_t)(qv ? qi : 0) * a.q_sn + (size_t)head * a.q_sh;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            qraw[ks] = qv ? *reinterpret_cast<const uint4*>(qp + ks * 16 + hh * 8) : make_uint4(0, 0, 0, 0);
+    }
+    const int pre = min(kP2S - 1, ntiles);
+    for (int p = 0; p < pre; ++p) issue(p, p);
+    bf16x8_t qf[KS];
+    {
+        float x[KS][8];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) unpack8(qraw[ks], x[ks]);
+        if (a.rope_q) {
+            const float pos = (float)(qi + a.q_pos_off);
+#pragma unroll
+            for (int ks = 0; ks < KS / 2; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int d = ks * 16 + hh * 8 + e;
+                    float sn, cs;
+                    sincosf(pos * a.rope.inv_freq[d], &sn, &cs);
+                    const float x0 = x[ks][e], x1 = x[ks + KS / 2][e];
+                    x[ks][e] = x0 * cs - x1 * sn;
+                    x[ks + KS / 2][e] = x1 * cs + x0 * sn;
+                }
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            Pack8 pk;
+            pk.u = pack8(x[ks]);
+            qf[ks] = pk.v;
+        }
+    }
+
+    f32x16_t oacc[DT];
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[tt][e] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    const float scale = a.sm_scale_log2;
+    const int wave_last_key = q0 + 31 + diag;   // causal: last key any row of this wave sees
+
+    // tr-read source of this lane: row offset (g / 2) * 4 + e and d offset 16 (g % 2) + 4 q
+    // inside a 16-key block, from group g = lane / 16, j = lane % 16 = 4 e + q
+    const int tr_g = lane >> 4, tr_j = lane & 15;
+    const int tr_row = (tr_g >> 1) * 4 + (tr_j >> 2);
+    const int tr_d = 16 * (tr_g & 1) + 4 * (tr_j & 3);
+
+    for (int kt = 0; kt < ntiles; ++kt) {
+        p2_vm_wait_tiles(min(kP2S - 2, ntiles - 1 - kt));
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + kP2S - 1 < ntiles) issue(kt + kP2S - 1, (kt + kP2S - 1) % kP2S);
+        if (q0 >= a.S) continue;                      // rows past the end: barriers only
+        const uint32_t kb_lds = lds0 + (uint32_t)((kt % kP2S) * kP2Stage);
+        const uint32_t vb_lds = kb_lds + kP2Tile;
+#pragma unroll
+        for (int sub = 0; sub < kP2KV / 32; ++sub) {
+            const int kb0 = kt * kP2KV + sub * 32;
+            if (kb0 >= kv_end || (a.causal && kb0 > wave_last_key)) break;
+            // K operand (8 x b128) then V^T operand (2 blocks x 4 d tiles x 2 tr reads)
+            bf16x8_t kf[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const uint32_t addr = kb_lds + p2_off(sub * 32 + ql, ks * 2 + hh);
+                asm volatile("ds_read_b128 %0, %1" : "=v"(kf[ks]) : "v"(addr) : "memory");
+            }
+            typedef short s4_t __attribute__((ext_vector_type(4)));
+            s4_t vf[2][DT][2];
+            auto read_v = [&](int kb) {
+#pragma unroll
+                for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) {
+                        const int row = sub * 32 + kb * 16 + 8 * c + tr_row;
+                        const int d = tt * 32 + tr_d;
+                        const uint32_t addr = vb_lds + p2_off(row, d >> 3) + ((d & 7) << 1);
+                        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(vf[kb][tt][c]) : "v"(addr) : "memory");
+                    }
+            };
+            read_v(0);
+            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");   // the K reads (issued first) are done
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kf[ks]));
+            f32x16_t s;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[e] = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
+            read_v(1);
+            // element e: key = kb0 + (e/4)*8 + hh*4 + e%4, query = qi
+            const bool edge = (kb0 + 32 > kv_end) || (a.causal && kb0 + 31 > q0 + diag);
+            if (edge) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int j = kb0 + (e / 4) * 8 + hh * 4 + (e % 4);
+                    const bool ok = (j < kv_end) && (!a.causal || j <= qi + diag);
+                    s[e] = ok ? s[e] : -INFINITY;
+                }
+            }
+            float mloc = s[0];
+#pragma unroll
+            for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * scale;
+            if (__any(mloc > m_run + kP2Lazy)) {
+                const float m_new = fmaxf(m_run, mloc);
+                const float alpha = exp2f(m_run - m_new);   // 0 on the first tile
+                l_run *= alpha;
+#pragma unroll
+                for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+                m_run = m_new;
+            }
+            const float mref = (m_run == -INFINITY) ? 0.f : m_run;
+            float p[16], psum = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                p[e] = exp2f(fmaf(s[e], scale, -mref));
+                psum += p[e];
+            }
+            l_run += psum + __shfl_xor(psum, 32, kWave);
+            Pack8 pb[2];
+            pb[0].u = pack8(&p[0]);
+            pb[1].u = pack8(&p[8]);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int tt = 0; tt < DT; ++tt) {
+                    if (tt == 0) {
+                        // block 0's reads were issued before block 1's eight
+                        if (kb == 0) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+                        else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    }
+                    asm volatile("" : "+v"(vf[kb][tt][0]), "+v"(vf[kb][tt][1]));
+                    union {
+                        s4_t h[2];
+                        bf16x8_t v;
+                    } va;
+                    va.h[0] = vf[kb][tt][0];   // A slots 0-3: keys 16 kb + 4 hh + 0..3
+                    va.h[1] = vf[kb][tt][1];   // A slots 4-7: keys 16 kb + 8 + 4 hh + 0..3
+                    oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, pb[kb].v, oacc[tt], 0, 0, 0);
+                }
+        }
+    }
+
+    if (qi >= a.S) return;
+    const float inv = (l_run > 0.f) ? 1.f / l_run : 0.f;
+    bf16_t* op = a.o + (size_t)qi * a.o_sn + (size_t)head * a.o_sh;
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = tt * 32 + g * 8 + hh * 4;
+            uint2 w;
+            w.x = pack_bf16x2(oacc[tt][g * 4 + 0] * inv, oacc[tt][g * 4 + 1] * inv);
+            w.y = pack_bf16x2(oacc[tt][g * 4 + 2] * inv, oacc[tt][g * 4 + 3] * inv);
+            *reinterpret_cast<uint2*>(op + d) = w;
+        }
+}
+
 int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
+
+// EFM_PREFILL_PIPE=0 selects the register-staged kernel (kept as the reference path of
+// the pipelined one in the tests).
+static bool prefill_pipe_enabled() {
+    const char* e = getenv("EFM_PREFILL_PIPE");
+    return e == nullptr || e[0] != '0';
+}
 
 }  // namespace efm
 
@@ -298,6 +557,11 @@ extern "C" int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q
     a.k_pos_off = (int)ctx->k_rope_pos_offset;
     rope_table_fill(&a.rope, hd, ctx->rope_theta, ctx->rope_scale);
     a.sm_scale_log2 = 1.4426950408889634f / sqrtf((float)hd);
+    if (hd == kP2HD && !a.rope_k && prefill_pipe_enabled()) {
+        const int nqt = (int)((qo_len + kP2Q - 1) / kP2Q);
+        hipLaunchKernelGGL(prefill_attn_pipe_kernel, dim3(nqt * a.Hq), dim3(kP2Threads), 0, stream, a, nqt);
+        return check_launch("attention_prefill");
+    }
     dim3 grid((qo_len + kPfQ - 1) / kPfQ, a.Hq), block(kPfThreads);
     if (hd == 128) hipLaunchKernelGGL(prefill_attn_kernel<128>, grid, block, 0, stream, a);
     else hipLaunchKernelGGL(prefill_attn_kernel<64>, grid, block, 0, stream, a);

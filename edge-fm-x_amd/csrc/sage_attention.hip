@@ -17,6 +17,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace efm {
 
@@ -297,6 +298,235 @@ __global__ __launch_bounds__(kSageThreads) void sage_attn_kernel(SageArgs a) {
         }
 }
 
+// ---------------------------------------------------------------------------------
+// Pipelined variant (head_dim 128): 8 wave64s = 256 query rows of one head per
+// workgroup; 64-key int8 K tiles (8 KB, 128-byte rows, 16-byte chunks XOR-swizzled by
+// (row >> 1) & 7) and bf16 V tiles (16 KB, 256-byte rows, swizzled by (row & 7) << 1)
+// stream global -> LDS with global_load_lds into a 4-deep ring. The int8 K operand is
+// read with ds_read_b128, the V^T operand from the row-major V tile with
+// ds_read_b64_tr_b16 (see the pipelined bf16 prefill kernel for the lane mapping). The
+// running max is only raised when a row's tile max exceeds it by more than 2^8.
+// ---------------------------------------------------------------------------------
+constexpr int kSPThreads = 512;
+constexpr int kSPQ = 256;
+constexpr int kSPKV = 64;
+constexpr int kSPS = 4;
+constexpr int kSPHD = 128;
+constexpr int kSPKTile = kSPKV * kSPHD;          // int8 bytes
+constexpr int kSPVTile = kSPKV * kSPHD * 2;      // bf16 bytes
+constexpr int kSPStage = kSPKTile + kSPVTile;
+constexpr int kSPLPW = kSPStage / 1024 / (kSPThreads / kWave);
+constexpr float kSPLazy = 8.0f;
+
+template <int N>
+__device__ __forceinline__ void sp_vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void sp_vm_wait_tiles(int tiles) {
+    switch (tiles) {
+        case 0: sp_vm_wait<0>(); break;
+        case 1: sp_vm_wait<1 * kSPLPW>(); break;
+        default: sp_vm_wait<2 * kSPLPW>(); break;
+    }
+}
+
+__device__ __forceinline__ uint32_t sp_koff(int row, int chunk) {
+    return (uint32_t)(row * kSPHD + ((chunk ^ ((row >> 1) & 7)) << 4));
+}
+
+__device__ __forceinline__ uint32_t sp_voff(int row, int chunk) {
+    return (uint32_t)(row * (kSPHD * 2) + ((chunk ^ ((row & 7) << 1)) << 4));
+}
+
+__global__ __launch_bounds__(kSPThreads) void sage_attn_pipe_kernel(SageArgs a, int nqt) {
+    constexpr int KS8 = kSPHD / 32;    // int8 k-steps
+    constexpr int DT = kSPHD / 32;
+    static_assert(kSPLPW * (kSPThreads / kWave) * 1024 == kSPStage, "tile not a whole number of wave loads");
+    __shared__ __align__(1024) unsigned char smem[kSPS * kSPStage];
+
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave, lane = tid % kWave;
+    const int ql = lane % 32, hh = lane / 32;
+    const int t = (int)blockIdx.x;
+    const int qt = nqt - 1 - t / a.Hq;
+    const int head = t % a.Hq;
+    const int kvh = head / (a.Hq / a.Hkv);
+    const int q0 = qt * kSPQ + wave * 32;
+    const int qi = q0 + ql;
+    const int diag = a.L - a.S;
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
+
+    const int q_last = min(a.S - 1, qt * kSPQ + kSPQ - 1);
+    const int kv_end = a.causal ? min(a.L, q_last + diag + 1) : a.L;
+    const int ntiles = (kv_end + kSPKV - 1) / kSPKV;
+
+    // Q8 B operand (lane row qi, k = ks*32 + hh*16 + byte), requested first
+    int32x4_t qf[KS8];
+    {
+        const bool qv = qi < a.S;
+        const int8_t* qp = a.q8 + ((size_t)(qv ? qi : 0) * a.Hq + head) * kSPHD + hh * 16;
+#pragma unroll
+        for (int ks = 0; ks < KS8; ++ks) {
+            const uint4 u = qv ? *reinterpret_cast<const uint4*>(qp + ks * 32) : make_uint4(0, 0, 0, 0);
+            qf[ks] = int32x4_t{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+        }
+    }
+    const float qscale = (qi < a.S) ? a.sq[(qi / kSageBlock) * a.Hq + head] : 0.f;
+
+    // wave load q of a stage: K8 loads (8 rows x 8 chunks) first, then V (4 rows x 16)
+    auto issue = [&](int tile, int slot) {
+        const int k0 = tile * kSPKV;
+#pragma unroll
+        for (int i = 0; i < kSPLPW; ++i) {
+            const int q = wave + i * (kSPThreads / kWave);
+            const void* src;
+            if (q < kSPKTile / 1024) {
+                const int row = q * 8 + (lane >> 3), pc = lane & 7;
+                const int c = pc ^ ((row >> 1) & 7);
+                const int j = min(k0 + row, a.L - 1);
+                src = a.k8 + ((size_t)j * a.Hkv + kvh) * kSPHD + c * 16;
+            } else {
+                const int row = (q - kSPKTile / 1024) * 4 + (lane >> 4), pc = lane & 15;
+                const int c = pc ^ ((row & 7) << 1);
+                const int j = min(k0 + row, a.L - 1);
+                src = a.v + (size_t)j * a.v_sn + (size_t)kvh * a.v_sh + c * 8;
+            }
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(smem + slot * kSPStage + q * 1024),
+                                             16, 0, 0);
+        }
+    };
+    const int pre = min(kSPS - 1, ntiles);
+    for (int p = 0; p < pre; ++p) issue(p, p);
+
+    f32x16_t oacc[DT];
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[tt][e] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    const int wave_last_key = q0 + 31 + diag;
+    const int tr_g = lane >> 4, tr_j = lane & 15;
+    const int tr_row = (tr_g >> 1) * 4 + (tr_j >> 2);
+    const int tr_d = 16 * (tr_g & 1) + 4 * (tr_j & 3);
+    typedef short s4_t __attribute__((ext_vector_type(4)));
+
+    for (int kt = 0; kt < ntiles; ++kt) {
+        sp_vm_wait_tiles(min(kSPS - 2, ntiles - 1 - kt));
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + kSPS - 1 < ntiles) issue(kt + kSPS - 1, (kt + kSPS - 1) % kSPS);
+        if (q0 >= a.S) continue;
+        const int k0 = kt * kSPKV;
+        const uint32_t kb_lds = lds0 + (uint32_t)((kt % kSPS) * kSPStage);
+        const uint32_t vb_lds = kb_lds + kSPKTile;
+        // sk is per 128-key block; a 64-key tile lies inside one block
+        const float coef = (qscale * a.sk[(k0 / kSageBlock) * a.Hkv + kvh]) * a.scale_log2;
+#pragma unroll
+        for (int sub = 0; sub < kSPKV / 32; ++sub) {
+            const int kb0 = k0 + sub * 32;
+            if (kb0 >= kv_end || (a.causal && kb0 > wave_last_key)) break;
+            int32x4_t kf[KS8];
+#pragma unroll
+            for (int ks = 0; ks < KS8; ++ks) {
+                const uint32_t addr = kb_lds + sp_koff(sub * 32 + ql, ks * 2 + hh);
+                asm volatile("ds_read_b128 %0, %1" : "=v"(kf[ks]) : "v"(addr) : "memory");
+            }
+            s4_t vf[2][DT][2];
+            auto read_v = [&](int kb) {
+#pragma unroll
+                for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) {
+                        const int row = sub * 32 + kb * 16 + 8 * c + tr_row;
+                        const int d = tt * 32 + tr_d;
+                        const uint32_t addr = vb_lds + sp_voff(row, d >> 3) + ((d & 7) << 1);
+                        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(vf[kb][tt][c]) : "v"(addr) : "memory");
+                    }
+            };
+            read_v(0);
+            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");   // the K reads (issued first) are done
+#pragma unroll
+            for (int ks = 0; ks < KS8; ++ks) asm volatile("" : "+v"(kf[ks]));
+            int32x16_t acc;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[e] = 0;
+#pragma unroll
+            for (int ks = 0; ks < KS8; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[ks], qf[ks], acc, 0, 0, 0);
+            read_v(1);
+            float s[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[e] = (float)acc[e];
+            const bool edge = (kb0 + 32 > kv_end) || (a.causal && kb0 + 31 > q0 + diag);
+            if (edge) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int j = kb0 + (e / 4) * 8 + hh * 4 + (e % 4);
+                    const bool ok = (j < kv_end) && (!a.causal || j <= qi + diag);
+                    s[e] = ok ? s[e] : -INFINITY;
+                }
+            }
+            float mloc = s[0];
+#pragma unroll
+            for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * coef;
+            if (__any(mloc > m_run + kSPLazy)) {
+                const float m_new = fmaxf(m_run, mloc);
+                const float alpha = exp2f(m_run - m_new);
+                l_run *= alpha;
+#pragma unroll
+                for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+                m_run = m_new;
+            }
+            const float mref = (m_run == -INFINITY) ? 0.f : m_run;
+            float p[16], psum = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                p[e] = exp2f(fmaf(s[e], coef, -mref));
+                psum += p[e];
+            }
+            l_run += psum + __shfl_xor(psum, 32, kWave);
+            Pack8 pb[2];
+            pb[0].u = pack8(&p[0]);
+            pb[1].u = pack8(&p[8]);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int tt = 0; tt < DT; ++tt) {
+                    if (tt == 0) {
+                        if (kb == 0) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+                        else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    }
+                    asm volatile("" : "+v"(vf[kb][tt][0]), "+v"(vf[kb][tt][1]));
+                    union {
+                        s4_t h[2];
+                        bf16x8_t v;
+                    } va;
+                    va.h[0] = vf[kb][tt][0];
+                    va.h[1] = vf[kb][tt][1];
+                    oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, pb[kb].v, oacc[tt], 0, 0, 0);
+                }
+        }
+    }
+
+    if (qi >= a.S) return;
+    const float inv = (l_run > 0.f) ? 1.f / l_run : 0.f;
+    bf16_t* op = a.o + ((size_t)qi * a.Hq + head) * kSPHD;
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = tt * 32 + g * 8 + hh * 4;
+            uint2 w;
+            w.x = pack_bf16x2(oacc[tt][g * 4 + 0] * inv, oacc[tt][g * 4 + 1] * inv);
+            w.y = pack_bf16x2(oacc[tt][g * 4 + 2] * inv, oacc[tt][g * 4 + 3] * inv);
+            *reinterpret_cast<uint2*>(op + d) = w;
+        }
+}
+
 int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
 
 static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -407,6 +637,12 @@ extern "C" int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, con
     a.v_sh = ctx->kv_stride_h ? (int)ctx->kv_stride_h : hd;
     a.causal = causal != 0;
     a.scale_log2 = (float)(1.4426950408889634 / sqrt((double)hd));
+    const char* pipe_env = getenv("EFM_PREFILL_PIPE");
+    if (hd == kSPHD && (pipe_env == nullptr || pipe_env[0] != '0')) {
+        const int nqt = (int)((qo_len + kSPQ - 1) / kSPQ);
+        hipLaunchKernelGGL(sage_attn_pipe_kernel, dim3(nqt * a.Hq), dim3(kSPThreads), 0, stream, a, nqt);
+        return check_launch("sage_attention");
+    }
     dim3 grid((qo_len + kSageQ - 1) / kSageQ, a.Hq), block(kSageThreads);
     if (hd == 128) hipLaunchKernelGGL(sage_attn_kernel<128>, grid, block, 0, stream, a);
     else hipLaunchKernelGGL(sage_attn_kernel<64>, grid, block, 0, stream, a);

@@ -509,6 +509,67 @@ def test_attention_prefill_strided_qkv_no_rope_and_noncausal(gpu):
         assert_close_bf16(o.reshape(S, hq, hd), ref, rtol=2e-2, atol=2e-2, what=f"causal={causal}")
 
 
+PIPE_CASES = [
+    pytest.param(12, 2, 1, 1, 1, "none", id="s1"),
+    pytest.param(12, 2, 77, 77, 1, "prerot", id="s77_prerot"),
+    pytest.param(16, 2, 300, 1100, 1, "prerot", id="3b_prefix800_prerot"),
+    pytest.param(28, 4, 513, 513, 0, "none", id="7b_s513_noncausal"),
+    pytest.param(28, 4, 1000, 1000, 1, "none", id="7b_s1000"),
+    pytest.param(16, 2, 1344, 1344, 1, "none", id="vl3b_s1344"),
+    pytest.param(12, 2, 255, 1025, 0, "prerot", id="noncausal_prefix"),
+]
+
+
+@pytest.mark.parametrize("hq,hkv,S,L,causal,mode", PIPE_CASES)
+def test_attention_prefill_pipelined_matches_oracle(gpu, hq, hkv, S, L, causal, mode):
+    """head_dim 128 with keys already rotated (pos NONE, or RoPE on q only with
+    k_already_prerotated) runs the global_load_lds ring kernel."""
+    torch.manual_seed(S + L)
+    hd = 128
+    q = torch.randn(S, hq, hd, dtype=torch.bfloat16)
+    k = torch.randn(L, hkv, hd, dtype=torch.bfloat16)
+    v = torch.randn(L, hkv, hd, dtype=torch.bfloat16)
+    if mode == "none":
+        octx = O.AttnCtx(hq, hkv, hd, rope=False)
+        ctx = C.make_attention_ctx(hq, hkv, hd, rope=False)
+        kin = k
+    else:
+        octx = O.AttnCtx(hq, hkv, hd, q_rope_pos_offset=L - S)
+        ctx = C.make_attention_ctx(hq, hkv, hd, q_rope_pos_offset=L - S, k_already_prerotated=True)
+        kin = O.rope_llama(k, torch.arange(L), 1.0e6).to(torch.bfloat16)
+    ref = O.attention(q, k, v, torch.arange(S) + (L - S), octx, causal_offset=(L - S) if causal else None)
+    qg, kg, vg = q.to(gpu), kin.to(gpu), v.to(gpu)
+    o = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_attention_prefill", ctx, ptr(qg), ptr(kg), ptr(vg), ptr(o), S, L, causal, stream())
+    torch.cuda.synchronize()
+    assert_close_bf16(o.reshape(S, hq, hd), ref, rtol=2e-2, atol=2e-2, what=f"pipelined S={S} L={L} {mode}")
+
+
+def test_attention_prefill_pipelined_matches_register_kernel_c4(gpu, monkeypatch):
+    """BASELINE C4 shape (28/4 heads, S = 4096, causal): the pipelined kernel against the
+    register-staged one (EFM_PREFILL_PIPE=0) on the same inputs."""
+    torch.manual_seed(44)
+    hq, hkv, hd, S = 28, 4, 128, 4096
+    q = torch.randn(S, hq, hd, dtype=torch.bfloat16, device=gpu)
+    k = torch.randn(S, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    v = torch.randn(S, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    ctx = C.make_attention_ctx(hq, hkv, hd, rope=False)
+    outs = []
+    for pipe in ("1", "0"):
+        monkeypatch.setenv("EFM_PREFILL_PIPE", pipe)
+        o = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
+        C.call("efm_attention_prefill", ctx, ptr(q), ptr(k), ptr(v), ptr(o), S, S, 1, stream())
+        torch.cuda.synchronize()
+        outs.append(o)
+    assert torch.isfinite(outs[0].float()).all()
+    assert_close_bf16(outs[0], outs[1], rtol=2e-2, atol=2e-2, what="pipelined vs register kernel")
+    # spot rows against the oracle (first, middle, last query rows of every head)
+    for r in (0, 1, 2047, 4095):
+        ref = O.attention(q[r:r + 1].cpu(), k[:r + 1].cpu(), v[:r + 1].cpu(), torch.tensor([r]),
+                          O.AttnCtx(hq, hkv, hd, rope=False), causal_offset=None)
+        assert_close_bf16(outs[0][r].reshape(1, hq, hd), ref, rtol=2e-2, atol=2e-2, what=f"C4 row {r} vs oracle")
+
+
 def test_attention_prefill_last_row_equals_decode(gpu):
     """The last prefill row equals single-query decode over the same cache (the
     reference's prefill/decode consistency)."""
@@ -674,3 +735,27 @@ def test_sage_attention_c4_shape_vs_bf16_kernel(gpu):
     err = (o8.float() - ob.float()).abs()
     cos = torch.nn.functional.cosine_similarity(o8.float().flatten(), ob.float().flatten(), dim=0)
     assert float(err.mean()) < 5e-3 and float(cos) > 0.999, (float(err.mean()), float(cos))
+
+
+@pytest.mark.parametrize("S,L,causal", [(4096, 4096, 1), (1000, 1300, 1), (77, 77, 0)])
+def test_sage_attention_pipelined_matches_register_kernel(gpu, monkeypatch, S, L, causal):
+    """head_dim 128 runs the global_load_lds ring kernel; it must agree with the
+    register-staged kernel (EFM_PREFILL_PIPE=0) on the same quantised inputs."""
+    hq, hkv, hd = 28, 4, 128
+    g = torch.Generator(device=gpu).manual_seed(S + L)
+    q = torch.randn(S, hq, hd, generator=g, device=gpu).to(torch.bfloat16)
+    k = torch.randn(L, hkv, hd, generator=g, device=gpu).to(torch.bfloat16)
+    v = torch.randn(L, hkv, hd, generator=g, device=gpu).to(torch.bfloat16)
+    ctx = C.make_attention_ctx(hq, hkv, hd, rope=False)
+    ws = torch.zeros(C.load().efm_attention_prefill_sage_int8_workspace_bytes(ctx, S, L), dtype=torch.uint8,
+                     device=gpu)
+    outs = []
+    for pipe in ("1", "0"):
+        monkeypatch.setenv("EFM_PREFILL_PIPE", pipe)
+        o = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
+        C.call("efm_attention_prefill_sage_int8", ctx, ptr(q), ptr(k), ptr(v), ptr(o), S, L, causal, ptr(ws),
+               ws.numel(), stream())
+        torch.cuda.synchronize()
+        outs.append(o)
+    assert torch.isfinite(outs[0].float()).all()
+    assert_close_bf16(outs[0], outs[1], rtol=2e-2, atol=2e-2, what="sage pipelined vs register kernel")
