@@ -18,9 +18,11 @@
 //  * RoPE is applied while staging: q pairs (d, d+hd/2) sit in the same lane, K pairs
 //    are loaded together by one thread before the LDS store.
 //  * Causal tiles past the diagonal are skipped; late query tiles are scheduled first.
+#include "attn_pipe.hpp"
 #include "common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 
 namespace efm {
@@ -260,49 +262,29 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
 // Pipelined variant (head_dim 128, keys already rotated): one workgroup = 8 wave64s =
 // 256 query rows of one head, 32 per wave. 64-key K and V tiles stream global -> LDS
 // with global_load_lds into a 4-deep ring (no staging registers), so three tiles are
-// in flight while the matrix cores work on one; both tiles keep the row-major layout
-// with 16-byte chunks XOR-swizzled by ((row & 7) << 1). The K operand of S^T = K . Q^T
-// is read with ds_read_b128; the V^T operand of O^T = V^T . P^T is read from the
-// row-major V tile with ds_read_b64_tr_b16, whose 16-lane groups return the transpose
-// of four 4-element rows: lane i of a group receives element i % 4 of the rows read by
-// lanes i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4. The scale is applied in the exponent
-// (exp2(s * scale - m)); the running max is only raised when a row's tile max exceeds
-// it by more than 2^8 (p <= 256 otherwise), which skips most rescales of O; tiles that
-// neither cross the diagonal nor the end are not masked.
+// in flight while the matrix cores work on one; the tile layouts and operand reads are
+// described in attn_pipe.hpp (K read with ds_read_b128, the V^T operand of
+// O^T = V^T . P^T with ds_read_b64_tr_b16 from the row-major V tile). The scale is
+// applied in the exponent (exp2(s * scale - m)); the running max is only raised when a
+// row's tile max exceeds it by more than 2^8 (p <= 256 otherwise), which skips most
+// rescales of O; tiles that neither cross the diagonal nor the end are not masked.
 // ---------------------------------------------------------------------------------
-constexpr int kP2Threads = 512;
-constexpr int kP2Q = 256;          // query rows per workgroup
 constexpr int kP2KV = 64;          // keys per tile
-constexpr int kP2S = 4;            // ring depth
 constexpr int kP2HD = 128;
 constexpr int kP2Row = kP2HD * 2;  // bytes per K / V row in LDS
 constexpr int kP2Tile = kP2KV * kP2Row;
 constexpr int kP2Stage = 2 * kP2Tile;
-constexpr int kP2LPW = kP2Stage / 1024 / (kP2Threads / kWave);   // 1 KB wave loads per wave per tile
 constexpr float kP2Lazy = 8.0f;
 
-template <int N>
-__device__ __forceinline__ void p2_vm_wait() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ void p2_vm_wait_tiles(int tiles) {
-    switch (tiles) {
-        case 0: p2_vm_wait<0>(); break;
-        case 1: p2_vm_wait<1 * kP2LPW>(); break;
-        default: p2_vm_wait<2 * kP2LPW>(); break;
-    }
-}
-
-__device__ __forceinline__ uint32_t p2_off(int row, int chunk) {
-    return (uint32_t)(row * kP2Row + ((chunk ^ ((row & 7) << 1)) << 4));
-}
-
-__global__ __launch_bounds__(kP2Threads) void prefill_attn_pipe_kernel(PrefillArgs a, int nqt) {
+template <int WAVES, int S>
+__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kernel(PrefillArgs a, int nqt) {
+    constexpr int THREADS = WAVES * 64;
+    constexpr int QR = WAVES * 32;                         // query rows per workgroup
+    constexpr int LPW = kP2Stage / 1024 / WAVES;           // 1 KB wave loads per wave per tile
     constexpr int KS = kP2HD / 16;     // 8 k-steps
     constexpr int DT = kP2HD / 32;     // 4 d tiles
-    static_assert(kP2LPW * (kP2Threads / kWave) * 1024 == kP2Stage, "tile not a whole number of wave loads");
-    __shared__ __align__(1024) unsigned char smem[kP2S * kP2Stage];
+    static_assert(LPW * WAVES * 1024 == kP2Stage && S >= 2 && S <= 4, "bad pipeline shape");
+    __shared__ __align__(1024) unsigned char smem[S * kP2Stage];
 
     const int tid = threadIdx.x;
     const int wave = tid / kWave, lane = tid % kWave;
@@ -311,12 +293,12 @@ __global__ __launch_bounds__(kP2Threads) void prefill_attn_pipe_kernel(PrefillAr
     const int qt = nqt - 1 - t / a.Hq;       // heavy (late) query tiles first
     const int head = t % a.Hq;
     const int kvh = head / (a.Hq / a.Hkv);
-    const int q0 = qt * kP2Q + wave * 32;
+    const int q0 = qt * QR + wave * 32;
     const int qi = q0 + ql;
     const int diag = a.L - a.S;
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
 
-    const int q_last = min(a.S - 1, qt * kP2Q + kP2Q - 1);
+    const int q_last = min(a.S - 1, qt * QR + QR - 1);
     const int kv_end = a.causal ? min(a.L, q_last + diag + 1) : a.L;
     const int ntiles = (kv_end + kP2KV - 1) / kP2KV;
     const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
@@ -327,11 +309,11 @@ __global__ __launch_bounds__(kP2Threads) void prefill_attn_pipe_kernel(PrefillAr
         const int k0 = tile * kP2KV;
         const int pr = lane >> 4, pc = lane & 15;
 #pragma unroll
-        for (int i = 0; i < kP2LPW; ++i) {
-            const int q = wave + i * (kP2Threads / kWave);   // wave-load index in the stage
+        for (int i = 0; i < LPW; ++i) {
+            const int q = wave + i * (THREADS / kWave);   // wave-load index in the stage
             const bool isv = q >= kP2Tile / 1024;
             const int row = (q % (kP2Tile / 1024)) * 4 + pr;
-            const int c = pc ^ ((row & 7) << 1);
+            const int c = isv ? (pc ^ ((row & 3) << 2)) : (pc ^ (row & 15));
             const int j = min(k0 + row, a.L - 1);
             const bf16_t* src = (isv ? vbase + (size_t)j * a.v_sn : kbase + (size_t)j * a.k_sn) + c * 8;
             __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
@@ -349,7 +331,7 @@ __global__ __launch_bounds__(kP2Threads) void prefill_attn_pipe_kernel(PrefillAr
         for (int ks = 0; ks < KS; ++ks)
             qraw[ks] = qv ? *reinterpret_cast<const uint4*>(qp + ks * 16 + hh * 8) : make_uint4(0, 0, 0, 0);
     }
-    const int pre = min(kP2S - 1, ntiles);
+    const int pre = min(S - 1, ntiles);
     for (int p = 0; p < pre; ++p) issue(p, p);
     bf16x8_t qf[KS];
     {
@@ -387,108 +369,146 @@ __global__ __launch_bounds__(kP2Threads) void prefill_attn_pipe_kernel(PrefillAr
     const float scale = a.sm_scale_log2;
     const int wave_last_key = q0 + 31 + diag;   // causal: last key any row of this wave sees
 
-    // tr-read source of this lane: row offset (g / 2) * 4 + e and d offset 16 (g % 2) + 4 q
-    // inside a 16-key block, from group g = lane / 16, j = lane % 16 = 4 e + q
-    const int tr_g = lane >> 4, tr_j = lane & 15;
-    const int tr_row = (tr_g >> 1) * 4 + (tr_j >> 2);
-    const int tr_d = 16 * (tr_g & 1) + 4 * (tr_j & 3);
+    // lane parts of the operand addresses inside a stage (rows of the tile and the
+    // (kb, c) parts of the V reads are immediates)
+    uint32_t koff[KS], voff[DT];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) koff[ks] = attn_pipe::k_off(ql, ks * 2 + hh);
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt) voff[tt] = (uint32_t)kP2Tile + attn_pipe::v_tr_lane_off(lane, tt);
+    typedef short s4_t __attribute__((ext_vector_type(4)));
 
     for (int kt = 0; kt < ntiles; ++kt) {
-        p2_vm_wait_tiles(min(kP2S - 2, ntiles - 1 - kt));
+        attn_pipe::vm_wait_tiles<LPW>(min(S - 2, ntiles - 1 - kt));
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (kt + kP2S - 1 < ntiles) issue(kt + kP2S - 1, (kt + kP2S - 1) % kP2S);
+        if (kt + S - 1 < ntiles) issue(kt + S - 1, (kt + S - 1) % S);
         if (q0 >= a.S) continue;                      // rows past the end: barriers only
-        const uint32_t kb_lds = lds0 + (uint32_t)((kt % kP2S) * kP2Stage);
-        const uint32_t vb_lds = kb_lds + kP2Tile;
+        const int kb0 = kt * kP2KV;
+        if (a.causal && kb0 > wave_last_key) continue;   // the whole tile is above this wave's rows
+        const bool two = kb0 + 32 < kv_end && !(a.causal && kb0 + 32 > wave_last_key);   // keys 32..63 needed
+        const uint32_t stage = lds0 + (uint32_t)((kt % S) * kP2Stage);
+        uint32_t ka[KS], va[DT];
 #pragma unroll
-        for (int sub = 0; sub < kP2KV / 32; ++sub) {
-            const int kb0 = kt * kP2KV + sub * 32;
-            if (kb0 >= kv_end || (a.causal && kb0 > wave_last_key)) break;
-            // K operand (8 x b128) then V^T operand (2 blocks x 4 d tiles x 2 tr reads)
-            bf16x8_t kf[KS];
+        for (int ks = 0; ks < KS; ++ks) ka[ks] = stage + koff[ks];
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const uint32_t addr = kb_lds + p2_off(sub * 32 + ql, ks * 2 + hh);
-                asm volatile("ds_read_b128 %0, %1" : "=v"(kf[ks]) : "v"(addr) : "memory");
+        for (int tt = 0; tt < DT; ++tt) va[tt] = stage + voff[tt];
+
+        // ---- S^T for keys 0..31 (s0) and 32..63 (s1) of the tile
+        bf16x8_t kf0[KS], kf1[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) attn_pipe::read_b128<0>(kf0[ks], ka[ks]);
+        if (two) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) attn_pipe::read_b128<32 * attn_pipe::kRow>(kf1[ks], ka[ks]);
+            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kf0[ks]));
+        // keys 32..63 are all masked when !two (the edge masking below sets them to -inf)
+        f32x16_t s0 = {}, s1 = {};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf0[ks], qf[ks], s0, 0, 0, 0);
+        if (two) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kf1[ks]));
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf1[ks], qf[ks], s1, 0, 0, 0);
+        }
+        // ---- V^T operand reads for key blocks 0 and 1 go out under the softmax
+        s4_t vf[4][DT][2];
+        auto read_v = [&](auto kbc) {
+            constexpr int kb = decltype(kbc)::value;
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt) {
+                attn_pipe::read_tr16<(kb * 16) * attn_pipe::kRow>(vf[kb][tt][0], va[tt]);
+                attn_pipe::read_tr16<(kb * 16 + 8) * attn_pipe::kRow>(vf[kb][tt][1], va[tt]);
             }
-            typedef short s4_t __attribute__((ext_vector_type(4)));
-            s4_t vf[2][DT][2];
-            auto read_v = [&](int kb) {
-#pragma unroll
-                for (int tt = 0; tt < DT; ++tt)
-#pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const int row = sub * 32 + kb * 16 + 8 * c + tr_row;
-                        const int d = tt * 32 + tr_d;
-                        const uint32_t addr = vb_lds + p2_off(row, d >> 3) + ((d & 7) << 1);
-                        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(vf[kb][tt][c]) : "v"(addr) : "memory");
-                    }
-            };
-            read_v(0);
-            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");   // the K reads (issued first) are done
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kf[ks]));
-            f32x16_t s;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) s[e] = 0.f;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
-            read_v(1);
-            // element e: key = kb0 + (e/4)*8 + hh*4 + e%4, query = qi
-            const bool edge = (kb0 + 32 > kv_end) || (a.causal && kb0 + 31 > q0 + diag);
-            if (edge) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int j = kb0 + (e / 4) * 8 + hh * 4 + (e % 4);
-                    const bool ok = (j < kv_end) && (!a.causal || j <= qi + diag);
-                    s[e] = ok ? s[e] : -INFINITY;
-                }
-            }
-            float mloc = s[0];
-#pragma unroll
-            for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * scale;
-            if (__any(mloc > m_run + kP2Lazy)) {
-                const float m_new = fmaxf(m_run, mloc);
-                const float alpha = exp2f(m_run - m_new);   // 0 on the first tile
-                l_run *= alpha;
-#pragma unroll
-                for (int tt = 0; tt < DT; ++tt)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
-                m_run = m_new;
-            }
-            const float mref = (m_run == -INFINITY) ? 0.f : m_run;
-            float p[16], psum = 0.f;
+        };
+        read_v(std::integral_constant<int, 0>{});
+        read_v(std::integral_constant<int, 1>{});
+
+        // ---- online softmax over the 64 keys (element e of s0 / s1: key kb0 + 32 * half
+        //      + (e/4)*8 + hh*4 + e%4, query qi)
+        if (kb0 + kP2KV > kv_end || (a.causal && kb0 + kP2KV - 1 > q0 + diag)) {
+            const int lim = a.causal ? min(kv_end, qi + diag + 1) : kv_end;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                p[e] = exp2f(fmaf(s[e], scale, -mref));
-                psum += p[e];
+                const int j = kb0 + (e / 4) * 8 + hh * 4 + (e % 4);
+                s0[e] = (j < lim) ? s0[e] : -INFINITY;
+                s1[e] = (j + 32 < lim) ? s1[e] : -INFINITY;
             }
-            l_run += psum + __shfl_xor(psum, 32, kWave);
-            Pack8 pb[2];
-            pb[0].u = pack8(&p[0]);
-            pb[1].u = pack8(&p[8]);
+        }
+        float mloc = fmaxf(s0[0], s1[0]);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+        for (int e = 1; e < 16; ++e) mloc = fmaxf(fmaxf(mloc, s0[e]), s1[e]);
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scale;
+        }
+        if (__any(mloc > m_run + kP2Lazy)) {
+            // a real (wave-uniform) branch: most tiles skip the rescale of O
+            asm volatile("" ::: "memory");
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 on the first tile
+            l_run *= alpha;
 #pragma unroll
-                for (int tt = 0; tt < DT; ++tt) {
-                    if (tt == 0) {
-                        // block 0's reads were issued before block 1's eight
-                        if (kb == 0) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
-                        else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                    }
-                    asm volatile("" : "+v"(vf[kb][tt][0]), "+v"(vf[kb][tt][1]));
-                    union {
-                        s4_t h[2];
-                        bf16x8_t v;
-                    } va;
-                    va.h[0] = vf[kb][tt][0];   // A slots 0-3: keys 16 kb + 4 hh + 0..3
-                    va.h[1] = vf[kb][tt][1];   // A slots 4-7: keys 16 kb + 8 + 4 hh + 0..3
-                    oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, pb[kb].v, oacc[tt], 0, 0, 0);
-                }
+            for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+            m_run = m_new;
+        }
+        const float mref = (m_run == -INFINITY) ? 0.f : m_run;
+        float p0[16], p1[16], psum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            p0[e] = __builtin_amdgcn_exp2f(fmaf(s0[e], scale, -mref));
+            p1[e] = __builtin_amdgcn_exp2f(fmaf(s1[e], scale, -mref));
+            psum += p0[e] + p1[e];
+        }
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(psum), __float_as_uint(psum), false, false);
+            l_run += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        Pack8 pb[4];
+        pb[0].u = pack8(&p0[0]);
+        pb[1].u = pack8(&p0[8]);
+        pb[2].u = pack8(&p1[0]);
+        pb[3].u = pack8(&p1[8]);
+
+        // ---- O^T += V^T . P^T, key block by key block (the reads of block kb + 2 are
+        //      issued once block kb has landed, so at most 16 are outstanding)
+        auto pv = [&](int kb) {
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt) {
+                asm volatile("" : "+v"(vf[kb][tt][0]), "+v"(vf[kb][tt][1]));
+                union {
+                    s4_t h[2];
+                    bf16x8_t v;
+                } vv;
+                vv.h[0] = vf[kb][tt][0];   // A slots 0-3: keys 16 kb + 4 hh + 0..3
+                vv.h[1] = vf[kb][tt][1];   // A slots 4-7: keys 16 kb + 8 + 4 hh + 0..3
+                oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv.v, pb[kb].v, oacc[tt], 0, 0, 0);
+            }
+        };
+        asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+        pv(0);
+        if (two) {
+            read_v(std::integral_constant<int, 2>{});
+            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+            pv(1);
+            read_v(std::integral_constant<int, 3>{});
+            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+            pv(2);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            pv(3);
+        } else {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            pv(1);
         }
     }
 
@@ -558,8 +578,19 @@ extern "C" int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q
     rope_table_fill(&a.rope, hd, ctx->rope_theta, ctx->rope_scale);
     a.sm_scale_log2 = 1.4426950408889634f / sqrtf((float)hd);
     if (hd == kP2HD && !a.rope_k && prefill_pipe_enabled()) {
-        const int nqt = (int)((qo_len + kP2Q - 1) / kP2Q);
-        hipLaunchKernelGGL(prefill_attn_pipe_kernel, dim3(nqt * a.Hq), dim3(kP2Threads), 0, stream, a, nqt);
+        // up to 8K rows: 4 waves (128 rows) over a 2-deep ring, two workgroups per CU
+        // (twice the workgroups, and the two drift out of phase so that one's softmax
+        // overlaps the other's matrix work); longer: 8 waves (256 rows) over a 4-deep
+        // ring, one per CU. EFM_PREFILL_SHAPE=4 / 8 forces one of them.
+        const char* shape = getenv("EFM_PREFILL_SHAPE");
+        const bool small = (shape != nullptr && shape[0] != '\0') ? shape[0] == '4' : qo_len <= 8192;
+        if (small) {
+            const int nqt = (int)((qo_len + 127) / 128);
+            hipLaunchKernelGGL((prefill_attn_pipe_kernel<4, 2>), dim3(nqt * a.Hq), dim3(256), 0, stream, a, nqt);
+        } else {
+            const int nqt = (int)((qo_len + 255) / 256);
+            hipLaunchKernelGGL((prefill_attn_pipe_kernel<8, 4>), dim3(nqt * a.Hq), dim3(512), 0, stream, a, nqt);
+        }
         return check_launch("attention_prefill");
     }
     dim3 grid((qo_len + kPfQ - 1) / kPfQ, a.Hq), block(kPfThreads);

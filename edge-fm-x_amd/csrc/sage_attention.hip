@@ -14,9 +14,11 @@
 // Three launches: K mean (one workgroup per KV head and 8 channels, float64), block
 // quantisation of Q and K (one workgroup per block x head), attention (one workgroup =
 // 128 query rows of one head, 64-key tiles staged in LDS as int8 K and transposed V).
+#include "attn_pipe.hpp"
 #include "common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 
 namespace efm {
@@ -300,50 +302,26 @@ __global__ __launch_bounds__(kSageThreads) void sage_attn_kernel(SageArgs a) {
 
 // ---------------------------------------------------------------------------------
 // Pipelined variant (head_dim 128): 8 wave64s = 256 query rows of one head per
-// workgroup; 64-key int8 K tiles (8 KB, 128-byte rows, 16-byte chunks XOR-swizzled by
-// (row >> 1) & 7) and bf16 V tiles (16 KB, 256-byte rows, swizzled by (row & 7) << 1)
-// stream global -> LDS with global_load_lds into a 4-deep ring. The int8 K operand is
-// read with ds_read_b128, the V^T operand from the row-major V tile with
-// ds_read_b64_tr_b16 (see the pipelined bf16 prefill kernel for the lane mapping). The
+// workgroup; 64-key int8 K tiles (8 KB) and bf16 V tiles (16 KB) stream global -> LDS
+// with global_load_lds into a 4-deep ring, laid out and read as described in
+// attn_pipe.hpp (int8 K operand via ds_read_b128, V^T via ds_read_b64_tr_b16). The
 // running max is only raised when a row's tile max exceeds it by more than 2^8.
 // ---------------------------------------------------------------------------------
-constexpr int kSPThreads = 512;
-constexpr int kSPQ = 256;
 constexpr int kSPKV = 64;
-constexpr int kSPS = 4;
 constexpr int kSPHD = 128;
 constexpr int kSPKTile = kSPKV * kSPHD;          // int8 bytes
 constexpr int kSPVTile = kSPKV * kSPHD * 2;      // bf16 bytes
 constexpr int kSPStage = kSPKTile + kSPVTile;
-constexpr int kSPLPW = kSPStage / 1024 / (kSPThreads / kWave);
 constexpr float kSPLazy = 8.0f;
 
-template <int N>
-__device__ __forceinline__ void sp_vm_wait() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ void sp_vm_wait_tiles(int tiles) {
-    switch (tiles) {
-        case 0: sp_vm_wait<0>(); break;
-        case 1: sp_vm_wait<1 * kSPLPW>(); break;
-        default: sp_vm_wait<2 * kSPLPW>(); break;
-    }
-}
-
-__device__ __forceinline__ uint32_t sp_koff(int row, int chunk) {
-    return (uint32_t)(row * kSPHD + ((chunk ^ ((row >> 1) & 7)) << 4));
-}
-
-__device__ __forceinline__ uint32_t sp_voff(int row, int chunk) {
-    return (uint32_t)(row * (kSPHD * 2) + ((chunk ^ ((row & 7) << 1)) << 4));
-}
-
-__global__ __launch_bounds__(kSPThreads) void sage_attn_pipe_kernel(SageArgs a, int nqt) {
+template <int WAVES, int S>
+__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(SageArgs a, int nqt) {
+    constexpr int QR = WAVES * 32;                          // query rows per workgroup
+    constexpr int LPW = kSPStage / 1024 / WAVES;            // 1 KB wave loads per wave per tile
     constexpr int KS8 = kSPHD / 32;    // int8 k-steps
     constexpr int DT = kSPHD / 32;
-    static_assert(kSPLPW * (kSPThreads / kWave) * 1024 == kSPStage, "tile not a whole number of wave loads");
-    __shared__ __align__(1024) unsigned char smem[kSPS * kSPStage];
+    static_assert(LPW * WAVES * 1024 == kSPStage && S >= 2 && S <= 4, "bad pipeline shape");
+    __shared__ __align__(1024) unsigned char smem[S * kSPStage];
 
     const int tid = threadIdx.x;
     const int wave = tid / kWave, lane = tid % kWave;
@@ -352,12 +330,12 @@ __global__ __launch_bounds__(kSPThreads) void sage_attn_pipe_kernel(SageArgs a, 
     const int qt = nqt - 1 - t / a.Hq;
     const int head = t % a.Hq;
     const int kvh = head / (a.Hq / a.Hkv);
-    const int q0 = qt * kSPQ + wave * 32;
+    const int q0 = qt * QR + wave * 32;
     const int qi = q0 + ql;
     const int diag = a.L - a.S;
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
 
-    const int q_last = min(a.S - 1, qt * kSPQ + kSPQ - 1);
+    const int q_last = min(a.S - 1, qt * QR + QR - 1);
     const int kv_end = a.causal ? min(a.L, q_last + diag + 1) : a.L;
     const int ntiles = (kv_end + kSPKV - 1) / kSPKV;
 
@@ -378,17 +356,17 @@ __global__ __launch_bounds__(kSPThreads) void sage_attn_pipe_kernel(SageArgs a, 
     auto issue = [&](int tile, int slot) {
         const int k0 = tile * kSPKV;
 #pragma unroll
-        for (int i = 0; i < kSPLPW; ++i) {
-            const int q = wave + i * (kSPThreads / kWave);
+        for (int i = 0; i < LPW; ++i) {
+            const int q = wave + i * (WAVES);
             const void* src;
             if (q < kSPKTile / 1024) {
                 const int row = q * 8 + (lane >> 3), pc = lane & 7;
-                const int c = pc ^ ((row >> 1) & 7);
+                const int c = pc ^ ((row >> 1) & 7);   // attn_pipe::k8_off
                 const int j = min(k0 + row, a.L - 1);
                 src = a.k8 + ((size_t)j * a.Hkv + kvh) * kSPHD + c * 16;
             } else {
                 const int row = (q - kSPKTile / 1024) * 4 + (lane >> 4), pc = lane & 15;
-                const int c = pc ^ ((row & 7) << 1);
+                const int c = pc ^ ((row & 3) << 2);   // attn_pipe::v_off
                 const int j = min(k0 + row, a.L - 1);
                 src = a.v + (size_t)j * a.v_sn + (size_t)kvh * a.v_sh + c * 8;
             }
@@ -396,7 +374,7 @@ __global__ __launch_bounds__(kSPThreads) void sage_attn_pipe_kernel(SageArgs a, 
                                              16, 0, 0);
         }
     };
-    const int pre = min(kSPS - 1, ntiles);
+    const int pre = min(S - 1, ntiles);
     for (int p = 0; p < pre; ++p) issue(p, p);
 
     f32x16_t oacc[DT];
@@ -406,109 +384,145 @@ __global__ __launch_bounds__(kSPThreads) void sage_attn_pipe_kernel(SageArgs a, 
         for (int e = 0; e < 16; ++e) oacc[tt][e] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
     const int wave_last_key = q0 + 31 + diag;
-    const int tr_g = lane >> 4, tr_j = lane & 15;
-    const int tr_row = (tr_g >> 1) * 4 + (tr_j >> 2);
-    const int tr_d = 16 * (tr_g & 1) + 4 * (tr_j & 3);
+    uint32_t koff[KS8], voff[DT];
+#pragma unroll
+    for (int ks = 0; ks < KS8; ++ks) koff[ks] = attn_pipe::k8_off(ql, ks * 2 + hh);
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt) voff[tt] = (uint32_t)kSPKTile + attn_pipe::v_tr_lane_off(lane, tt);
     typedef short s4_t __attribute__((ext_vector_type(4)));
 
     for (int kt = 0; kt < ntiles; ++kt) {
-        sp_vm_wait_tiles(min(kSPS - 2, ntiles - 1 - kt));
+        attn_pipe::vm_wait_tiles<LPW>(min(S - 2, ntiles - 1 - kt));
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (kt + kSPS - 1 < ntiles) issue(kt + kSPS - 1, (kt + kSPS - 1) % kSPS);
+        if (kt + S - 1 < ntiles) issue(kt + S - 1, (kt + S - 1) % S);
         if (q0 >= a.S) continue;
-        const int k0 = kt * kSPKV;
-        const uint32_t kb_lds = lds0 + (uint32_t)((kt % kSPS) * kSPStage);
-        const uint32_t vb_lds = kb_lds + kSPKTile;
+        const int kb0 = kt * kSPKV;
+        if (a.causal && kb0 > wave_last_key) continue;   // the whole tile is above this wave's rows
+        const bool two = kb0 + 32 < kv_end && !(a.causal && kb0 + 32 > wave_last_key);   // keys 32..63 needed
+        const uint32_t stage = lds0 + (uint32_t)((kt % S) * kSPStage);
+        uint32_t ka[KS8], va[DT];
+#pragma unroll
+        for (int ks = 0; ks < KS8; ++ks) ka[ks] = stage + koff[ks];
+#pragma unroll
+        for (int tt = 0; tt < DT; ++tt) va[tt] = stage + voff[tt];
         // sk is per 128-key block; a 64-key tile lies inside one block
-        const float coef = (qscale * a.sk[(k0 / kSageBlock) * a.Hkv + kvh]) * a.scale_log2;
+        const float coef = (qscale * a.sk[(kb0 / kSageBlock) * a.Hkv + kvh]) * a.scale_log2;
+
+        // ---- int32 S^T for keys 0..31 (acc0) and 32..63 (acc1) of the tile
+        int32x4_t kf0[KS8], kf1[KS8];
 #pragma unroll
-        for (int sub = 0; sub < kSPKV / 32; ++sub) {
-            const int kb0 = k0 + sub * 32;
-            if (kb0 >= kv_end || (a.causal && kb0 > wave_last_key)) break;
-            int32x4_t kf[KS8];
+        for (int ks = 0; ks < KS8; ++ks) attn_pipe::read_b128<0>(kf0[ks], ka[ks]);
+        if (two) {
 #pragma unroll
-            for (int ks = 0; ks < KS8; ++ks) {
-                const uint32_t addr = kb_lds + sp_koff(sub * 32 + ql, ks * 2 + hh);
-                asm volatile("ds_read_b128 %0, %1" : "=v"(kf[ks]) : "v"(addr) : "memory");
+            for (int ks = 0; ks < KS8; ++ks) attn_pipe::read_b128<32 * 128>(kf1[ks], ka[ks]);
+            asm volatile("s_waitcnt lgkmcnt(4)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS8; ++ks) asm volatile("" : "+v"(kf0[ks]));
+        int32x16_t acc0 = {}, acc1 = {};
+#pragma unroll
+        for (int ks = 0; ks < KS8; ++ks) acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf0[ks], qf[ks], acc0, 0, 0, 0);
+        if (two) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int ks = 0; ks < KS8; ++ks) asm volatile("" : "+v"(kf1[ks]));
+#pragma unroll
+            for (int ks = 0; ks < KS8; ++ks) acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf1[ks], qf[ks], acc1, 0, 0, 0);
+        }
+        s4_t vf[4][DT][2];
+        auto read_v = [&](auto kbc) {
+            constexpr int kb = decltype(kbc)::value;
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt) {
+                attn_pipe::read_tr16<(kb * 16) * attn_pipe::kRow>(vf[kb][tt][0], va[tt]);
+                attn_pipe::read_tr16<(kb * 16 + 8) * attn_pipe::kRow>(vf[kb][tt][1], va[tt]);
             }
-            s4_t vf[2][DT][2];
-            auto read_v = [&](int kb) {
+        };
+        read_v(std::integral_constant<int, 0>{});
+        read_v(std::integral_constant<int, 1>{});
+
+        float s0[16], s1[16];
 #pragma unroll
-                for (int tt = 0; tt < DT; ++tt)
-#pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const int row = sub * 32 + kb * 16 + 8 * c + tr_row;
-                        const int d = tt * 32 + tr_d;
-                        const uint32_t addr = vb_lds + sp_voff(row, d >> 3) + ((d & 7) << 1);
-                        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(vf[kb][tt][c]) : "v"(addr) : "memory");
-                    }
-            };
-            read_v(0);
-            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");   // the K reads (issued first) are done
-#pragma unroll
-            for (int ks = 0; ks < KS8; ++ks) asm volatile("" : "+v"(kf[ks]));
-            int32x16_t acc;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[e] = 0;
-#pragma unroll
-            for (int ks = 0; ks < KS8; ++ks) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[ks], qf[ks], acc, 0, 0, 0);
-            read_v(1);
-            float s[16];
-#pragma unroll
-            for (int e = 0; e < 16; ++e) s[e] = (float)acc[e];
-            const bool edge = (kb0 + 32 > kv_end) || (a.causal && kb0 + 31 > q0 + diag);
-            if (edge) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int j = kb0 + (e / 4) * 8 + hh * 4 + (e % 4);
-                    const bool ok = (j < kv_end) && (!a.causal || j <= qi + diag);
-                    s[e] = ok ? s[e] : -INFINITY;
-                }
-            }
-            float mloc = s[0];
-#pragma unroll
-            for (int e = 1; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * coef;
-            if (__any(mloc > m_run + kSPLazy)) {
-                const float m_new = fmaxf(m_run, mloc);
-                const float alpha = exp2f(m_run - m_new);
-                l_run *= alpha;
-#pragma unroll
-                for (int tt = 0; tt < DT; ++tt)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
-                m_run = m_new;
-            }
-            const float mref = (m_run == -INFINITY) ? 0.f : m_run;
-            float p[16], psum = 0.f;
+        for (int e = 0; e < 16; ++e) {
+            s0[e] = (float)acc0[e];
+            s1[e] = (float)acc1[e];   // all masked below when !two
+        }
+        if (kb0 + kSPKV > kv_end || (a.causal && kb0 + kSPKV - 1 > q0 + diag)) {
+            const int lim = a.causal ? min(kv_end, qi + diag + 1) : kv_end;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                p[e] = exp2f(fmaf(s[e], coef, -mref));
-                psum += p[e];
+                const int j = kb0 + (e / 4) * 8 + hh * 4 + (e % 4);
+                s0[e] = (j < lim) ? s0[e] : -INFINITY;
+                s1[e] = (j + 32 < lim) ? s1[e] : -INFINITY;
             }
-            l_run += psum + __shfl_xor(psum, 32, kWave);
-            Pack8 pb[2];
-            pb[0].u = pack8(&p[0]);
-            pb[1].u = pack8(&p[8]);
+        }
+        float mloc = fmaxf(s0[0], s1[0]);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+        for (int e = 1; e < 16; ++e) mloc = fmaxf(fmaxf(mloc, s0[e]), s1[e]);
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * coef;
+        }
+        if (__any(mloc > m_run + kSPLazy)) {
+            // a real (wave-uniform) branch: most tiles skip the rescale of O
+            asm volatile("" ::: "memory");
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
 #pragma unroll
-                for (int tt = 0; tt < DT; ++tt) {
-                    if (tt == 0) {
-                        if (kb == 0) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
-                        else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                    }
-                    asm volatile("" : "+v"(vf[kb][tt][0]), "+v"(vf[kb][tt][1]));
-                    union {
-                        s4_t h[2];
-                        bf16x8_t v;
-                    } va;
-                    va.h[0] = vf[kb][tt][0];
-                    va.h[1] = vf[kb][tt][1];
-                    oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, pb[kb].v, oacc[tt], 0, 0, 0);
-                }
+            for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+            m_run = m_new;
+        }
+        const float mref = (m_run == -INFINITY) ? 0.f : m_run;
+        float p0[16], p1[16], psum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            p0[e] = __builtin_amdgcn_exp2f(fmaf(s0[e], coef, -mref));
+            p1[e] = __builtin_amdgcn_exp2f(fmaf(s1[e], coef, -mref));
+            psum += p0[e] + p1[e];
+        }
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(psum), __float_as_uint(psum), false, false);
+            l_run += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        Pack8 pb[4];
+        pb[0].u = pack8(&p0[0]);
+        pb[1].u = pack8(&p0[8]);
+        pb[2].u = pack8(&p1[0]);
+        pb[3].u = pack8(&p1[8]);
+        auto pv = [&](int kb) {
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt) {
+                asm volatile("" : "+v"(vf[kb][tt][0]), "+v"(vf[kb][tt][1]));
+                union {
+                    s4_t h[2];
+                    bf16x8_t v;
+                } vv;
+                vv.h[0] = vf[kb][tt][0];
+                vv.h[1] = vf[kb][tt][1];
+                oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv.v, pb[kb].v, oacc[tt], 0, 0, 0);
+            }
+        };
+        asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+        pv(0);
+        if (two) {
+            read_v(std::integral_constant<int, 2>{});
+            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+            pv(1);
+            read_v(std::integral_constant<int, 3>{});
+            asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+            pv(2);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            pv(3);
+        } else {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            pv(1);
         }
     }
 
@@ -639,8 +653,17 @@ extern "C" int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, con
     a.scale_log2 = (float)(1.4426950408889634 / sqrt((double)hd));
     const char* pipe_env = getenv("EFM_PREFILL_PIPE");
     if (hd == kSPHD && (pipe_env == nullptr || pipe_env[0] != '0')) {
-        const int nqt = (int)((qo_len + kSPQ - 1) / kSPQ);
-        hipLaunchKernelGGL(sage_attn_pipe_kernel, dim3(nqt * a.Hq), dim3(kSPThreads), 0, stream, a, nqt);
+        // as the bf16 kernel: 4 waves / two workgroups per CU up to 8K rows (a 3-deep ring
+        // of 24 KB stages fits twice), 8 waves over a 4-deep ring beyond
+        const char* shape = getenv("EFM_PREFILL_SHAPE");
+        const bool small = (shape != nullptr && shape[0] != '\0') ? shape[0] == '4' : qo_len <= 8192;
+        if (small) {
+            const int nqt = (int)((qo_len + 127) / 128);
+            hipLaunchKernelGGL((sage_attn_pipe_kernel<4, 3>), dim3(nqt * a.Hq), dim3(256), 0, stream, a, nqt);
+        } else {
+            const int nqt = (int)((qo_len + 255) / 256);
+            hipLaunchKernelGGL((sage_attn_pipe_kernel<8, 4>), dim3(nqt * a.Hq), dim3(512), 0, stream, a, nqt);
+        }
         return check_launch("sage_attention");
     }
     dim3 grid((qo_len + kSageQ - 1) / kSageQ, a.Hq), block(kSageThreads);

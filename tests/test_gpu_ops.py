@@ -520,10 +520,13 @@ PIPE_CASES = [
 ]
 
 
+@pytest.mark.parametrize("shape", ["4", "8"])
 @pytest.mark.parametrize("hq,hkv,S,L,causal,mode", PIPE_CASES)
-def test_attention_prefill_pipelined_matches_oracle(gpu, hq, hkv, S, L, causal, mode):
+def test_attention_prefill_pipelined_matches_oracle(gpu, monkeypatch, shape, hq, hkv, S, L, causal, mode):
     """head_dim 128 with keys already rotated (pos NONE, or RoPE on q only with
-    k_already_prerotated) runs the global_load_lds ring kernel."""
+    k_already_prerotated) runs the global_load_lds ring kernel, in both workgroup shapes
+    (4 waves over a 2-deep ring, 8 waves over a 4-deep ring)."""
+    monkeypatch.setenv("EFM_PREFILL_SHAPE", shape)
     torch.manual_seed(S + L)
     hd = 128
     q = torch.randn(S, hq, hd, dtype=torch.bfloat16)
@@ -545,9 +548,11 @@ def test_attention_prefill_pipelined_matches_oracle(gpu, hq, hkv, S, L, causal, 
     assert_close_bf16(o.reshape(S, hq, hd), ref, rtol=2e-2, atol=2e-2, what=f"pipelined S={S} L={L} {mode}")
 
 
-def test_attention_prefill_pipelined_matches_register_kernel_c4(gpu, monkeypatch):
-    """BASELINE C4 shape (28/4 heads, S = 4096, causal): the pipelined kernel against the
-    register-staged one (EFM_PREFILL_PIPE=0) on the same inputs."""
+@pytest.mark.parametrize("shape", ["4", "8"])
+def test_attention_prefill_pipelined_matches_register_kernel_c4(gpu, monkeypatch, shape):
+    """BASELINE C4 shape (28/4 heads, S = 4096, causal): the pipelined kernel (both
+    workgroup shapes) against the register-staged one (EFM_PREFILL_PIPE=0)."""
+    monkeypatch.setenv("EFM_PREFILL_SHAPE", shape)
     torch.manual_seed(44)
     hq, hkv, hd, S = 28, 4, 128, 4096
     q = torch.randn(S, hq, hd, dtype=torch.bfloat16, device=gpu)
@@ -737,10 +742,12 @@ def test_sage_attention_c4_shape_vs_bf16_kernel(gpu):
     assert float(err.mean()) < 5e-3 and float(cos) > 0.999, (float(err.mean()), float(cos))
 
 
+@pytest.mark.parametrize("shape", ["4", "8"])
 @pytest.mark.parametrize("S,L,causal", [(4096, 4096, 1), (1000, 1300, 1), (77, 77, 0)])
-def test_sage_attention_pipelined_matches_register_kernel(gpu, monkeypatch, S, L, causal):
-    """head_dim 128 runs the global_load_lds ring kernel; it must agree with the
-    register-staged kernel (EFM_PREFILL_PIPE=0) on the same quantised inputs."""
+def test_sage_attention_pipelined_matches_register_kernel(gpu, monkeypatch, shape, S, L, causal):
+    """head_dim 128 runs the global_load_lds ring kernel (both workgroup shapes); it must
+    agree with the register-staged kernel (EFM_PREFILL_PIPE=0) on the same inputs."""
+    monkeypatch.setenv("EFM_PREFILL_SHAPE", shape)
     hq, hkv, hd = 28, 4, 128
     g = torch.Generator(device=gpu).manual_seed(S + L)
     q = torch.randn(S, hq, hd, generator=g, device=gpu).to(torch.bfloat16)
