@@ -91,19 +91,37 @@ __global__ __launch_bounds__(kSageThreads) void sage_quant_kernel(const bf16_t* 
     const int cpr = hd / 8;  // 16-byte chunks per row
     const int nch = rows * cpr;
     constexpr int kMaxPer = kSageBlock * 128 / 8 / kSageThreads;  // 8
+    // every chunk of a thread covers the same 8 channels (the thread count is a multiple
+    // of the chunks per row), so their K means are loaded once, beside the data
+    const int d0 = (threadIdx.x % cpr) * 8;
+    float km[8];
+    if (kmean != nullptr) {
+        const float4 k0 = *reinterpret_cast<const float4*>(kmean + h * hd + d0);
+        const float4 k1 = *reinterpret_cast<const float4*>(kmean + h * hd + d0 + 4);
+        km[0] = k0.x; km[1] = k0.y; km[2] = k0.z; km[3] = k0.w;
+        km[4] = k1.x; km[5] = k1.y; km[6] = k1.z; km[7] = k1.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) km[e] = 0.f;
+    }
+    uint4 raw[kMaxPer];
+#pragma unroll
+    for (int i = 0; i < kMaxPer; ++i) {
+        const int c = threadIdx.x + i * kSageThreads;
+        raw[i] = (c < nch) ? *reinterpret_cast<const uint4*>(src + (size_t)(t0 + c / cpr) * sn + (size_t)h * sh + d0)
+                           : make_uint4(0, 0, 0, 0);
+    }
     float x[kMaxPer][8];
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < kMaxPer; ++i) {
         const int c = threadIdx.x + i * kSageThreads;
-        if (c < nch) {
-            const int r = c / cpr, d0 = (c % cpr) * 8;
-            unpack8(*reinterpret_cast<const uint4*>(src + (size_t)(t0 + r) * sn + (size_t)h * sh + d0), x[i]);
+        unpack8(raw[i], x[i]);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                if (kmean != nullptr) x[i][e] -= kmean[h * hd + d0 + e];
-                amax = fmaxf(amax, fabsf(x[i][e]));
-            }
+        for (int e = 0; e < 8; ++e) {
+            // x - kmean in fp32 (subtracting 0 for Q leaves it unchanged)
+            x[i][e] = (c < nch) ? x[i][e] - km[e] : 0.f;
+            amax = fmaxf(amax, fabsf(x[i][e]));
         }
     }
     amax = wave_max(amax);
@@ -118,7 +136,7 @@ __global__ __launch_bounds__(kSageThreads) void sage_quant_kernel(const bf16_t* 
     for (int i = 0; i < kMaxPer; ++i) {
         const int c = threadIdx.x + i * kSageThreads;
         if (c < nch) {
-            const int r = c / cpr, d0 = (c % cpr) * 8;
+            const int r = c / cpr;
             uint32_t w[2] = {0u, 0u};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -133,6 +151,8 @@ __global__ __launch_bounds__(kSageThreads) void sage_quant_kernel(const bf16_t* 
 
 // ---- attention -----------------------------------------------------------------
 struct SageArgs {
+    const bf16_t* q;     // bf16 queries (quantised inside the pipelined kernel)
+    int q_sn, q_sh;
     const int8_t* q8;    // [S][Hq][hd]
     const int8_t* k8;    // [L][Hkv][hd]
     const float* sq;     // [ceil(S/128)][Hq]
@@ -339,19 +359,26 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
     const int kv_end = a.causal ? min(a.L, q_last + diag + 1) : a.L;
     const int ntiles = (kv_end + kSPKV - 1) / kSPKV;
 
-    // Q8 B operand (lane row qi, k = ks*32 + hh*16 + byte), requested first
-    int32x4_t qf[KS8];
+    // Q: bf16 row qi at d = ks*32 + hh*16 + 0..15 (the int8 B-operand layout), requested
+    // first and quantised here with the scale of its 128-row block (max |q| over the
+    // block, scale = max / 127 or 1, q8 = clamp(rint(q / scale), -127, 127): the
+    // per-block definition of sage_quant_kernel, computed by the block's 4 waves)
+    float xq[KS8][16];
     {
         const bool qv = qi < a.S;
-        const int8_t* qp = a.q8 + ((size_t)(qv ? qi : 0) * a.Hq + head) * kSPHD + hh * 16;
+        const bf16_t* qp = a.q + (size_t)(qv ? qi : 0) * a.q_sn + (size_t)head * a.q_sh + hh * 16;
+        uint4 u[KS8][2];
 #pragma unroll
         for (int ks = 0; ks < KS8; ++ks) {
-            const uint4 u = qv ? *reinterpret_cast<const uint4*>(qp + ks * 32) : make_uint4(0, 0, 0, 0);
-            qf[ks] = int32x4_t{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+            u[ks][0] = qv ? *reinterpret_cast<const uint4*>(qp + ks * 32) : make_uint4(0, 0, 0, 0);
+            u[ks][1] = qv ? *reinterpret_cast<const uint4*>(qp + ks * 32 + 8) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS8; ++ks) {
+            unpack8(u[ks][0], &xq[ks][0]);
+            unpack8(u[ks][1], &xq[ks][8]);
         }
     }
-    const float qscale = (qi < a.S) ? a.sq[(qi / kSageBlock) * a.Hq + head] : 0.f;
-
     // wave load q of a stage: K8 loads (8 rows x 8 chunks) first, then V (4 rows x 16)
     auto issue = [&](int tile, int slot) {
         const int k0 = tile * kSPKV;
@@ -376,6 +403,35 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
     };
     const int pre = min(S - 1, ntiles);
     for (int p = 0; p < pre; ++p) issue(p, p);
+
+    __shared__ float s_qmax[WAVES];
+    int32x4_t qf[KS8];
+    float qscale;
+    {
+        float amax = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS8; ++ks)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(xq[ks][e]));
+        amax = wave_max(amax);
+        if (lane == 0) s_qmax[wave] = amax;
+        __syncthreads();
+        const int w0 = (wave / 4) * 4;   // the 4 waves of this 128-row block
+        const float m = fmaxf(fmaxf(s_qmax[w0], s_qmax[w0 + 1]), fmaxf(s_qmax[w0 + 2], s_qmax[w0 + 3]));
+        const float scale = (m > 0.f) ? m / 127.0f : 1.0f;
+        qscale = (qi < a.S) ? scale : 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS8; ++ks) {
+            uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                float qv = rintf(xq[ks][e] / scale);
+                qv = fminf(fmaxf(qv, -127.f), 127.f);
+                w[e / 4] |= ((uint32_t)((int)qv & 0xff)) << (8 * (e % 4));
+            }
+            qf[ks] = int32x4_t{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        }
+    }
 
     f32x16_t oacc[DT];
 #pragma unroll
@@ -562,7 +618,8 @@ static SageWs sage_ws(const efm_attention_ctx* c, uint32_t S, uint32_t L) {
 }
 
 static int sage_quantize_impl(const efm_attention_ctx* c, const void* q, const void* k, uint32_t S, uint32_t L,
-                              int8_t* q8, float* sq, int8_t* k8, float* sk, float* kmean, hipStream_t stream) {
+                              int8_t* q8, float* sq, int8_t* k8, float* sk, float* kmean, hipStream_t stream,
+                              bool quant_q = true) {
     const int hd = (int)c->head_dim;
     const int q_sn = c->q_stride_n ? (int)c->q_stride_n : (int)(c->num_qo_heads * hd);
     const int q_sh = c->q_stride_h ? (int)c->q_stride_h : hd;
@@ -572,11 +629,13 @@ static int sage_quantize_impl(const efm_attention_ctx* c, const void* q, const v
                        static_cast<const bf16_t*>(k), (int)L, k_sn, k_sh, hd, kmean);
     int rc = check_launch("sage kmean");
     if (rc) return rc;
-    hipLaunchKernelGGL(sage_quant_kernel, dim3((S + kSageBlock - 1) / kSageBlock, c->num_qo_heads),
-                       dim3(kSageThreads), 0, stream, static_cast<const bf16_t*>(q), (int)S, (int)c->num_qo_heads,
-                       q_sn, q_sh, hd, (const float*)nullptr, q8, sq);
-    rc = check_launch("sage quant q");
-    if (rc) return rc;
+    if (quant_q) {
+        hipLaunchKernelGGL(sage_quant_kernel, dim3((S + kSageBlock - 1) / kSageBlock, c->num_qo_heads),
+                           dim3(kSageThreads), 0, stream, static_cast<const bf16_t*>(q), (int)S,
+                           (int)c->num_qo_heads, q_sn, q_sh, hd, (const float*)nullptr, q8, sq);
+        rc = check_launch("sage quant q");
+        if (rc) return rc;
+    }
     hipLaunchKernelGGL(sage_quant_kernel, dim3((L + kSageBlock - 1) / kSageBlock, c->num_kv_heads),
                        dim3(kSageThreads), 0, stream, static_cast<const bf16_t*>(k), (int)L, (int)c->num_kv_heads,
                        k_sn, k_sh, hd, (const float*)kmean, k8, sk);
@@ -633,10 +692,16 @@ extern "C" int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, con
     float* sq = reinterpret_cast<float*>(p + w.q8 + w.k8);
     float* sk = reinterpret_cast<float*>(p + w.q8 + w.k8 + w.sq);
     float* km = reinterpret_cast<float*>(p + w.q8 + w.k8 + w.sq + w.sk);
-    rc = sage_quantize_impl(ctx, q, k, qo_len, kv_len, q8, sq, k8, sk, km, stream);
-    if (rc) return rc;
     const int hd = (int)ctx->head_dim;
+    const char* pipe_env = getenv("EFM_PREFILL_PIPE");
+    const bool pipe = hd == kSPHD && (pipe_env == nullptr || pipe_env[0] != '0');
+    // the pipelined kernel quantises Q itself (one 128-row block per 4 waves)
+    rc = sage_quantize_impl(ctx, q, k, qo_len, kv_len, q8, sq, k8, sk, km, stream, !pipe);
+    if (rc) return rc;
     SageArgs a;
+    a.q = static_cast<const bf16_t*>(q);
+    a.q_sn = ctx->q_stride_n ? (int)ctx->q_stride_n : (int)(ctx->num_qo_heads * hd);
+    a.q_sh = ctx->q_stride_h ? (int)ctx->q_stride_h : hd;
     a.q8 = q8;
     a.k8 = k8;
     a.sq = sq;
@@ -651,8 +716,7 @@ extern "C" int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, con
     a.v_sh = ctx->kv_stride_h ? (int)ctx->kv_stride_h : hd;
     a.causal = causal != 0;
     a.scale_log2 = (float)(1.4426950408889634 / sqrt((double)hd));
-    const char* pipe_env = getenv("EFM_PREFILL_PIPE");
-    if (hd == kSPHD && (pipe_env == nullptr || pipe_env[0] != '0')) {
+    if (pipe) {
         // as the bf16 kernel: 4 waves / two workgroups per CU up to 8K rows (a 3-deep ring
         // of 24 KB stages fits twice), 8 waves over a 4-deep ring beyond
         const char* shape = getenv("EFM_PREFILL_SHAPE");
