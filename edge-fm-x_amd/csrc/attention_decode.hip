@@ -45,7 +45,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / kWave;
 constexpr int kTileKeys = 32;
-constexpr int kMaxSplits = 256;  // split_cap <= 256 / num_kv_heads
+constexpr int kMaxSplits = 512;  // split_cap <= 512 / num_kv_heads (two workgroups per CU)
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeArgs {
@@ -84,7 +84,8 @@ union BfPack {
 // (written by the QKV projection of this step): the two lanes holding it rotate it,
 // use it and store it back rotated, so the cache is fully rotated after the call.
 template <int HD, int G, bool MERGE, bool ROTK>
-__global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs a) {
+// ROTK = false fits 2 workgroups per CU (<= 256 VGPRs); rotate-on-read keeps 1.
+__global__ __launch_bounds__(kAttnThreads, ROTK ? 1 : 2) void decode_attn_kernel(DecodeArgs a) {
     constexpr int HALF = HD / 2;
     constexpr int KS = HD / 16;        // MFMA k-steps over head_dim
     constexpr int DT = HD / 32;        // d tiles of O^T
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void decode_attn_kernel(DecodeArgs
     const int ql = lane % 32, hh = lane / 32;
     const int kvh = blockIdx.y;
     const int b = blockIdx.x;
-    const int kps = a.keys_per_split;   // a multiple of 4 x 32 keys, fixed per launch
+    const int kps = a.keys_per_split;   // a multiple of 32 keys (>= 128), fixed per launch
     const int start = b * kps;
 
     const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
@@ -472,16 +473,17 @@ __global__ __launch_bounds__(kAttnThreads) void decode_merge_kernel(DecodeArgs a
 }
 
 // Split geometry: 128 keys (one 32-key tile per wave) per workgroup, so that every K/V
-// load of a workgroup is in flight at once, until the grid reaches 256 workgroups; past
-// that the keys per split grow in steps of 128. Split b covers keys [b * kps, (b+1) * kps)
-// whatever the current length, so its first loads need not wait for *d_kv_len.
+// load of a workgroup is in flight at once, until the grid reaches 512 workgroups (two per
+// CU); past that the keys per split grow in 32-key tiles. Split b covers keys
+// [b * kps, (b + 1) * kps) whatever the current length, so its first loads need not wait
+// for *d_kv_len.
 constexpr int kKeysPerSplit = 128;
 
 int decode_keys_per_split(int num_kv_heads, uint32_t max_kv_len) {
     const uint32_t bound = std::max<uint32_t>(max_kv_len, 1u);
     const uint32_t by_chip = (uint32_t)std::max(1, kMaxSplits / std::max(1, num_kv_heads));
-    const uint32_t steps = (bound + kKeysPerSplit * by_chip - 1) / (kKeysPerSplit * by_chip);
-    return (int)(steps * kKeysPerSplit);
+    const uint32_t tiles = (bound + kTileKeys * by_chip - 1) / (kTileKeys * by_chip);
+    return (int)std::max<uint32_t>(kKeysPerSplit, tiles * kTileKeys);
 }
 
 int decode_split_cap(int num_kv_heads, uint32_t max_kv_len) {

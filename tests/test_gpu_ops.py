@@ -288,6 +288,47 @@ def test_linear_fp32_logits(gpu, m):
     torch.testing.assert_close(y.cpu(), O.linear(x, w, out_f32=True), rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("m,k,n,bias,kind", [
+    pytest.param(1300, 1024, 12345, True, "bf16", id="ragged_bias"),
+    pytest.param(2048, 1536, 8192, False, "bf16", id="1p5b_like"),
+    pytest.param(1344, 2048, 11008, False, "swiglu", id="vl3b_gate_up"),
+    pytest.param(300, 1536, 151936, False, "f32", id="logits_f32"),
+])
+def test_gemm_large_tile_matches_128_tile_bit_exact(gpu, monkeypatch, m, k, n, bias, kind):
+    """Shapes with >= 256 output tiles of 256 x 256 run the large-tile GEMM. Both kernels
+    accumulate the same 16-wide MFMA k-steps in the same order, so the outputs must be
+    identical to the 128 x 128 kernel's (EFM_GEMM_BIG=0); a row sample is also checked
+    against the oracle."""
+    torch.manual_seed(m + n)
+    x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
+    nw = 2 * n if kind == "swiglu" else n
+    w = (torch.randn(nw, k, device=gpu) * 0.05).to(torch.bfloat16)
+    b = (torch.randn(n, device=gpu) * 0.05).to(torch.bfloat16) if bias else None
+    outs = []
+    for big in ("1", "0"):
+        monkeypatch.setenv("EFM_GEMM_BIG", big)
+        if kind == "swiglu":
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+            C.call("efm_fused_gate_up_swiglu", m, k, n, ptr(x), ptr(w), ptr(y), stream())
+        else:
+            dt = torch.float32 if kind == "f32" else torch.bfloat16
+            y = torch.empty(m, n, dtype=dt, device=gpu)
+            C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y),
+                   C.EFM_DTYPE_F32 if kind == "f32" else C.EFM_DTYPE_BF16, stream())
+        torch.cuda.synchronize()
+        outs.append(y)
+    assert torch.equal(outs[0], outs[1]), "large-tile GEMM differs from the 128 x 128 kernel"
+    rows = torch.tensor([0, m // 2, m - 1])
+    xs = x[rows].cpu()
+    if kind == "swiglu":
+        ref = O.gate_up_swiglu(xs, w.cpu())
+        assert_close_bf16(outs[0][rows], ref, rtol=2e-2, atol=6.25e-2)
+    elif kind == "f32":
+        torch.testing.assert_close(outs[0][rows].cpu(), O.linear(xs, w.cpu(), out_f32=True), rtol=1e-4, atol=1e-4)
+    else:
+        assert_close_bf16(outs[0][rows], O.linear(xs, w.cpu(), b.cpu() if bias else None))
+
+
 @pytest.mark.parametrize("hidden,inter", [(896, 4864), (1536, 8960), (3584, 18944)])
 @pytest.mark.parametrize("m", [1, 5, 300])
 def test_fused_gate_up_swiglu(gpu, hidden, inter, m):
