@@ -807,3 +807,62 @@ def test_sage_attention_pipelined_matches_register_kernel(gpu, monkeypatch, shap
         outs.append(o)
     assert torch.isfinite(outs[0].float()).all()
     assert_close_bf16(outs[0], outs[1], rtol=2e-2, atol=2e-2, what="sage pipelined vs register kernel")
+
+
+@pytest.mark.parametrize("hq,hkv", [(12, 2), (28, 4), (16, 2), (8, 8)])
+@pytest.mark.parametrize("kv_len,max_kv", [(1, 1), (100, 128), (767, 768), (1025, 2000), (16385, 16513)])
+def test_decode_attention_lds_kernel_matches_register_kernel(gpu, monkeypatch, hq, hkv, kv_len, max_kv):
+    """head_dim 128 with a rotated cache runs the LDS-staged kernel; it must agree with
+    the register kernel (EFM_DECODE_LDS=0) on the same cache, through both the merged
+    entry point and the partials + fused o_proj merge, and store the same rotated newest
+    row. Rows past the length hold NaN."""
+    torch.manual_seed(kv_len + hq)
+    hd = 128
+    q = torch.randn(1, hq * hd, dtype=torch.bfloat16, device=gpu)
+    k0 = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    v = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    k0[kv_len:] = float("nan")
+    v[kv_len:] = float("nan")
+    ctx = C.make_attention_ctx(hq, hkv, hd)
+    ctx.k_already_prerotated = C.EFM_K_PREROTATED_EXCEPT_NEWEST
+    d_len = torch.tensor([kv_len], dtype=torch.int32, device=gpu)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=gpu)
+    outs, caches = [], []
+    for lds in ("1", "0"):
+        monkeypatch.setenv("EFM_DECODE_LDS", lds)
+        k = k0.clone()
+        o = torch.empty_like(q)
+        C.call("efm_attention_decode", ctx, ptr(q), ptr(k), ptr(v), ptr(o), 0, ptr(d_len), max_kv, ptr(ws),
+               ws.numel(), stream())
+        torch.cuda.synchronize()
+        outs.append(o)
+        caches.append(k)
+    assert torch.isfinite(outs[0].float()).all()
+    assert_close_bf16(outs[0], outs[1], what="lds vs register decode kernel")
+    assert torch.equal(caches[0][: kv_len - 1], k0[: kv_len - 1])
+    # the newest row: both rotate with the same cos/sin table and rounding
+    assert torch.equal(caches[0][kv_len - 1], caches[1][kv_len - 1])
+
+
+@pytest.mark.parametrize("lds", ["0", "1"])
+@pytest.mark.parametrize("kv_len,max_kv", [(161, 40000), (321, 70000), (1025, 40000), (129, 40000)])
+def test_decode_newest_row_owned_by_one_split(gpu, monkeypatch, lds, kv_len, max_kv):
+    """With keys-per-split not a multiple of 128 (large max_kv_len) a split's last round has
+    idle tiles that lie in the next split; they must not touch the newest row, which only
+    its owning split rotates and stores (regression: the idle tile stored zeros)."""
+    monkeypatch.setenv("EFM_DECODE_LDS", lds)
+    torch.manual_seed(0)
+    hq, hkv, hd = 12, 2, 128
+    q = torch.randn(1, hq * hd, dtype=torch.bfloat16, device=gpu)
+    k = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    v = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16, device=gpu)
+    raw = k[kv_len - 1].clone().cpu()
+    ctx = C.make_attention_ctx(hq, hkv, hd)
+    ctx.k_already_prerotated = C.EFM_K_PREROTATED_EXCEPT_NEWEST
+    d_len = torch.tensor([kv_len], dtype=torch.int32, device=gpu)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=gpu)
+    C.call("efm_decode_attention_partials", ctx, ptr(q), ptr(k), ptr(v), ptr(d_len), max_kv, ptr(ws), ws.numel(),
+           stream())
+    torch.cuda.synchronize()
+    want = O.rope_llama(raw.unsqueeze(0), torch.tensor([kv_len - 1]), 1.0e6).to(torch.bfloat16)[0]
+    assert_close_bf16(k[kv_len - 1], want, rtol=1e-2, atol=1e-2, what="newest row")
