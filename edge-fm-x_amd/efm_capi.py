@@ -156,6 +156,14 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         return _lib
     if not os.path.exists(path):
         raise RuntimeError(f"edgefm_hip library not built: {path} is missing (run __graft_entry__.build())")
+    # PyTorch-ROCm ships its own HIP runtime, loaded by file path: if this library were
+    # loaded first it would bind /opt/rocm's copy and the process would hold two
+    # runtimes whose device state does not mix. Loading torch first makes this library
+    # resolve libamdhip64.so.7 to torch's already-loaded copy.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

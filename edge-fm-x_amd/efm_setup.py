@@ -73,10 +73,25 @@ def write_model_dir(path: str, shape: ModelShape, eos_token_id=None) -> str:
     return path
 
 
+def write_compact_vocab_mapping(path: str, original_vocab_size: int, new_to_old, special_token_ids,
+                                fmt: str = "edgefm.compact_vocab.v1") -> str:
+    """Write an ``edgefm.compact_vocab.v1`` mapping: compact id n is original id new_to_old[n];
+    every other original id maps to -1."""
+    old_to_new = [-1] * original_vocab_size
+    for n, o in enumerate(new_to_old):
+        old_to_new[o] = n
+    with open(path, "w") as f:
+        json.dump({"format": fmt, "original_vocab_size": original_vocab_size,
+                   "compact_vocab_size": len(new_to_old), "old_to_new": old_to_new,
+                   "new_to_old": list(new_to_old), "special_token_ids": list(special_token_ids)}, f)
+    return path
+
+
 def write_engine_config(path: str, model_dir: str, *, max_tokens: int = 4096, max_new_tokens: int = 256,
                         prefix_token_ids=None, use_graph: bool = True, temperature: float = 0.0,
                         top_p: float = 1.0, seed: int = 0, lm_head_top1: bool = True, model_name: str = "",
-                        operator_impl_table_path: str = "", extra_slots=None, decode_chain: bool = False) -> str:
+                        operator_impl_table_path: str = "", extra_slots=None, decode_chain: bool = False,
+                        stop_token_ids=None, compact_vocab=None) -> str:
     slots = [{"request_id": 0, "prefix_token_ids": list(prefix_token_ids or []), "max_tokens": max_tokens}]
     for s in extra_slots or []:
         slots.append(s)
@@ -88,8 +103,10 @@ def write_engine_config(path: str, model_dir: str, *, max_tokens: int = 4096, ma
         "operator_impl_table_path": operator_impl_table_path,
         "kvcache": {"dtype": "bf16", "requests": slots},
         "sampling": {"max_new_tokens": max_new_tokens, "temperature": temperature, "top_p": top_p, "seed": seed,
-                     "stop_token_ids": []},
+                     "stop_token_ids": list(stop_token_ids or [])},
     }
+    if compact_vocab is not None:
+        cfg["compact_vocab"] = compact_vocab
     with open(path, "w") as f:
         json.dump(cfg, f)
     return path

@@ -246,6 +246,11 @@ std::vector<int32_t> EngineConfig::eos_token_ids() const {
     return out;
 }
 
+Json EngineConfig::compact_vocab() const {
+    if (json_.contains("compact_vocab") && json_.at("compact_vocab").is_object()) return json_.at("compact_vocab");
+    return Json::object();
+}
+
 ModelConfig ModelConfig::from_json(const Json& j0) {
     // Qwen2.5-VL keeps the language model hyper-parameters under text_config.
     const Json& j = j0.contains("text_config") ? j0.at("text_config") : j0;
@@ -771,7 +776,7 @@ struct EventTimer {
 };
 }  // namespace
 
-StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_path) {
+StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_path), compact_vocab_(cfg_) {
     // sampling parameters are validated before any device work (src/layers/sampler.cu:130-132)
     check<ConfigurationError>(cfg_.temperature() >= 0.0f,
                               "temperature must be non-negative. Got: " + std::to_string(cfg_.temperature()));
@@ -785,7 +790,12 @@ StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_pat
         loader.load_weights_from_file(cfg_.prefill_model_path(), ModelStage::Prefill, device_id_);
     }
     model_ = std::make_unique<Qwen2_5>(cfg_, m, loader.get(ModelStage::Prefill), device_id_);
-    kv_ = std::make_unique<KVManager>(cfg_.kv_slots(), m, device_id_);
+    // fixed KV prefixes are configuration ids: remapped like EOS ids (kv_manager.cpp:151-155)
+    std::vector<KVSlotConfig> slots = cfg_.kv_slots();
+    for (auto& s : slots)
+        s.prefix_token_ids = compact_vocab_.remap_required_token_ids(s.prefix_token_ids,
+                                                                     "kvcache.requests[].prefix_token_ids");
+    kv_ = std::make_unique<KVManager>(slots, m, device_id_);
     state_ = Tensor::zeros({16}, DType::Int32, Device::GPU, device_id_);
     int32_t max_resp = 1;
     for (const auto& s : cfg_.kv_slots()) {
@@ -870,8 +880,13 @@ void StandardEngine::run_decode_step(int32_t request_id, bool) {
     if (model_->config().mrope) efm_check(efm_increment_int32_triplet(st + 3, stream_), "advance mrope position");
 }
 
-Response StandardEngine::generate(const Request& req) {
+Response StandardEngine::generate(const Request& request) {
     hip_check(hipSetDevice(device_id_), "hipSetDevice");
+    // compact vocabulary: the request is remapped into the checkpoint's ids and the
+    // response restored (standard_engine.cpp:877-882,1070-1072)
+    std::unique_ptr<Request> remapped;
+    if (compact_vocab_.enabled()) remapped = std::make_unique<Request>(compact_vocab_.remap_request(request));
+    const Request& req = remapped ? *remapped : request;
     check<InvalidRequestError>(!req.token_ids.empty(), "Request must contain at least one token id");
     KVSlot& slot = kv_->slot(req.request_id);
     const ModelConfig& m = model_->config();
@@ -993,8 +1008,10 @@ Response StandardEngine::generate(const Request& req) {
     // stop tokens truncate after the first hit, inclusive (standard_engine.cpp:1060-1068)
     if (!req.ignore_stop_tokens) {
         std::unordered_set<int32_t> stop;
-        for (int32_t t : cfg_.eos_token_ids()) stop.insert(t);
-        for (int32_t t : cfg_.stop_token_ids()) stop.insert(t);
+        for (int32_t t : compact_vocab_.remap_required_token_ids(cfg_.eos_token_ids(), "model eos_token_ids"))
+            stop.insert(t);
+        for (int32_t t : compact_vocab_.remap_required_token_ids(cfg_.stop_token_ids(), "sampling.stop_token_ids"))
+            stop.insert(t);
         for (int32_t t : req.stop_token_ids) stop.insert(t);
         for (size_t i = 0; i < host.size(); ++i)
             if (stop.count(host[i])) {
@@ -1017,7 +1034,7 @@ Response StandardEngine::generate(const Request& req) {
     metrics_["use_hip_graph"] = cfg_.use_graph() ? 1.0 : 0.0;
     metrics_["decode_chain"] = model_->uses_decode_chain((uint32_t)slot.cfg.max_tokens) ? 1.0 : 0.0;
     Response r;
-    r.token_ids = std::move(host);
+    r.token_ids = compact_vocab_.restore_token_ids(host, "response token_ids");
     return r;
 }
 

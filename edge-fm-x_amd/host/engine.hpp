@@ -14,6 +14,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "compact_vocab.hpp"
 #include "core.hpp"
 #include "json.hpp"
 #include "operators.hpp"
@@ -82,6 +83,10 @@ public:
     std::vector<int32_t> stop_token_ids() const;
     const Json& model_config() const { return model_json_; }
     std::vector<int32_t> eos_token_ids() const;
+    // "compact_vocab" object of the merged config, or an empty object.
+    Json compact_vocab() const;
+    // Directory of the user config file (relative paths in it resolve against it).
+    const std::string& config_dir() const { return base_dir_; }
 
 private:
     Json json_;
@@ -203,10 +208,12 @@ public:
     std::unordered_map<std::string, double> last_generate_metrics() const { return metrics_; }
     const ModelConfig& model_config() const { return model_->config(); }
     const EngineConfig& engine_config() const { return cfg_; }
+    const CompactVocab& compact_vocab() const { return compact_vocab_; }
     void warmup();
 
 private:
     EngineConfig cfg_;
+    CompactVocab compact_vocab_;
     int32_t device_id_;
     hipStream_t stream_ = nullptr;
     std::unique_ptr<Qwen2_5> model_;

@@ -35,6 +35,7 @@ public:
     bool is_null() const { return type_ == Type::Null; }
     bool is_bool() const { return type_ == Type::Bool; }
     bool is_number() const { return type_ == Type::Number; }
+    bool is_integer() const { return type_ == Type::Number && is_int_; }
     bool is_string() const { return type_ == Type::String; }
     bool is_array() const { return type_ == Type::Array; }
     bool is_object() const { return type_ == Type::Object; }

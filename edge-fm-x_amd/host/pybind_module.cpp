@@ -160,6 +160,21 @@ PYBIND11_MODULE(edge_fm, m) {
             return d;
         });
 
+    // Compact-vocabulary id mapping of an engine config (compact_vocab.h:12-53); host
+    // only, so it is usable without a GPU.
+    py::class_<CompactVocab>(m, "CompactVocab")
+        .def(py::init([](const std::string& config_path) { return CompactVocab(EngineConfig(config_path)); }),
+             py::arg("config_path"))
+        .def("enabled", &CompactVocab::enabled)
+        .def("original_vocab_size", &CompactVocab::original_vocab_size)
+        .def("compact_vocab_size", &CompactVocab::compact_vocab_size)
+        .def("mapping_path", &CompactVocab::mapping_path)
+        .def("remap_token_ids", &CompactVocab::remap_token_ids, py::arg("ids"), py::arg("context"))
+        .def("remap_required_token_ids", &CompactVocab::remap_required_token_ids, py::arg("ids"), py::arg("context"))
+        .def("remap_optional_token_ids", &CompactVocab::remap_optional_token_ids, py::arg("ids"), py::arg("context"))
+        .def("restore_token_ids", &CompactVocab::restore_token_ids, py::arg("ids"), py::arg("context"))
+        .def("remap_request", &CompactVocab::remap_request, py::arg("request"));
+
     py::class_<WeightLoader, std::unique_ptr<WeightLoader, py::nodelete>>(m, "WeightLoader")
         .def_static("instance", &WeightLoader::instance, py::return_value_policy::reference)
         .def("load_weights_from_file", &WeightLoader::load_weights_from_file, py::arg("model_path"),

@@ -4,6 +4,9 @@ import os
 import sys
 
 import pytest
+# before any test module imports edge_fm / loads libedgefm_hip.so: one HIP runtime per
+# process (torch's), see efm_capi.load
+import torch  # noqa: F401
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "edge-fm-x_amd")

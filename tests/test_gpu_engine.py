@@ -269,3 +269,39 @@ def test_decode_chain_matches_per_operator_path(gpu, shape_id, use_graph):
             assert eng.last_generate_metrics()["decode_chain"] == (1.0 if chain else 0.0)
             del eng, keep
     assert toks[True][0] == toks[True][1] == toks[False][0] == toks[False][1]
+
+
+def test_compact_vocab_generate_matches_unmapped_run(gpu):
+    """A pre-pruned checkpoint (vocab 600 of an original 1000, non-monotonic id map) run
+    with compact_vocab enabled takes and returns original ids: its tokens are the
+    unmapped run's tokens mapped through new_to_old, also with a remapped fixed KV
+    prefix; request stop ids are remapped and pruned request ids are rejected
+    (standard_engine.cpp:877-917,1070-1072; kv_manager.cpp:151-155)."""
+    shape = S.ModelShape(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=64, inter=512, vocab=600)
+    w = O.random_weights(_oracle_cfg(shape), seed=31, std=0.2)
+    g = torch.Generator().manual_seed(8)
+    new_to_old = torch.randperm(1000, generator=g)[:600].tolist()
+    prompt = torch.randint(0, 600, (40,), generator=g).tolist()
+    external = [new_to_old[t] for t in prompt]
+    with tempfile.TemporaryDirectory() as tmp:
+        eng, keep = _engine(tmp, shape, w, max_tokens=96, max_new_tokens=20)
+        req = edge_fm.Request(0, prompt)
+        req.set_ignore_stop_tokens(True)
+        base = eng.generate(req).token_ids()
+        del eng
+        S.write_compact_vocab_mapping(os.path.join(tmp, "compact_vocab.json"), 1000, new_to_old, [new_to_old[0]])
+        cv = {"enabled": True, "mapping_path": "compact_vocab.json", "reject_unknown_input_ids": True}
+        eng, keep = _engine(tmp, shape, w, max_tokens=96, max_new_tokens=20, compact_vocab=cv,
+                            prefix_token_ids=external[:12])
+        req = edge_fm.Request(0, external)
+        req.set_ignore_stop_tokens(True)
+        got = eng.generate(req).token_ids()
+        assert got == [new_to_old[t] for t in base]
+        assert eng.last_generate_metrics()["prefill_tokens"] == 40 - 12
+        req2 = edge_fm.Request(0, external)
+        req2.set_stop_token_ids([got[4]])
+        assert eng.generate(req2).token_ids() == got[: got.index(got[4]) + 1]
+        pruned = sorted(set(range(1000)) - set(new_to_old))[0]
+        with pytest.raises(edge_fm.InvalidRequestError):
+            eng.generate(edge_fm.Request(0, external[:5] + [pruned]))
+        del eng
