@@ -33,8 +33,7 @@
 //    graph. A single split writes the output itself; otherwise every split writes fp32
 //    (o, m, l) partials that a second kernel (one workgroup per query head) merges, or
 //    that the o_proj GEMV merges in its prologue (efm_decode_attention_merge_o_proj).
-#include "attn_pipe.hpp"
-#include "common.hpp"
+#include "decode_attn_impl.hpp"
 
 #include <algorithm>
 #include <cstdlib>
@@ -42,42 +41,7 @@
 
 namespace efm {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kAttnThreads = 256;
-constexpr int kAttnWaves = kAttnThreads / kWave;
-constexpr int kTileKeys = 32;
-constexpr int kMaxSplits = 512;  // split_cap <= 512 / num_kv_heads (two workgroups per CU)
-constexpr float kLog2e = 1.4426950408889634f;
-
-struct DecodeArgs {
-    const bf16_t* q;
-    const bf16_t* k;
-    const bf16_t* v;
-    bf16_t* o;
-    uint32_t kv_len;
-    const uint32_t* d_kv_len;
-    uint32_t max_kv_len;
-    int num_kv_heads;
-    int q_sn, q_sh, k_sn, k_sh, v_sn, v_sh;   // element strides
-    int q_pos_off, k_pos_off;
-    int rope_q;                               // rotate q (and, by ROTK / fix_last, keys)
-    int fix_last;                             // rotate + store back row L - 1 (ROTK = false)
-    int row_bound;                            // rows that may be read (allocation bound)
-    int split_cap;                            // gridDim.x
-    int keys_per_split;                       // keys of split b: [b * kps, (b + 1) * kps)
-    float* o_part;                            // [Hkv][split_cap][G][HD]
-    float* ml_part;                           // [Hkv][split_cap][G][2]
-    uint32_t* counter;                        // [Hkv] (reserved in the workspace, unused)
-    RopeTable rope;
-};
-
-union BfPack {
-    bf16x8_t v;
-    uint4 u;
-    uint32_t w[4];
-};
 
 // MERGE = true: a single split (split_cap == 1) writes the normalised output directly.
 // MERGE = false: every split writes its (o, m, l) partial; a consumer merges them
@@ -383,292 +347,10 @@ __global__ __launch_bounds__(kAttnThreads, ROTK ? 1 : 2) void decode_attn_kernel
     }
 }
 
-// LDS-staged variant for head_dim 128 with a rotated cache (ROTK = false): each round
-// stages 128 keys of K and V with global_load_lds (1 KB wave loads: 4 rows x 256 bytes,
-// so every load instruction reads whole 256-byte row pieces), in the layouts of
-// attn_pipe.hpp. Wave w then takes the keys [32 w, 32 w + 32) of the round: the K operand
-// of S^T = K . Q^T comes from ds_read_b128, the V^T operand of O^T = V^T . P^T from
-// ds_read_b64_tr_b16 (no transpose through registers). Rows past the length are masked
-// in the scores and their V rows are zeroed in LDS (stale cache rows may hold NaN).
+// LDS-staged kernel (head_dim 128, rotated cache); body in decode_attn_impl.hpp.
 template <int G, bool MERGE>
 __global__ __launch_bounds__(kAttnThreads, 2) void decode_attn_lds_kernel(DecodeArgs a) {
-    constexpr int HD = 128, HALF = 64, KS = 8, DT = 4;
-    constexpr int RK = kAttnWaves * kTileKeys;                // keys per round
-    constexpr int TILE = RK * attn_pipe::kRow;                 // bytes of K (or V) per round
-    constexpr int LPW = 2 * TILE / 1024 / kAttnWaves;          // 1 KB wave loads per wave per round
-    static_assert(G <= 32, "group too large");
-    static_assert(kAttnWaves * G * HD * 4 + 2 * kAttnWaves * 32 * 4 <= 2 * TILE, "merge buffers must fit the tiles");
-    __shared__ __align__(1024) unsigned char smem[2 * TILE];   // K | V of one round; then the wave merge
-    __shared__ float2 cs_qk[2][HALF];
-
-    const int tid = threadIdx.x;
-    const int wave = tid / kWave, lane = tid % kWave;
-    const int ql = lane % 32, hh = lane / 32;
-    const int kvh = blockIdx.y;
-    const int b = blockIdx.x;
-    const int kps = a.keys_per_split;
-    const int start = b * kps;
-    const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
-    const bf16_t* vbase = a.v + (size_t)kvh * a.v_sh;
-    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
-
-    // ---- 1. loads that do not depend on L: the query, the first round of K / V (rows
-    //         below the allocation bound), the RoPE frequencies
-    uint4 qraw[KS];
-    {
-        const bool qv = ql < G;
-        const bf16_t* qp = a.q + (size_t)(kvh * G + (qv ? ql : 0)) * a.q_sh + hh * 8;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qraw[ks] = qv ? *reinterpret_cast<const uint4*>(qp + ks * 16) : make_uint4(0, 0, 0, 0);
-    }
-    const int lim = min(a.row_bound, start + kps) - 1;   // last row this split may read
-    auto issue = [&](int r) {
-        const int k0 = start + r * RK;
-        const int pr = lane >> 4, pc = lane & 15;
-#pragma unroll
-        for (int i = 0; i < LPW; ++i) {
-            const int q = wave + i * kAttnWaves;               // wave-load index: K 0..31, V 32..63
-            const bool isv = q >= TILE / 1024;
-            const int row = (q % (TILE / 1024)) * 4 + pr;
-            const int c = isv ? (pc ^ ((row & 3) << 2)) : (pc ^ (row & 15));
-            const int j = min(k0 + row, lim);
-            const bf16_t* src = (isv ? vbase + (size_t)j * a.v_sn : kbase + (size_t)j * a.k_sn) + c * 8;
-            __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                             (__attribute__((address_space(3))) void*)(smem + q * 1024), 16, 0, 0);
-        }
-    };
-    issue(0);
-    const float freq = (a.rope_q && tid < 2 * HALF) ? a.rope.inv_freq[tid % HALF] : 0.f;
-
-    // ---- 2. the context length and this split's key range [start, end)
-    uint32_t L = a.kv_len;
-    if (a.d_kv_len != nullptr) L = min(a.d_kv_len[0], a.max_kv_len);
-    const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
-    if (b >= nsplit) {
-        attn_pipe::vm_wait<0>();   // no LDS write may outlive the workgroup
-        return;
-    }
-    const int end = min((int)L, start + kps);
-    const int rounds = (end > start) ? (end - start + RK - 1) / RK : 0;
-
-    // ---- 3. RoPE at the query position and at the newest key's position
-    if (a.rope_q && tid < 2 * HALF) {
-        const int pos = (int)L - 1 + (tid < HALF ? a.q_pos_off : a.k_pos_off);
-        float sn, cs;
-        sincos_reduced((float)pos * freq, &sn, &cs);
-        cs_qk[tid / HALF][tid % HALF] = make_float2(cs, sn);
-    }
-    __syncthreads();
-    bf16x8_t qf[KS];
-    {
-        float x[KS][8];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) unpack8(qraw[ks], x[ks]);
-        if (a.rope_q) {
-#pragma unroll
-            for (int ks = 0; ks < KS / 2; ++ks)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float2 c2 = cs_qk[0][ks * 16 + hh * 8 + e];
-                    const float x0 = x[ks][e], x1 = x[ks + KS / 2][e];
-                    x[ks][e] = x0 * c2.x - x1 * c2.y;
-                    x[ks + KS / 2][e] = x1 * c2.x + x0 * c2.y;
-                }
-        }
-        const float qscale = kLog2e / sqrtf((float)HD);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) x[ks][e] *= qscale;
-            BfPack pk;
-            pk.u = pack8(x[ks]);
-            qf[ks] = pk.v;
-        }
-    }
-    const int fix_row = (a.rope_q && a.fix_last && L > 0) ? (int)L - 1 : -1;
-
-    f32x16_t oacc[DT];
-#pragma unroll
-    for (int tt = 0; tt < DT; ++tt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) oacc[tt][e] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
-    uint32_t koff[KS], voff[DT];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) koff[ks] = lds0 + attn_pipe::k_off(wave * 32 + ql, ks * 2 + hh);
-#pragma unroll
-    for (int tt = 0; tt < DT; ++tt) voff[tt] = lds0 + (uint32_t)TILE + (uint32_t)(wave * 32 * attn_pipe::kRow) +
-                                               attn_pipe::v_tr_lane_off(lane, tt);
-    typedef short s4_t __attribute__((ext_vector_type(4)));
-
-    for (int r = 0; r < rounds; ++r) {
-        const int k0 = start + r * RK;
-        if (r > 0) {
-            __syncthreads();   // every wave is done with the previous round's tiles
-            issue(r);
-        }
-        attn_pipe::vm_wait<0>();
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        if (end < k0 + RK) {
-            // zero the V rows past the length (P is 0 there, but the rows may hold NaN)
-            for (int i = tid; i < (k0 + RK - end) * 16; i += kAttnThreads) {
-                const int row = end - k0 + i / 16;
-                *reinterpret_cast<uint4*>(smem + TILE + row * attn_pipe::kRow + (i % 16) * 16) = make_uint4(0, 0, 0, 0);
-            }
-            __syncthreads();
-        }
-        const int t0 = k0 + wave * 32;
-        if (t0 >= end) continue;
-        bf16x8_t kf[KS];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) attn_pipe::read_b128<0>(kf[ks], koff[ks]);
-        s4_t vf[2][DT][2];
-        auto read_v = [&](auto kbc) {
-            constexpr int kb = decltype(kbc)::value;
-#pragma unroll
-            for (int tt = 0; tt < DT; ++tt) {
-                attn_pipe::read_tr16<(kb * 16) * attn_pipe::kRow>(vf[kb][tt][0], voff[tt]);
-                attn_pipe::read_tr16<(kb * 16 + 8) * attn_pipe::kRow>(vf[kb][tt][1], voff[tt]);
-            }
-        };
-        read_v(std::integral_constant<int, 0>{});
-        asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");   // the K reads (issued first) are done
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kf[ks]));
-        if (t0 + ql == fix_row && fix_row < end) {
-            // the newest key: rotate at its position, use it and store it back rotated
-            bf16_t* kw = const_cast<bf16_t*>(kbase) + (size_t)fix_row * a.k_sn + hh * 8;
-#pragma unroll
-            for (int ks = 0; ks < KS / 2; ++ks) {
-                BfPack u0, u1;
-                u0.v = kf[ks];
-                u1.v = kf[ks + KS / 2];
-                float x0[8], x1[8];
-                unpack8(u0.u, x0);
-                unpack8(u1.u, x1);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float2 c2 = cs_qk[1][ks * 16 + hh * 8 + e];
-                    const float y0 = x0[e] * c2.x - x1[e] * c2.y;
-                    const float y1 = x1[e] * c2.x + x0[e] * c2.y;
-                    x0[e] = y0;
-                    x1[e] = y1;
-                }
-                u0.u = pack8(x0);
-                u1.u = pack8(x1);
-                kf[ks] = u0.v;
-                kf[ks + KS / 2] = u1.v;
-                *reinterpret_cast<uint4*>(kw + ks * 16) = u0.u;
-                *reinterpret_cast<uint4*>(kw + (ks + KS / 2) * 16) = u1.u;
-            }
-        }
-        f32x16_t s = {};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
-        read_v(std::integral_constant<int, 1>{});
-        // element e: key = t0 + (e/4)*8 + hh*4 + e%4, head = ql
-        if (t0 + 32 > end) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int j = t0 + (e / 4) * 8 + hh * 4 + (e % 4);
-                s[e] = (j < end) ? s[e] : -INFINITY;
-            }
-        }
-        float mloc = fmaxf(s[0], s[1]);
-#pragma unroll
-        for (int e = 2; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
-        {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
-            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
-        const float m_new = fmaxf(m_run, mloc);   // finite: the tile holds a valid key
-        float p[16], psum = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            p[e] = __builtin_amdgcn_exp2f(s[e] - m_new);
-            psum += p[e];
-        }
-        {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(psum), __float_as_uint(psum), false, false);
-            psum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-        }
-        if (r == 0) {
-            l_run = psum;
-        } else {
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run = l_run * alpha + psum;
-#pragma unroll
-            for (int tt = 0; tt < DT; ++tt)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
-        }
-        m_run = m_new;
-        BfPack pb[2];
-        pb[0].u = pack8(&p[0]);
-        pb[1].u = pack8(&p[8]);
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int tt = 0; tt < DT; ++tt) {
-                if (tt == 0) {
-                    if (kb == 0) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
-                    else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                }
-                asm volatile("" : "+v"(vf[kb][tt][0]), "+v"(vf[kb][tt][1]));
-                union {
-                    s4_t h[2];
-                    bf16x8_t v;
-                } vv;
-                vv.h[0] = vf[kb][tt][0];   // A slots 0-3: keys 16 kb + 4 hh + 0..3
-                vv.h[1] = vf[kb][tt][1];   // A slots 4-7: keys 16 kb + 8 + 4 hh + 0..3
-                oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv.v, pb[kb].v, oacc[tt], 0, 0, 0);
-            }
-    }
-
-    // ---- merge the 4 waves through LDS (the tile buffers are free now)
-    __syncthreads();
-    float* om = reinterpret_cast<float*>(smem);                  // [4][32]
-    float* ol = om + kAttnWaves * 32;                            // [4][32]
-    float* ob = ol + kAttnWaves * 32;                            // [4][G][HD]
-    if (hh == 0) {
-        om[wave * 32 + ql] = m_run;
-        ol[wave * 32 + ql] = l_run;
-    }
-    if (ql < G) {
-#pragma unroll
-        for (int tt = 0; tt < DT; ++tt)
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-                ob[(wave * G + ql) * HD + tt * 32 + (e / 4) * 8 + hh * 4 + (e % 4)] = oacc[tt][e];
-    }
-    __syncthreads();
-    float* o_part = a.o_part + ((size_t)kvh * a.split_cap + b) * G * HD;
-    float* ml_part = a.ml_part + ((size_t)kvh * a.split_cap + b) * G * 2;
-    for (int i = tid; i < G * HD; i += kAttnThreads) {
-        const int g = i / HD, d = i % HD;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, om[w * 32 + g]);
-        float num = 0.f, den = 0.f;
-#pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) {
-            const float mw = om[w * 32 + g];
-            const float sc = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-            num = fmaf(sc, ob[(w * G + g) * HD + d], num);
-            den = fmaf(sc, ol[w * 32 + g], den);
-        }
-        if (MERGE) {
-            a.o[(size_t)(kvh * G + g) * HD + d] = (bf16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
-        } else {
-            o_part[i] = num;
-            if (d == 0) {
-                ml_part[g * 2 + 0] = M;
-                ml_part[g * 2 + 1] = den;
-            }
-        }
-    }
+    decode_attn_lds_body<G, MERGE, false>(a, blockIdx.x, blockIdx.y, FusedAttnArgs{});
 }
 
 // Split merge of efm_attention_decode: one workgroup per query head, 256 threads =

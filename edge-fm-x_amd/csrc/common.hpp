@@ -184,6 +184,21 @@ __device__ __forceinline__ void sincos_reduced(float a, float* s, float* c) {
     *c = __builtin_amdgcn_cosf(rev);
 }
 
+// ---- tagged-word exchange between workgroups of one launch ----
+// Tag of the current launch: epoch % 65535 + 1, never 0 (zeroed words never match) and
+// different from the previous launch's, whose words are the stale ones a poll can see.
+__device__ __forceinline__ uint32_t launch_tag(const uint32_t* epoch) {
+    const uint32_t e = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return e % 65535u + 1u;
+}
+
+// One tagged word (16-bit payload | tag << 16), written with an agent-scope atomic
+// exchange: performed where the atomics of every XCD meet, so a poll from another XCD
+// sees it without a cache flush on either side.
+__device__ __forceinline__ void tagged_publish(uint32_t* p, uint32_t tag, uint32_t bits16) {
+    (void)__hip_atomic_exchange(p, (tag << 16) | (bits16 & 0xffffu), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace efm
 
 // Error reporting shared by every entry point of the C ABI.

@@ -1,0 +1,451 @@
+// Batch-1 decode GEMV family for gfx950: device code shared by the GEMV kernels
+// (gemv.hip) and the fused QKV projection + decode attention kernel
+// (decode_qkv_attention.hip).
+//
+// y[n] = x . W[n, :] with W row-major [rows, K] bf16 (the reference's cuBLASLt layout,
+// TRANSA=T on [out, in], src/layers/linear.cu:740). The kernel is HBM-bound: every
+// weight byte is read exactly once per decode step, so the design goal is to keep
+// enough 16-byte loads in flight on all 256 CUs and to do nothing else on the
+// critical path.
+//
+//  * 256-thread workgroups (4 wave64s). A "row group" of R logical rows is owned by
+//    KS waves that split the K dimension; a workgroup owns 4/KS row groups.
+//  * Each lane loads 16 B (8 bf16) per row per step with non-temporal loads; a wave
+//    covers 1 KiB contiguous of a row per load instruction (fully coalesced).
+//  * All weight loads of a row block are issued first; the input-vector prologue
+//    (plain copy, RMSNorm, or residual add + RMSNorm) runs while they are in flight and
+//    leaves x in LDS as bf16, exactly as the unfused reference would have written it.
+//  * Workgroups walk row blocks grid-stride; the next block's loads are issued before
+//    the current block's cross-lane reductions and epilogue.
+//  * Epilogues: bf16 store (+bias), fp32 store, QKV split with K/V written straight
+//    into the KV-cache slot (optionally also published as tagged words), SwiGLU over
+//    paired up/gate rows, and greedy top-1 with a last-workgroup grid reduction (no
+//    second launch, self-resetting counter).
+#pragma once
+
+#include "common.hpp"
+
+namespace efm {
+
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ADD_NORM = 2, PRO_ATTN_MERGE = 3 };
+enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_TOP1 = 4, EPI_QKV_TAG = 5 };
+
+// Weight-stream load used by the GEMV main loop (non-temporal: weights are read once
+// per decode step and must not evict the activation working set).
+#ifndef EFM_WEIGHT_LOAD
+#define EFM_WEIGHT_LOAD load_stream16
+#endif
+
+constexpr int kGemvThreads = 256;
+constexpr int kNJMax = 6;
+constexpr int kTop1MaxGridDev = 2048;  // top-1 workspace slots (its first 8 bytes hold the best key)
+constexpr int kProMax = 4;       // max prologue chunks per thread (K <= 8192)
+
+struct GemvArgs {
+    int K;                      // input features
+    int N;                      // logical output rows
+    const bf16_t* W;            // [physical rows, K]
+    const bf16_t* x;            // input vector (PLAIN) or h (NORM / ADD_NORM)
+    const bf16_t* r_in;         // ADD_NORM residual input
+    bf16_t* r_out;              // NORM / ADD_NORM residual output (written by block 0)
+    const bf16_t* norm_w;       // RMSNorm weight
+    float eps;
+    const bf16_t* bias;         // optional, per logical row
+    void* y;                    // output
+    int q_dim, kv_dim;          // QKV split
+    bf16_t* k_cache;
+    bf16_t* v_cache;
+    const uint32_t* d_kv_len;
+    ArgMax* partials;           // TOP1: one per workgroup
+    uint32_t* counter;          // TOP1: arrival counter (zero between launches)
+    int32_t* token_out;
+    // ATTN_MERGE: decode-attention split partials (efm_decode_attention_partials)
+    const float* o_part;        // [Hkv][split_cap][G][hd]
+    const float* ml_part;       // [Hkv][split_cap][G][2]
+    int split_cap, keys_per_split, head_dim, group;
+    const uint32_t* attn_len;   // *attn_len = attended rows (clamped to attn_max_len)
+    uint32_t attn_max_len;
+    // QKV_TAG: every output row n is also published as the tagged word tag_words[n]
+    // (bf16 bits | launch tag << 16) for the attention workgroups of the same launch
+    uint32_t* tag_words;
+    const uint32_t* epoch;      // launch counter the tag derives from (launch_tag)
+};
+
+
+constexpr int kMergeMaxSplits = 8;
+constexpr int kMergeMaxHeads = 64;
+
+template <int PRO>
+__device__ __forceinline__ void gemv_prologue(const GemvArgs& a, bf16_t* xs, float* red, int blk) {
+    const int C = a.K >> 3;
+    const uint4* x4 = reinterpret_cast<const uint4*>(a.x);
+    uint4* xs4 = reinterpret_cast<uint4*>(xs);
+    if (PRO == PRO_PLAIN) {
+        for (int c = threadIdx.x; c < C; c += kGemvThreads) xs4[c] = x4[c];
+        return;
+    }
+    if (PRO == PRO_ATTN_MERGE && a.K <= 2 * 4 * kGemvThreads && a.split_cap <= kMergeMaxSplits) {
+        // Same merge as below with every load issued up front (the cache length, each head's
+        // split statistics and this thread's partial outputs for every split slot; slots
+        // beyond the live split count get weight 0): one memory round trip instead of two.
+        __shared__ float swf[kMergeMaxHeads * kMergeMaxSplits];
+        const int hd = a.head_dim, G = a.group, cap = a.split_cap;
+        const int Hq = a.K / hd;
+        const uint32_t L = min(a.attn_len[0], a.attn_max_len);
+        float2 ml[kMergeMaxSplits];
+        if ((int)threadIdx.x < Hq) {
+            const int h = threadIdx.x;
+#pragma unroll
+            for (int j = 0; j < kMergeMaxSplits; ++j) {
+                const size_t idx = ((size_t)(h / G) * cap + j) * G + (h % G);
+                ml[j] = (j < cap) ? *reinterpret_cast<const float2*>(a.ml_part + idx * 2) : make_float2(0.f, 0.f);
+            }
+        }
+        float4 op[2][kMergeMaxSplits];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int c = threadIdx.x + q * kGemvThreads;
+            if (c < (a.K >> 2)) {
+                const int n0 = c * 4, h = n0 / hd, d0 = n0 % hd;
+                const float* base = a.o_part + ((size_t)(h / G) * cap * G + (h % G)) * hd + d0;
+#pragma unroll
+                for (int j = 0; j < kMergeMaxSplits; ++j)
+                    op[q][j] = (j < cap) ? *reinterpret_cast<const float4*>(base + (size_t)j * G * hd)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+        const int kps = a.keys_per_split;
+        const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
+        if ((int)threadIdx.x < Hq) {
+            const int h = threadIdx.x;
+            float M = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < kMergeMaxSplits; ++j)
+                if (j < nsplit) M = fmaxf(M, ml[j].x);
+            float den = 0.f, w[kMergeMaxSplits];
+#pragma unroll
+            for (int j = 0; j < kMergeMaxSplits; ++j) {
+                if (j < nsplit) {
+                    w[j] = (ml[j].x == -INFINITY) ? 0.f : exp2f(ml[j].x - M);
+                    den = fmaf(w[j], ml[j].y, den);
+                }
+            }
+            const float inv = (den > 0.f) ? 1.f / den : 0.f;
+#pragma unroll
+            for (int j = 0; j < kMergeMaxSplits; ++j)
+                if (j < nsplit) swf[h * nsplit + j] = w[j] * inv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int c = threadIdx.x + q * kGemvThreads;
+            if (c < (a.K >> 2)) {
+                const int h = (c * 4) / hd;
+                float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < kMergeMaxSplits; ++j) {
+                    if (j < nsplit) {
+                        const float wj = swf[h * nsplit + j];
+                        acc[0] = fmaf(wj, op[q][j].x, acc[0]);
+                        acc[1] = fmaf(wj, op[q][j].y, acc[1]);
+                        acc[2] = fmaf(wj, op[q][j].z, acc[2]);
+                        acc[3] = fmaf(wj, op[q][j].w, acc[3]);
+                    }
+                }
+                uint2 pk;
+                pk.x = pack_bf16x2(acc[0], acc[1]);
+                pk.y = pack_bf16x2(acc[2], acc[3]);
+                reinterpret_cast<uint2*>(xs)[c] = pk;
+            }
+        }
+        return;
+    }
+    if (PRO == PRO_ATTN_MERGE) {
+        // x[h*hd + d] = bf16( sum_s w[h][s] * o_part[kvh][s][g][d] ),
+        // w[h][s] = exp2(m_s - M) / sum_s exp2(m_s - M) l_s  (log-sum-exp merge of the splits)
+        __shared__ float sw[kMergeMaxHeads * kMergeMaxSplits];
+        const uint32_t L = min(a.attn_len[0], a.attn_max_len);
+        const int kps = a.keys_per_split;
+        const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
+        const int hd = a.head_dim, G = a.group;
+        const int Hq = a.K / hd;
+        for (int i = threadIdx.x; i < Hq * nsplit; i += kGemvThreads) {
+            const int h = i / nsplit, sidx = i % nsplit;
+            const size_t idx = ((size_t)(h / G) * a.split_cap + sidx) * G + (h % G);
+            sw[i] = a.ml_part[idx * 2];
+        }
+        __syncthreads();
+        if (threadIdx.x < Hq) {
+            const int h = threadIdx.x;
+            float M = -INFINITY;
+            for (int j = 0; j < nsplit; ++j) M = fmaxf(M, sw[h * nsplit + j]);
+            float den = 0.f, w[kMergeMaxSplits];
+            for (int j = 0; j < nsplit; ++j) {
+                const size_t idx = ((size_t)(h / G) * a.split_cap + j) * G + (h % G);
+                const float m = sw[h * nsplit + j];
+                w[j] = (m == -INFINITY) ? 0.f : exp2f(m - M);
+                den = fmaf(w[j], a.ml_part[idx * 2 + 1], den);
+            }
+            const float inv = (den > 0.f) ? 1.f / den : 0.f;
+            for (int j = 0; j < nsplit; ++j) sw[h * nsplit + j] = w[j] * inv;
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < (a.K >> 2); c += kGemvThreads) {
+            const int n0 = c * 4, h = n0 / hd, d0 = n0 % hd;
+            const float* op = a.o_part + ((size_t)(h / G) * a.split_cap * G + (h % G)) * hd + d0;
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < nsplit; ++j) {
+                const float4 v = *reinterpret_cast<const float4*>(op + (size_t)j * G * hd);
+                const float wj = sw[h * nsplit + j];
+                acc[0] = fmaf(wj, v.x, acc[0]);
+                acc[1] = fmaf(wj, v.y, acc[1]);
+                acc[2] = fmaf(wj, v.z, acc[2]);
+                acc[3] = fmaf(wj, v.w, acc[3]);
+            }
+            uint2 pk;
+            pk.x = pack_bf16x2(acc[0], acc[1]);
+            pk.y = pack_bf16x2(acc[2], acc[3]);
+            reinterpret_cast<uint2*>(xs)[c] = pk;
+        }
+        return;
+    }
+    float s[kProMax][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kProMax; ++i) {
+        const int c = threadIdx.x + i * kGemvThreads;
+        if (c < C) {
+            uint4 hv = x4[c];
+            unpack8(hv, s[i]);
+            if (PRO == PRO_ADD_NORM) {
+                float r[8];
+                unpack8(reinterpret_cast<const uint4*>(a.r_in)[c], r);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s[i][e] += r[e];
+            }
+            if (blk == 0 && a.r_out != nullptr) {
+                reinterpret_cast<uint4*>(a.r_out)[c] = (PRO == PRO_ADD_NORM) ? pack8(s[i]) : hv;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(s[i][e], s[i][e], ss);
+        }
+    }
+    const float tot = block_sum<kGemvThreads>(ss, red);
+    const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+    const uint4* w4 = reinterpret_cast<const uint4*>(a.norm_w);
+#pragma unroll
+    for (int i = 0; i < kProMax; ++i) {
+        const int c = threadIdx.x + i * kGemvThreads;
+        if (c < C) {
+            float w[8], o[8];
+            unpack8(w4[c], w);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (s[i][e] * inv) * w[e];
+            xs4[c] = pack8(o);
+        }
+    }
+}
+
+// 64-bit key of a top-1 candidate whose unsigned order is the argmax order: the value's
+// bits mapped to an order-preserving unsigned word (-0 as +0; NaN lowest, so it never
+// wins) in the high half, the inverted index in the low half (equal values -> lowest
+// index wins). 0 is below every key.
+__device__ __forceinline__ unsigned long long top1_key(ArgMax c) {
+    uint32_t bits = __float_as_uint(c.v == 0.f ? 0.f : c.v);
+    if (c.v != c.v) bits = 0u;
+    else bits = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+    return ((unsigned long long)bits << 32) | (unsigned long long)(~(uint32_t)c.i);
+}
+
+// Physical weight row of logical row n, part p (SwiGLU: p=0 up row n, p=1 gate row N+n).
+template <int EPI>
+__device__ __forceinline__ int phys_row(int n, int p, int N) {
+    return (EPI == EPI_SWIGLU && p == 1) ? (N + n) : n;
+}
+
+// Body of the GEMV kernel for workgroup `blk` of `nblk` (grid-stride over row blocks),
+// shared by gemv_kernel and the fused QKV + attention kernel.
+template <int R, int KS, int PRO, int EPI>
+__device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, int blk, int nblk) {
+    constexpr int P = (EPI == EPI_SWIGLU) ? 2 : 1;
+    constexpr int G = 4 / KS;          // row groups per block
+    constexpr int RB = G * R;          // logical rows per block
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    bf16_t* xs = reinterpret_cast<bf16_t*>(smem_raw);
+    __shared__ float red[kGemvThreads / kWave];
+    __shared__ float part[G][KS][R * P];
+    __shared__ ArgMax amx[G];
+
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int grp = wave / KS;
+    const int kw = wave % KS;
+    const int C = a.K >> 3;
+    const int segC = nj * kWave * KS;
+    const int nrb = (a.N + RB - 1) / RB;
+
+    ArgMax best;
+    best.v = -INFINITY;
+    best.i = 0x7fffffff;
+
+    uint4 wr[R][P][kNJMax];
+    auto issue = [&](int rb, int seg) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = rb * RB + grp * R + r;
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const bf16_t* row = a.W + (size_t)phys_row<EPI>(n, p, a.N) * (size_t)a.K;
+#pragma unroll
+                for (int j = 0; j < kNJMax; ++j) {
+                    const int c = seg * segC + kw * kWave + lane + j * kWave * KS;
+                    if (j < nj && n < a.N && c < C) {
+                        wr[r][p][j] = EFM_WEIGHT_LOAD(row + (size_t)c * 8);
+                    } else {
+                        wr[r][p][j] = make_uint4(0u, 0u, 0u, 0u);
+                    }
+                }
+            }
+        }
+    };
+
+    const uint32_t tag = (EPI == EPI_QKV_TAG) ? launch_tag(a.epoch) : 0u;
+    int rb = blk;
+    if (rb < nrb) issue(rb, 0);
+    gemv_prologue<PRO>(a, xs, red, blk);
+    __syncthreads();
+    const uint4* xs4 = reinterpret_cast<const uint4*>(xs);
+
+    while (rb < nrb) {
+        float acc[R][P];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int p = 0; p < P; ++p) acc[r][p] = 0.f;
+
+        for (int seg = 0; seg < nseg; ++seg) {
+            if (seg > 0) issue(rb, seg);
+#pragma unroll
+            for (int j = 0; j < kNJMax; ++j) {
+                const int c = seg * segC + kw * kWave + lane + j * kWave * KS;
+                if (j < nj && c < C) {
+                    const uint4 xv = xs4[c];
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int p = 0; p < P; ++p) acc[r][p] = dot8(wr[r][p][j], xv, acc[r][p]);
+                }
+            }
+        }
+        const int next = rb + nblk;
+        if (next < nrb) issue(next, 0);
+
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int p = 0; p < P; ++p) acc[r][p] = wave_sum(acc[r][p]);
+        if (KS > 1) {
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int p = 0; p < P; ++p) part[grp][kw][r * P + p] = acc[r][p];
+            }
+            __syncthreads();
+            if (kw == 0 && lane == 0) {
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int p = 0; p < P; ++p) {
+                        float t = 0.f;
+#pragma unroll
+                        for (int k = 0; k < KS; ++k) t += part[grp][k][r * P + p];
+                        acc[r][p] = t;
+                    }
+            }
+            __syncthreads();
+        }
+
+        if (kw == 0 && lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int n = rb * RB + grp * R + r;
+                if (n >= a.N) continue;
+                float v = acc[r][0];
+                if (a.bias != nullptr) v += bf16_to_f32(a.bias[n]);
+                if (EPI == EPI_BF16) {
+                    reinterpret_cast<bf16_t*>(a.y)[n] = (bf16_t)f32_to_bf16(v);
+                } else if (EPI == EPI_F32) {
+                    reinterpret_cast<float*>(a.y)[n] = v;
+                } else if (EPI == EPI_QKV || EPI == EPI_QKV_TAG) {
+                    // QKV_TAG: q and the K / V row go to the attention workgroups as tagged
+                    // words (K / V only when there is a slot); the K row reaches the cache
+                    // from the attention split that rotates it, the V row is stored here
+                    const bf16_t bv = (bf16_t)f32_to_bf16(v);
+                    if (n < a.q_dim) {
+                        if (EPI == EPI_QKV) reinterpret_cast<bf16_t*>(a.y)[n] = bv;
+                        else tagged_publish(a.tag_words + n, tag, (uint32_t)bv);
+                    } else {
+                        const uint32_t L = a.d_kv_len[0];
+                        if (L > 0) {
+                            const size_t slot = (size_t)(L - 1) * (size_t)a.kv_dim;
+                            const int m = n - a.q_dim;
+                            if (EPI == EPI_QKV_TAG) tagged_publish(a.tag_words + n, tag, (uint32_t)bv);
+                            if (m < a.kv_dim) {
+                                if (EPI == EPI_QKV) a.k_cache[slot + m] = bv;
+                            } else {
+                                a.v_cache[slot + (m - a.kv_dim)] = bv;
+                            }
+                        }
+                    }
+                } else if (EPI == EPI_SWIGLU) {
+                    const float u = round_bf16(acc[r][0]);
+                    const float g = round_bf16(acc[r][P - 1]);
+                    const float sg = g / (1.0f + expf(-g));
+                    reinterpret_cast<bf16_t*>(a.y)[n] = (bf16_t)f32_to_bf16(sg * u);
+                } else if (EPI == EPI_TOP1) {
+                    ArgMax c;
+                    c.v = v;
+                    c.i = n;
+                    best = argmax_pick(best, c);
+                }
+            }
+        }
+        rb = next;
+    }
+
+    if (EPI == EPI_TOP1) {
+        if (kw == 0 && lane == 0) amx[grp] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            ArgMax b = amx[0];
+#pragma unroll
+            for (int g = 1; g < G; ++g) b = argmax_pick(b, amx[g]);
+            // Grid reduction without fences: every workgroup max-combines one 64-bit key
+            // (top1_key) at the point where the atomics of every XCD meet, waits for that
+            // atomic to return, then counts itself in; the last to arrive reads the winner
+            // and clears both words for the next launch.
+            unsigned long long* best_key = reinterpret_cast<unsigned long long*>(a.partials);
+            const unsigned long long old =
+                __hip_atomic_fetch_max(best_key, top1_key(b), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" : : "v"(old) : "memory");
+            const uint32_t prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (prev == (uint32_t)nblk - 1u) {
+                const unsigned long long k = __hip_atomic_load(best_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                a.token_out[0] = (int32_t)~(uint32_t)k;
+                __hip_atomic_store(best_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+}
+
+// Host: launch geometry of a GEMV over K inputs and N logical rows of P physical rows
+// (R rows per wave group, KS-way K split, nj chunks per lane per segment, nseg segments,
+// grid workgroups over nrb row blocks).
+struct GemvCfg {
+    int R, KS, nj, nseg, grid, nrb;
+};
+GemvCfg gemv_pick_config(int K, int N, int P, int max_grid, bool tall);
+
+}  // namespace efm

@@ -286,14 +286,17 @@ __global__ void __launch_bounds__(kSampleThreads) sample_locate_kernel(SampleArg
     }
     own = block_sum_u64(own, redu);
     if (threadIdx.x == 0) {
-        __hip_atomic_store(&a.ws->bmass[blockIdx.x], own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t prev =
-            __hip_atomic_fetch_add(&a.ws->counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        // publish the block mass, wait for that atomic to return (it is then performed
+        // where every XCD's atomics meet), then count in: no cache flush needed, and the
+        // last block reads every mass with agent-scope atomic loads
+        const uint64_t old =
+            __hip_atomic_exchange(&a.ws->bmass[blockIdx.x], own, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" : : "v"(old) : "memory");
+        const uint32_t prev = __hip_atomic_fetch_add(&a.ws->counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = (prev == (uint32_t)a.nblocks - 1) ? 1u : 0u;
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
 
     // last block: N, r, the block that holds r (blocks in index order) ...
     const int per = (a.nblocks + kSampleThreads - 1) / kSampleThreads;   // <= 4

@@ -133,6 +133,12 @@ SIGNATURES = {
     "efm_increment_int32_triplet": (c_int32, [c_void_p, c_void_p]),
     "efm_decode_norm_qkv": (c_int32, [c_int32, c_int32, c_int32, c_float, c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "efm_decode_qkv_attention_sync_bytes": (c_size_t, [c_int32, c_int32]),
+    "efm_decode_norm_qkv_attention_supported": (c_int32, [POINTER(AttentionCtx), c_int32, c_uint32]),
+    "efm_decode_norm_qkv_attention": (c_int32, [POINTER(AttentionCtx), c_int32, c_float, c_void_p, c_void_p, c_void_p,
+                                                c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
+                                                c_void_p, c_size_t, c_void_p, c_size_t, c_void_p]),
+    "efm_decode_qkv_attention_status": (c_int32, [c_void_p, c_void_p]),
     "efm_decode_norm_gate_up_swiglu": (c_int32, [c_int32, c_int32, c_float, c_void_p, c_void_p, c_void_p, c_void_p,
                                                  c_void_p, c_void_p, c_void_p]),
     "efm_decode_norm_lm_head_top1": (c_int32, [c_int32, c_int64, c_float, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -183,6 +183,11 @@ bool EngineConfig::use_graph() const {
 bool EngineConfig::lm_head_top1() const {
     return json_.contains("runtime") ? json_.at("runtime").get_bool("lm_head_top1", true) : true;
 }
+bool EngineConfig::decode_fused_qkv_attention() const {
+    const char* env = std::getenv("EDGE_FM_DECODE_FUSED_QKV_ATTENTION");
+    if (env != nullptr && env[0] != '\0') return std::string(env) != "0";
+    return json_.contains("runtime") ? json_.at("runtime").get_bool("decode_fused_qkv_attention", true) : true;
+}
 bool EngineConfig::decode_chain() const {
     const char* env = std::getenv("EDGE_FM_DECODE_CHAIN");
     if (env != nullptr && env[0] != '\0') return std::string(env) != "0";
@@ -373,6 +378,7 @@ Qwen2_5::Qwen2_5(const EngineConfig& cfg, const ModelConfig& m, const std::unord
     model_name_ = cfg.model_name();
     hw_profile_ = cfg.hw_profile();
     chain_enabled_ = cfg.decode_chain() && !m.mrope;
+    fused_front_enabled_ = cfg.decode_fused_qkv_attention() && !m.mrope;
     table_path_ = cfg.operator_table_path();
     hip_check(hipSetDevice(device_id), "hipSetDevice");
     check<ConfigurationError>(m.hidden % 8 == 0 && m.inter % 8 == 0 && m.q_dim() % 8 == 0,
@@ -463,6 +469,18 @@ void Qwen2_5::reserve_decode(uint32_t max_kv_len) {
         const size_t cb = efm_decode_chain_workspace_bytes(m_.hidden, m_.inter);
         chain_ws_ = Tensor::zeros({(int64_t)cb}, DType::UInt8, Device::GPU, device_id_);
     }
+    if (uses_fused_front(max_kv_len) && front_sync_ws_.empty()) {
+        const size_t sb = efm_decode_qkv_attention_sync_bytes(m_.q_dim(), m_.kv_dim());
+        front_sync_ws_ = Tensor::zeros({(int64_t)sb}, DType::UInt8, Device::GPU, device_id_);
+    }
+}
+
+// Fused norm + QKV + attention partials (one launch per layer instead of two) for text
+// models whose cache needs at most 8 splits (the merge folds into the o_proj prologue).
+bool Qwen2_5::uses_fused_front(uint32_t max_kv_len) const {
+    if (!fused_front_enabled_ || max_kv_len > 1024 || m_.heads > 64) return false;
+    const efm_attention_ctx c = decode_ctx();
+    return efm_decode_norm_qkv_attention_supported(&c, m_.hidden, max_kv_len) == EFM_OK;
 }
 
 bool Qwen2_5::uses_decode_chain(uint32_t max_kv_len) const {
@@ -472,6 +490,8 @@ bool Qwen2_5::uses_decode_chain(uint32_t max_kv_len) const {
 }
 
 void Qwen2_5::check_decode_status(hipStream_t stream) {
+    if (!front_sync_ws_.empty())
+        efm_check(efm_decode_qkv_attention_status(front_sync_ws_.data_ptr(), stream), "decode qkv + attention");
     if (chain_ws_.empty()) return;
     efm_check(efm_decode_chain_status(chain_ws_.data_ptr(), m_.hidden, m_.inter, stream), "decode chain");
 }
@@ -690,8 +710,31 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
     // The merge folds into the o_proj prologue when the cache needs at most 8 splits of
     // 128 keys (max_kv_len <= 1024) and the model has at most 64 query heads.
     fused_attn_merge_ = max_kv_len <= 1024 && m_.heads <= 64;
+    const bool front = !front_sync_ws_.empty() && uses_fused_front(max_kv_len);
     for (int l = 0; l < m_.layers; ++l) {
         const Layer& Ly = layers_[l];
+        if (front) {
+            // input norm (+ residual) + QKV + attention split partials in one launch; the
+            // partials merge in the o_proj prologue
+            efm_check(efm_decode_norm_qkv_attention(
+                          &c, H, m_.eps, dec_h_.data_ptr(), (l == 0) ? nullptr : dec_res_[1].data_ptr(),
+                          dec_res_[0].data_ptr(), Ly.in_norm.data_ptr(), Ly.qkv_w.data_ptr(), Ly.qkv_b.data_ptr(),
+                          k_caches[l], v_caches[l], d_kv_len, max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(),
+                          front_sync_ws_.data_ptr(), front_sync_ws_.nbytes(), stream),
+                      "decode norm+qkv+attention");
+            efm_check(efm_decode_attention_merge_o_proj(&c, d_kv_len, max_kv_len, attn_ws_.data_ptr(),
+                                                        attn_ws_.nbytes(), Ly.o_w.data_ptr(), H, dec_a_.data_ptr(),
+                                                        stream),
+                      "decode attention merge + o_proj");
+            efm_check(efm_decode_norm_gate_up_swiglu(H, m_.inter, m_.eps, dec_a_.data_ptr(), dec_res_[0].data_ptr(),
+                                                     dec_res_[1].data_ptr(), Ly.post_norm.data_ptr(),
+                                                     Ly.gu_w.data_ptr(), dec_mid_.data_ptr(), stream),
+                      "decode norm+gate_up+swiglu");
+            efm_check(efm_linear(1, m_.inter, H, dec_mid_.data_ptr(), Ly.down_w.data_ptr(), nullptr,
+                                 dec_h_.data_ptr(), EFM_DTYPE_BF16, stream),
+                      "decode down_proj");
+            continue;
+        }
         // input norm (+ residual) + QKV + bias, K/V straight into the cache slot
         void* kdst = k_caches[l];
         void* vdst = v_caches[l];
@@ -1033,6 +1076,9 @@ Response StandardEngine::generate(const Request& request) {
     metrics_["tokens_per_second"] = (prefill_ms + decode_ms) > 0 ? n_gen * 1000.0 / (prefill_ms + decode_ms) : 0.0;
     metrics_["use_hip_graph"] = cfg_.use_graph() ? 1.0 : 0.0;
     metrics_["decode_chain"] = model_->uses_decode_chain((uint32_t)slot.cfg.max_tokens) ? 1.0 : 0.0;
+    metrics_["decode_fused_qkv_attention"] =
+        (!model_->uses_decode_chain((uint32_t)slot.cfg.max_tokens) &&
+         model_->uses_fused_front((uint32_t)slot.cfg.max_tokens)) ? 1.0 : 0.0;
     Response r;
     r.token_ids = compact_vocab_.restore_token_ids(host, "response token_ids");
     return r;

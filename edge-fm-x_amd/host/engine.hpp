@@ -73,6 +73,10 @@ public:
     // MI355X its cross-workgroup exchanges cost more than the kernel boundaries they
     // remove; EDGE_FM_DECODE_CHAIN=1 / 0 overrides the config).
     bool decode_chain() const;
+    // One launch for the input norm + QKV + attention partials of each decode layer
+    // (runtime.decode_fused_qkv_attention, default on; EDGE_FM_DECODE_FUSED_QKV_ATTENTION
+    // = 1 / 0 overrides the config).
+    bool decode_fused_qkv_attention() const;
     std::string operator_table_path() const;
     std::string prefill_model_path() const;
     std::vector<KVSlotConfig> kv_slots() const;
@@ -162,8 +166,11 @@ public:
     // Whether decode steps with caches of max_kv_len rows run the persistent
     // post-attention chain (efm_decode_layer_chain) instead of the per-operator kernels.
     bool uses_decode_chain(uint32_t max_kv_len) const;
-    // Throws DeviceError if a chain launch since the last check could not exchange its
-    // vectors in time (synchronises the stream).
+    // Whether decode steps run efm_decode_norm_qkv_attention (input norm + QKV +
+    // attention partials in one launch per layer).
+    bool uses_fused_front(uint32_t max_kv_len) const;
+    // Throws DeviceError if a chain or fused QKV + attention launch since the last check
+    // could not exchange its vectors in time (synchronises the stream).
     void check_decode_status(hipStream_t stream);
 
 private:
@@ -187,6 +194,8 @@ private:
     bool fused_attn_merge_ = false;
     bool chain_enabled_ = false;   // config switch (text models only)
     Tensor chain_ws_;
+    bool fused_front_enabled_ = false;
+    Tensor front_sync_ws_;
     // prefill scratch (grow-only)
     int32_t pf_cap_ = 0;
     Tensor pf_hidden_, pf_res_, pf_norm_, pf_qkv_, pf_attn_, pf_mid_;

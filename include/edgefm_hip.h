@@ -208,7 +208,10 @@ int efm_fused_gate_up_swiglu(int64_t m, int64_t hidden, int64_t inter, const voi
 
 /* ------------------------------------------------------------------------------------
  * LM head with fused greedy top-1 (src/layers/linear.cu:140-276, 2288-2369):
- * token_out[0] = argmax_v (x . W[v,:]) with ties to the lowest id.
+ * token_out[0] = argmax_v (x . W[v,:]) with ties to the lowest id (a NaN score never
+ * wins). workspace: efm_lm_head_top1_workspace_bytes(vocab) bytes, zero-filled before its
+ * first use; every launch leaves it zeroed again, so it is reused as is (launches that
+ * share it must be stream-ordered).
  * ---------------------------------------------------------------------------------- */
 size_t efm_lm_head_top1_workspace_bytes(int64_t vocab);
 int efm_lm_head_top1(int64_t hidden, int64_t vocab, const void* x, const void* w, int32_t* token_out,
@@ -338,6 +341,33 @@ int efm_decode_norm_qkv(int32_t hidden, int32_t q_dim, int32_t kv_dim, float eps
                         const void* residual_in, void* residual_out, const void* norm_w,
                         const void* w_qkv, const void* b_qkv, void* q_out, void* k_cache,
                         void* v_cache, const uint32_t* d_kv_len, hipStream_t stream);
+
+/* Fused front half of a decode layer: efm_decode_norm_qkv followed by
+ * efm_decode_attention_partials, in one launch, with bit-identical results. Replaces the
+ * input_layernorm -> fused_qkv -> AttentionLayer::forward_decode sequence of
+ * qwen2_5.cpp:600-790 (RMSNormLayer, FusedQKVLinearLayer::forward_fp16_bf16
+ * linear.cu:1387-1461, FlashInferAttentionOp::forward_decode attention_op.cu:1565-1604)
+ * for the engine's rotated cache: ctx needs head_dim 128, RoPE and
+ * k_already_prerotated = EFM_K_PREROTATED_EXCEPT_NEWEST. The query never reaches memory:
+ * the projection hands it (and the newest K / V row) to the attention splits of the same
+ * launch, which write their (o, m, l) partials into attn_workspace for
+ * efm_decode_attention_merge_o_proj. Cache slot *d_kv_len - 1 receives V and the rotated
+ * K; *d_kv_len >= 1. sync_workspace: efm_decode_qkv_attention_sync_bytes(q_dim, kv_dim)
+ * bytes, zero-filled once and then reused by every launch (launches sharing it must be
+ * stream-ordered). A split that does not receive its inputs in time flags the workspace:
+ * efm_decode_qkv_attention_status reports and clears the flag (it synchronises the
+ * stream). efm_decode_norm_qkv_attention_supported tells whether a shape qualifies
+ * (hidden <= 4096, at most 128 attention splits of 128 keys, contiguous cache rows);
+ * otherwise call the two unfused entry points. */
+size_t efm_decode_qkv_attention_sync_bytes(int32_t q_dim, int32_t kv_dim);
+int efm_decode_norm_qkv_attention_supported(const efm_attention_ctx* ctx, int32_t hidden, uint32_t max_kv_len);
+int efm_decode_norm_qkv_attention(const efm_attention_ctx* ctx, int32_t hidden, float eps, const void* h,
+                                  const void* residual_in, void* residual_out, const void* norm_w,
+                                  const void* w_qkv, const void* b_qkv, void* k_cache, void* v_cache,
+                                  const uint32_t* d_kv_len, uint32_t max_kv_len, void* attn_workspace,
+                                  size_t attn_workspace_bytes, void* sync_workspace, size_t sync_workspace_bytes,
+                                  hipStream_t stream);
+int efm_decode_qkv_attention_status(void* sync_workspace, hipStream_t stream);
 
 /* Post-attention fused add-norm + gate/up projection + SwiGLU (qwen2_5.cpp:849-875):
  * s = a + residual_in; residual_out <- bf16(s); x = bf16(s * rsqrt(...) * norm_w);

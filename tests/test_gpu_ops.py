@@ -383,6 +383,30 @@ def test_lm_head_top1_ties_pick_lowest_index(gpu):
     assert int(tok.item()) == 1234
 
 
+def test_lm_head_top1_negative_scores_edges_and_clean_workspace(gpu):
+    """All scores negative (the order-preserving key must rank negative values by
+    magnitude), winner in the last row, then tied with row 0 (row 0 wins); every launch
+    leaves the workspace zeroed for the next."""
+    torch.manual_seed(6)
+    hidden, vocab = 1536, 151936
+    x = torch.rand(1, hidden).add(0.5).to(torch.bfloat16)
+    w = -(torch.rand(vocab, hidden) * 0.02 + 0.01)
+    w[vocab - 1] *= 0.25
+    w = w.to(torch.bfloat16)
+    ws = torch.zeros(C.load().efm_lm_head_top1_workspace_bytes(vocab), dtype=torch.uint8, device=gpu)
+    tok = torch.full((1,), -1, dtype=torch.int32, device=gpu)
+    xg, wg = x.to(gpu), w.to(gpu)
+    ref = O.linear(x, w, out_f32=True)[0]
+    assert float(ref.max()) < 0
+    for expect in (vocab - 1, 0):
+        if expect == 0:
+            wg[0] = wg[vocab - 1]
+        C.call("efm_lm_head_top1", hidden, vocab, ptr(xg), ptr(wg), ptr(tok), ptr(ws), ws.numel(), stream())
+        torch.cuda.synchronize()
+        assert int(tok.item()) == expect
+        assert int(ws.count_nonzero()) == 0
+
+
 def test_sampler_greedy_ties(gpu):
     torch.manual_seed(0)
     rows, vocab = 4, 151936
