@@ -120,10 +120,12 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
     constexpr int TILE = RK * attn_pipe::kRow;                 // bytes of K (or V) per round
     constexpr int LPW = 2 * TILE / 1024 / kAttnWaves;          // 1 KB wave loads per wave per round
     static_assert(G <= 32, "group too large");
-    static_assert(kAttnWaves * G * HD * 4 + 2 * kAttnWaves * 32 * 4 <= 2 * TILE, "merge buffers must fit the tiles");
+    static_assert((kAttnWaves * G * HD + 2 * kAttnWaves * 32 + kAttnWaves * G + 2 * G) * 4 <= 2 * TILE,
+                  "merge buffers must fit the tiles");
     __shared__ __align__(1024) unsigned char smem[2 * TILE];   // K | V of one round; then the wave merge
     __shared__ float2 cs_qk[2][HALF];
-    __shared__ __align__(16) bf16_t qs[FUSED ? G * HD : 8];   // FUSED: the group's queries
+    __shared__ __align__(16) bf16_t qs[G * HD];   // the group's queries as read
+    __shared__ __align__(16) bf16_t qr[G * HD];   // rotated and scaled: the MFMA operand
 
     const int tid = threadIdx.x;
     const int wave = tid / kWave, lane = tid % kWave;
@@ -137,13 +139,10 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
     // ---- 1. loads that do not depend on L: the query, the first round of K / V (rows
     //         below the allocation bound), the RoPE frequencies
     const uint32_t tag = FUSED ? launch_tag(f.sync) : 0u;
-    uint4 qraw[KS];
-    if (!FUSED) {
-        const bool qv = ql < G;
-        const bf16_t* qp = a.q + (size_t)(kvh * G + (qv ? ql : 0)) * a.q_sh + hh * 8;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qraw[ks] = qv ? *reinterpret_cast<const uint4*>(qp + ks * 16) : make_uint4(0, 0, 0, 0);
-    }
+    // the group's G x 128 queries, 16 bytes per thread (staged in LDS below)
+    uint4 qld = make_uint4(0, 0, 0, 0);
+    if (!FUSED && tid < G * (HD / 8))
+        qld = *reinterpret_cast<const uint4*>(a.q + (size_t)(kvh * G + tid / (HD / 8)) * a.q_sh + (tid % (HD / 8)) * 8);
     const int lim = min(a.row_bound, start + kps) - 1;   // last row this split may read
     auto issue = [&](int r) {
         const int k0 = start + r * RK;
@@ -182,6 +181,7 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
         sincos_reduced((float)pos * freq, &sn, &cs);
         cs_qk[tid / HALF][tid % HALF] = make_float2(cs, sn);
     }
+    if (!FUSED && tid < G * (HD / 8)) *reinterpret_cast<uint4*>(&qs[tid * 8]) = qld;
     __syncthreads();
     // FUSED: wait for this step's query words (and, in the split that owns row L - 1,
     // the newest K / V row: thread t < 128 takes K[t], t >= 128 takes V[t - 128])
@@ -204,35 +204,36 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
             if (tid + k * kAttnThreads < G * HD) qs[tid + k * kAttnThreads] = (bf16_t)(w[k] & 0xffffu);
         newest = w[NQW] & 0xffffu;
         __syncthreads();
-        if (tid == 0) fused_attn_done(f);   // every word this workgroup needs has arrived
-        const bool qv = ql < G;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-            qraw[ks] = qv ? *reinterpret_cast<const uint4*>(&qs[ql * HD + ks * 16 + hh * 8]) : make_uint4(0, 0, 0, 0);
     }
-    bf16x8_t qf[KS];
+    // rotate (pairs d, d + 64 at the query position) and scale by log2(e) / sqrt(hd), one
+    // element per thread and step (independent LDS reads, no serial chain), then every
+    // lane reads its MFMA operand fragments
     {
-        float x[KS][8];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) unpack8(qraw[ks], x[ks]);
-        if (a.rope_q) {
-#pragma unroll
-            for (int ks = 0; ks < KS / 2; ++ks)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float2 c2 = cs_qk[0][ks * 16 + hh * 8 + e];
-                    const float x0 = x[ks][e], x1 = x[ks + KS / 2][e];
-                    x[ks][e] = x0 * c2.x - x1 * c2.y;
-                    x[ks + KS / 2][e] = x1 * c2.x + x0 * c2.y;
-                }
-        }
         const float qscale = kLog2e / sqrtf((float)HD);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
+        for (int k = 0; k < (G * HD + kAttnThreads - 1) / kAttnThreads; ++k) {
+            const int i = tid + k * kAttnThreads;
+            if (i < G * HD) {
+                const int d = i % HD;
+                const float x = bf16_to_f32(qs[i]);
+                float r = x;
+                if (a.rope_q) {
+                    const float y = bf16_to_f32(qs[i ^ HALF]);   // the pair partner d +- 64
+                    const float2 c2 = cs_qk[0][d % HALF];
+                    r = (d < HALF) ? x * c2.x - y * c2.y : x * c2.x + y * c2.y;
+                }
+                qr[i] = (bf16_t)f32_to_bf16(r * qscale);
+            }
+        }
+    }
+    __syncthreads();
+    bf16x8_t qf[KS];
+    {
+        const bool qv = ql < G;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[ks][e] *= qscale;
+        for (int ks = 0; ks < KS; ++ks) {
             BfPack pk;
-            pk.u = pack8(x[ks]);
+            pk.u = qv ? *reinterpret_cast<const uint4*>(&qr[ql * HD + ks * 16 + hh * 8]) : make_uint4(0, 0, 0, 0);
             qf[ks] = pk.v;
         }
     }
@@ -386,11 +387,15 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
             }
     }
 
-    // ---- merge the 4 waves through LDS (the tile buffers are free now)
+    // ---- merge the 4 waves through LDS (the tile buffers are free now): per head the
+    //      running max M, the wave weights sc_w = exp2(m_w - M) and den = sum sc_w l_w are
+    //      computed once, then every output is the fixed-order sum of sc_w o_w
     __syncthreads();
     float* om = reinterpret_cast<float*>(smem);                  // [4][32]
     float* ol = om + kAttnWaves * 32;                            // [4][32]
     float* ob = ol + kAttnWaves * 32;                            // [4][G][HD]
+    float* sw = ob + kAttnWaves * G * HD;                        // [4][G]
+    float* md = sw + kAttnWaves * G;                             // [G][2]: M, den
     if (hh == 0) {
         om[wave * 32 + ql] = m_run;
         ol[wave * 32 + ql] = l_run;
@@ -399,35 +404,50 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
 #pragma unroll
         for (int tt = 0; tt < DT; ++tt)
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                ob[(wave * G + ql) * HD + tt * 32 + (e / 4) * 8 + hh * 4 + (e % 4)] = oacc[tt][e];
+            for (int eb = 0; eb < 4; ++eb)
+                *reinterpret_cast<float4*>(&ob[(wave * G + ql) * HD + tt * 32 + eb * 8 + hh * 4]) =
+                    make_float4(oacc[tt][eb * 4 + 0], oacc[tt][eb * 4 + 1], oacc[tt][eb * 4 + 2], oacc[tt][eb * 4 + 3]);
     }
     __syncthreads();
-    float* o_part = a.o_part + ((size_t)kvh * a.split_cap + b) * G * HD;
-    float* ml_part = a.ml_part + ((size_t)kvh * a.split_cap + b) * G * 2;
-    for (int i = tid; i < G * HD; i += kAttnThreads) {
-        const int g = i / HD, d = i % HD;
+    if (tid < G) {
+        const int g = tid;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, om[w * 32 + g]);
-        float num = 0.f, den = 0.f;
+        float den = 0.f;
 #pragma unroll
         for (int w = 0; w < kAttnWaves; ++w) {
             const float mw = om[w * 32 + g];
             const float sc = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-            num = fmaf(sc, ob[(w * G + g) * HD + d], num);
+            sw[w * G + g] = sc;
             den = fmaf(sc, ol[w * 32 + g], den);
         }
+        md[g * 2 + 0] = M;
+        md[g * 2 + 1] = den;
+    }
+    __syncthreads();
+    float* o_part = a.o_part + ((size_t)kvh * a.split_cap + b) * G * HD;
+    float* ml_part = a.ml_part + ((size_t)kvh * a.split_cap + b) * G * 2;
+    constexpr int NO = (G * HD + kAttnThreads - 1) / kAttnThreads;
+#pragma unroll
+    for (int k = 0; k < NO; ++k) {
+        const int i = tid + k * kAttnThreads;
+        if (i >= G * HD) break;
+        const int g = i / HD, d = i % HD;
+        float num = 0.f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) num = fmaf(sw[w * G + g], ob[(w * G + g) * HD + d], num);
         if (MERGE) {
+            const float den = md[g * 2 + 1];
             a.o[(size_t)(kvh * G + g) * HD + d] = (bf16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
         } else {
             o_part[i] = num;
-            if (d == 0) {
-                ml_part[g * 2 + 0] = M;
-                ml_part[g * 2 + 1] = den;
-            }
+            if (d == 0) *reinterpret_cast<float2*>(&ml_part[g * 2]) = make_float2(md[g * 2 + 0], md[g * 2 + 1]);
         }
     }
+    // FUSED: counted in only now (the returning atomic stays off the critical path); every
+    // word this workgroup needed arrived long before
+    if (FUSED && tid == 0) fused_attn_done(f);
 }
 
 }  // namespace efm

@@ -588,14 +588,21 @@ static int gemm_dispatch(int M, int N, int K, const bf16_t* A, const bf16_t* B, 
     const char* big_env = getenv("EFM_GEMM_BIG");
     const bool big_ok = big_env == nullptr || big_env[0] != '0';
     if (K % kPBK == 0) {
-        if (big_ok && tiles(256, 256) >= 256) {
+        // Tile choice from a sweep of the prefill shapes on MI355X: the 256 x 256 tile
+        // once there are >= 3 tiles per CU; else 128 x 128 double-buffered (two workgroups
+        // per CU), which needs >= 1.5 tiles per CU (>= 1 for SwiGLU); else 128 x 64
+        // double-buffered; else 64 x 64 (or 64 x 128 for SwiGLU) with shallow pipelines.
+        // Every tile shape sums each output over K in the same order: results are
+        // bit-identical whichever is chosen.
+        if (big_ok && tiles(256, 256) >= 768) {
             gemm_big_launch<EPI>(M, N, K, A, B, bias, C, ldc, stream);
-        } else if (tiles(128, 128) >= 256) {
-            gemm_pipe_launch<128, 128, 4, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+        } else if (tiles(128, 128) >= ((EPI == GEPI_SWIGLU) ? 256 : 384)) {
+            gemm_pipe_launch<128, 128, 2, EPI>(M, N, K, A, B, bias, C, ldc, stream);
         } else if constexpr (EPI == GEPI_SWIGLU) {
-            gemm_pipe_launch<64, 128, 5, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+            gemm_pipe_launch<64, 128, 3, EPI>(M, N, K, A, B, bias, C, ldc, stream);
         } else {
-            gemm_pipe_launch<64, 64, 8, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+            if (tiles(128, 64) >= 256) gemm_pipe_launch<128, 64, 2, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+            else gemm_pipe_launch<64, 64, 4, EPI>(M, N, K, A, B, bias, C, ldc, stream);
         }
         return check_launch("gemm_bf16");
     }

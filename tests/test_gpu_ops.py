@@ -289,13 +289,13 @@ def test_linear_fp32_logits(gpu, m):
 
 
 @pytest.mark.parametrize("m,k,n,bias,kind", [
-    pytest.param(1300, 1024, 12345, True, "bf16", id="ragged_bias"),
-    pytest.param(2048, 1536, 8192, False, "bf16", id="1p5b_like"),
-    pytest.param(1344, 2048, 11008, False, "swiglu", id="vl3b_gate_up"),
+    pytest.param(4100, 1024, 12345, True, "bf16", id="ragged_bias"),
+    pytest.param(6144, 1536, 8192, False, "bf16", id="1p5b_like"),
+    pytest.param(4096, 2048, 11008, False, "swiglu", id="vl3b_gate_up"),
     pytest.param(300, 1536, 151936, False, "f32", id="logits_f32"),
 ])
 def test_gemm_large_tile_matches_128_tile_bit_exact(gpu, monkeypatch, m, k, n, bias, kind):
-    """Shapes with >= 256 output tiles of 256 x 256 run the large-tile GEMM. Both kernels
+    """Shapes with >= 768 output tiles of 256 x 256 run the large-tile GEMM. Both kernels
     accumulate the same 16-wide MFMA k-steps in the same order, so the outputs must be
     identical to the 128 x 128 kernel's (EFM_GEMM_BIG=0); a row sample is also checked
     against the oracle."""
@@ -405,6 +405,37 @@ def test_lm_head_top1_negative_scores_edges_and_clean_workspace(gpu):
         torch.cuda.synchronize()
         assert int(tok.item()) == expect
         assert int(ws.count_nonzero()) == 0
+
+
+@pytest.mark.parametrize("kind", ["bf16", "swiglu"])
+def test_gemm_tile_shapes_agree_bit_exact(gpu, kind):
+    """The tile shape follows M: 100 rows run 64 x 64 (SwiGLU 64 x 128), 300 rows
+    128 x 64, 1344 rows 128 x 128 and 6144 rows the 256 x 256 tile. Every kernel sums
+    each output over K in the same order, so the first 100 rows must agree bit for bit
+    across all four launches (and with the oracle on a sample)."""
+    torch.manual_seed(17)
+    k, n = 1024, 8192
+    x = torch.randn(6144, k, dtype=torch.bfloat16, device=gpu)
+    nw = 2 * n if kind == "swiglu" else n
+    w = (torch.randn(nw, k, device=gpu) * 0.05).to(torch.bfloat16)
+    b = (torch.randn(n, device=gpu) * 0.05).to(torch.bfloat16) if kind == "bf16" else None
+    heads = []
+    for m in (100, 300, 1344, 6144):
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+        if kind == "swiglu":
+            C.call("efm_fused_gate_up_swiglu", m, k, n, ptr(x), ptr(w), ptr(y), stream())
+        else:
+            C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), C.EFM_DTYPE_BF16, stream())
+        torch.cuda.synchronize()
+        heads.append(y[:100].clone())
+    for m, h in zip((300, 1344, 6144), heads[1:]):
+        assert torch.equal(h, heads[0]), f"{kind}: rows of the M={m} launch differ from the M=100 launch"
+    rows = torch.tensor([0, 57, 99])
+    xs = x[rows].cpu()
+    if kind == "swiglu":
+        assert_close_bf16(heads[0][rows], O.gate_up_swiglu(xs, w.cpu()), rtol=2e-2, atol=6.25e-2)
+    else:
+        assert_close_bf16(heads[0][rows], O.linear(xs, w.cpu(), b.cpu()))
 
 
 def test_sampler_greedy_ties(gpu):
