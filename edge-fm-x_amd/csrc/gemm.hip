@@ -3,11 +3,13 @@
 // row per token) and B the weights in their [out, in] layout, so both operands are
 // K-contiguous and feed the MFMA lanes with plain 16-byte loads.
 //
-//  * Workgroup tile BM x BN x 32, 256 threads as a 2 x 2 grid of wave64s; each wave
-//    owns a (BM/2) x (BN/2) block of 32 x 32 MFMA tiles.
-//  * Global -> register prefetch of the next K slab overlaps the MFMAs of the current
-//    one; slabs are double-buffered in LDS with a padded row pitch (40 bf16) so the
-//    32 rows read by one MFMA operand fetch spread over the LDS banks.
+//  * Workgroup tile BM x BN (128 x 128, 128 x 64 or 64 x 64 by tile count), 256
+//    threads as a 2 x 2 grid of wave64s; each wave owns a (BM/2) x (BN/2) block of
+//    32 x 32 MFMA tiles.
+//  * K % 64 == 0 (every Qwen2.5 projection): the pipelined kernel below (DMA ring of
+//    64-key slabs, XOR-swizzled LDS, operand reads software-pipelined against the
+//    MFMAs, grouped tile order per XCD). Other K: a register-staged kernel with a
+//    padded LDS row pitch (40 bf16).
 //  * Epilogues: bf16 (+bias, the cuBLASLt BIAS epilogue), fp32, and SwiGLU, where the
 //    B tile interleaves 32-row blocks of up and gate weights so that each lane holds u
 //    and g of the same output element: out = bf16(silu(bf16(g)) * bf16(u)).
@@ -185,6 +187,21 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(const bf16_t* _
 // (dispatch is round-robin over the 8 XCDs), so workgroups that share weight columns
 // share an L2.
 // ---------------------------------------------------------------------------------
+// Tile order within one XCD's contiguous range of tile indices: groups of kGroupM row
+// tiles are walked column by column, so the workgroups resident on an XCD at one time
+// cover a kGroupM x (resident / kGroupM) block of output tiles and share its A and B
+// slabs in that XCD's L2 (walking M first, as a plain index split does, re-reads a fresh
+// A slab for every tile once M spans many tiles).
+constexpr int kGroupM = 8;
+__device__ __forceinline__ void tile_of(int t, int mt, int nt, int& tm, int& tn) {
+    const int in_group = kGroupM * nt;
+    const int first = (t / in_group) * kGroupM;
+    const int gm = min(mt - first, kGroupM);
+    const int r = t % in_group;
+    tm = first + r % gm;
+    tn = r / gm;
+}
+
 constexpr int kPBK = 64;            // K per slab
 constexpr int kPRow = kPBK * 2;     // bytes per operand row in LDS
 
@@ -225,7 +242,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
     const int per = (T + 7) / 8;
     const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
     if (t >= T) return;
-    const int tm = t % mt, tn = t / mt;
+    int tm, tn;
+    tile_of(t, mt, nt, tm, tn);
     const int m0 = tm * BM;
     const int n0 = (EPI == GEPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
 
@@ -273,45 +291,50 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
+    // Operand reads of one 16-key step: TM A fragments and TN B fragments (ds_read_b128).
+    auto read_step = [&](uint32_t base, int ks, bf16x8_t (&af)[TM], bf16x8_t (&bfr)[TN]) {
+        const int c = ks * 2 + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int r = wm * WM + i * 32 + (lane & 31);
+            const uint32_t addr = base + (uint32_t)(r * kPRow + ((c ^ (r & 7)) << 4));
+            asm volatile("ds_read_b128 %0, %1" : "=v"(af[i]) : "v"(addr) : "memory");
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int r = wn * WN + j * 32 + (lane & 31);
+            const uint32_t addr = base + (uint32_t)(BM * kPRow + r * kPRow + ((c ^ (r & 7)) << 4));
+            asm volatile("ds_read_b128 %0, %1" : "=v"(bfr[j]) : "v"(addr) : "memory");
+        }
+    };
+    // Software pipeline over the slab's four 16-key steps: the reads of step ks + 2 are
+    // issued behind the MFMAs of step ks, so LDS latency hides behind matrix work within
+    // the wave. The fragments come from inline-asm reads the compiler cannot track: each
+    // step waits for its own reads (lgkmcnt = the reads issued after them), then passes
+    // its fragments through an asm "write" so that no MFMA is scheduled above the wait.
     auto compute = [&](int slot) {
         const uint32_t base = lds0 + (uint32_t)(slot * STAGE);
         constexpr int KSN = kPBK / 16;
+        constexpr int RPS = TM + TN;   // reads per step
+        static_assert(RPS <= 15, "lgkmcnt holds at most 15 outstanding reads");
         bf16x8_t af[KSN][TM], bfr[KSN][TN];
-        // all operand reads of the slab first (one LDS latency per slab), then the MFMAs
+        read_step(base, 0, af[0], bfr[0]);
+        read_step(base, 1, af[1], bfr[1]);
 #pragma unroll
         for (int ks = 0; ks < KSN; ++ks) {
-            const int c = ks * 2 + (lane >> 5);
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int r = wm * WM + i * 32 + (lane & 31);
-                const uint32_t addr = base + (uint32_t)(r * kPRow + ((c ^ (r & 7)) << 4));
-                asm volatile("ds_read_b128 %0, %1" : "=v"(af[ks][i]) : "v"(addr) : "memory");
-            }
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int r = wn * WN + j * 32 + (lane & 31);
-                const uint32_t addr = base + (uint32_t)(BM * kPRow + r * kPRow + ((c ^ (r & 7)) << 4));
-                asm volatile("ds_read_b128 %0, %1" : "=v"(bfr[ks][j]) : "v"(addr) : "memory");
-            }
-        }
-        // The fragments come from inline-asm reads the compiler cannot track: wait for
-        // them, then pass every fragment through an asm "write" so that no MFMA can be
-        // scheduled above the wait.
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int ks = 0; ks < KSN; ++ks) {
+            if (ks + 1 < KSN) asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(RPS) : "memory");
+            else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
             for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[ks][i]));
 #pragma unroll
             for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bfr[ks][j]));
-        }
-#pragma unroll
-        for (int ks = 0; ks < KSN; ++ks)
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][i], bfr[ks][j], acc[i][j], 0, 0, 0);
+            if (ks + 2 < KSN) read_step(base, ks + 2, af[ks + 2], bfr[ks + 2]);
+        }
     };
 
     const int nk = K / kPBK;
@@ -373,209 +396,6 @@ static void gemm_pipe_launch(int M, int N, int K, const bf16_t* A, const bf16_t*
                        M, N, K, ldc, mt, nt);
 }
 
-// ---------------------------------------------------------------------------------
-// Large-tile variant: 256 x 256 output tile per workgroup, 4 waves in a 2 x 2 grid and
-// 128 x 128 (4 x 4 MFMA tiles, 256 accumulator registers) per wave, so that each 16-key
-// MFMA step issues 16 MFMAs for 8 ds_read_b128 operand reads (the 128 x 128 tile issues
-// one read per MFMA and is bound by LDS bandwidth). K slabs of 32 stream global -> LDS
-// with global_load_lds into a 4-deep ring (32 KB per slab); each wave load covers 16 rows
-// x 64 bytes and lane l fetches chunk (l % 4) ^ ((row >> 2) & 3) of its row, so the 16
-// rows read by one operand fetch phase hit distinct LDS banks.
-// ---------------------------------------------------------------------------------
-constexpr int kBBK = 32;            // K per slab
-constexpr int kBRow = kBBK * 2;     // bytes per operand row in LDS
-
-template <int LPW>
-__device__ __forceinline__ void vm_wait_big(int slabs) {
-    switch (slabs) {
-        case 0: vm_wait<0>(); break;
-        case 1: vm_wait<1 * LPW>(); break;
-        default: vm_wait<2 * LPW>(); break;
-    }
-}
-
-template <int S, int EPI>
-__global__ __launch_bounds__(kGemmThreads) void gemm_big_kernel(const bf16_t* __restrict__ A,
-                                                                const bf16_t* __restrict__ B,
-                                                                const bf16_t* __restrict__ bias,
-                                                                void* __restrict__ Cout, int M, int N, int K, int ldc,
-                                                                int mt, int nt) {
-    constexpr int BM = 256, BN = 256;
-    constexpr int WM = BM / 2, WN = BN / 2;
-    constexpr int TM = WM / 32, TN = WN / 32;
-    constexpr int STAGE = (BM + BN) * kBRow;
-    constexpr int QA = BM / 16, QB = BN / 16;   // 1 KB wave loads per operand per slab
-    constexpr int LPW = (QA + QB) / 4;
-    static_assert(S >= 2 && S <= 4 && (S - 2) * LPW <= 63, "bad pipeline shape");
-    __shared__ __align__(1024) unsigned char smem[S * STAGE];
-
-    const int T = mt * nt;
-    const int per = (T + 7) / 8;
-    const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
-    if (t >= T) return;
-    const int tm = t % mt, tn = t / mt;
-    const int m0 = tm * BM;
-    const int n0 = (EPI == GEPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
-
-    const int tid = threadIdx.x;
-    const int wave = tid / kWave, lane = tid % kWave;
-    const int wm = wave / 2, wn = wave % 2;
-    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
-
-    auto b_row = [&](int r) -> int {
-        if (EPI == GEPI_SWIGLU) {
-            const int blk = r / 32;
-            const int col = n0 + (blk / 2) * 32 + (r % 32);
-            return (col < N) ? ((blk % 2 == 0) ? col : N + col) : -1;
-        }
-        const int n = n0 + r;
-        return (n < N) ? n : -1;
-    };
-
-    // Per-lane source offsets (elements) of the wave loads are fixed for the whole kernel.
-    const int rr = lane >> 2, cs = lane & 3;
-    uint32_t srcoff[LPW];
-#pragma unroll
-    for (int i = 0; i < LPW; ++i) {
-        const int q = wave + i * 4;
-        if (q < QA) {
-            const int row = q * 16 + rr;
-            srcoff[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)K + ((cs ^ ((row >> 2) & 3)) << 3);
-        } else {
-            const int row = (q - QA) * 16 + rr;
-            int br = b_row(row);
-            if (br < 0) br = 0;
-            srcoff[i] = (uint32_t)br * (uint32_t)K + ((cs ^ ((row >> 2) & 3)) << 3);
-        }
-    }
-    auto issue = [&](int kk, int slot) {
-        const int k0 = kk * kBBK;
-#pragma unroll
-        for (int i = 0; i < LPW; ++i) {
-            const int q = wave + i * 4;
-            const bf16_t* src = (q < QA ? A : B) + srcoff[i] + k0;
-            __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                             (__attribute__((address_space(3))) void*)(smem + slot * STAGE + q * 1024),
-                                             16, 0, 0);
-        }
-    };
-
-    f32x16_t acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-
-    // lane parts of the operand addresses: row (lane & 31) of the first 32-row tile, chunk
-    // 2 ks + (lane >> 5) swizzled by ((row >> 2) & 3); the other tiles are 32 rows
-    // (2048 bytes) further and share the swizzle, so their offsets are immediates
-    uint32_t aoff[2], boff[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int c = ks * 2 + (lane >> 5);
-        const int ra = wm * WM + (lane & 31), rb = wn * WN + (lane & 31);
-        aoff[ks] = (uint32_t)(ra * kBRow + ((c ^ ((ra >> 2) & 3)) << 4));
-        boff[ks] = (uint32_t)(BM * kBRow + rb * kBRow + ((c ^ ((rb >> 2) & 3)) << 4));
-    }
-
-    auto compute = [&](int slot) {
-        const uint32_t base = lds0 + (uint32_t)(slot * STAGE);
-        bf16x8_t af[2][TM], bfr[2][TN];
-        auto rd = [&](auto ic, bf16x8_t& dst, uint32_t addr) {
-            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "n"(decltype(ic)::value * 32 * kBRow)
-                         : "memory");
-        };
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const uint32_t a0 = base + aoff[ks], b0 = base + boff[ks];
-            rd(std::integral_constant<int, 0>{}, af[ks][0], a0);
-            rd(std::integral_constant<int, 1>{}, af[ks][1], a0);
-            rd(std::integral_constant<int, 2>{}, af[ks][2], a0);
-            rd(std::integral_constant<int, 3>{}, af[ks][3], a0);
-            rd(std::integral_constant<int, 0>{}, bfr[ks][0], b0);
-            rd(std::integral_constant<int, 1>{}, bfr[ks][1], b0);
-            rd(std::integral_constant<int, 2>{}, bfr[ks][2], b0);
-            rd(std::integral_constant<int, 3>{}, bfr[ks][3], b0);
-        }
-        // k-step 0's 8 reads were issued first: wait for them, then the second 8
-        asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
-#pragma unroll
-        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[0][i]));
-#pragma unroll
-        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bfr[0][j]));
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0][i], bfr[0][j], acc[i][j], 0, 0, 0);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(af[1][i]));
-#pragma unroll
-        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(bfr[1][j]));
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1][i], bfr[1][j], acc[i][j], 0, 0, 0);
-    };
-
-    const int nk = K / kBBK;
-    const int pre = min(S - 1, nk);
-    for (int p = 0; p < pre; ++p) issue(p, p);
-    for (int kt = 0; kt < nk; ++kt) {
-        vm_wait_big<LPW>(min(S - 2, nk - 1 - kt));
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
-        compute(kt % S);
-    }
-
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int row = m0 + wm * WM + i * 32 + (e / 4) * 8 + (lane / 32) * 4 + (e % 4);
-            if (row >= M) continue;
-            if (EPI == GEPI_SWIGLU) {
-#pragma unroll
-                for (int j = 0; j < TN; j += 2) {
-                    const int col = n0 + ((wn * WN + j * 32) / 64) * 32 + (lane % 32);
-                    if (col < N) {
-                        const float u = round_bf16(acc[i][j][e]);
-                        const float g = round_bf16(acc[i][j + 1][e]);
-                        const float o = (g / (1.0f + expf(-g))) * u;
-                        reinterpret_cast<bf16_t*>(Cout)[(size_t)row * ldc + col] = (bf16_t)f32_to_bf16(o);
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const int col = n0 + wn * WN + j * 32 + (lane % 32);
-                    if (col >= N) continue;
-                    float v = acc[i][j][e];
-                    if (bias != nullptr) v += bf16_to_f32(bias[col]);
-                    if (EPI == GEPI_F32) reinterpret_cast<float*>(Cout)[(size_t)row * ldc + col] = v;
-                    else reinterpret_cast<bf16_t*>(Cout)[(size_t)row * ldc + col] = (bf16_t)f32_to_bf16(v);
-                }
-            }
-        }
-    }
-}
-
-template <int EPI>
-static void gemm_big_launch(int M, int N, int K, const bf16_t* A, const bf16_t* B, const bf16_t* bias, void* C,
-                            int ldc, hipStream_t stream) {
-    const int ocols = (EPI == GEPI_SWIGLU) ? 128 : 256;
-    const int mt = (M + 255) / 256, nt = (N + ocols - 1) / ocols;
-    const int grid = 8 * ((mt * nt + 7) / 8);
-    hipLaunchKernelGGL((gemm_big_kernel<4, EPI>), dim3(grid), dim3(kGemmThreads), 0, stream, A, B, bias, C, M, N, K,
-                       ldc, mt, nt);
-}
-
 template <int EPI>
 static int gemm_dispatch(int M, int N, int K, const bf16_t* A, const bf16_t* B, const bf16_t* bias, void* C, int ldc,
                          hipStream_t stream) {
@@ -585,18 +405,13 @@ static int gemm_dispatch(int M, int N, int K, const bf16_t* A, const bf16_t* B, 
         return (long)((M + bm - 1) / bm) * ((N + ocols - 1) / ocols);
     };
     const dim3 block(kGemmThreads);
-    const char* big_env = getenv("EFM_GEMM_BIG");
-    const bool big_ok = big_env == nullptr || big_env[0] != '0';
     if (K % kPBK == 0) {
-        // Tile choice from a sweep of the prefill shapes on MI355X: the 256 x 256 tile
-        // once there are >= 3 tiles per CU; else 128 x 128 double-buffered (two workgroups
-        // per CU), which needs >= 1.5 tiles per CU (>= 1 for SwiGLU); else 128 x 64
-        // double-buffered; else 64 x 64 (or 64 x 128 for SwiGLU) with shallow pipelines.
-        // Every tile shape sums each output over K in the same order: results are
-        // bit-identical whichever is chosen.
-        if (big_ok && tiles(256, 256) >= 768) {
-            gemm_big_launch<EPI>(M, N, K, A, B, bias, C, ldc, stream);
-        } else if (tiles(128, 128) >= ((EPI == GEPI_SWIGLU) ? 256 : 384)) {
+        // Tile choice from a sweep of the prefill shapes on MI355X: 128 x 128 double-
+        // buffered (two workgroups per CU) once there are >= 1.5 tiles per CU (>= 1 for
+        // SwiGLU); else 128 x 64 double-buffered; else 64 x 64 (64 x 128 for SwiGLU) with
+        // shallow pipelines. Every tile shape sums each output over K in the same order:
+        // results are bit-identical whichever is chosen.
+        if (tiles(128, 128) >= ((EPI == GEPI_SWIGLU) ? 256 : 384)) {
             gemm_pipe_launch<128, 128, 2, EPI>(M, N, K, A, B, bias, C, ldc, stream);
         } else if constexpr (EPI == GEPI_SWIGLU) {
             gemm_pipe_launch<64, 128, 3, EPI>(M, N, K, A, B, bias, C, ldc, stream);
