@@ -29,6 +29,9 @@ int gemv_swiglu(int64_t K, int64_t inter, const void* x, const void* W, void* y,
 int gemm_bf16(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* bias, void* C,
               int32_t out_dtype, hipStream_t stream);
 int gemm_swiglu(int64_t M, int64_t inter, int64_t K, const void* A, const void* W, void* out, hipStream_t stream);
+size_t gemm_bf16_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int gemm_bf16_ws(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* bias, void* C,
+                 int32_t out_dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 }  // namespace efm
 
@@ -46,6 +49,22 @@ extern "C" int efm_linear(int64_t m, int64_t in_features, int64_t out_features, 
     if (m == 0) return EFM_OK;
     if (m == 1) return gemv_plain(in_features, out_features, x, w, bias, y, out_dtype, stream);
     return gemm_bf16(m, out_features, in_features, x, w, bias, y, out_dtype, stream);
+}
+
+extern "C" size_t efm_linear_workspace_bytes(int64_t m, int64_t in_features, int64_t out_features) {
+    if (m <= 1 || in_features <= 0 || out_features <= 0) return 0;
+    return gemm_bf16_workspace_bytes(m, out_features, in_features);
+}
+
+extern "C" int efm_linear_ws(int64_t m, int64_t in_features, int64_t out_features, const void* x, const void* w,
+                             const void* bias, void* y, int32_t out_dtype, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+    if (m < 0 || in_features <= 0 || out_features <= 0)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "linear: bad shape m=%lld in=%lld out=%lld", (long long)m,
+                         (long long)in_features, (long long)out_features);
+    if (m == 0) return EFM_OK;
+    if (m == 1) return gemv_plain(in_features, out_features, x, w, bias, y, out_dtype, stream);
+    return gemm_bf16_ws(m, out_features, in_features, x, w, bias, y, out_dtype, workspace, workspace_bytes, stream);
 }
 
 extern "C" int efm_fused_gate_up_swiglu(int64_t m, int64_t hidden, int64_t inter, const void* x,

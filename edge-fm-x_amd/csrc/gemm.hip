@@ -24,7 +24,7 @@ namespace efm {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-enum { GEPI_BF16 = 0, GEPI_F32 = 1, GEPI_SWIGLU = 2 };
+enum { GEPI_BF16 = 0, GEPI_F32 = 1, GEPI_SWIGLU = 2, GEPI_PARTIAL = 3 };
 
 constexpr int kGemmThreads = 256;
 constexpr int kBK = 32;
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
                                                                  const bf16_t* __restrict__ B,
                                                                  const bf16_t* __restrict__ bias,
                                                                  void* __restrict__ Cout, int M, int N, int K, int ldc,
-                                                                 int mt, int nt) {
+                                                                 int mt, int nt, int ksplit, int kt_per) {
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr int STAGE = (BM + BN) * kPRow;
@@ -238,12 +238,16 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
     static_assert(EPI != GEPI_SWIGLU || TN % 2 == 0, "SwiGLU needs paired N tiles");
     __shared__ __align__(1024) unsigned char smem[S * STAGE];
 
-    const int T = mt * nt;
+    // split-K (GEPI_PARTIAL): work unit t covers K slice t / (mt * nt), slabs
+    // [slice * kt_per, (slice + 1) * kt_per), and writes fp32 partial sums
+    const int T = mt * nt * ksplit;
     const int per = (T + 7) / 8;
     const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
     if (t >= T) return;
+    const int slice = t / (mt * nt);
     int tm, tn;
-    tile_of(t, mt, nt, tm, tn);
+    tile_of(t % (mt * nt), mt, nt, tm, tn);
+    const int kt0 = slice * kt_per;
     const int m0 = tm * BM;
     const int n0 = (EPI == GEPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
 
@@ -263,7 +267,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
     };
 
     auto issue = [&](int kk, int slot) {
-        const int k0 = kk * kPBK;
+        const int k0 = (kt0 + kk) * kPBK;
         const int rr = lane >> 3, cs = lane & 7;
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
@@ -337,7 +341,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
         }
     };
 
-    const int nk = K / kPBK;
+    const int nk = min(K / kPBK, kt0 + kt_per) - kt0;
     const int pre = min(S - 1, nk);
     for (int p = 0; p < pre; ++p) issue(p, p);
     for (int kt = 0; kt < nk; ++kt) {
@@ -377,12 +381,50 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
                     const int col = n0 + wn * WN + j * 32 + (lane % 32);
                     if (col >= N) continue;
                     float v = acc[i][j][e];
+                    if (EPI == GEPI_PARTIAL) {
+                        reinterpret_cast<float*>(Cout)[((size_t)slice * M + row) * N + col] = v;
+                        continue;
+                    }
                     if (bias != nullptr) v += bf16_to_f32(bias[col]);
                     if (EPI == GEPI_F32) reinterpret_cast<float*>(Cout)[(size_t)row * ldc + col] = v;
                     else reinterpret_cast<bf16_t*>(Cout)[(size_t)row * ldc + col] = (bf16_t)f32_to_bf16(v);
                 }
             }
         }
+    }
+}
+
+// Split-K reduction: out[r, c] = sum over slices s = 0, 1, ... (in that order) of
+// part[s, r, c], + bias[c], as bf16 or fp32. Four columns per thread (N % 4 == 0).
+template <bool F32OUT>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, int ksplit, int M,
+                                                                 int N, const bf16_t* __restrict__ bias,
+                                                                 void* __restrict__ Cout) {
+    const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;   // float4 index
+    const size_t plane = (size_t)M * N;
+    if (q * 4 >= plane) return;
+    float4 acc = *reinterpret_cast<const float4*>(part + q * 4);
+    for (int sl = 1; sl < ksplit; ++sl) {
+        const float4 v = *reinterpret_cast<const float4*>(part + (size_t)sl * plane + q * 4);
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    }
+    const int col = (int)((q * 4) % (size_t)N);
+    if (bias != nullptr) {
+        acc.x += bf16_to_f32(bias[col + 0]);
+        acc.y += bf16_to_f32(bias[col + 1]);
+        acc.z += bf16_to_f32(bias[col + 2]);
+        acc.w += bf16_to_f32(bias[col + 3]);
+    }
+    if (F32OUT) {
+        reinterpret_cast<float4*>(Cout)[q] = acc;
+    } else {
+        uint2 pk;
+        pk.x = pack_bf16x2(acc.x, acc.y);
+        pk.y = pack_bf16x2(acc.z, acc.w);
+        reinterpret_cast<uint2*>(Cout)[q] = pk;
     }
 }
 
@@ -393,7 +435,46 @@ static void gemm_pipe_launch(int M, int N, int K, const bf16_t* A, const bf16_t*
     const int mt = (M + BM - 1) / BM, nt = (N + ocols - 1) / ocols;
     const int grid = 8 * ((mt * nt + 7) / 8);
     hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, S, EPI>), dim3(grid), dim3(kGemmThreads), 0, stream, A, B, bias, C,
-                       M, N, K, ldc, mt, nt);
+                       M, N, K, ldc, mt, nt, 1, K / kPBK);
+}
+
+// Split-K plan for a plain (non-SwiGLU) projection with K % 64 == 0: worth it when the
+// 128 x 128 tiles cannot fill half the chip's workgroup slots and K >= 4096 (measured:
+// 512 x 8960 -> 1536 goes 51 -> 32 us; at 176 tiles, 1344 x 11008 -> 2048, it gains
+// nothing); 0 = no split.
+struct SplitK {
+    int ksplit = 0, kt_per = 0;
+};
+static SplitK splitk_plan(int M, int N, int K) {
+    SplitK p;
+    if (K % kPBK != 0 || N % 4 != 0) return p;
+    const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
+    const int nk = K / kPBK;
+    if (tiles >= 128 || nk < 64) return p;
+    int ks = (int)std::min<long>(8, (384 + tiles - 1) / tiles);
+    ks = std::min(ks, nk / 16);                 // at least 16 slabs (1024 keys) per slice
+    if (ks < 2) return p;
+    p.kt_per = (nk + ks - 1) / ks;
+    p.ksplit = (nk + p.kt_per - 1) / p.kt_per;
+    return p;
+}
+static size_t splitk_bytes(int M, int N, int K) {
+    const SplitK p = splitk_plan(M, N, K);
+    return p.ksplit == 0 ? 0 : (size_t)p.ksplit * M * N * sizeof(float);
+}
+
+// C = A . B^T (+ bias) through ksplit fp32 partial planes in `part`, then the ordered
+// reduction.
+static void gemm_splitk_launch(int M, int N, int K, const bf16_t* A, const bf16_t* B, const bf16_t* bias, void* C,
+                               bool f32out, float* part, const SplitK& p, hipStream_t stream) {
+    const int mt = (M + 127) / 128, nt = (N + 127) / 128;
+    const int grid = 8 * ((mt * nt * p.ksplit + 7) / 8);
+    hipLaunchKernelGGL((gemm_pipe_kernel<128, 128, 2, GEPI_PARTIAL>), dim3(grid), dim3(kGemmThreads), 0, stream, A, B,
+                       nullptr, part, M, N, K, N, mt, nt, p.ksplit, p.kt_per);
+    const size_t quads = (size_t)M * N / 4;
+    const dim3 rgrid((unsigned)((quads + 255) / 256));
+    if (f32out) hipLaunchKernelGGL((gemm_splitk_reduce_kernel<true>), rgrid, dim3(256), 0, stream, part, p.ksplit, M, N, bias, C);
+    else hipLaunchKernelGGL((gemm_splitk_reduce_kernel<false>), rgrid, dim3(256), 0, stream, part, p.ksplit, M, N, bias, C);
 }
 
 template <int EPI>
@@ -460,6 +541,29 @@ int gemm_bf16(int64_t M, int64_t N, int64_t K, const void* A, const void* B, con
     if (out_dtype == EFM_DTYPE_BF16) return gemm_dispatch<GEPI_BF16>((int)M, (int)N, (int)K, a, b, bi, C, (int)N, stream);
     if (out_dtype == EFM_DTYPE_F32) return gemm_dispatch<GEPI_F32>((int)M, (int)N, (int)K, a, b, bi, C, (int)N, stream);
     return set_error(EFM_ERR_UNSUPPORTED, "linear: output dtype %d not supported", out_dtype);
+}
+
+size_t gemm_bf16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 1 || M > 0x7fffffff / 2 || N > 0x7fffffff / 2 || K > 0x7fffffff / 2) return 0;
+    return splitk_bytes((int)M, (int)N, (int)K);
+}
+
+int gemm_bf16_ws(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* bias, void* C,
+                 int32_t out_dtype, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    int rc = gemm_check(M, N, K, A, B, C);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return EFM_OK;
+    if (out_dtype != EFM_DTYPE_BF16 && out_dtype != EFM_DTYPE_F32)
+        return set_error(EFM_ERR_UNSUPPORTED, "linear: output dtype %d not supported", out_dtype);
+    const SplitK p = splitk_plan((int)M, (int)N, (int)K);
+    const size_t need = (p.ksplit == 0) ? 0 : (size_t)p.ksplit * M * N * sizeof(float);
+    if (p.ksplit == 0 || workspace == nullptr || workspace_bytes < need ||
+        (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+        return gemm_bf16(M, N, K, A, B, bias, C, out_dtype, stream);
+    gemm_splitk_launch((int)M, (int)N, (int)K, static_cast<const bf16_t*>(A), static_cast<const bf16_t*>(B),
+                       static_cast<const bf16_t*>(bias), C, out_dtype == EFM_DTYPE_F32, static_cast<float*>(workspace),
+                       p, stream);
+    return check_launch("gemm_bf16 split-K");
 }
 
 int gemm_swiglu(int64_t M, int64_t inter, int64_t K, const void* A, const void* W, void* out, hipStream_t stream) {

@@ -111,6 +111,9 @@ SIGNATURES = {
     "efm_fused_add_rms_norm": (c_int32, [c_uint32, c_uint32, c_float, c_void_p, c_void_p, c_void_p, c_void_p]),
     "efm_act_and_mul": (c_int32, [c_int64, c_int64, c_int32, c_void_p, c_void_p, c_void_p]),
     "efm_linear": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),
+    "efm_linear_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
+    "efm_linear_ws": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p,
+                                c_size_t, c_void_p]),
     "efm_fused_gate_up_swiglu": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]),
     "efm_lm_head_top1_workspace_bytes": (c_size_t, [c_int64]),
     "efm_lm_head_top1": (c_int32, [c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),

@@ -2,6 +2,8 @@
 
 #include <cctype>
 #include <filesystem>
+#include <map>
+#include <mutex>
 
 namespace edge_fm {
 
@@ -347,6 +349,19 @@ std::string linear_shape_sig(const LinearShape& s) {
 }
 
 namespace {
+// Grow-only per-device scratch for the split-K prefill GEMMs (the reference's linear impls
+// take theirs from StaticBufferManager::get_cache_buf, src/utils/memory.h:31-109). Grows
+// only outside graph capture: decode (m = 1) never needs it.
+void* linear_scratch(size_t bytes, int32_t device_id, size_t* have) {
+    static std::mutex mu;
+    static std::map<int32_t, Tensor> bufs;
+    std::lock_guard<std::mutex> lock(mu);
+    Tensor& t = bufs[device_id];
+    if (t.empty() || t.nbytes() < bytes) t = Tensor::empty({(int64_t)bytes}, DType::UInt8, Device::GPU, device_id);
+    *have = t.nbytes();
+    return t.data_ptr();
+}
+
 class HipLinearImpl final : public LinearImpl {
 public:
     std::string impl_id() const override { return "hip_gfx950_linear"; }
@@ -358,9 +373,12 @@ public:
     }
     void forward(const LinearOpContext& c, const Tensor& w, const Tensor* bias, const Tensor& in, Tensor& out,
                  hipStream_t s) override {
-        efm_check(efm_linear(c.shape.m, c.shape.in_features, c.shape.out_features, in.data_ptr(), w.data_ptr(),
-                             bias ? bias->data_ptr() : nullptr, out.data_ptr(),
-                             c.shape.output == DType::Float32 ? EFM_DTYPE_F32 : EFM_DTYPE_BF16, s),
+        const size_t need = efm_linear_workspace_bytes(c.shape.m, c.shape.in_features, c.shape.out_features);
+        size_t have = 0;
+        void* ws = need > 0 ? linear_scratch(need, w.device().second, &have) : nullptr;
+        efm_check(efm_linear_ws(c.shape.m, c.shape.in_features, c.shape.out_features, in.data_ptr(), w.data_ptr(),
+                                bias ? bias->data_ptr() : nullptr, out.data_ptr(),
+                                c.shape.output == DType::Float32 ? EFM_DTYPE_F32 : EFM_DTYPE_BF16, ws, have, s),
                   "linear " + c.layer_prefix);
     }
 };

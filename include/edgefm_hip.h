@@ -198,6 +198,19 @@ int efm_act_and_mul(int64_t batch, int64_t hidden, int32_t layout, const void* i
 int efm_linear(int64_t m, int64_t in_features, int64_t out_features, const void* x, const void* w,
                const void* bias, void* y, int32_t out_dtype, hipStream_t stream);
 
+/* efm_linear with a caller workspace (the scratch the reference's linear impls take from
+ * StaticBufferManager, src/utils/memory.h:31-109): shapes whose output tiles are too
+ * few to fill the chip and whose K is long (prefill down_proj at a few hundred to a
+ * few thousand tokens) split K into slices that write fp32 partial sums into the
+ * workspace, then reduce them in slice order. efm_linear_workspace_bytes returns the
+ * bytes that enables the split (0: no split for this shape); with less workspace the
+ * call runs efm_linear. The split sums K in a different order than efm_linear, so the
+ * two agree to fp32 rounding, not bit for bit; each is deterministic. */
+size_t efm_linear_workspace_bytes(int64_t m, int64_t in_features, int64_t out_features);
+int efm_linear_ws(int64_t m, int64_t in_features, int64_t out_features, const void* x, const void* w,
+                  const void* bias, void* y, int32_t out_dtype, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream);
+
 /* Fused gate/up projection + SwiGLU: W is the fused [up; gate] matrix [2*inter, hidden]
  * (src/layers/linear.cu:1923-1943); out[m, i] = bf16(silu(bf16(g_i)) * bf16(u_i)).
  * Replaces FusedGateUpActivationOp::run / TrtLlmDecodeSwigluOp

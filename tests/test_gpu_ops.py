@@ -431,6 +431,58 @@ def test_gemm_tile_shapes_agree_bit_exact(gpu, kind):
         assert_close_bf16(heads[0][rows], O.linear(xs, w.cpu(), b.cpu()))
 
 
+@pytest.mark.parametrize("m,k,n,kind", [
+    pytest.param(512, 8960, 1536, "bf16", id="c2_down"),
+    pytest.param(300, 18944, 3584, "bf16", id="7b_down"),
+    pytest.param(300, 4096, 1000, "bias", id="ragged_bias"),
+    pytest.param(200, 8192, 2048, "f32", id="f32"),
+])
+def test_linear_split_k_matches_unsplit_and_oracle(gpu, m, k, n, kind):
+    """efm_linear_ws splits K for these under-filled, long-K shapes: its result equals
+    efm_linear to fp32 rounding, is deterministic, matches the oracle on a row sample, and
+    with too small a workspace the call is exactly efm_linear."""
+    torch.manual_seed(m + k)
+    need = C.load().efm_linear_workspace_bytes(m, k, n)
+    assert need > 0
+    x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
+    w = (torch.randn(n, k, device=gpu) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(n, device=gpu) * 0.05).to(torch.bfloat16) if kind == "bias" else None
+    f32 = kind == "f32"
+    dt, cd = (torch.float32, C.EFM_DTYPE_F32) if f32 else (torch.bfloat16, C.EFM_DTYPE_BF16)
+    ws = torch.full((need,), 0x7f, dtype=torch.uint8, device=gpu)
+    outs = []
+    for wsz in (need, need, 64):
+        y = torch.empty(m, n, dtype=dt, device=gpu)
+        C.call("efm_linear_ws", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), cd, ptr(ws), wsz, stream())
+        torch.cuda.synchronize()
+        outs.append(y)
+    ref = torch.empty(m, n, dtype=dt, device=gpu)
+    C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(ref), cd, stream())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]), "split-K is not deterministic"
+    assert torch.equal(outs[2], ref), "too small a workspace must run the unsplit GEMM"
+    if f32:
+        torch.testing.assert_close(outs[0], ref, rtol=1e-5, atol=1e-4)
+    else:
+        diff = (outs[0].float() - ref.float()).abs()
+        assert float(diff.max()) <= float(ref.float().abs().max()) * 2 ** -7, "split-K differs beyond one bf16 ulp"
+    rows = torch.tensor([0, m // 2, m - 1])
+    exp = O.linear(x[rows].cpu(), w.cpu(), None if b is None else b.cpu(), out_f32=f32)
+    if f32:
+        torch.testing.assert_close(outs[0][rows].cpu(), exp, rtol=1e-4, atol=1e-4)
+    else:
+        assert_close_bf16(outs[0][rows], exp)
+
+
+def test_linear_workspace_bytes_zero_without_split(gpu):
+    lib = C.load()
+    assert lib.efm_linear_workspace_bytes(1, 8960, 1536) == 0          # GEMV
+    assert lib.efm_linear_workspace_bytes(16384, 18944, 3584) == 0     # enough tiles
+    assert lib.efm_linear_workspace_bytes(512, 1536, 1536) == 0        # short K
+    assert lib.efm_linear_workspace_bytes(1344, 11008, 2048) == 0      # 176 tiles: no gain
+    assert lib.efm_linear_workspace_bytes(512, 8960, 1536) > 0
+
+
 def test_sampler_greedy_ties(gpu):
     torch.manual_seed(0)
     rows, vocab = 4, 151936
