@@ -363,6 +363,62 @@ __global__ void decode_mrope_write_kv_kernel(const bf16_t* q_src, const bf16_t* 
     }
 }
 
+// Prefill: rotate the S new tokens' queries in place in the fused QKV buffer, rotate their
+// keys into the K cache rows and copy their values into the V cache rows, in one pass.
+// One workgroup per token: the cos / sin of the token's hd/2 angles are computed once
+// (sincosf, as mrope_kernel) into LDS and shared by every head; each thread then rotates
+// 4 consecutive pairs (d .. d+3 with d+half .. d+half+3) of one head with 8-byte loads.
+struct RopeWriteArgs {
+    bf16_t* qkv;            // [S, qkv_sn]: q at 0, k at Hq*hd, v at (Hq+Hkv)*hd
+    bf16_t* k_dst;          // [S, kv_sn] cache rows of this prefill
+    bf16_t* v_dst;
+    const int32_t* pos;     // [3, pos_stride] M-RoPE, or NULL: pos_offset + token
+    int pos_stride, pos_offset;
+    int S, Hq, Hkv, hd, qkv_sn, kv_sn, cum0, cum1;
+    RopeTable rope;
+};
+
+__global__ __launch_bounds__(256) void rope_write_kv_kernel(RopeWriteArgs a) {
+    __shared__ float2 cs[kMaxHalfDim];
+    const int t = blockIdx.x;
+    const int half = a.hd / 2;
+    for (int d = threadIdx.x; d < half; d += blockDim.x) {
+        const int sec = (d < a.cum0) ? 0 : (d < a.cum1 ? 1 : 2);
+        const int p = (a.pos != nullptr) ? a.pos[sec * a.pos_stride + t] : a.pos_offset + t;
+        float sn, c;
+        sincosf((float)p * a.rope.inv_freq[d], &sn, &c);
+        cs[d] = make_float2(c, sn);
+    }
+    __syncthreads();
+    bf16_t* row = a.qkv + (size_t)t * a.qkv_sn;
+    const int qd = a.Hq * a.hd, kvd = a.Hkv * a.hd;
+    const int quads = half / 4;   // 4-pair groups per head
+    // rotated heads: q (in place) and k (into the cache)
+    for (int i = threadIdx.x; i < (a.Hq + a.Hkv) * quads; i += blockDim.x) {
+        const int h = i / quads, d = (i % quads) * 4;
+        const bf16_t* src = row + h * a.hd;   // k heads follow the q heads in the row
+        bf16_t* dst = (h < a.Hq) ? row + h * a.hd : a.k_dst + (size_t)t * a.kv_sn + (h - a.Hq) * a.hd;
+        const uint2 lo = *reinterpret_cast<const uint2*>(src + d);
+        const uint2 hi = *reinterpret_cast<const uint2*>(src + d + half);
+        const uint32_t lw[2] = {lo.x, lo.y}, hw[2] = {hi.x, hi.y};
+        uint32_t ol[2], oh[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float2 c0 = cs[d + 2 * e], c1 = cs[d + 2 * e + 1];
+            const float x0a = bf16_to_f32(lw[e] & 0xffffu), x0b = bf16_to_f32(lw[e] >> 16);
+            const float x1a = bf16_to_f32(hw[e] & 0xffffu), x1b = bf16_to_f32(hw[e] >> 16);
+            ol[e] = f32_to_bf16(x0a * c0.x - x1a * c0.y) | (f32_to_bf16(x0b * c1.x - x1b * c1.y) << 16);
+            oh[e] = f32_to_bf16(x1a * c0.x + x0a * c0.y) | (f32_to_bf16(x1b * c1.x + x0b * c1.y) << 16);
+        }
+        *reinterpret_cast<uint2*>(dst + d) = make_uint2(ol[0], ol[1]);
+        *reinterpret_cast<uint2*>(dst + d + half) = make_uint2(oh[0], oh[1]);
+    }
+    // values: plain copy into the cache, 16 bytes per thread
+    const uint4* vs = reinterpret_cast<const uint4*>(row + qd + kvd);
+    uint4* vd = reinterpret_cast<uint4*>(a.v_dst + (size_t)t * a.kv_sn);
+    for (int i = threadIdx.x; i < kvd / 8; i += blockDim.x) vd[i] = vs[i];
+}
+
 static int mrope_check_sections(int hd, int s0, int s1, int s2) {
     if (s0 < 0 || s1 < 0 || s2 < 0 || s0 + s1 + s2 != hd / 2)
         return set_error(EFM_ERR_INVALID_ARGUMENT, "mrope: sections %d+%d+%d must sum to head_dim/2 = %d", s0, s1, s2,
@@ -430,6 +486,51 @@ extern "C" int efm_rope_llama_inplace(void* q, void* k, int32_t seq_len, int32_t
     hipLaunchKernelGGL(mrope_kernel, dim3(seq_len, num_qo_heads + num_kv_heads), dim3(((head_dim / 2) + 63) / 64 * 64),
                        0, stream, a);
     return check_launch("rope_llama_inplace");
+}
+
+extern "C" int efm_prefill_rope_write_kv(void* qkv, int32_t qkv_stride_n, void* k_dst, void* v_dst,
+                                         int32_t kv_stride_n, int32_t seq_len, int32_t num_qo_heads,
+                                         int32_t num_kv_heads, int32_t head_dim, const int32_t* position_ids,
+                                         int32_t position_stride, int32_t pos_offset, int32_t section0,
+                                         int32_t section1, int32_t section2, float rope_theta, float rope_scale,
+                                         hipStream_t stream) {
+    if (!qkv || !k_dst || !v_dst) return set_error(EFM_ERR_INVALID_ARGUMENT, "prefill_rope_write_kv: null pointer");
+    if (head_dim <= 0 || head_dim % 8 || head_dim > 2 * kMaxHalfDim)
+        return set_error(EFM_ERR_UNSUPPORTED, "prefill_rope_write_kv: head_dim %d (multiple of 8, <= %d)", head_dim,
+                         2 * kMaxHalfDim);
+    if (seq_len < 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || pos_offset < 0)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "prefill_rope_write_kv: bad sizes");
+    const int kvd = num_kv_heads * head_dim, tot = num_qo_heads * head_dim + 2 * kvd;
+    const int qsn = qkv_stride_n ? qkv_stride_n : tot, ksn = kv_stride_n ? kv_stride_n : kvd;
+    if (qsn < tot || ksn < kvd || qsn % 8 || ksn % 8 ||
+        ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(k_dst) | reinterpret_cast<uintptr_t>(v_dst)) &
+         15u))
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "prefill_rope_write_kv: strides / alignment");
+    if (position_ids != nullptr) {
+        int rc = mrope_check_sections(head_dim, section0, section1, section2);
+        if (rc) return rc;
+        if (position_stride < seq_len)
+            return set_error(EFM_ERR_INVALID_ARGUMENT, "prefill_rope_write_kv: position_stride < seq_len");
+    }
+    if (seq_len == 0) return EFM_OK;
+    RopeWriteArgs a;
+    a.qkv = static_cast<bf16_t*>(qkv);
+    a.k_dst = static_cast<bf16_t*>(k_dst);
+    a.v_dst = static_cast<bf16_t*>(v_dst);
+    a.pos = position_ids;
+    a.pos_stride = position_stride;
+    a.pos_offset = pos_offset;
+    a.S = seq_len;
+    a.Hq = num_qo_heads;
+    a.Hkv = num_kv_heads;
+    a.hd = head_dim;
+    a.qkv_sn = qsn;
+    a.kv_sn = ksn;
+    a.cum0 = position_ids ? section0 : head_dim / 2;
+    a.cum1 = position_ids ? section0 + section1 : head_dim / 2;
+    rope_table_fill(&a.rope, head_dim, rope_theta, rope_scale);
+    hipLaunchKernelGGL(rope_write_kv_kernel, dim3(seq_len), dim3(256), 0, stream, a);
+    return check_launch("prefill_rope_write_kv");
 }
 
 extern "C" int efm_decode_mrope_write_kv(const void* q_src, const void* k_src, const void* v_src, void* q_dst,

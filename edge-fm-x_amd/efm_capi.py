@@ -103,6 +103,9 @@ SIGNATURES = {
                                          c_int32, c_float, c_float, c_void_p]),
     "efm_mrope": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
                             c_int32, c_int32, c_int32, c_int32, c_float, c_float, c_void_p]),
+    "efm_prefill_rope_write_kv": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
+                                            c_int32, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_float,
+                                            c_float, c_void_p]),
     "efm_decode_mrope_write_kv": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
                                             c_int32, c_int32, c_void_p, c_int32, c_int32, c_int32, c_float, c_float,
                                             c_void_p, c_void_p]),

@@ -578,24 +578,15 @@ void Qwen2_5::prefill(int32_t S, int32_t base, const int32_t* ids, const Tensor*
         // 2c. K / V rows into cache rows [base, base + S) (qwen2_5.cpp:743-746)
         char* kc = static_cast<char*>(k_caches[l]);
         char* vc = static_cast<char*>(v_caches[l]);
-        const char* qkvp = static_cast<const char*>(qkv.data_ptr());
-        hip_check(hipMemcpy2DAsync(kc + (size_t)base * row, row, qkvp + (size_t)QD * 2, (size_t)TOT * 2, row, S,
-                                   hipMemcpyDeviceToDevice, stream),
-                  "copy K to cache");
-        hip_check(hipMemcpy2DAsync(vc + (size_t)base * row, row, qkvp + (size_t)(QD + KVD) * 2, (size_t)TOT * 2, row,
-                                   S, hipMemcpyDeviceToDevice, stream),
-                  "copy V to cache");
-        if (m_.mrope) {
-            // rotate q in the fused buffer and the freshly written K rows (attention.cu:17-118)
-            efm_check(efm_mrope(qkv.data_ptr(), kc + (size_t)base * row, position_ids, S, S, m_.heads, m_.kv_heads,
-                                m_.head_dim, (int32_t)TOT, (int32_t)KVD, m_.mrope_section[0], m_.mrope_section[1],
-                                m_.mrope_section[2], m_.theta, 1.0f, stream),
-                      "prefill mrope");
-        } else {
-            efm_check(efm_rope_llama_inplace(qkv.data_ptr(), kc + (size_t)base * row, S, m_.heads, m_.kv_heads,
-                                             m_.head_dim, (int32_t)TOT, (int32_t)KVD, base, m_.theta, 1.0f, stream),
-                      "prefill rope");
-        }
+        // rotate q in the fused buffer, rotate K into the cache rows [base, base + S) and
+        // copy V there, in one pass (attention.cu:17-118 for M-RoPE; text models rotate
+        // at position base + t)
+        efm_check(efm_prefill_rope_write_kv(qkv.data_ptr(), (int32_t)TOT, kc + (size_t)base * row,
+                                            vc + (size_t)base * row, (int32_t)KVD, S, m_.heads, m_.kv_heads,
+                                            m_.head_dim, m_.mrope ? position_ids : nullptr, S, m_.mrope ? 0 : base,
+                                            m_.mrope_section[0], m_.mrope_section[1], m_.mrope_section[2], m_.theta,
+                                            1.0f, stream),
+                  "prefill rope + kv write");
         // 2d. attention over cache rows [0, L)
         Tensor qv = Tensor::view(qkv.data_ptr(), {S, m_.heads, m_.head_dim}, DType::BFloat16, Device::GPU, device_id_);
         Tensor kv_k = Tensor::view(kc, {L, m_.kv_heads, m_.head_dim}, DType::BFloat16, Device::GPU, device_id_);

@@ -323,6 +323,20 @@ int efm_finalize_decode_token(const int32_t* sampled_token, int32_t* response_to
                               hipStream_t stream);
 /* values[0..2] += 1 (decode M-RoPE positions). */
 int efm_increment_int32_triplet(int32_t* values, hipStream_t stream);
+/* Prefill position encoding + KV write in one pass: rotate the S new tokens' queries in
+ * place in the fused QKV buffer ([S, qkv_stride_n], q at column 0, k at Hq*hd, v at
+ * (Hq+Hkv)*hd), write their rotated keys into k_dst rows and copy their values into
+ * v_dst rows ([S, kv_stride_n], the cache rows [base, base + S)). position_ids NULL:
+ * RoPE-Llama at position pos_offset + t (attention_op.cu:327-371, applied at the cache
+ * write instead of inside attention); else M-RoPE with position rows [3, position_stride]
+ * and sections (attention.cu:17-118). Replaces the two cudaMemcpy2DAsync of
+ * qwen2_5.cpp:743-746 and the rotation of the prefill attention. head_dim % 8 == 0. */
+int efm_prefill_rope_write_kv(void* qkv, int32_t qkv_stride_n, void* k_dst, void* v_dst, int32_t kv_stride_n,
+                              int32_t seq_len, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                              const int32_t* position_ids, int32_t position_stride, int32_t pos_offset,
+                              int32_t section0, int32_t section1, int32_t section2, float rope_theta,
+                              float rope_scale, hipStream_t stream);
+
 /* Decode M-RoPE on q (q_src -> q_dst) and k, then rotated K and raw V rows into cache slot
  * (*d_kv_len - 1); position_ids is the device [3] decode position
  * (launch_decode_mrope_apply_q_write_kv, decode_runtime_kernels.cu:152-225, 406-472). */

@@ -189,6 +189,59 @@ def test_rope_llama_inplace_matches_oracle(gpu, S, base, hq, hkv, hd):
     assert_close_bf16(kc_g, want_k, rtol=1e-2, atol=1e-2, what="k")
 
 
+@pytest.mark.parametrize("mode,S,base,hq,hkv,hd", [
+    ("text", 77, 0, 12, 2, 128), ("text", 300, 513, 28, 4, 128), ("text", 33, 5, 14, 2, 64),
+    ("mrope", 70, 0, 16, 2, 128),
+])
+def test_prefill_rope_write_kv_matches_two_step_and_oracle(gpu, mode, S, base, hq, hkv, hd):
+    """One-pass q rotation + rotated K / raw V into the cache rows equals the two-step
+    path (K / V copies, then efm_rope_llama_inplace or efm_mrope over the cache rows) bit
+    for bit, and the oracle's rotation within one bf16 rounding; cache rows outside
+    [base, base + S) and the QKV buffer's K / V columns stay untouched."""
+    torch.manual_seed(S + hd)
+    kvd, qd = hkv * hd, hq * hd
+    tot = qd + 2 * kvd
+    rows = base + S + 9
+    qkv = torch.randn(S, tot, dtype=torch.bfloat16)
+    kc0 = torch.randn(rows, kvd, dtype=torch.bfloat16)
+    vc0 = torch.randn(rows, kvd, dtype=torch.bfloat16)
+    if mode == "mrope":
+        sections = (16, 24, 24)
+        pos = (torch.stack([torch.zeros(S, dtype=torch.int32), torch.arange(S, dtype=torch.int32) // 7,
+                            torch.arange(S, dtype=torch.int32) % 7]) + 3).contiguous()
+        pos_g = pos.to(gpu)
+    else:
+        sections, pos_g = (hd // 2, 0, 0), None
+    # one pass
+    q1, k1, v1 = qkv.to(gpu), kc0.to(gpu), vc0.to(gpu)
+    C.call("efm_prefill_rope_write_kv", ptr(q1), tot, ptr(k1[base:]), ptr(v1[base:]), kvd, S, hq, hkv, hd,
+           ptr(pos_g), S, base if mode == "text" else 0, *sections, 1.0e6, 1.0, stream())
+    # two steps
+    q2, k2, v2 = qkv.to(gpu), kc0.to(gpu), vc0.to(gpu)
+    k2[base:base + S] = q2[:, qd:qd + kvd]
+    v2[base:base + S] = q2[:, qd + kvd:]
+    if mode == "mrope":
+        C.call("efm_mrope", ptr(q2), ptr(k2[base:]), ptr(pos_g), S, S, hq, hkv, hd, tot, kvd, *sections, 1.0e6,
+               1.0, stream())
+    else:
+        C.call("efm_rope_llama_inplace", ptr(q2), ptr(k2[base:]), S, hq, hkv, hd, tot, kvd, base, 1.0e6, 1.0,
+               stream())
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2), "differs from the two-step path"
+    assert torch.equal(k1[:base].cpu(), kc0[:base]) and torch.equal(k1[base + S:].cpu(), kc0[base + S:])
+    assert torch.equal(q1[:, qd:].cpu(), qkv[:, qd:]), "K / V columns of the QKV buffer untouched"
+    if mode == "mrope":
+        want_q = O.mrope(qkv[:, :qd].reshape(S, hq, hd), pos, sections, 1.0e6)
+        want_k = O.mrope(qkv[:, qd:qd + kvd].reshape(S, hkv, hd), pos, sections, 1.0e6)
+    else:
+        p = base + torch.arange(S)
+        want_q = O.rope_llama(qkv[:, :qd].reshape(S, hq, hd), p, 1.0e6).to(torch.bfloat16)
+        want_k = O.rope_llama(qkv[:, qd:qd + kvd].reshape(S, hkv, hd), p, 1.0e6).to(torch.bfloat16)
+    assert_close_bf16(q1[:, :qd].reshape(S, hq, hd), want_q, rtol=1e-2, atol=1e-2, what="q")
+    assert_close_bf16(k1[base:base + S].reshape(S, hkv, hd), want_k, rtol=1e-2, atol=1e-2, what="k")
+    assert torch.equal(v1[base:base + S].cpu(), qkv[:, qd + kvd:]), "V rows copied"
+
+
 def test_attention_decode_strided_views(gpu):
     """q read from a fused QKV row and K/V from strided views equals contiguous inputs
     (tests/operators/test_attention_prefill.py:167-300)."""
