@@ -362,7 +362,7 @@ template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void decode_merge_kernel(DecodeArgs a, int G) {
     constexpr int NCOL = HD / 4;
     constexpr int NPART = kAttnThreads / NCOL;
-    constexpr int CH = 8;   // loads in flight per thread
+    constexpr int CH = 16;  // loads in flight per thread: up to 128 splits (hd 128) in one round trip
     __shared__ float sw[kMaxSplits];
     __shared__ float4 red[NPART][NCOL];
     const int tid = threadIdx.x;
