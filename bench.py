@@ -220,7 +220,10 @@ def run_c1(args):
     """C1: one decode step of a single Qwen2.5-0.5B-shaped layer (hidden 896, 14/2 heads,
     hd 64, inter 4864), KV cache of 1024 N(0,1) positions, input hidden N(0,1). 16 copies
     of the layer (weights + cache, 485 MB) are rotated so the 256 MB Infinity Cache does
-    not serve the weights."""
+    not serve the weights. The cache follows the engine's convention: rows hold keys
+    rotated at their positions (the prefill rotates them before the cache write), and
+    this step's key, written un-rotated by the QKV projection, is rotated by the attention
+    call (k_already_prerotated = EFM_K_PREROTATED_EXCEPT_NEWEST)."""
     import torch
     import efm_capi as C
     import efm_setup as S
@@ -248,6 +251,7 @@ def run_c1(args):
     res_in = torch.randn(1, H, device=dev, generator=g).to(torch.bfloat16)
     d_len = torch.tensor([max_kv], dtype=torch.int32, device=dev)
     ctx = C.make_attention_ctx(sh.heads, sh.kv_heads, hd)
+    ctx.k_already_prerotated = C.EFM_K_PREROTATED_EXCEPT_NEWEST
     ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=dev)
     r0 = torch.empty(1, H, device=dev, dtype=torch.bfloat16)
     r1 = torch.empty_like(r0)
