@@ -29,6 +29,9 @@ int gemv_swiglu(int64_t K, int64_t inter, const void* x, const void* W, void* y,
 int gemm_bf16(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* bias, void* C,
               int32_t out_dtype, hipStream_t stream);
 int gemm_swiglu(int64_t M, int64_t inter, int64_t K, const void* A, const void* W, void* out, hipStream_t stream);
+size_t gemm_swiglu_workspace_bytes(int64_t M, int64_t inter, int64_t K);
+int gemm_swiglu_ws(int64_t M, int64_t inter, int64_t K, const void* A, const void* W, void* out, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream);
 size_t gemm_bf16_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int gemm_bf16_ws(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* bias, void* C,
                  int32_t out_dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
@@ -74,4 +77,19 @@ extern "C" int efm_fused_gate_up_swiglu(int64_t m, int64_t hidden, int64_t inter
     if (m == 0) return EFM_OK;
     if (m == 1) return gemv_swiglu(hidden, inter, x, w_up_gate, out, stream);
     return gemm_swiglu(m, inter, hidden, x, w_up_gate, out, stream);
+}
+
+extern "C" size_t efm_fused_gate_up_swiglu_workspace_bytes(int64_t m, int64_t hidden, int64_t inter) {
+    if (m <= 1 || hidden <= 0 || inter <= 0) return 0;
+    return gemm_swiglu_workspace_bytes(m, inter, hidden);
+}
+
+extern "C" int efm_fused_gate_up_swiglu_ws(int64_t m, int64_t hidden, int64_t inter, const void* x,
+                                           const void* w_up_gate, void* out, void* workspace, size_t workspace_bytes,
+                                           hipStream_t stream) {
+    if (m < 0 || hidden <= 0 || inter <= 0)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "fused_gate_up_swiglu: bad shape");
+    if (m == 0) return EFM_OK;
+    if (m == 1) return gemv_swiglu(hidden, inter, x, w_up_gate, out, stream);
+    return gemm_swiglu_ws(m, inter, hidden, x, w_up_gate, out, workspace, workspace_bytes, stream);
 }

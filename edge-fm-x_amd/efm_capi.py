@@ -34,6 +34,9 @@ EFM_K_PREROTATED_EXCEPT_NEWEST = 2
 EFM_LAYOUT_GATE_UP = 0
 EFM_LAYOUT_UP_GATE = 1
 
+EFM_GEMM_BACKEND_AUTO = 0
+EFM_GEMM_BACKEND_OWN = 1
+
 
 class AttentionCtx(ctypes.Structure):
     """efm_attention_ctx (mirror of edge_fm::AttentionOpContext)."""
@@ -118,6 +121,11 @@ SIGNATURES = {
     "efm_linear_ws": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_void_p,
                                 c_size_t, c_void_p]),
     "efm_fused_gate_up_swiglu": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "efm_fused_gate_up_swiglu_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
+    "efm_fused_gate_up_swiglu_ws": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                              c_size_t, c_void_p]),
+    "efm_set_gemm_backend": (c_int32, [c_int32]),
+    "efm_get_gemm_backend": (c_int32, []),
     "efm_lm_head_top1_workspace_bytes": (c_size_t, [c_int64]),
     "efm_lm_head_top1": (c_int32, [c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "efm_sampler_greedy_workspace_bytes": (c_size_t, [c_int64, c_int64]),

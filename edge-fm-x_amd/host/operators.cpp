@@ -424,8 +424,11 @@ public:
     bool run(const FusedGateUpActivationContext& c, const Tensor& w, const Tensor& in, Tensor& out,
              hipStream_t s) override {
         if (!supports(c)) return false;  // fast path unavailable -> caller falls back
-        efm_check(efm_fused_gate_up_swiglu(c.m, c.hidden, c.intermediate, in.data_ptr(), w.data_ptr(),
-                                           out.data_ptr(), s),
+        const size_t need = efm_fused_gate_up_swiglu_workspace_bytes(c.m, c.hidden, c.intermediate);
+        size_t have = 0;
+        void* ws = need > 0 ? linear_scratch(need, w.device().second, &have) : nullptr;
+        efm_check(efm_fused_gate_up_swiglu_ws(c.m, c.hidden, c.intermediate, in.data_ptr(), w.data_ptr(),
+                                              out.data_ptr(), ws, have, s),
                   "fused_gate_up_swiglu");
         return true;
     }

@@ -191,7 +191,8 @@ int efm_act_and_mul(int64_t batch, int64_t hidden, int32_t layout, const void* i
 /* ------------------------------------------------------------------------------------
  * Linear: y[m, out] = x[m, in] . W[out, in]^T (+ bias[out]), fp32 accumulate,
  * output bf16 (EFM_DTYPE_BF16) or fp32 (EFM_DTYPE_F32, the LM-head logits).
- * m == 1 runs the bandwidth-bound GEMV, m > 1 the MFMA GEMM.
+ * m == 1 runs the bandwidth-bound GEMV; m > 1 a GEMM: hipBLASLt for bf16 outputs under
+ * EFM_GEMM_BACKEND_AUTO (see efm_set_gemm_backend), else this library's MFMA kernels.
  * Replaces LinearLayer::LinearImpl::forward (src/layers/linear.h:131-153) backed by
  * LinearCublasLtImpl (src/operators/linear_impl.cu:315-480).
  * ---------------------------------------------------------------------------------- */
@@ -199,13 +200,15 @@ int efm_linear(int64_t m, int64_t in_features, int64_t out_features, const void*
                const void* bias, void* y, int32_t out_dtype, hipStream_t stream);
 
 /* efm_linear with a caller workspace (the scratch the reference's linear impls take from
- * StaticBufferManager, src/utils/memory.h:31-109): shapes whose output tiles are too
+ * StaticBufferManager, src/utils/memory.h:31-109). Under EFM_GEMM_BACKEND_AUTO a bf16
+ * output runs hipBLASLt with this workspace available to its algorithm. Otherwise (and
+ * for fp32 outputs), with this library's kernels: shapes whose output tiles are too
  * few to fill the chip and whose K is long (prefill down_proj at a few hundred to a
  * few thousand tokens) split K into slices that write fp32 partial sums into the
  * workspace, then reduce them in slice order. efm_linear_workspace_bytes returns the
- * bytes that enables the split (0: no split for this shape); with less workspace the
- * call runs efm_linear. The split sums K in a different order than efm_linear, so the
- * two agree to fp32 rounding, not bit for bit; each is deterministic. */
+ * bytes that serve both (0: none used for this shape); with less workspace the call
+ * runs as efm_linear does. The split sums K in a different order than efm_linear, so
+ * the two agree to fp32 rounding, not bit for bit; each is deterministic. */
 size_t efm_linear_workspace_bytes(int64_t m, int64_t in_features, int64_t out_features);
 int efm_linear_ws(int64_t m, int64_t in_features, int64_t out_features, const void* x, const void* w,
                   const void* bias, void* y, int32_t out_dtype, void* workspace, size_t workspace_bytes,
@@ -218,6 +221,30 @@ int efm_linear_ws(int64_t m, int64_t in_features, int64_t out_features, const vo
  * gate_up GEMM + act_and_mul fallback (src/layers/gated_mlp.cu:19-67). */
 int efm_fused_gate_up_swiglu(int64_t m, int64_t hidden, int64_t inter, const void* x,
                              const void* w_up_gate, void* out, hipStream_t stream);
+
+/* The same with a caller workspace (efm_fused_gate_up_swiglu_workspace_bytes; 0 means
+ * none is used): for m > 1 under EFM_GEMM_BACKEND_AUTO the [m, 2*inter] product runs as a
+ * plain hipBLASLt GEMM into the workspace (256-byte aligned) and efm_act_and_mul
+ * (EFM_LAYOUT_UP_GATE) forms the output, the reference's two-stage path
+ * (src/layers/gated_mlp.cu:19-67) with the same bf16 roundings of u and g. Without enough
+ * workspace, or under EFM_GEMM_BACKEND_OWN, it is efm_fused_gate_up_swiglu. */
+size_t efm_fused_gate_up_swiglu_workspace_bytes(int64_t m, int64_t hidden, int64_t inter);
+int efm_fused_gate_up_swiglu_ws(int64_t m, int64_t hidden, int64_t inter, const void* x,
+                                const void* w_up_gate, void* out, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream);
+
+/* Prefill GEMM backend (process-wide; no counterpart in the reference, whose prefill
+ * linears call cuBLASLt): EFM_GEMM_BACKEND_AUTO (default) runs the plain bf16-output
+ * GEMMs of efm_linear / efm_linear_ws (m > 1) and the product of
+ * efm_fused_gate_up_swiglu_ws through hipBLASLt, with the library's heuristic first
+ * algorithm for the shape and the workspace given (cached, so a shape and workspace
+ * always run the same algorithm), falling back to this library's MFMA kernels where
+ * hipBLASLt has no algorithm or a pointer is not 16-byte aligned; EFM_GEMM_BACKEND_OWN
+ * runs this library's MFMA kernels only (fp32 outputs always do). */
+#define EFM_GEMM_BACKEND_AUTO 0
+#define EFM_GEMM_BACKEND_OWN 1
+int efm_set_gemm_backend(int32_t backend);
+int32_t efm_get_gemm_backend(void);
 
 /* ------------------------------------------------------------------------------------
  * LM head with fused greedy top-1 (src/layers/linear.cu:140-276, 2288-2369):

@@ -22,6 +22,16 @@ HEAD_CASES = [
 ]
 
 
+@pytest.fixture
+def own_gemm():
+    """Runs a test on this library's MFMA GEMM kernels (EFM_GEMM_BACKEND_OWN), restoring the
+    process-wide backend afterwards."""
+    prev = C.load().efm_get_gemm_backend()
+    C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_OWN)
+    yield
+    C.call("efm_set_gemm_backend", prev)
+
+
 def _decode(ctx, q, k, v, kv_len, d_kv_len=None, max_kv_len=0):
     ws_bytes = C.load().efm_attention_decode_workspace_bytes(ctx, max_kv_len if d_kv_len is not None else kv_len)
     ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=q.device)
@@ -453,7 +463,7 @@ def test_lm_head_top1_negative_scores_edges_and_clean_workspace(gpu):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "swiglu"])
-def test_gemm_tile_shapes_agree_bit_exact(gpu, kind):
+def test_gemm_tile_shapes_agree_bit_exact(gpu, own_gemm, kind):
     """The tile shape follows M: 100 rows run 64 x 64 (SwiGLU 64 x 128), 300 rows
     128 x 64 (SwiGLU 128 x 128), 1344 and 6144 rows 128 x 128 (many tiles per XCD: the
     grouped tile order). Every kernel sums each output over K in the same order, so the
@@ -490,7 +500,7 @@ def test_gemm_tile_shapes_agree_bit_exact(gpu, kind):
     pytest.param(300, 4096, 1000, "bias", id="ragged_bias"),
     pytest.param(200, 8192, 2048, "f32", id="f32"),
 ])
-def test_linear_split_k_matches_unsplit_and_oracle(gpu, m, k, n, kind):
+def test_linear_split_k_matches_unsplit_and_oracle(gpu, own_gemm, m, k, n, kind):
     """efm_linear_ws splits K for these under-filled, long-K shapes: its result equals
     efm_linear to fp32 rounding, is deterministic, matches the oracle on a row sample, and
     with too small a workspace the call is exactly efm_linear."""
@@ -527,13 +537,94 @@ def test_linear_split_k_matches_unsplit_and_oracle(gpu, m, k, n, kind):
         assert_close_bf16(outs[0][rows], exp)
 
 
-def test_linear_workspace_bytes_zero_without_split(gpu):
+def test_linear_workspace_bytes_zero_without_split(gpu, own_gemm):
     lib = C.load()
     assert lib.efm_linear_workspace_bytes(1, 8960, 1536) == 0          # GEMV
     assert lib.efm_linear_workspace_bytes(16384, 18944, 3584) == 0     # enough tiles
     assert lib.efm_linear_workspace_bytes(512, 1536, 1536) == 0        # short K
     assert lib.efm_linear_workspace_bytes(1344, 11008, 2048) == 0      # 176 tiles: no gain
     assert lib.efm_linear_workspace_bytes(512, 8960, 1536) > 0
+
+
+@pytest.mark.parametrize("m,k,n,bias", [
+    pytest.param(1344, 2048, 2560, True, id="c3_qkv"),
+    pytest.param(1344, 11008, 2048, False, id="c3_down"),
+    pytest.param(512, 8960, 1536, False, id="c2_down"),
+    pytest.param(77, 1536, 2048, True, id="ragged_m"),
+    pytest.param(2, 896, 1000, False, id="m2"),
+])
+def test_linear_library_backend_matches_own_kernels_and_oracle(gpu, m, k, n, bias):
+    """EFM_GEMM_BACKEND_AUTO runs the bf16 prefill GEMMs through hipBLASLt: with and without
+    a workspace the result matches this library's MFMA kernels to bf16 rounding (different
+    K summation order), matches the oracle on a row sample, and repeats bit for bit."""
+    assert C.load().efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_AUTO
+    torch.manual_seed(m + n)
+    x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
+    w = (torch.randn(n, k, device=gpu) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(n, device=gpu) * 0.05).to(torch.bfloat16) if bias else None
+    need = C.load().efm_linear_workspace_bytes(m, k, n)
+    ws = torch.full((max(need, 256),), 0x7f, dtype=torch.uint8, device=gpu)
+    outs = []
+    for use_ws in (True, True, False):
+        y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+        if use_ws:
+            C.call("efm_linear_ws", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), C.EFM_DTYPE_BF16, ptr(ws), ws.numel(),
+                   stream())
+        else:
+            C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), C.EFM_DTYPE_BF16, stream())
+        torch.cuda.synchronize()
+        outs.append(y)
+    assert torch.equal(outs[0], outs[1]), "library GEMM is not deterministic"
+    C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_OWN)
+    try:
+        own = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+        C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(own), C.EFM_DTYPE_BF16, stream())
+        torch.cuda.synchronize()
+    finally:
+        C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_AUTO)
+    scale = float(own.float().abs().max())
+    for y in (outs[0], outs[2]):
+        assert torch.isfinite(y.float()).all()
+        assert float((y.float() - own.float()).abs().max()) <= scale * 2 ** -7, "library vs own beyond one bf16 ulp"
+    rows = torch.tensor([0, m // 2, m - 1])
+    exp = O.linear(x[rows].cpu(), w.cpu(), None if b is None else b.cpu())
+    assert_close_bf16(outs[0][rows], exp)
+    assert_close_bf16(outs[2][rows], exp)
+
+
+@pytest.mark.parametrize("m,hidden,inter", [(1344, 2048, 11008), (512, 1536, 8960), (33, 896, 4864)])
+def test_gate_up_swiglu_ws_library_path(gpu, m, hidden, inter):
+    """efm_fused_gate_up_swiglu_ws under EFM_GEMM_BACKEND_AUTO (hipBLASLt product +
+    efm_act_and_mul) equals efm_linear into [m, 2 inter] followed by efm_act_and_mul bit for
+    bit when both get the same library workspace, agrees with the fused MFMA kernel to bf16
+    rounding, and with too little workspace is the fused kernel exactly."""
+    torch.manual_seed(m)
+    x = torch.randn(m, hidden, dtype=torch.bfloat16, device=gpu)
+    w = (torch.randn(2 * inter, hidden, device=gpu) * 0.03).to(torch.bfloat16)
+    need = C.load().efm_fused_gate_up_swiglu_workspace_bytes(m, hidden, inter)
+    gu_bytes = (m * 2 * inter * 2 + 255) // 256 * 256
+    assert need >= gu_bytes
+    ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
+    out = torch.empty(m, inter, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_fused_gate_up_swiglu_ws", m, hidden, inter, ptr(x), ptr(w), ptr(out), ptr(ws), need, stream())
+    gu = torch.empty(m, 2 * inter, dtype=torch.bfloat16, device=gpu)
+    lws = torch.zeros(max(need - gu_bytes, 256), dtype=torch.uint8, device=gpu)
+    C.call("efm_linear_ws", m, hidden, 2 * inter, ptr(x), ptr(w), None, ptr(gu), C.EFM_DTYPE_BF16, ptr(lws),
+           need - gu_bytes, stream())
+    ref = torch.empty_like(out)
+    C.call("efm_act_and_mul", m, inter, C.EFM_LAYOUT_UP_GATE, ptr(gu), ptr(ref), stream())
+    fused = torch.empty_like(out)
+    C.call("efm_fused_gate_up_swiglu", m, hidden, inter, ptr(x), ptr(w), ptr(fused), stream())
+    small = torch.empty_like(out)
+    C.call("efm_fused_gate_up_swiglu_ws", m, hidden, inter, ptr(x), ptr(w), ptr(small), ptr(ws), gu_bytes - 256,
+           stream())
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), "library path differs from linear + act_and_mul"
+    assert torch.equal(small, fused), "too small a workspace must run the fused kernel"
+    diff = (out.float() - fused.float()).abs()
+    assert float(diff.max()) <= float(fused.float().abs().max()) * 2 ** -6
+    rows = torch.tensor([0, m - 1])
+    assert_close_bf16(out[rows], O.gate_up_swiglu(x[rows].cpu(), w.cpu()), rtol=2e-2, atol=6.25e-2)
 
 
 def test_sampler_greedy_ties(gpu):
