@@ -150,6 +150,12 @@ int gemm_lib(int64_t M, int64_t N, int64_t K, const void* A, const void* W, cons
     if (((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(bias) |
           reinterpret_cast<uintptr_t>(workspace)) & 15u) != 0)
         return EFM_ERR_UNSUPPORTED;
+    // Under stream capture the library is not used (its first call per shape creates
+    // handles and plans, and an algorithm may record memory fills into the graph): the
+    // MFMA kernels run instead.
+    hipStreamCaptureStatus cap_status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap_status) != hipSuccess || cap_status != hipStreamCaptureStatusNone)
+        return EFM_ERR_UNSUPPORTED;
     const size_t cap = (workspace == nullptr) ? 0 : std::min(workspace_bytes, kLibMaxWorkspace);
     hipblasLtHandle_t h;
     LibPlan p;

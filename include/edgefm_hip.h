@@ -239,8 +239,9 @@ int efm_fused_gate_up_swiglu_ws(int64_t m, int64_t hidden, int64_t inter, const 
  * efm_fused_gate_up_swiglu_ws through hipBLASLt, with the library's heuristic first
  * algorithm for the shape and the workspace given (cached, so a shape and workspace
  * always run the same algorithm), falling back to this library's MFMA kernels where
- * hipBLASLt has no algorithm or a pointer is not 16-byte aligned; EFM_GEMM_BACKEND_OWN
- * runs this library's MFMA kernels only (fp32 outputs always do). */
+ * hipBLASLt has no algorithm, a pointer is not 16-byte aligned or the stream is being
+ * captured into a graph; EFM_GEMM_BACKEND_OWN runs this library's MFMA kernels only (fp32
+ * outputs always do). */
 #define EFM_GEMM_BACKEND_AUTO 0
 #define EFM_GEMM_BACKEND_OWN 1
 int efm_set_gemm_backend(int32_t backend);

@@ -592,6 +592,38 @@ def test_linear_library_backend_matches_own_kernels_and_oracle(gpu, m, k, n, bia
     assert_close_bf16(outs[2][rows], exp)
 
 
+def test_linear_under_graph_capture_runs_own_kernels(gpu):
+    """A prefill GEMM captured into a HIP graph runs this library's MFMA kernels (the
+    hipBLASLt path stays out of captures): every replay equals an eager
+    EFM_GEMM_BACKEND_OWN call bit for bit, with eager library calls between replays."""
+    torch.manual_seed(5)
+    m, k, n = 96, 1536, 2048
+    x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
+    w = (torch.randn(n, k, device=gpu) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(n, device=gpu) * 0.05).to(torch.bfloat16)
+    C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_OWN)
+    try:
+        own = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+        C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(own), C.EFM_DTYPE_BF16, stream())
+        torch.cuda.synchronize()
+    finally:
+        C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_AUTO)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    st = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st, capture_error_mode="thread_local"):
+        C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), C.EFM_DTYPE_BF16, st.cuda_stream)
+    for rep in range(3):
+        y.fill_(float("nan"))
+        lib = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+        C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(lib), C.EFM_DTYPE_BF16, stream())
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, own), f"replay {rep}"
+        assert float((lib.float() - own.float()).abs().max()) <= float(own.float().abs().max()) * 2 ** -7
+
+
 @pytest.mark.parametrize("m,hidden,inter", [(1344, 2048, 11008), (512, 1536, 8960), (33, 896, 4864)])
 def test_gate_up_swiglu_ws_library_path(gpu, m, hidden, inter):
     """efm_fused_gate_up_swiglu_ws under EFM_GEMM_BACKEND_AUTO (hipBLASLt product +
