@@ -592,6 +592,35 @@ def test_linear_library_backend_matches_own_kernels_and_oracle(gpu, m, k, n, bia
     assert_close_bf16(outs[2][rows], exp)
 
 
+def test_linear_library_falls_back_for_unaligned_output(gpu):
+    """An output pointer that is not 16-byte aligned keeps the GEMM off hipBLASLt: the call
+    equals an EFM_GEMM_BACKEND_OWN call bit for bit (both write through the same offset)."""
+    torch.manual_seed(8)
+    m, k, n = 64, 1024, 1000
+    x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
+    w = (torch.randn(n, k, device=gpu) * 0.02).to(torch.bfloat16)
+    buf = torch.zeros(m * n + 8, dtype=torch.bfloat16, device=gpu)
+    out = buf[1:1 + m * n]                       # 2-byte offset
+    assert out.data_ptr() % 16 != 0
+    C.call("efm_linear", m, k, n, ptr(x), ptr(w), None, ptr(out), C.EFM_DTYPE_BF16, stream())
+    torch.cuda.synchronize()
+    got = out.clone()
+    C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_OWN)
+    try:
+        C.call("efm_linear", m, k, n, ptr(x), ptr(w), None, ptr(out), C.EFM_DTYPE_BF16, stream())
+        torch.cuda.synchronize()
+    finally:
+        C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_AUTO)
+    assert torch.equal(got, out)
+    assert_close_bf16(got.reshape(m, n)[:3], O.linear(x[:3].cpu(), w.cpu()))
+
+
+def test_gemm_backend_setter_rejects_unknown_values(gpu):
+    with pytest.raises(C.EfmError):
+        C.call("efm_set_gemm_backend", 7)
+    assert C.load().efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_AUTO
+
+
 def test_linear_under_graph_capture_runs_own_kernels(gpu):
     """A prefill GEMM captured into a HIP graph runs this library's MFMA kernels (the
     hipBLASLt path stays out of captures): every replay equals an eager
