@@ -26,6 +26,7 @@
 namespace efm {
 
 constexpr size_t kLibMaxWorkspace = 64ull << 20;
+constexpr size_t kLibMaxPlans = 4096;   // cached (shape, workspace) plans before the cache restarts
 
 static std::atomic<int> g_gemm_backend{EFM_GEMM_BACKEND_AUTO};
 
@@ -125,6 +126,7 @@ bool lib_plan(int64_t M, int64_t N, int64_t K, bool has_bias, size_t ws_cap, hip
             }
             hipblasLtMatmulPreferenceDestroy(pref);
         }
+        if (s.plans.size() >= kLibMaxPlans) s.plans.clear();   // bounded: one entry per distinct M
         pit = s.plans.emplace(key, p).first;
     }
     *plan = pit->second;
