@@ -46,3 +46,22 @@ def test_host_side_validation_without_gpu():
     rc = lib.efm_linear(1, 1530, 8, 16, 16, None, 16, C.EFM_DTYPE_BF16, None)
     assert rc == C.EFM_ERR_UNSUPPORTED
     assert lib.efm_attention_decode_workspace_bytes(C.make_attention_ctx(12, 2, 128), 4096) > 0
+
+
+def test_gemm_backend_switch_without_gpu():
+    """The prefill GEMM backend is a process-wide host setting: AUTO by default, OWN on
+    request, unknown values rejected with an argument error."""
+    lib = C.load()
+    assert lib.efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_AUTO
+    try:
+        assert lib.efm_set_gemm_backend(C.EFM_GEMM_BACKEND_OWN) == C.EFM_OK
+        assert lib.efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_OWN
+        # under OWN the workspace query is the split-K need of the MFMA kernels alone
+        assert lib.efm_linear_workspace_bytes(1344, 11008, 2048) == 0
+        assert lib.efm_linear_workspace_bytes(512, 8960, 1536) > 0
+        assert lib.efm_fused_gate_up_swiglu_workspace_bytes(512, 1536, 8960) == 0
+        assert lib.efm_set_gemm_backend(5) == C.EFM_ERR_INVALID_ARGUMENT
+        assert lib.efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_OWN
+    finally:
+        lib.efm_set_gemm_backend(C.EFM_GEMM_BACKEND_AUTO)
+    assert lib.efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_AUTO
