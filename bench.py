@@ -466,7 +466,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the single-request decode path of this build runs on one MI355X; "
-              "multi-GPU sharding is design-only (see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "multi-GPU sharding is a design, not a measured path. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -1,8 +1,8 @@
 """End-to-end GPU tests of the C++ engine (pybind `edge_fm.EdgeFM.generate`) against
 the CPU oracle: greedy token ids are compared step by step with the oracle
 teacher-forced on the GPU's own tokens, so a mismatch is accepted only where the
-oracle's top-1 / chosen-token logit gap is below the bf16 accumulation noise
-(SURVEY "near-tie flip" rule). Mirrors tests/engine/test_qwen2_generate.py of the
+oracle's top-1 / chosen-token logit gap is below the bf16 accumulation noise (a
+near-tie flip). Mirrors tests/engine/test_qwen2_generate.py of the
 reference (HF transformers dumps there; the oracle here is pinned to HF in
 tests/test_oracle.py)."""
 import os
