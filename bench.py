@@ -14,7 +14,10 @@ Extra fields:
                 8 TB/s HBM; `traffic` is read from the committed rocprofv3 --pmc summary.
   decode_loop   algorithmic bytes per decode token / measured ms per token.
   cpu_baseline  the CPU oracle (PyTorch, fp32 math on bf16 values) on this host,
-                same model, a bounded sample (16-token prefill + 48 decode steps).
+                same model and prompt: 512-token prefill, then 8 decode steps at
+                context 513-520 (timed), with nproc, physical cores and CPU model.
+  parity_vs_oracle  the GPU's first 9 greedy tokens against the oracle's argmax at
+                the same steps (teacher-forced), near-tie rule stated in the line.
 """
 import argparse
 import json
@@ -131,6 +134,81 @@ def kernel_only(torch, C, S, shape, seed):
     print(json.dumps({"kernel_only": ROOFLINE_KERNEL, "launches": 2 * shape.layers,
                       "bytes_per_launch": gate_up_bytes(shape), "copy_calibration_bytes": 256 << 20}))
 
+
+
+def host_cpu_info(torch):
+    """Host CPU facts for the cpu_baseline line: model name, logical CPUs, physical
+    cores (distinct (package, core) pairs in /proc/cpuinfo) and torch's thread count."""
+    model, pairs, phys, core = "unknown", set(), None, None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model == "unknown":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None and core is not None:
+                    pairs.add((phys, core))
+                    phys = core = None
+        if phys is not None and core is not None:
+            pairs.add((phys, core))
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": affinity,
+            "physical_cores": len(pairs) or None, "torch_threads": torch.get_num_threads()}
+
+
+def c2_cpu_baseline(torch, shape, weights, prompt, gpu_tokens, n_dec=8):
+    """The CPU oracle (PyTorch fp32 math on bf16 values) on this host, on the benchmark's
+    own model and prompt: the 512-token prefill (timed separately), then n_dec decode
+    steps at context 513.. teacher-forced with the GPU's tokens (timed: decode tokens/s).
+    Returns (cpu_baseline, parity): parity compares the GPU's first n_dec + 1 greedy
+    tokens with the oracle's argmax at the same step; a differing token is accepted only
+    as a near tie (oracle top-1 minus the GPU token's logit below 0.05)."""
+    from oracle import efm_oracle as O
+
+    ocfg = O.QwenConfig(hidden=shape.hidden, layers=shape.layers, heads=shape.heads, kv_heads=shape.kv_heads,
+                        head_dim=shape.head_dim, inter=shape.inter, vocab=shape.vocab)
+    wcpu = {k: v.cpu() for k, v in weights.items()}
+    orc = O.Qwen2Oracle(ocfg, O.fuse_weights(ocfg, wcpu), max_tokens=len(prompt) + n_dec + 8, cache_f32=True)
+    del wcpu
+    st = orc.new_state()
+    c0 = time.perf_counter()
+    logits = orc.forward(st, torch.tensor(prompt, dtype=torch.int32))
+    pf_s = time.perf_counter() - c0
+    steps = []
+
+    def judge(lg, tok):
+        ref = int(O.argmax_lowest(lg.unsqueeze(0))[0])
+        steps.append((tok, ref, float(lg[ref] - lg[tok])))
+
+    judge(logits, gpu_tokens[0])
+    dec_s = 0.0
+    for i in range(n_dec):
+        c0 = time.perf_counter()
+        logits = orc.forward(st, torch.tensor([gpu_tokens[i]], dtype=torch.int32))
+        dec_s += time.perf_counter() - c0
+        judge(logits, gpu_tokens[i + 1])
+    exact = sum(1 for t, r, _ in steps if t == r)
+    worst = max((gap for t, r, gap in steps if t != r), default=0.0)
+    parity = {"steps": len(steps), "exact": exact, "near_tie_flips": len(steps) - exact,
+              "max_gap_of_flips": round(worst, 5), "ok": worst < 0.05,
+              "rule": "GPU greedy token == oracle argmax, or oracle logit gap < 0.05 (bf16 near tie)"}
+    info = host_cpu_info(torch)
+    cpu = {"value": round(n_dec / dec_s, 3), "unit": "tokens/s", "cores": info["torch_threads"], "kind": "port",
+           "sample": f"CPU oracle (PyTorch fp32 math on bf16 values), same 1.5B-shaped weights and 512-token prompt; "
+                     f"{n_dec} decode steps at context {len(prompt) + 1}-{len(prompt) + n_dec}, teacher-forced with "
+                     f"the GPU's tokens; decode tokens/s",
+           "prefill_tokens_per_s": round(len(prompt) / pf_s, 2), **info}
+    return cpu, parity
 
 
 # ---------------------------------------------------------------------------------
@@ -385,7 +463,8 @@ def run_c5(args):
     H, I, L, V = shape.hidden, shape.inter, shape.layers, shape.vocab
     per_layer = ((shape.q_dim + 2 * shape.kv_dim) * (H + 1) + shape.q_dim * H + 3 * I * H + 2 * H) * 2
     mean_ctx = P + (G + 1) / 2.0
-    nbytes = L * per_layer + V * H * 2 * 2 + H * 2 + 2 * mean_ctx * shape.kv_dim * 2 * L
+    # untied LM head read whole, one embedding row, final norm weight, K/V at the mean context
+    nbytes = L * per_layer + V * H * 2 + H * 2 + H * 2 + 2 * mean_ctx * shape.kv_dim * 2 * L
     gbs = nbytes * tps / 1e9
     print(json.dumps({
         "metric": "bs=1 decode tokens/s, Qwen2.5-7B shape at 16k context, top-p 0.9 / T 0.7 sampling (C5)",
@@ -459,6 +538,7 @@ def main():
     ap.add_argument("--gen", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=8, help="decode steps the C2 CPU baseline times")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                     help="BASELINE configuration (default c2, the headline decode benchmark)")
     ap.add_argument("--kernel-only", action="store_true",
@@ -520,26 +600,10 @@ def main():
 
     kern = roofline_kernel(torch, C, shape, weights, dev, graph=True)
 
-    # ---- CPU baseline: the oracle on this host, bounded sample
-    cpu = None
+    # ---- CPU baseline: the oracle on this host, bounded sample at the benchmark's context
+    cpu, parity = None, None
     if not args.no_cpu_baseline:
-        from oracle import efm_oracle as O
-
-        ocfg = O.QwenConfig(hidden=shape.hidden, layers=shape.layers, heads=shape.heads, kv_heads=shape.kv_heads,
-                            head_dim=shape.head_dim, inter=shape.inter, vocab=shape.vocab)
-        wcpu = {k: v.cpu() for k, v in weights.items()}
-        orc = O.Qwen2Oracle(ocfg, O.fuse_weights(ocfg, wcpu), max_tokens=16 + 48 + 8, cache_f32=True)
-        del wcpu
-        st = orc.new_state()
-        orc.forward(st, torch.tensor(prompt[:16], dtype=torch.int32))
-        n_dec = 48
-        c0 = time.perf_counter()
-        for i in range(n_dec):
-            orc.forward(st, torch.tensor([toks[i]], dtype=torch.int32))
-        c_s = time.perf_counter() - c0
-        cpu = {"value": round(n_dec / c_s, 3), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-               "sample": f"CPU oracle (PyTorch fp32 math on bf16 values), same 1.5B-shaped weights, 16-token "
-                         f"prefill then {n_dec} decode steps at context 17-{16 + n_dec}; decode tokens/s"}
+        cpu, parity = c2_cpu_baseline(torch, shape, weights, prompt, toks, n_dec=args.cpu_steps)
 
     line = {
         "metric": "bs=1 decode tokens/s (Qwen2.5-1.5B shape, greedy, 512-token prompt + 256 generated)",
@@ -565,6 +629,7 @@ def main():
         "roofline": kern,
         "cpu_baseline": cpu,
         "tokens_head": toks[:8],
+        "parity_vs_oracle": parity,
     }
     print(json.dumps(line))
     del eng

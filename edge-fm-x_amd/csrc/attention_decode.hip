@@ -569,8 +569,7 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
     dim3 grid(a.split_cap, ctx->num_kv_heads), block(kAttnThreads);
     // one split: that workgroup writes the output; more: partials, then the merge kernel
     const bool direct = merge && a.split_cap == 1;
-    const char* lds_env = getenv("EFM_DECODE_LDS");
-    if (hd == 128 && !rotk && (lds_env == nullptr || lds_env[0] != '0')) {
+    if (hd == 128 && !rotk && kernel_knob(EFM_KNOB_DECODE_REGISTER) == 0) {
 #define EFM_DEC_LDS_CASE(GV)                                                                                   \
         if (G == GV) {                                                                                         \
             if (direct) hipLaunchKernelGGL((decode_attn_lds_kernel<GV, true>), grid, block, 0, stream, a);     \

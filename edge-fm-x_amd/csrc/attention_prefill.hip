@@ -529,12 +529,9 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kerne
 
 int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
 
-// EFM_PREFILL_PIPE=0 selects the register-staged kernel (kept as the reference path of
-// the pipelined one in the tests).
-static bool prefill_pipe_enabled() {
-    const char* e = getenv("EFM_PREFILL_PIPE");
-    return e == nullptr || e[0] != '0';
-}
+// EFM_KNOB_PREFILL_REGISTER selects the register-staged kernel (kept as the reference
+// path of the pipelined one in the tests).
+static bool prefill_pipe_enabled() { return kernel_knob(EFM_KNOB_PREFILL_REGISTER) == 0; }
 
 }  // namespace efm
 
@@ -581,9 +578,9 @@ extern "C" int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q
         // up to 8K rows: 4 waves (128 rows) over a 2-deep ring, two workgroups per CU
         // (twice the workgroups, and the two drift out of phase so that one's softmax
         // overlaps the other's matrix work); longer: 8 waves (256 rows) over a 4-deep
-        // ring, one per CU. EFM_PREFILL_SHAPE=4 / 8 forces one of them.
-        const char* shape = getenv("EFM_PREFILL_SHAPE");
-        const bool small = (shape != nullptr && shape[0] != '\0') ? shape[0] == '4' : qo_len <= 8192;
+        // ring, one per CU. EFM_KNOB_PREFILL_SHAPE = 4 / 8 forces one of them.
+        const int shape = kernel_knob(EFM_KNOB_PREFILL_SHAPE);
+        const bool small = shape != 0 ? shape == 4 : qo_len <= 8192;
         if (small) {
             const int nqt = (int)((qo_len + 127) / 128);
             hipLaunchKernelGGL((prefill_attn_pipe_kernel<4, 2>), dim3(nqt * a.Hq), dim3(256), 0, stream, a, nqt);

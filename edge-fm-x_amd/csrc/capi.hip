@@ -2,10 +2,17 @@
 // GEMV (m == 1) and the prefill MFMA GEMM (m > 1).
 #include "common.hpp"
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 
 namespace efm {
+
+static std::atomic<int> g_knobs[EFM_KNOB_COUNT];
+
+int kernel_knob(int knob) {
+    return (knob >= 0 && knob < EFM_KNOB_COUNT) ? g_knobs[knob].load(std::memory_order_relaxed) : 0;
+}
 
 static thread_local char g_last_error[512] = "";
 
@@ -42,7 +49,17 @@ using namespace efm;
 
 extern "C" const char* efm_last_error(void) { return g_last_error; }
 
-extern "C" const char* efm_version(void) { return "edgefm-hip 0.1.0 gfx950"; }
+extern "C" const char* efm_version(void) { return "edgefm-hip 0.2.0 gfx950"; }
+
+extern "C" int efm_testing_set_kernel_path(int32_t knob, int32_t value) {
+    if (knob < 0 || knob >= EFM_KNOB_COUNT)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "testing_set_kernel_path: unknown knob %d", knob);
+    const bool ok = (knob == EFM_KNOB_PREFILL_SHAPE) ? (value == 0 || value == 4 || value == 8)
+                                                    : (value == 0 || value == 1);
+    if (!ok) return set_error(EFM_ERR_INVALID_ARGUMENT, "testing_set_kernel_path: bad value %d for knob %d", value, knob);
+    g_knobs[knob].store(value, std::memory_order_relaxed);
+    return EFM_OK;
+}
 
 extern "C" int efm_linear(int64_t m, int64_t in_features, int64_t out_features, const void* x, const void* w,
                           const void* bias, void* y, int32_t out_dtype, hipStream_t stream) {

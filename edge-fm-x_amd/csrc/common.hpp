@@ -205,4 +205,7 @@ __device__ __forceinline__ void tagged_publish(uint32_t* p, uint32_t tag, uint32
 namespace efm {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Kernel-path override set through efm_testing_set_kernel_path (EFM_KNOB_*); 0 = the
+// library's own choice.
+int kernel_knob(int knob);
 }  // namespace efm

@@ -530,24 +530,11 @@ static int gemm_check(int64_t M, int64_t N, int64_t K, const void* A, const void
     return EFM_OK;
 }
 
-// Plain GEMMs through hipBLASLt (gemm_lib.hip): taken for bf16 outputs under
-// EFM_GEMM_BACKEND_AUTO; EFM_ERR_UNSUPPORTED from it means "no library algorithm for this
-// shape or these pointers", and this file's kernels run instead.
-bool gemm_lib_applies(int32_t out_dtype);
-size_t gemm_lib_workspace_bytes(int64_t M, int64_t N, int64_t K);
-int gemm_lib(int64_t M, int64_t N, int64_t K, const void* A, const void* W, const void* bias, void* C,
-             void* workspace, size_t workspace_bytes, hipStream_t stream);
-int gemm_backend();
-
 int gemm_bf16(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* bias, void* C,
               int32_t out_dtype, hipStream_t stream) {
     int rc = gemm_check(M, N, K, A, B, C);
     if (rc) return rc;
     if (M == 0 || N == 0) return EFM_OK;
-    if (gemm_lib_applies(out_dtype)) {
-        rc = gemm_lib(M, N, K, A, B, bias, C, nullptr, 0, stream);
-        if (rc != EFM_ERR_UNSUPPORTED) return rc;
-    }
     const bf16_t* a = static_cast<const bf16_t*>(A);
     const bf16_t* b = static_cast<const bf16_t*>(B);
     const bf16_t* bi = static_cast<const bf16_t*>(bias);
@@ -558,9 +545,7 @@ int gemm_bf16(int64_t M, int64_t N, int64_t K, const void* A, const void* B, con
 
 size_t gemm_bf16_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     if (M <= 1 || M > 0x7fffffff / 2 || N > 0x7fffffff / 2 || K > 0x7fffffff / 2) return 0;
-    const size_t own = splitk_bytes((int)M, (int)N, (int)K);   // also what fp32 outputs use
-    if (gemm_backend() != EFM_GEMM_BACKEND_AUTO) return own;
-    return std::max(own, gemm_lib_workspace_bytes(M, N, K));
+    return splitk_bytes((int)M, (int)N, (int)K);
 }
 
 int gemm_bf16_ws(int64_t M, int64_t N, int64_t K, const void* A, const void* B, const void* bias, void* C,
@@ -570,10 +555,6 @@ int gemm_bf16_ws(int64_t M, int64_t N, int64_t K, const void* A, const void* B, 
     if (M == 0 || N == 0) return EFM_OK;
     if (out_dtype != EFM_DTYPE_BF16 && out_dtype != EFM_DTYPE_F32)
         return set_error(EFM_ERR_UNSUPPORTED, "linear: output dtype %d not supported", out_dtype);
-    if (gemm_lib_applies(out_dtype)) {
-        rc = gemm_lib(M, N, K, A, B, bias, C, workspace, workspace_bytes, stream);
-        if (rc != EFM_ERR_UNSUPPORTED) return rc;
-    }
     const SplitK p = splitk_plan((int)M, (int)N, (int)K);
     const size_t need = (p.ksplit == 0) ? 0 : (size_t)p.ksplit * M * N * sizeof(float);
     if (p.ksplit == 0 || workspace == nullptr || workspace_bytes < need ||
@@ -593,32 +574,12 @@ int gemm_swiglu(int64_t M, int64_t inter, int64_t K, const void* A, const void* 
                                       static_cast<const bf16_t*>(W), nullptr, out, (int)inter, stream);
 }
 
-// Gate/up + SwiGLU with a workspace: under EFM_GEMM_BACKEND_AUTO the plain [M, 2 inter]
-// product runs through hipBLASLt into the workspace and the SiLU-and-mul kernel reads it
-// (the reference's two-stage fallback, src/layers/gated_mlp.cu:19-67; same bf16
-// roundings of u and g as the fused epilogue); otherwise, or without enough workspace,
-// the fused MFMA kernel.
-static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+// Gate/up + SwiGLU with a workspace: the SwiGLU is the MFMA kernel's epilogue, so no
+// shape uses the workspace.
+size_t gemm_swiglu_workspace_bytes(int64_t, int64_t, int64_t) { return 0; }
 
-size_t gemm_swiglu_workspace_bytes(int64_t M, int64_t inter, int64_t K) {
-    if (M <= 1 || gemm_backend() != EFM_GEMM_BACKEND_AUTO || M > 0x7fffffff / 2 || inter > 0x3fffffff / 2)
-        return 0;
-    return align256((size_t)M * 2 * inter * sizeof(bf16_t)) + gemm_lib_workspace_bytes(M, 2 * inter, K);
-}
-
-int gemm_swiglu_ws(int64_t M, int64_t inter, int64_t K, const void* A, const void* W, void* out, void* workspace,
-                   size_t workspace_bytes, hipStream_t stream) {
-    int rc = gemm_check(M, inter, K, A, W, out);
-    if (rc) return rc;
-    if (M == 0) return EFM_OK;
-    const size_t gu = align256((size_t)M * 2 * inter * sizeof(bf16_t));
-    if (gemm_backend() == EFM_GEMM_BACKEND_AUTO && workspace != nullptr && workspace_bytes >= gu &&
-        (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0) {
-        rc = gemm_lib(M, 2 * inter, K, A, W, nullptr, workspace, static_cast<char*>(workspace) + gu,
-                      workspace_bytes - gu, stream);
-        if (rc == EFM_OK) return efm_act_and_mul(M, inter, EFM_LAYOUT_UP_GATE, workspace, out, stream);
-        if (rc != EFM_ERR_UNSUPPORTED) return rc;
-    }
+int gemm_swiglu_ws(int64_t M, int64_t inter, int64_t K, const void* A, const void* W, void* out, void*, size_t,
+                   hipStream_t stream) {
     return gemm_swiglu(M, inter, K, A, W, out, stream);
 }
 

@@ -693,8 +693,7 @@ extern "C" int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, con
     float* sk = reinterpret_cast<float*>(p + w.q8 + w.k8 + w.sq);
     float* km = reinterpret_cast<float*>(p + w.q8 + w.k8 + w.sq + w.sk);
     const int hd = (int)ctx->head_dim;
-    const char* pipe_env = getenv("EFM_PREFILL_PIPE");
-    const bool pipe = hd == kSPHD && (pipe_env == nullptr || pipe_env[0] != '0');
+    const bool pipe = hd == kSPHD && kernel_knob(EFM_KNOB_PREFILL_REGISTER) == 0;
     // the pipelined kernel quantises Q itself (one 128-row block per 4 waves)
     rc = sage_quantize_impl(ctx, q, k, qo_len, kv_len, q8, sq, k8, sk, km, stream, !pipe);
     if (rc) return rc;
@@ -719,8 +718,8 @@ extern "C" int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, con
     if (pipe) {
         // as the bf16 kernel: 4 waves / two workgroups per CU up to 8K rows (a 3-deep ring
         // of 24 KB stages fits twice), 8 waves over a 4-deep ring beyond
-        const char* shape = getenv("EFM_PREFILL_SHAPE");
-        const bool small = (shape != nullptr && shape[0] != '\0') ? shape[0] == '4' : qo_len <= 8192;
+        const int shape = kernel_knob(EFM_KNOB_PREFILL_SHAPE);
+        const bool small = shape != 0 ? shape == 4 : qo_len <= 8192;
         if (small) {
             const int nqt = (int)((qo_len + 127) / 128);
             hipLaunchKernelGGL((sage_attn_pipe_kernel<4, 3>), dim3(nqt * a.Hq), dim3(256), 0, stream, a, nqt);

@@ -34,8 +34,9 @@ EFM_K_PREROTATED_EXCEPT_NEWEST = 2
 EFM_LAYOUT_GATE_UP = 0
 EFM_LAYOUT_UP_GATE = 1
 
-EFM_GEMM_BACKEND_AUTO = 0
-EFM_GEMM_BACKEND_OWN = 1
+EFM_KNOB_DECODE_REGISTER = 0
+EFM_KNOB_PREFILL_REGISTER = 1
+EFM_KNOB_PREFILL_SHAPE = 2
 
 
 class AttentionCtx(ctypes.Structure):
@@ -124,8 +125,7 @@ SIGNATURES = {
     "efm_fused_gate_up_swiglu_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
     "efm_fused_gate_up_swiglu_ws": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
                                               c_size_t, c_void_p]),
-    "efm_set_gemm_backend": (c_int32, [c_int32]),
-    "efm_get_gemm_backend": (c_int32, []),
+    "efm_testing_set_kernel_path": (c_int32, [c_int32, c_int32]),
     "efm_lm_head_top1_workspace_bytes": (c_size_t, [c_int64]),
     "efm_lm_head_top1": (c_int32, [c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "efm_sampler_greedy_workspace_bytes": (c_size_t, [c_int64, c_int64]),

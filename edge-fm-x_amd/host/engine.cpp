@@ -1,4 +1,5 @@
 #include "engine.hpp"
+#include "roctx_range.hpp"
 
 #include <dlfcn.h>
 #include <fcntl.h>
@@ -11,6 +12,7 @@
 #include <chrono>
 #include <cstring>
 #include <filesystem>
+#include <optional>
 #include <fstream>
 #include <set>
 #include <unordered_set>
@@ -802,12 +804,34 @@ struct EventTimer {
         hipEventDestroy(a);
         hipEventDestroy(b);
     }
-    double ms() {
+    double ms() { return between(a, b); }
+    static double between(hipEvent_t x, hipEvent_t y) {
         float t = 0.f;
-        hip_check(hipEventElapsedTime(&t, a, b), "event elapsed");
+        hip_check(hipEventElapsedTime(&t, x, y), "event elapsed");
         return t;
     }
 };
+
+// Per-stage GPU time of the eager decode loop: events recorded between the model, the
+// sampler and the finalize of every step, summed after the loop's one synchronisation
+// (the reference's GenerateMetricsAccum, standard_engine.cpp:420-460).
+struct StageEvents {
+    std::vector<hipEvent_t> ev;
+    ~StageEvents() {
+        for (hipEvent_t e : ev) hipEventDestroy(e);
+    }
+    hipEvent_t record(hipStream_t s) {
+        hipEvent_t e = nullptr;
+        hip_check(hipEventCreate(&e), "event");
+        ev.push_back(e);
+        hip_check(hipEventRecord(e, s), "event");
+        return e;
+    }
+};
+
+double host_ms_since(std::chrono::steady_clock::time_point t0) {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
 }  // namespace
 
 StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_path), compact_vocab_(cfg_) {
@@ -896,7 +920,8 @@ void StandardEngine::sample_logits(uint32_t) {
               "top-p sampler");
 }
 
-void StandardEngine::run_decode_step(int32_t request_id, bool) {
+void StandardEngine::run_decode_step(int32_t request_id, void* stage_events) {
+    StageEvents* se = static_cast<StageEvents*>(stage_events);
     int32_t* st = static_cast<int32_t*>(state_.data_ptr());
     uint32_t* d_kv_len = reinterpret_cast<uint32_t*>(st + 0);
     uint32_t* d_step = reinterpret_cast<uint32_t*>(st + 1);
@@ -905,17 +930,30 @@ void StandardEngine::run_decode_step(int32_t request_id, bool) {
     KVSlot& slot = kv_->slot(request_id);
     auto kc = caches(request_id, true), vc = caches(request_id, false);
     const bool greedy_fused = cfg_.temperature() < 1e-6f && cfg_.lm_head_top1();
-    model_->decode_step(tok, d_kv_len, (uint32_t)slot.cfg.max_tokens, pos3, kc.data(), vc.data(),
-                        greedy_fused ? nullptr : static_cast<float*>(logits_.data_ptr()), stream_);
-    if (!greedy_fused) sample_logits(0);
+    if (se) se->record(stream_);
+    {
+        RoctxRange r(se ? "EDGEFM_DECODE_MODEL" : nullptr);
+        model_->decode_step(tok, d_kv_len, (uint32_t)slot.cfg.max_tokens, pos3, kc.data(), vc.data(),
+                            greedy_fused ? nullptr : static_cast<float*>(logits_.data_ptr()), stream_);
+    }
+    if (se) se->record(stream_);
+    if (!greedy_fused) {
+        RoctxRange r(se ? "EDGEFM_DECODE_SAMPLER" : nullptr);
+        sample_logits(0);
+    }
+    if (se) se->record(stream_);
     efm_check(efm_finalize_decode_token_indexed(tok, static_cast<int32_t*>(response_dev_.data_ptr()), d_step, d_kv_len,
                                                 (uint32_t)response_dev_.numel(), stream_),
               "finalize decode token");
     if (model_->config().mrope) efm_check(efm_increment_int32_triplet(st + 3, stream_), "advance mrope position");
+    if (se) se->record(stream_);
 }
 
 Response StandardEngine::generate(const Request& request) {
+    RoctxRange generate_range("EDGEFM_GENERATE");
     hip_check(hipSetDevice(device_id_), "hipSetDevice");
+    const auto prep_t0 = std::chrono::steady_clock::now();
+    std::optional<RoctxRange> prepare_range(std::in_place, "EDGEFM_PREFILL_PREPARE");
     // compact vocabulary: the request is remapped into the checkpoint's ids and the
     // response restored (standard_engine.cpp:877-882,1070-1072)
     std::unique_ptr<Request> remapped;
@@ -938,7 +976,12 @@ Response StandardEngine::generate(const Request& request) {
     int32_t base = 0;
     if (slot.prefix_size > 0 && n_ids > slot.prefix_size &&
         std::equal(slot.cfg.prefix_token_ids.begin(), slot.cfg.prefix_token_ids.end(), req.token_ids.begin())) {
+        // a request that did not start with the prefix overwrote its rows: restore them first
+        if (!slot.prefix_ready) warmup();
         base = slot.prefix_size;
+    } else if (slot.prefix_size > 0) {
+        // this prefill writes rows [0, n_ids) over the stored prefix
+        slot.prefix_ready = false;
     }
     const int32_t S = n_ids - base;
     // max_generated = min(max_new_tokens, max_tokens - len(ids) + 1) (scheduler.cpp:123-134)
@@ -996,27 +1039,46 @@ Response StandardEngine::generate(const Request& request) {
     int32_t init[6] = {base + S, 0, 0, last_pos[0] + 1, last_pos[1] + 1, last_pos[2] + 1};
     hip_check(hipMemcpyAsync(st, init, sizeof(init), hipMemcpyHostToDevice, stream_), "decode state H2D");
 
+    const double prefill_prepare_host_ms = host_ms_since(prep_t0);
+    prepare_range.reset();
+
+    EventTimer pf_model;  // pf.a .. pf_model.b: model; pf_model.b .. pf.b: sampler + finalize
     hip_check(hipEventRecord(pf.a, stream_), "event");
     const bool greedy_fused = cfg_.temperature() < 1e-6f && cfg_.lm_head_top1();
-    model_->prefill(S, base, static_cast<int32_t*>(ids_dev_.data_ptr()), emb.empty() ? nullptr : &emb,
-                    req.embed_token_id, pos.empty() ? nullptr : static_cast<int32_t*>(pos.data_ptr()), kc.data(),
-                    vc.data(), st + 2, greedy_fused ? nullptr : static_cast<float*>(logits_.data_ptr()), stream_);
-    if (!greedy_fused) sample_logits(0);
-    efm_check(efm_finalize_decode_token_indexed(st + 2, static_cast<int32_t*>(response_dev_.data_ptr()),
-                                                reinterpret_cast<uint32_t*>(st + 1), reinterpret_cast<uint32_t*>(st),
-                                                (uint32_t)response_dev_.numel(), stream_),
-              "finalize prefill token");
+    {
+        RoctxRange prefill_range("EDGEFM_PREFILL");
+        {
+            RoctxRange model_range("EDGEFM_PREFILL_MODEL");
+            model_->prefill(S, base, static_cast<int32_t*>(ids_dev_.data_ptr()), emb.empty() ? nullptr : &emb,
+                            req.embed_token_id, pos.empty() ? nullptr : static_cast<int32_t*>(pos.data_ptr()),
+                            kc.data(), vc.data(), st + 2,
+                            greedy_fused ? nullptr : static_cast<float*>(logits_.data_ptr()), stream_);
+        }
+        hip_check(hipEventRecord(pf_model.b, stream_), "event");
+        RoctxRange sampler_range("EDGEFM_PREFILL_SAMPLER");
+        if (!greedy_fused) sample_logits(0);
+        efm_check(efm_finalize_decode_token_indexed(st + 2, static_cast<int32_t*>(response_dev_.data_ptr()),
+                                                    reinterpret_cast<uint32_t*>(st + 1),
+                                                    reinterpret_cast<uint32_t*>(st), (uint32_t)response_dev_.numel(),
+                                                    stream_),
+                  "finalize prefill token");
+    }
     hip_check(hipEventRecord(pf.b, stream_), "event");
 
+    const auto dprep_t0 = std::chrono::steady_clock::now();
+    double decode_prepare_host_ms = 0.0;
+    StageEvents stage;
     hip_check(hipEventRecord(dc.a, stream_), "event");
     const int32_t steps = n_gen - 1;
     if (steps > 0) {
+        RoctxRange decode_range("EDGEFM_GENERATION");
         if (cfg_.use_graph()) {
             GraphEntry& g = graphs_[req.request_id];
             if (g.exec == nullptr) {
+                RoctxRange capture_range("EDGEFM_DECODE_PREPARE");
                 hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
                 try {
-                    run_decode_step(req.request_id, true);
+                    run_decode_step(req.request_id, nullptr);
                 } catch (...) {
                     hipGraph_t tmp = nullptr;
                     hipStreamEndCapture(stream_, &tmp);
@@ -1026,20 +1088,30 @@ Response StandardEngine::generate(const Request& request) {
                 hip_check(hipStreamEndCapture(stream_, &g.graph), "end capture");
                 hip_check(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0), "graph instantiate");
             }
+            decode_prepare_host_ms = host_ms_since(dprep_t0);
+            RoctxRange replay_range("EDGEFM_DECODE_GRAPH_REPLAY");
             for (int32_t i = 0; i < steps; ++i) hip_check(hipGraphLaunch(g.exec, stream_), "graph launch");
         } else {
-            for (int32_t i = 0; i < steps; ++i) run_decode_step(req.request_id, false);
+            for (int32_t i = 0; i < steps; ++i) run_decode_step(req.request_id, &stage);
         }
     }
     hip_check(hipEventRecord(dc.b, stream_), "event");
 
     std::vector<int32_t> host((size_t)n_gen);
-    hip_check(hipMemcpyAsync(host.data(), response_dev_.data_ptr(), (size_t)n_gen * 4, hipMemcpyDeviceToHost, stream_),
-              "response D2H");
-    hip_check(hipStreamSynchronize(stream_), "generate sync");
+    EventTimer copy;
+    {
+        RoctxRange copy_range("EDGEFM_RESPONSE_COPY");
+        hip_check(hipEventRecord(copy.a, stream_), "event");
+        hip_check(hipMemcpyAsync(host.data(), response_dev_.data_ptr(), (size_t)n_gen * 4, hipMemcpyDeviceToHost,
+                                 stream_),
+                  "response D2H");
+        hip_check(hipEventRecord(copy.b, stream_), "event");
+        hip_check(hipStreamSynchronize(stream_), "generate sync");
+    }
     model_->check_decode_status(stream_);
 
     // stop tokens truncate after the first hit, inclusive (standard_engine.cpp:1060-1068)
+    const auto stop_t0 = std::chrono::steady_clock::now();
     if (!req.ignore_stop_tokens) {
         std::unordered_set<int32_t> stop;
         for (int32_t t : compact_vocab_.remap_required_token_ids(cfg_.eos_token_ids(), "model eos_token_ids"))
@@ -1053,19 +1125,45 @@ Response StandardEngine::generate(const Request& request) {
                 break;
             }
     }
+    const double stop_check_host_ms = host_ms_since(stop_t0);
     const double prefill_ms = pf.ms(), decode_ms = dc.ms();
+    // eager decode: per-step model / sampler / finalize spans (four events per step)
+    double d_model = 0.0, d_sampler = 0.0, d_finalize = 0.0;
+    for (size_t i = 0; i + 3 < stage.ev.size(); i += 4) {
+        d_model += EventTimer::between(stage.ev[i], stage.ev[i + 1]);
+        d_sampler += EventTimer::between(stage.ev[i + 1], stage.ev[i + 2]);
+        d_finalize += EventTimer::between(stage.ev[i + 2], stage.ev[i + 3]);
+    }
+    const bool graph = cfg_.use_graph() && steps > 0;
+    const double returned = (double)host.size();
+    const double returned_steps = std::max(0.0, returned - 1.0);
+    // the reference's keys (standard_engine.cpp:462-507), then this engine's own
     metrics_["prefill_ms"] = prefill_ms;
     metrics_["decode_ms"] = decode_ms;
     metrics_["total_stage_ms"] = prefill_ms + decode_ms;
-    metrics_["decode_steps"] = steps;
     metrics_["decode_step_avg_ms"] = steps > 0 ? decode_ms / steps : 0.0;
-    metrics_["generated_tokens_total"] = n_gen;
-    metrics_["returned_tokens"] = (double)host.size();
+    metrics_["generated_tokens_total"] = returned;
+    metrics_["decode_steps"] = steps;
+    metrics_["prefill_prepare_host_ms"] = prefill_prepare_host_ms;
+    metrics_["prefill_model_ms"] = EventTimer::between(pf.a, pf_model.b);
+    metrics_["prefill_sampler_ms"] = EventTimer::between(pf_model.b, pf.b);
+    metrics_["decode_prepare_host_ms"] = decode_prepare_host_ms;
+    metrics_["decode_graph_replay_ms"] = graph ? decode_ms : 0.0;
+    metrics_["decode_model_ms"] = d_model;
+    metrics_["decode_sampler_ms"] = d_sampler;
+    metrics_["decode_finalize_ms"] = d_finalize;
+    metrics_["stop_check_host_ms"] = stop_check_host_ms;
+    metrics_["response_copy_ms"] = copy.ms();
+    metrics_["tokens_per_second"] = (prefill_ms + decode_ms) > 0 ? returned * 1000.0 / (prefill_ms + decode_ms) : 0.0;
+    metrics_["decode_tokens_per_second"] = decode_ms > 0 ? returned_steps * 1000.0 / decode_ms : 0.0;
+    metrics_["executed_generated_tokens_total"] = n_gen;
+    metrics_["returned_generated_tokens_total"] = returned;
+    metrics_["cuda_graph_enabled"] = cfg_.use_graph() ? 1.0 : 0.0;
+    metrics_["lm_head_top1_enabled"] = greedy_fused ? 1.0 : 0.0;
+    metrics_["lm_head_top1_decode_steps"] = greedy_fused ? steps : 0.0;
+    metrics_["response_tokens_capacity"] = (double)response_dev_.numel();
     metrics_["prefill_tokens"] = S;
     metrics_["prefill_tokens_per_second"] = prefill_ms > 0 ? S * 1000.0 / prefill_ms : 0.0;
-    metrics_["decode_tokens_per_second"] = decode_ms > 0 ? steps * 1000.0 / decode_ms : 0.0;
-    metrics_["tokens_per_second"] = (prefill_ms + decode_ms) > 0 ? n_gen * 1000.0 / (prefill_ms + decode_ms) : 0.0;
-    metrics_["use_hip_graph"] = cfg_.use_graph() ? 1.0 : 0.0;
     metrics_["decode_chain"] = model_->uses_decode_chain((uint32_t)slot.cfg.max_tokens) ? 1.0 : 0.0;
     metrics_["decode_fused_qkv_attention"] =
         (!model_->uses_decode_chain((uint32_t)slot.cfg.max_tokens) &&

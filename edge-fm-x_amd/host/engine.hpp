@@ -240,7 +240,8 @@ private:
     };
     std::map<int32_t, GraphEntry> graphs_;  // per request slot
 
-    void run_decode_step(int32_t request_id, bool capture);
+    // stage_events: StageEvents of the eager loop's per-step timing, or null (captured)
+    void run_decode_step(int32_t request_id, void* stage_events);
     void sample_logits(uint32_t step_index);
     std::vector<void*> caches(int32_t request_id, bool k);
 };

@@ -373,12 +373,14 @@ public:
     }
     void forward(const LinearOpContext& c, const Tensor& w, const Tensor* bias, const Tensor& in, Tensor& out,
                  hipStream_t s) override {
+        // The shape's own figure, not the scratch's capacity: the kernels chosen must not
+        // depend on how far earlier, longer prompts have grown the buffer.
         const size_t need = efm_linear_workspace_bytes(c.shape.m, c.shape.in_features, c.shape.out_features);
         size_t have = 0;
         void* ws = need > 0 ? linear_scratch(need, w.device().second, &have) : nullptr;
         efm_check(efm_linear_ws(c.shape.m, c.shape.in_features, c.shape.out_features, in.data_ptr(), w.data_ptr(),
                                 bias ? bias->data_ptr() : nullptr, out.data_ptr(),
-                                c.shape.output == DType::Float32 ? EFM_DTYPE_F32 : EFM_DTYPE_BF16, ws, have, s),
+                                c.shape.output == DType::Float32 ? EFM_DTYPE_F32 : EFM_DTYPE_BF16, ws, need, s),
                   "linear " + c.layer_prefix);
     }
 };
@@ -428,7 +430,7 @@ public:
         size_t have = 0;
         void* ws = need > 0 ? linear_scratch(need, w.device().second, &have) : nullptr;
         efm_check(efm_fused_gate_up_swiglu_ws(c.m, c.hidden, c.intermediate, in.data_ptr(), w.data_ptr(),
-                                              out.data_ptr(), ws, have, s),
+                                              out.data_ptr(), ws, need, s),
                   "fused_gate_up_swiglu");
         return true;
     }

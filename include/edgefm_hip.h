@@ -51,6 +51,22 @@ const char* efm_last_error(void);
 /* Library version string. */
 const char* efm_version(void);
 
+/* Test hook (no counterpart in the reference): process-wide choice between kernels that
+ * compute the same operator, so that tests can compare a fast kernel with the simpler
+ * one it replaces on the same inputs. value 0 restores the library's own choice.
+ *   EFM_KNOB_DECODE_REGISTER   1: decode attention (head_dim 128, rotated cache) runs the
+ *                              register-staged kernel instead of the LDS-staged one
+ *   EFM_KNOB_PREFILL_REGISTER  1: prefill and Sage attention (head_dim 128) run the
+ *                              register-staged kernels instead of the pipelined ones
+ *   EFM_KNOB_PREFILL_SHAPE     4 or 8: the pipelined prefill / Sage kernels run with
+ *                              4-wave (128-row) or 8-wave (256-row) workgroups
+ * Unknown knobs or values: EFM_ERR_INVALID_ARGUMENT. Not for production callers. */
+#define EFM_KNOB_DECODE_REGISTER 0
+#define EFM_KNOB_PREFILL_REGISTER 1
+#define EFM_KNOB_PREFILL_SHAPE 2
+#define EFM_KNOB_COUNT 3
+int efm_testing_set_kernel_path(int32_t knob, int32_t value);
+
 /* ------------------------------------------------------------------------------------
  * Attention.  Mirrors edge_fm::AttentionOpContext (src/operators/attention_op.h:20-39).
  * Strides are in elements; 0 means contiguous ([n, heads, head_dim] NHD layout).
@@ -191,8 +207,7 @@ int efm_act_and_mul(int64_t batch, int64_t hidden, int32_t layout, const void* i
 /* ------------------------------------------------------------------------------------
  * Linear: y[m, out] = x[m, in] . W[out, in]^T (+ bias[out]), fp32 accumulate,
  * output bf16 (EFM_DTYPE_BF16) or fp32 (EFM_DTYPE_F32, the LM-head logits).
- * m == 1 runs the bandwidth-bound GEMV; m > 1 a GEMM: hipBLASLt for bf16 outputs under
- * EFM_GEMM_BACKEND_AUTO (see efm_set_gemm_backend), else this library's MFMA kernels.
+ * m == 1 runs the bandwidth-bound GEMV; m > 1 this library's bf16 MFMA GEMM kernels.
  * Replaces LinearLayer::LinearImpl::forward (src/layers/linear.h:131-153) backed by
  * LinearCublasLtImpl (src/operators/linear_impl.cu:315-480).
  * ---------------------------------------------------------------------------------- */
@@ -200,15 +215,15 @@ int efm_linear(int64_t m, int64_t in_features, int64_t out_features, const void*
                const void* bias, void* y, int32_t out_dtype, hipStream_t stream);
 
 /* efm_linear with a caller workspace (the scratch the reference's linear impls take from
- * StaticBufferManager, src/utils/memory.h:31-109). Under EFM_GEMM_BACKEND_AUTO a bf16
- * output runs hipBLASLt with this workspace available to its algorithm. Otherwise (and
- * for fp32 outputs), with this library's kernels: shapes whose output tiles are too
- * few to fill the chip and whose K is long (prefill down_proj at a few hundred to a
- * few thousand tokens) split K into slices that write fp32 partial sums into the
- * workspace, then reduce them in slice order. efm_linear_workspace_bytes returns the
- * bytes that serve both (0: none used for this shape); with less workspace the call
- * runs as efm_linear does. The split sums K in a different order than efm_linear, so
- * the two agree to fp32 rounding, not bit for bit; each is deterministic. */
+ * StaticBufferManager, src/utils/memory.h:31-109). Shapes whose output tiles are too few
+ * to fill the chip and whose K is long (prefill down_proj at a few hundred to a few
+ * thousand tokens) split K into slices that write fp32 partial sums into the workspace,
+ * then reduce them in slice order. efm_linear_workspace_bytes returns the bytes the
+ * shape uses (0: none); the split runs only when workspace_bytes >= that figure, and
+ * with less workspace the call runs as efm_linear does. The plan depends on the shape
+ * alone, so a shape given its figure always runs the same kernels. The split sums K in
+ * a different order than efm_linear, so the two agree to fp32 rounding, not bit for
+ * bit; each is deterministic. */
 size_t efm_linear_workspace_bytes(int64_t m, int64_t in_features, int64_t out_features);
 int efm_linear_ws(int64_t m, int64_t in_features, int64_t out_features, const void* x, const void* w,
                   const void* bias, void* y, int32_t out_dtype, void* workspace, size_t workspace_bytes,
@@ -223,29 +238,15 @@ int efm_fused_gate_up_swiglu(int64_t m, int64_t hidden, int64_t inter, const voi
                              const void* w_up_gate, void* out, hipStream_t stream);
 
 /* The same with a caller workspace (efm_fused_gate_up_swiglu_workspace_bytes; 0 means
- * none is used): for m > 1 under EFM_GEMM_BACKEND_AUTO the [m, 2*inter] product runs as a
- * plain hipBLASLt GEMM into the workspace (256-byte aligned) and efm_act_and_mul
- * (EFM_LAYOUT_UP_GATE) forms the output, the reference's two-stage path
- * (src/layers/gated_mlp.cu:19-67) with the same bf16 roundings of u and g. Without enough
- * workspace, or under EFM_GEMM_BACKEND_OWN, it is efm_fused_gate_up_swiglu. */
+ * none is used). The SwiGLU is the epilogue of the MFMA kernel, so no shape needs a
+ * workspace today and the call is efm_fused_gate_up_swiglu; the entry point keeps the
+ * signature of the reference's workspace-taking fused op (fused_gate_up_activation_op.h:
+ * 14-61) for callers that pass one. */
 size_t efm_fused_gate_up_swiglu_workspace_bytes(int64_t m, int64_t hidden, int64_t inter);
 int efm_fused_gate_up_swiglu_ws(int64_t m, int64_t hidden, int64_t inter, const void* x,
                                 const void* w_up_gate, void* out, void* workspace, size_t workspace_bytes,
                                 hipStream_t stream);
 
-/* Prefill GEMM backend (process-wide; no counterpart in the reference, whose prefill
- * linears call cuBLASLt): EFM_GEMM_BACKEND_AUTO (default) runs the plain bf16-output
- * GEMMs of efm_linear / efm_linear_ws (m > 1) and the product of
- * efm_fused_gate_up_swiglu_ws through hipBLASLt, with the library's heuristic first
- * algorithm for the shape and the workspace given (cached, so a shape and workspace
- * always run the same algorithm), falling back to this library's MFMA kernels where
- * hipBLASLt has no algorithm, a pointer is not 16-byte aligned or the stream is being
- * captured into a graph; EFM_GEMM_BACKEND_OWN runs this library's MFMA kernels only (fp32
- * outputs always do). */
-#define EFM_GEMM_BACKEND_AUTO 0
-#define EFM_GEMM_BACKEND_OWN 1
-int efm_set_gemm_backend(int32_t backend);
-int32_t efm_get_gemm_backend(void);
 
 /* ------------------------------------------------------------------------------------
  * LM head with fused greedy top-1 (src/layers/linear.cu:140-276, 2288-2369):

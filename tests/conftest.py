@@ -27,3 +27,17 @@ def gpu():
         pytest.fail("GPU test selected but no GPU is visible")
     torch.cuda.set_device(0)
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def knob():
+    """Setter for the library's test-only kernel-path knobs (efm_testing_set_kernel_path);
+    every knob returns to the library's own choice (0) after the test."""
+    import efm_capi as C
+
+    def set_knob(which, value):
+        C.call("efm_testing_set_kernel_path", which, int(value))
+
+    yield set_knob
+    for k in (C.EFM_KNOB_DECODE_REGISTER, C.EFM_KNOB_PREFILL_REGISTER, C.EFM_KNOB_PREFILL_SHAPE):
+        C.call("efm_testing_set_kernel_path", k, 0)

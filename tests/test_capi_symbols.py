@@ -48,20 +48,29 @@ def test_host_side_validation_without_gpu():
     assert lib.efm_attention_decode_workspace_bytes(C.make_attention_ctx(12, 2, 128), 4096) > 0
 
 
-def test_gemm_backend_switch_without_gpu():
-    """The prefill GEMM backend is a process-wide host setting: AUTO by default, OWN on
-    request, unknown values rejected with an argument error."""
+def test_gemm_workspace_queries_without_gpu():
+    """The split-K plan, and so the workspace query, depends on the shape alone: long-K
+    shapes with few output tiles use a workspace; shapes that fill the chip, and the
+    SwiGLU GEMM (its activation is the MFMA epilogue), use none. The library links no
+    vendor GEMM library."""
     lib = C.load()
-    assert lib.efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_AUTO
-    try:
-        assert lib.efm_set_gemm_backend(C.EFM_GEMM_BACKEND_OWN) == C.EFM_OK
-        assert lib.efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_OWN
-        # under OWN the workspace query is the split-K need of the MFMA kernels alone
-        assert lib.efm_linear_workspace_bytes(1344, 11008, 2048) == 0
-        assert lib.efm_linear_workspace_bytes(512, 8960, 1536) > 0
-        assert lib.efm_fused_gate_up_swiglu_workspace_bytes(512, 1536, 8960) == 0
-        assert lib.efm_set_gemm_backend(5) == C.EFM_ERR_INVALID_ARGUMENT
-        assert lib.efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_OWN
-    finally:
-        lib.efm_set_gemm_backend(C.EFM_GEMM_BACKEND_AUTO)
-    assert lib.efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_AUTO
+    assert lib.efm_linear_workspace_bytes(1344, 11008, 2048) == 0
+    assert lib.efm_linear_workspace_bytes(512, 8960, 1536) > 0
+    assert lib.efm_linear_workspace_bytes(1, 8960, 1536) == 0
+    assert lib.efm_fused_gate_up_swiglu_workspace_bytes(512, 1536, 8960) == 0
+    assert not hasattr(lib, "efm_set_gemm_backend")
+    with open(C.LIB_PATH, "rb") as f:
+        assert b"libhipblaslt" not in f.read()
+
+
+def test_testing_kernel_path_setter_validates():
+    """The test-only kernel-path knobs accept their documented values, reject others, and
+    reset to the library's own choice (0)."""
+    lib = C.load()
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_DECODE_REGISTER, 1) == C.EFM_OK
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_DECODE_REGISTER, 0) == C.EFM_OK
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_PREFILL_SHAPE, 8) == C.EFM_OK
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_PREFILL_SHAPE, 0) == C.EFM_OK
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_PREFILL_SHAPE, 5) == C.EFM_ERR_INVALID_ARGUMENT
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_PREFILL_REGISTER, 2) == C.EFM_ERR_INVALID_ARGUMENT
+    assert lib.efm_testing_set_kernel_path(99, 0) == C.EFM_ERR_INVALID_ARGUMENT

@@ -130,6 +130,30 @@ def test_prefix_slot_and_stop_tokens_and_cap(gpu):
             eng.generate(edge_fm.Request(0, [1, 2, TINY.vocab]))
 
 
+def test_prefix_restored_after_non_matching_request(gpu):
+    """A request that does not start with the slot's prefix prefills over the prefix rows;
+    the next request that does start with it must see the prefix again (it is re-prefilled),
+    so its tokens equal a fresh engine's."""
+    w = O.random_weights(_oracle_cfg(TINY), seed=14, std=0.2)
+    prompt = list(range(200, 250))
+    other = list(range(600, 640))
+    with tempfile.TemporaryDirectory() as tmp:
+        eng, keep = _engine(tmp, TINY, w, max_tokens=128, max_new_tokens=12, prefix_token_ids=prompt[:20])
+        req = edge_fm.Request(0, prompt)
+        req.set_ignore_stop_tokens(True)
+        fresh = eng.generate(req).token_ids()
+        req_o = edge_fm.Request(0, other)
+        req_o.set_ignore_stop_tokens(True)
+        other_toks = eng.generate(req_o).token_ids()
+        again = eng.generate(req).token_ids()
+        del eng
+        eng, keep = _engine(tmp, TINY, w, max_tokens=128, max_new_tokens=12)
+        plain = edge_fm.Request(0, other)
+        plain.set_ignore_stop_tokens(True)
+        assert eng.generate(plain).token_ids() == other_toks
+    assert again == fresh
+
+
 def test_tiny_vl_mrope_with_custom_embeddings(gpu):
     shape = TINY_VL
     cfg = _oracle_cfg(shape)

@@ -22,16 +22,6 @@ HEAD_CASES = [
 ]
 
 
-@pytest.fixture
-def own_gemm():
-    """Runs a test on this library's MFMA GEMM kernels (EFM_GEMM_BACKEND_OWN), restoring the
-    process-wide backend afterwards."""
-    prev = C.load().efm_get_gemm_backend()
-    C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_OWN)
-    yield
-    C.call("efm_set_gemm_backend", prev)
-
-
 def _decode(ctx, q, k, v, kv_len, d_kv_len=None, max_kv_len=0):
     ws_bytes = C.load().efm_attention_decode_workspace_bytes(ctx, max_kv_len if d_kv_len is not None else kv_len)
     ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=q.device)
@@ -463,7 +453,7 @@ def test_lm_head_top1_negative_scores_edges_and_clean_workspace(gpu):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "swiglu"])
-def test_gemm_tile_shapes_agree_bit_exact(gpu, own_gemm, kind):
+def test_gemm_tile_shapes_agree_bit_exact(gpu, kind):
     """The tile shape follows M: 100 rows run 64 x 64 (SwiGLU 64 x 128), 300 rows
     128 x 64 (SwiGLU 128 x 128), 1344 and 6144 rows 128 x 128 (many tiles per XCD: the
     grouped tile order). Every kernel sums each output over K in the same order, so the
@@ -500,7 +490,7 @@ def test_gemm_tile_shapes_agree_bit_exact(gpu, own_gemm, kind):
     pytest.param(300, 4096, 1000, "bias", id="ragged_bias"),
     pytest.param(200, 8192, 2048, "f32", id="f32"),
 ])
-def test_linear_split_k_matches_unsplit_and_oracle(gpu, own_gemm, m, k, n, kind):
+def test_linear_split_k_matches_unsplit_and_oracle(gpu, m, k, n, kind):
     """efm_linear_ws splits K for these under-filled, long-K shapes: its result equals
     efm_linear to fp32 rounding, is deterministic, matches the oracle on a row sample, and
     with too small a workspace the call is exactly efm_linear."""
@@ -537,7 +527,7 @@ def test_linear_split_k_matches_unsplit_and_oracle(gpu, own_gemm, m, k, n, kind)
         assert_close_bf16(outs[0][rows], exp)
 
 
-def test_linear_workspace_bytes_zero_without_split(gpu, own_gemm):
+def test_linear_workspace_bytes_zero_without_split(gpu):
     lib = C.load()
     assert lib.efm_linear_workspace_bytes(1, 8960, 1536) == 0          # GEMV
     assert lib.efm_linear_workspace_bytes(16384, 18944, 3584) == 0     # enough tiles
@@ -553,11 +543,10 @@ def test_linear_workspace_bytes_zero_without_split(gpu, own_gemm):
     pytest.param(77, 1536, 2048, True, id="ragged_m"),
     pytest.param(2, 896, 1000, False, id="m2"),
 ])
-def test_linear_library_backend_matches_own_kernels_and_oracle(gpu, m, k, n, bias):
-    """EFM_GEMM_BACKEND_AUTO runs the bf16 prefill GEMMs through hipBLASLt: with and without
-    a workspace the result matches this library's MFMA kernels to bf16 rounding (different
-    K summation order), matches the oracle on a row sample, and repeats bit for bit."""
-    assert C.load().efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_AUTO
+def test_linear_workspace_path_matches_oracle_and_repeats(gpu, m, k, n, bias):
+    """The prefill GEMM with its workspace (split-K where the plan asks for it) and without
+    one: both match the oracle on a row sample, each repeats bit for bit, and the two agree
+    to bf16 rounding (the split sums K in another order)."""
     torch.manual_seed(m + n)
     x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
     w = (torch.randn(n, k, device=gpu) * 0.02).to(torch.bfloat16)
@@ -565,36 +554,46 @@ def test_linear_library_backend_matches_own_kernels_and_oracle(gpu, m, k, n, bia
     need = C.load().efm_linear_workspace_bytes(m, k, n)
     ws = torch.full((max(need, 256),), 0x7f, dtype=torch.uint8, device=gpu)
     outs = []
-    for use_ws in (True, True, False):
+    for use_ws in (True, True, False, False):
         y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
         if use_ws:
-            C.call("efm_linear_ws", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), C.EFM_DTYPE_BF16, ptr(ws), ws.numel(),
+            C.call("efm_linear_ws", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), C.EFM_DTYPE_BF16, ptr(ws), need,
                    stream())
         else:
             C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), C.EFM_DTYPE_BF16, stream())
         torch.cuda.synchronize()
         outs.append(y)
-    assert torch.equal(outs[0], outs[1]), "library GEMM is not deterministic"
-    C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_OWN)
-    try:
-        own = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
-        C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(own), C.EFM_DTYPE_BF16, stream())
-        torch.cuda.synchronize()
-    finally:
-        C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_AUTO)
-    scale = float(own.float().abs().max())
-    for y in (outs[0], outs[2]):
-        assert torch.isfinite(y.float()).all()
-        assert float((y.float() - own.float()).abs().max()) <= scale * 2 ** -7, "library vs own beyond one bf16 ulp"
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[2], outs[3]), "GEMM is not deterministic"
+    scale = float(outs[2].float().abs().max())
+    assert torch.isfinite(outs[0].float()).all()
+    assert float((outs[0].float() - outs[2].float()).abs().max()) <= scale * 2 ** -7
     rows = torch.tensor([0, m // 2, m - 1])
     exp = O.linear(x[rows].cpu(), w.cpu(), None if b is None else b.cpu())
     assert_close_bf16(outs[0][rows], exp)
     assert_close_bf16(outs[2][rows], exp)
 
 
-def test_linear_library_falls_back_for_unaligned_output(gpu):
-    """An output pointer that is not 16-byte aligned keeps the GEMM off hipBLASLt: the call
-    equals an EFM_GEMM_BACKEND_OWN call bit for bit (both write through the same offset)."""
+def test_linear_workspace_plan_ignores_spare_capacity(gpu):
+    """A caller whose grow-only scratch is larger than a shape needs gets the same bits as
+    one passing exactly the shape's figure: the split-K plan depends on the shape alone."""
+    torch.manual_seed(3)
+    m, k, n = 512, 8960, 1536
+    x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
+    w = (torch.randn(n, k, device=gpu) * 0.02).to(torch.bfloat16)
+    need = C.load().efm_linear_workspace_bytes(m, k, n)
+    big = 3 * need
+    assert need > 0
+    ws = torch.zeros(big, dtype=torch.uint8, device=gpu)
+    a = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    b = torch.empty_like(a)
+    C.call("efm_linear_ws", m, k, n, ptr(x), ptr(w), None, ptr(a), C.EFM_DTYPE_BF16, ptr(ws), need, stream())
+    C.call("efm_linear_ws", m, k, n, ptr(x), ptr(w), None, ptr(b), C.EFM_DTYPE_BF16, ptr(ws), big, stream())
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_linear_unaligned_output(gpu):
+    """An output pointer that is only 2-byte aligned is written correctly."""
     torch.manual_seed(8)
     m, k, n = 64, 1024, 1000
     x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
@@ -603,40 +602,25 @@ def test_linear_library_falls_back_for_unaligned_output(gpu):
     out = buf[1:1 + m * n]                       # 2-byte offset
     assert out.data_ptr() % 16 != 0
     C.call("efm_linear", m, k, n, ptr(x), ptr(w), None, ptr(out), C.EFM_DTYPE_BF16, stream())
+    aligned = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_linear", m, k, n, ptr(x), ptr(w), None, ptr(aligned), C.EFM_DTYPE_BF16, stream())
     torch.cuda.synchronize()
-    got = out.clone()
-    C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_OWN)
-    try:
-        C.call("efm_linear", m, k, n, ptr(x), ptr(w), None, ptr(out), C.EFM_DTYPE_BF16, stream())
-        torch.cuda.synchronize()
-    finally:
-        C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_AUTO)
-    assert torch.equal(got, out)
-    assert_close_bf16(got.reshape(m, n)[:3], O.linear(x[:3].cpu(), w.cpu()))
+    assert torch.equal(out.reshape(m, n), aligned)
+    assert float(buf[0]) == 0.0 and float(buf[1 + m * n]) == 0.0
+    assert_close_bf16(aligned[:3], O.linear(x[:3].cpu(), w.cpu()))
 
 
-def test_gemm_backend_setter_rejects_unknown_values(gpu):
-    with pytest.raises(C.EfmError):
-        C.call("efm_set_gemm_backend", 7)
-    assert C.load().efm_get_gemm_backend() == C.EFM_GEMM_BACKEND_AUTO
-
-
-def test_linear_under_graph_capture_runs_own_kernels(gpu):
-    """A prefill GEMM captured into a HIP graph runs this library's MFMA kernels (the
-    hipBLASLt path stays out of captures): every replay equals an eager
-    EFM_GEMM_BACKEND_OWN call bit for bit, with eager library calls between replays."""
+def test_linear_under_graph_capture(gpu):
+    """A prefill GEMM captured into a HIP graph: every replay equals the eager call bit for
+    bit, with eager calls between replays."""
     torch.manual_seed(5)
     m, k, n = 96, 1536, 2048
     x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
     w = (torch.randn(n, k, device=gpu) * 0.02).to(torch.bfloat16)
     b = (torch.randn(n, device=gpu) * 0.05).to(torch.bfloat16)
-    C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_OWN)
-    try:
-        own = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
-        C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(own), C.EFM_DTYPE_BF16, stream())
-        torch.cuda.synchronize()
-    finally:
-        C.call("efm_set_gemm_backend", C.EFM_GEMM_BACKEND_AUTO)
+    own = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(own), C.EFM_DTYPE_BF16, stream())
+    torch.cuda.synchronize()
     y = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
     st = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
@@ -644,45 +628,35 @@ def test_linear_under_graph_capture_runs_own_kernels(gpu):
         C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), C.EFM_DTYPE_BF16, st.cuda_stream)
     for rep in range(3):
         y.fill_(float("nan"))
-        lib = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
-        C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(lib), C.EFM_DTYPE_BF16, stream())
+        eager = torch.empty(m, n, dtype=torch.bfloat16, device=gpu)
+        C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(eager), C.EFM_DTYPE_BF16, stream())
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, own), f"replay {rep}"
-        assert float((lib.float() - own.float()).abs().max()) <= float(own.float().abs().max()) * 2 ** -7
+        assert torch.equal(eager, own)
 
 
 @pytest.mark.parametrize("m,hidden,inter", [(1344, 2048, 11008), (512, 1536, 8960), (33, 896, 4864)])
-def test_gate_up_swiglu_ws_library_path(gpu, m, hidden, inter):
-    """efm_fused_gate_up_swiglu_ws under EFM_GEMM_BACKEND_AUTO (hipBLASLt product +
-    efm_act_and_mul) equals efm_linear into [m, 2 inter] followed by efm_act_and_mul bit for
-    bit when both get the same library workspace, agrees with the fused MFMA kernel to bf16
-    rounding, and with too little workspace is the fused kernel exactly."""
+def test_gate_up_swiglu_ws_is_fused_kernel(gpu, m, hidden, inter):
+    """efm_fused_gate_up_swiglu_ws needs no workspace and equals efm_fused_gate_up_swiglu bit
+    for bit; it agrees with efm_linear into [m, 2 inter] + efm_act_and_mul (the reference's
+    two-stage path) to bf16 rounding, and with the oracle on sampled rows."""
     torch.manual_seed(m)
     x = torch.randn(m, hidden, dtype=torch.bfloat16, device=gpu)
     w = (torch.randn(2 * inter, hidden, device=gpu) * 0.03).to(torch.bfloat16)
-    need = C.load().efm_fused_gate_up_swiglu_workspace_bytes(m, hidden, inter)
-    gu_bytes = (m * 2 * inter * 2 + 255) // 256 * 256
-    assert need >= gu_bytes
-    ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
+    assert C.load().efm_fused_gate_up_swiglu_workspace_bytes(m, hidden, inter) == 0
     out = torch.empty(m, inter, dtype=torch.bfloat16, device=gpu)
-    C.call("efm_fused_gate_up_swiglu_ws", m, hidden, inter, ptr(x), ptr(w), ptr(out), ptr(ws), need, stream())
-    gu = torch.empty(m, 2 * inter, dtype=torch.bfloat16, device=gpu)
-    lws = torch.zeros(max(need - gu_bytes, 256), dtype=torch.uint8, device=gpu)
-    C.call("efm_linear_ws", m, hidden, 2 * inter, ptr(x), ptr(w), None, ptr(gu), C.EFM_DTYPE_BF16, ptr(lws),
-           need - gu_bytes, stream())
-    ref = torch.empty_like(out)
-    C.call("efm_act_and_mul", m, inter, C.EFM_LAYOUT_UP_GATE, ptr(gu), ptr(ref), stream())
+    C.call("efm_fused_gate_up_swiglu_ws", m, hidden, inter, ptr(x), ptr(w), ptr(out), None, 0, stream())
     fused = torch.empty_like(out)
     C.call("efm_fused_gate_up_swiglu", m, hidden, inter, ptr(x), ptr(w), ptr(fused), stream())
-    small = torch.empty_like(out)
-    C.call("efm_fused_gate_up_swiglu_ws", m, hidden, inter, ptr(x), ptr(w), ptr(small), ptr(ws), gu_bytes - 256,
-           stream())
+    gu = torch.empty(m, 2 * inter, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_linear", m, hidden, 2 * inter, ptr(x), ptr(w), None, ptr(gu), C.EFM_DTYPE_BF16, stream())
+    two = torch.empty_like(out)
+    C.call("efm_act_and_mul", m, inter, C.EFM_LAYOUT_UP_GATE, ptr(gu), ptr(two), stream())
     torch.cuda.synchronize()
-    assert torch.equal(out, ref), "library path differs from linear + act_and_mul"
-    assert torch.equal(small, fused), "too small a workspace must run the fused kernel"
-    diff = (out.float() - fused.float()).abs()
+    assert torch.equal(out, fused)
+    diff = (two.float() - fused.float()).abs()
     assert float(diff.max()) <= float(fused.float().abs().max()) * 2 ** -6
     rows = torch.tensor([0, m - 1])
     assert_close_bf16(out[rows], O.gate_up_swiglu(x[rows].cpu(), w.cpu()), rtol=2e-2, atol=6.25e-2)
@@ -868,11 +842,11 @@ PIPE_CASES = [
 
 @pytest.mark.parametrize("shape", ["4", "8"])
 @pytest.mark.parametrize("hq,hkv,S,L,causal,mode", PIPE_CASES)
-def test_attention_prefill_pipelined_matches_oracle(gpu, monkeypatch, shape, hq, hkv, S, L, causal, mode):
+def test_attention_prefill_pipelined_matches_oracle(gpu, knob, shape, hq, hkv, S, L, causal, mode):
     """head_dim 128 with keys already rotated (pos NONE, or RoPE on q only with
     k_already_prerotated) runs the global_load_lds ring kernel, in both workgroup shapes
     (4 waves over a 2-deep ring, 8 waves over a 4-deep ring)."""
-    monkeypatch.setenv("EFM_PREFILL_SHAPE", shape)
+    knob(C.EFM_KNOB_PREFILL_SHAPE, int(shape))
     torch.manual_seed(S + L)
     hd = 128
     q = torch.randn(S, hq, hd, dtype=torch.bfloat16)
@@ -895,10 +869,10 @@ def test_attention_prefill_pipelined_matches_oracle(gpu, monkeypatch, shape, hq,
 
 
 @pytest.mark.parametrize("shape", ["4", "8"])
-def test_attention_prefill_pipelined_matches_register_kernel_c4(gpu, monkeypatch, shape):
+def test_attention_prefill_pipelined_matches_register_kernel_c4(gpu, knob, shape):
     """BASELINE C4 shape (28/4 heads, S = 4096, causal): the pipelined kernel (both
-    workgroup shapes) against the register-staged one (EFM_PREFILL_PIPE=0)."""
-    monkeypatch.setenv("EFM_PREFILL_SHAPE", shape)
+    workgroup shapes) against the register-staged one (EFM_KNOB_PREFILL_REGISTER)."""
+    knob(C.EFM_KNOB_PREFILL_SHAPE, int(shape))
     torch.manual_seed(44)
     hq, hkv, hd, S = 28, 4, 128, 4096
     q = torch.randn(S, hq, hd, dtype=torch.bfloat16, device=gpu)
@@ -907,7 +881,7 @@ def test_attention_prefill_pipelined_matches_register_kernel_c4(gpu, monkeypatch
     ctx = C.make_attention_ctx(hq, hkv, hd, rope=False)
     outs = []
     for pipe in ("1", "0"):
-        monkeypatch.setenv("EFM_PREFILL_PIPE", pipe)
+        knob(C.EFM_KNOB_PREFILL_REGISTER, 1 if pipe == "0" else 0)
         o = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
         C.call("efm_attention_prefill", ctx, ptr(q), ptr(k), ptr(v), ptr(o), S, S, 1, stream())
         torch.cuda.synchronize()
@@ -1090,10 +1064,10 @@ def test_sage_attention_c4_shape_vs_bf16_kernel(gpu):
 
 @pytest.mark.parametrize("shape", ["4", "8"])
 @pytest.mark.parametrize("S,L,causal", [(4096, 4096, 1), (1000, 1300, 1), (77, 77, 0)])
-def test_sage_attention_pipelined_matches_register_kernel(gpu, monkeypatch, shape, S, L, causal):
+def test_sage_attention_pipelined_matches_register_kernel(gpu, knob, shape, S, L, causal):
     """head_dim 128 runs the global_load_lds ring kernel (both workgroup shapes); it must
-    agree with the register-staged kernel (EFM_PREFILL_PIPE=0) on the same inputs."""
-    monkeypatch.setenv("EFM_PREFILL_SHAPE", shape)
+    agree with the register-staged kernel (EFM_KNOB_PREFILL_REGISTER) on the same inputs."""
+    knob(C.EFM_KNOB_PREFILL_SHAPE, int(shape))
     hq, hkv, hd = 28, 4, 128
     g = torch.Generator(device=gpu).manual_seed(S + L)
     q = torch.randn(S, hq, hd, generator=g, device=gpu).to(torch.bfloat16)
@@ -1104,7 +1078,7 @@ def test_sage_attention_pipelined_matches_register_kernel(gpu, monkeypatch, shap
                      device=gpu)
     outs = []
     for pipe in ("1", "0"):
-        monkeypatch.setenv("EFM_PREFILL_PIPE", pipe)
+        knob(C.EFM_KNOB_PREFILL_REGISTER, 1 if pipe == "0" else 0)
         o = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
         C.call("efm_attention_prefill_sage_int8", ctx, ptr(q), ptr(k), ptr(v), ptr(o), S, L, causal, ptr(ws),
                ws.numel(), stream())
@@ -1116,9 +1090,9 @@ def test_sage_attention_pipelined_matches_register_kernel(gpu, monkeypatch, shap
 
 @pytest.mark.parametrize("hq,hkv", [(12, 2), (28, 4), (16, 2), (8, 8)])
 @pytest.mark.parametrize("kv_len,max_kv", [(1, 1), (100, 128), (767, 768), (1025, 2000), (16385, 16513)])
-def test_decode_attention_lds_kernel_matches_register_kernel(gpu, monkeypatch, hq, hkv, kv_len, max_kv):
+def test_decode_attention_lds_kernel_matches_register_kernel(gpu, knob, hq, hkv, kv_len, max_kv):
     """head_dim 128 with a rotated cache runs the LDS-staged kernel; it must agree with
-    the register kernel (EFM_DECODE_LDS=0) on the same cache, through both the merged
+    the register kernel (EFM_KNOB_DECODE_REGISTER) on the same cache, through both the merged
     entry point and the partials + fused o_proj merge, and store the same rotated newest
     row. Rows past the length hold NaN."""
     torch.manual_seed(kv_len + hq)
@@ -1134,7 +1108,7 @@ def test_decode_attention_lds_kernel_matches_register_kernel(gpu, monkeypatch, h
     ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=gpu)
     outs, caches = [], []
     for lds in ("1", "0"):
-        monkeypatch.setenv("EFM_DECODE_LDS", lds)
+        knob(C.EFM_KNOB_DECODE_REGISTER, 1 if lds == "0" else 0)
         k = k0.clone()
         o = torch.empty_like(q)
         C.call("efm_attention_decode", ctx, ptr(q), ptr(k), ptr(v), ptr(o), 0, ptr(d_len), max_kv, ptr(ws),
@@ -1151,11 +1125,11 @@ def test_decode_attention_lds_kernel_matches_register_kernel(gpu, monkeypatch, h
 
 @pytest.mark.parametrize("lds", ["0", "1"])
 @pytest.mark.parametrize("kv_len,max_kv", [(161, 40000), (321, 70000), (1025, 40000), (129, 40000)])
-def test_decode_newest_row_owned_by_one_split(gpu, monkeypatch, lds, kv_len, max_kv):
+def test_decode_newest_row_owned_by_one_split(gpu, knob, lds, kv_len, max_kv):
     """With keys-per-split not a multiple of 128 (large max_kv_len) a split's last round has
     idle tiles that lie in the next split; they must not touch the newest row, which only
     its owning split rotates and stores (regression: the idle tile stored zeros)."""
-    monkeypatch.setenv("EFM_DECODE_LDS", lds)
+    knob(C.EFM_KNOB_DECODE_REGISTER, 1 if lds == "0" else 0)
     torch.manual_seed(0)
     hq, hkv, hd = 12, 2, 128
     q = torch.randn(1, hq * hd, dtype=torch.bfloat16, device=gpu)
