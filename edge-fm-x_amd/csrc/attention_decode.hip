@@ -35,6 +35,8 @@
 //    that the o_proj GEMV merges in its prologue (efm_decode_attention_merge_o_proj).
 #include "decode_attn_impl.hpp"
 
+#include <mutex>
+
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
@@ -600,7 +602,61 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
     return set_error(EFM_ERR_UNSUPPORTED, "attention_decode: hd=%d G=%d", hd, G);
 }
 
+// ---- no-allocation variant (efm_attention_decode_noalloc) ----
+// The split partials live in `scratch`, a file-scope device array that every GPU the
+// library runs on holds until the process ends. In host code `scratch` names a host-side
+// stand-in, never the device memory: the device address comes from hipGetSymbolAddress,
+// fetched once per device (with that device current) on the entry point's first call
+// there, and only that address is passed to kernels. Nothing in the partials needs to
+// start at zero: every split writes its own slots before the merge reads them.
+constexpr size_t kNoAllocScratchBytes = EFM_ATTENTION_DECODE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kNoAllocMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kNoAllocMaxDevices];
+
+static int noalloc_scratch(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(EFM_ERR_DEVICE, "attention_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kNoAllocMaxDevices)
+        return set_error(EFM_ERR_UNSUPPORTED, "attention_decode_noalloc: device %d beyond %d", dev, kNoAllocMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_dev[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return set_error(EFM_ERR_DEVICE, "attention_decode_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return EFM_OK;
+}
+
+static int decode_noalloc(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v, void* o,
+                          uint32_t kv_len, const uint32_t* d_kv_len, uint32_t max_kv_len, hipStream_t stream) {
+    int rc = validate_attention_ctx(ctx, "attention_decode_noalloc");
+    if (rc) return rc;
+    const uint32_t bound = (d_kv_len != nullptr) ? max_kv_len : kv_len;
+    const size_t need = decode_ws(ctx, std::max<uint32_t>(bound, 1u)).total();
+    if (need > kNoAllocScratchBytes)
+        return set_error(EFM_ERR_UNSUPPORTED,
+                         "attention_decode_noalloc: this shape needs %zu bytes of split scratch; the library holds %zu "
+                         "(use efm_attention_decode with a workspace)", need, kNoAllocScratchBytes);
+    void* ptr = nullptr;
+    rc = noalloc_scratch(&ptr);
+    if (rc) return rc;
+    return decode_launch(ctx, q, k, v, o, kv_len, d_kv_len, max_kv_len, ptr, kNoAllocScratchBytes, true, stream);
+}
+
 }  // namespace efm
+
+extern "C" int efm_attention_decode_noalloc(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v,
+                                            void* o, uint32_t kv_len, const uint32_t* d_kv_len, uint32_t max_kv_len,
+                                            hipStream_t stream) {
+    return efm::decode_noalloc(ctx, q, k, v, o, kv_len, d_kv_len, max_kv_len, stream);
+}
 
 extern "C" size_t efm_attention_decode_workspace_bytes(const efm_attention_ctx* ctx, uint32_t max_kv_len) {
     return efm::decode_workspace_bytes(ctx, max_kv_len);

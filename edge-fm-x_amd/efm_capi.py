@@ -34,6 +34,8 @@ EFM_K_PREROTATED_EXCEPT_NEWEST = 2
 EFM_LAYOUT_GATE_UP = 0
 EFM_LAYOUT_UP_GATE = 1
 
+EFM_ATTENTION_DECODE_NOALLOC_SCRATCH_BYTES = 2359296
+
 EFM_KNOB_DECODE_REGISTER = 0
 EFM_KNOB_PREFILL_REGISTER = 1
 EFM_KNOB_PREFILL_SHAPE = 2
@@ -90,6 +92,8 @@ SIGNATURES = {
     "efm_last_error": (c_char_p, []),
     "efm_version": (c_char_p, []),
     "efm_attention_decode_workspace_bytes": (c_size_t, [POINTER(AttentionCtx), c_uint32]),
+    "efm_attention_decode_noalloc": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
+                                               c_void_p, c_uint32, c_void_p]),
     "efm_attention_decode": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
                                        c_void_p, c_uint32, c_void_p, c_size_t, c_void_p]),
     "efm_decode_attention_partials": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p,

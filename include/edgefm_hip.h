@@ -113,6 +113,22 @@ int efm_attention_decode(const efm_attention_ctx* ctx, const void* q, const void
                          void* o, uint32_t kv_len, const uint32_t* d_kv_len, uint32_t max_kv_len,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* efm_attention_decode without a workspace argument. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments, semantics and kernels
+ * as efm_attention_decode, and the same results bit for bit. The split partials live in
+ * a device array the library holds on every GPU it runs on until the process ends, of
+ * EFM_ATTENTION_DECODE_NOALLOC_SCRATCH_BYTES; that covers every shape whose
+ * efm_attention_decode_workspace_bytes fits in it (all head_dim <= 128, group <= 8 shapes
+ * with up to 512 KV heads, any length). Larger needs: EFM_ERR_UNSUPPORTED, nothing
+ * launched. The call allocates nothing (its first call on a device looks up the array's
+ * address). Every call on one GPU shares the array: calls that overlap on one GPU (on
+ * different streams, or from several threads without stream order) race. */
+#define EFM_ATTENTION_DECODE_NOALLOC_SCRATCH_BYTES 2359296
+int efm_attention_decode_noalloc(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v,
+                                 void* o, uint32_t kv_len, const uint32_t* d_kv_len, uint32_t max_kv_len,
+                                 hipStream_t stream);
+
 /* Decode attention split partials only (no in-kernel merge): every split writes its
  * unnormalised fp32 output and (max, sum) of exp2-domain scores into `workspace`
  * (efm_attention_decode_workspace_bytes(ctx, max_kv_len) bytes); the partials are
