@@ -71,22 +71,6 @@ def make_attention_ctx(num_qo_heads, num_kv_heads, head_dim, *, rope=True, rope_
                         EFM_DTYPE_BF16, EFM_POS_ROPE_LLAMA if rope else EFM_POS_NONE, int(k_already_prerotated))
 
 
-class DecodeChainLayer(ctypes.Structure):
-    """efm_decode_chain_layer: the weights of one layer and the next layer's QKV target."""
-    _fields_ = [
-        ("w_o", c_void_p),
-        ("post_norm", c_void_p),
-        ("w_up_gate", c_void_p),
-        ("w_down", c_void_p),
-        ("in_norm_next", c_void_p),
-        ("w_qkv_next", c_void_p),
-        ("b_qkv_next", c_void_p),
-        ("q_next", c_void_p),
-        ("k_cache_next", c_void_p),
-        ("v_cache_next", c_void_p),
-    ]
-
-
 # name -> (restype, argtypes)
 SIGNATURES = {
     "efm_last_error": (c_char_p, []),
@@ -130,16 +114,16 @@ SIGNATURES = {
     "efm_fused_gate_up_swiglu_ws": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
                                               c_size_t, c_void_p]),
     "efm_testing_set_kernel_path": (c_int32, [c_int32, c_int32]),
+    "efm_decode_stack_workspace_bytes": (c_size_t, [POINTER(AttentionCtx), c_int32, c_int32, c_int32, c_uint32]),
+    "efm_decode_stack_supported": (c_int32, [POINTER(AttentionCtx), c_int32, c_int32, c_int32, c_uint32]),
+    "efm_decode_stack": (c_int32, [POINTER(AttentionCtx), c_int32, c_int32, c_int32, c_float, c_void_p, c_void_p,
+                                   c_int64, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_size_t,
+                                   c_void_p]),
+    "efm_decode_stack_status": (c_int32, [c_void_p, c_void_p]),
     "efm_lm_head_top1_workspace_bytes": (c_size_t, [c_int64]),
     "efm_lm_head_top1": (c_int32, [c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "efm_sampler_greedy_workspace_bytes": (c_size_t, [c_int64, c_int64]),
     "efm_sampler_greedy": (c_int32, [c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
-    "efm_decode_chain_workspace_bytes": (c_size_t, [c_int32, c_int32]),
-    "efm_decode_chain_supported": (c_int32, [POINTER(AttentionCtx), c_int32, c_int32, c_uint32]),
-    "efm_decode_layer_chain": (c_int32, [POINTER(AttentionCtx), c_int32, c_int32, c_float, POINTER(DecodeChainLayer),
-                                         c_void_p, c_uint32, c_void_p, c_size_t, c_void_p, c_void_p, c_void_p,
-                                         c_void_p, c_size_t, c_void_p]),
-    "efm_decode_chain_status": (c_int32, [c_void_p, c_int32, c_int32, c_void_p]),
     "efm_sampler_top_p_workspace_bytes": (c_size_t, [c_int64]),
     "efm_sampler_top_p": (c_int32, [c_int64, c_void_p, c_float, c_float, c_uint64, c_uint64, c_void_p, c_void_p,
                                     c_void_p, c_size_t, c_void_p]),

@@ -90,21 +90,22 @@ def write_compact_vocab_mapping(path: str, original_vocab_size: int, new_to_old,
 def write_engine_config(path: str, model_dir: str, *, max_tokens: int = 4096, max_new_tokens: int = 256,
                         prefix_token_ids=None, use_graph: bool = True, temperature: float = 0.0,
                         top_p: float = 1.0, seed: int = 0, lm_head_top1: bool = True, model_name: str = "",
-                        operator_impl_table_path: str = "", extra_slots=None, decode_chain: bool = False,
+                        operator_impl_table_path: str = "", extra_slots=None, decode_stack=None,
                         stop_token_ids=None, compact_vocab=None) -> str:
     slots = [{"request_id": 0, "prefix_token_ids": list(prefix_token_ids or []), "max_tokens": max_tokens}]
     for s in extra_slots or []:
         slots.append(s)
     cfg = {
         "model_name": model_name,
-        "runtime": {"device": "gpu", "device_id": 0, "use_cuda_graph": use_graph, "lm_head_top1": lm_head_top1,
-                    "decode_chain": decode_chain},
+        "runtime": {"device": "gpu", "device_id": 0, "use_cuda_graph": use_graph, "lm_head_top1": lm_head_top1},
         "prefill_model_path": model_dir,
         "operator_impl_table_path": operator_impl_table_path,
         "kvcache": {"dtype": "bf16", "requests": slots},
         "sampling": {"max_new_tokens": max_new_tokens, "temperature": temperature, "top_p": top_p, "seed": seed,
                      "stop_token_ids": list(stop_token_ids or [])},
     }
+    if decode_stack is not None:
+        cfg["runtime"]["decode_stack"] = bool(decode_stack)
     if compact_vocab is not None:
         cfg["compact_vocab"] = compact_vocab
     with open(path, "w") as f:

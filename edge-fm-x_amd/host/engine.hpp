@@ -69,10 +69,11 @@ public:
     std::string hw_profile() const;
     bool use_graph() const;
     bool lm_head_top1() const;
-    // Persistent post-attention decode chain (runtime.decode_chain, default off: on
-    // MI355X its cross-workgroup exchanges cost more than the kernel boundaries they
-    // remove; EDGE_FM_DECODE_CHAIN=1 / 0 overrides the config).
-    bool decode_chain() const;
+    // Whole decode step of a text model in one persistent launch (efm_decode_stack;
+    // runtime.decode_stack, default off: on MI355X its six cross-workgroup hand-offs per
+    // layer cost more than the four kernel boundaries of the per-operator path;
+    // EDGE_FM_DECODE_STACK=1 / 0 overrides the config, read once when the engine is built).
+    bool decode_stack() const;
     // One launch for the input norm + QKV + attention partials of each decode layer
     // (runtime.decode_fused_qkv_attention, default on; EDGE_FM_DECODE_FUSED_QKV_ATTENTION
     // = 1 / 0 overrides the config).
@@ -163,14 +164,17 @@ public:
     // a decode step is captured into a graph: capture cannot allocate).
     void reserve_decode(uint32_t max_kv_len);
 
-    // Whether decode steps with caches of max_kv_len rows run the persistent
-    // post-attention chain (efm_decode_layer_chain) instead of the per-operator kernels.
-    bool uses_decode_chain(uint32_t max_kv_len) const;
+    // Whether decode steps with caches of max_kv_len rows run every layer in one
+    // persistent launch (efm_decode_stack) instead of the per-operator kernels.
+    bool uses_decode_stack(uint32_t max_kv_len) const;
+    // Builds the decode stack's device layer table for one request slot's caches (outside
+    // graph capture; no-op when the stack is not used or the table exists).
+    void prepare_decode_stack(uint32_t max_kv_len, void** k_caches, void** v_caches, hipStream_t stream);
     // Whether decode steps run efm_decode_norm_qkv_attention (input norm + QKV +
     // attention partials in one launch per layer).
     bool uses_fused_front(uint32_t max_kv_len) const;
-    // Throws DeviceError if a chain or fused QKV + attention launch since the last check
-    // could not exchange its vectors in time (synchronises the stream).
+    // Throws DeviceError if a decode-stack or fused QKV + attention launch since the last
+    // check could not exchange its vectors in time (synchronises the stream).
     void check_decode_status(hipStream_t stream);
 
 private:
@@ -192,8 +196,9 @@ private:
     Tensor dec_h_, dec_res_[2], dec_q_, dec_attn_, dec_a_, dec_mid_, dec_kvtmp_, dec_one_, top1_ws_;
     Tensor attn_ws_;
     bool fused_attn_merge_ = false;
-    bool chain_enabled_ = false;   // config switch (text models only)
-    Tensor chain_ws_;
+    bool stack_enabled_ = false;   // config switch (text models only)
+    Tensor stack_ws_;
+    std::map<void*, Tensor> stack_tables_;   // per request slot, keyed by its layer-0 K cache
     bool fused_front_enabled_ = false;
     Tensor front_sync_ws_;
     // prefill scratch (grow-only)
