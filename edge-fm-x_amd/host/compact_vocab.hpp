@@ -1,12 +1,14 @@
-// Compact vocabulary: the engine runs a pre-pruned checkpoint whose vocabulary holds
-// only a subset of the original token ids (smaller embedding table and LM head, so
-// the largest decode GEMV shrinks with it). Requests and responses stay in the
-// original id space: input ids, custom-embedding placeholder ids, stop ids and the
-// fixed KV prefixes are remapped old -> new on the way in, generated ids new -> old
-// on the way out.
+// Compact vocabulary: a pre-pruned checkpoint keeps only a subset of the original token
+// ids, so its embedding table and LM head are smaller (the LM head is the largest decode
+// GEMV). Callers keep speaking original ids: everything that enters the engine (request
+// ids, custom-embedding placeholder ids, stop / EOS ids, fixed KV prefixes) is translated
+// original -> compact, and generated ids compact -> original on the way out.
 //
-// Mirrors src/engine/tasks/token_generation/compact_vocab.{h,cpp} (class CompactVocab,
-// mapping format "edgefm.compact_vocab.v1") with the same checks and error types.
+// The public surface and the mapping file (format "edgefm.compact_vocab.v1": original and
+// compact sizes, old_to_new with -1 for pruned ids, new_to_old, special_token_ids) are the
+// reference's (src/engine/tasks/token_generation/compact_vocab.h); the implementation is a
+// single validated id bijection plus one translation routine whose failure policy decides
+// which error a caller sees.
 #pragma once
 
 #include <cstdint>
@@ -22,38 +24,52 @@ class EngineConfig;
 class CompactVocab {
 public:
     CompactVocab() = default;
-    // Reads config.compact_vocab() {enabled, mapping_path, reject_unknown_input_ids};
-    // disabled (the default) makes every call an identity (compact_vocab.cpp:86-149).
+    // Reads the engine config's compact_vocab section {enabled, mapping_path,
+    // reject_unknown_input_ids}; disabled (the default) makes every translation the identity.
     explicit CompactVocab(const EngineConfig& config);
 
-    bool enabled() const noexcept { return enabled_; }
-    int32_t original_vocab_size() const noexcept { return original_vocab_size_; }
-    int32_t compact_vocab_size() const noexcept { return compact_vocab_size_; }
-    const std::string& mapping_path() const noexcept { return mapping_path_; }
+    bool enabled() const noexcept { return map_.active(); }
+    int32_t original_vocab_size() const noexcept { return map_.original_size(); }
+    int32_t compact_vocab_size() const noexcept { return map_.compact_size(); }
+    const std::string& mapping_path() const noexcept { return path_; }
 
-    // Request-side ids: an id outside old_to_new raises InvalidRequestError.
+    // Request ids (original -> compact); an id with no compact slot is InvalidRequestError.
     std::vector<int32_t> remap_token_ids(const std::vector<int32_t>& ids, const std::string& context) const;
-    // Configuration ids (EOS, stop ids, KV prefixes): a pruned id raises ConfigurationError.
+    // Configuration ids (EOS, stop ids, KV prefixes); a pruned id is ConfigurationError.
     std::vector<int32_t> remap_required_token_ids(const std::vector<int32_t>& ids, const std::string& context) const;
     std::vector<int32_t> remap_optional_token_ids(const std::vector<int32_t>& ids, const std::string& context) const;
-    // Generated ids back to the original space: out-of-range raises InternalError.
+    // Generated ids (compact -> original); an id outside the compact range is InternalError.
     std::vector<int32_t> restore_token_ids(const std::vector<int32_t>& ids, const std::string& context) const;
-    // Copy of the request in compact ids (token ids, embed_token_id base, stop ids).
+    // The request in compact ids (token ids, custom-embedding base id, stop ids).
     Request remap_request(const Request& request) const;
 
-private:
-    int32_t remap_input_token_id(int32_t id, const std::string& context) const;
-    int32_t remap_required_token_id(int32_t id, const std::string& context) const;
-    int32_t restore_token_id(int32_t id, const std::string& context) const;
-    int32_t remap_embed_token_id(const Request& request) const;
+    // Which exception a failed translation raises.
+    enum class OnMissing { Reject, Misconfigured, Corrupt };
+    enum class Direction { ToCompact, ToOriginal };
 
-    bool enabled_ = false;
-    bool reject_unknown_input_ids_ = true;
-    int32_t original_vocab_size_ = 0;
-    int32_t compact_vocab_size_ = 0;
-    std::string mapping_path_;
-    std::vector<int32_t> old_to_new_;
-    std::vector<int32_t> new_to_old_;
+private:
+    // Two arrays that are inverse to each other on the kept ids: fwd (original -> compact,
+    // -1 where pruned) and inv (compact -> original). An empty map is the identity.
+    class IdBijection {
+    public:
+        void assign(std::vector<int32_t> fwd, std::vector<int32_t> inv);   // validates
+        bool active() const noexcept { return !inv_.empty(); }
+        int32_t original_size() const noexcept { return (int32_t)fwd_.size(); }
+        int32_t compact_size() const noexcept { return (int32_t)inv_.size(); }
+        // -1 when id has no image in that direction
+        int32_t image(Direction d, int32_t id) const noexcept;
+
+    private:
+        std::vector<int32_t> fwd_, inv_;
+    };
+
+    int32_t translate(int32_t id, Direction d, OnMissing policy, const std::string& what) const;
+    std::vector<int32_t> translate_all(const std::vector<int32_t>& ids, Direction d, OnMissing policy,
+                                       const std::string& what) const;
+    int32_t compact_embedding_base(const Request& request) const;
+
+    IdBijection map_;
+    std::string path_;
 };
 
 }  // namespace edge_fm
