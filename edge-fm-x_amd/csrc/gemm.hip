@@ -1,22 +1,26 @@
 // Prefill projections on the gfx950 matrix cores: C[M, N] = A[M, K] . B[N, K]^T in
 // bf16 with fp32 accumulation (v_mfma_f32_32x32x16_bf16). A holds activations (one
 // row per token) and B the weights in their [out, in] layout, so both operands are
-// K-contiguous and feed the MFMA lanes with plain 16-byte loads.
+// K-contiguous and feed the MFMA lanes with 16-byte loads.
 //
-//  * Workgroup tile BM x BN (128 x 128, 128 x 64 or 64 x 64 by tile count), 256
-//    threads as a 2 x 2 grid of wave64s; each wave owns a (BM/2) x (BN/2) block of
-//    32 x 32 MFMA tiles.
-//  * K % 64 == 0 (every Qwen2.5 projection): the pipelined kernel below (DMA ring of
-//    64-key slabs, XOR-swizzled LDS, operand reads software-pipelined against the
-//    MFMAs, grouped tile order per XCD). Other K: a register-staged kernel with a
-//    padded LDS row pitch (40 bf16).
+//  * K % 64 == 0 (every Qwen2.5 projection), two kernels fed by global_load_lds DMA into
+//    XOR-swizzled LDS rings, operand reads software-pipelined against the MFMAs and a
+//    grouped tile order per XCD:
+//      - the wide kernel: 256 x 256 tiles, one 8-wave workgroup per CU (large M);
+//      - the pipelined kernel: 128 x 128 (128 x 64, 64 x 64) tiles, two 4-wave
+//        workgroups per CU (few tiles), plus its split-K form.
+//    A cost model (rounds of resident workgroups) picks between them.
+//  * Other K: a register-staged kernel with a padded LDS row pitch (40 bf16).
 //  * Epilogues: bf16 (+bias, the cuBLASLt BIAS epilogue), fp32, and SwiGLU, where the
 //    B tile interleaves 32-row blocks of up and gate weights so that each lane holds u
 //    and g of the same output element: out = bf16(silu(bf16(g)) * bf16(u)).
+//  * Every kernel sums each output's keys 16 at a time in increasing order, so results
+//    are bit-identical across kernels and tile shapes (split-K aside).
 #include "common.hpp"
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 #include <cstdlib>
 
 namespace efm {
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(const bf16_t* _
 // Pipelined variant for K % 64 == 0: K slabs of 64 stream global -> LDS with
 // global_load_lds (no staging registers) into an S-deep ring, so S - 1 slabs are in
 // flight while the matrix cores work on one. Each wave's 1 KB DMA load covers 8 rows x 128
-// bytes; lane l fetches chunk (l % 8) ^ (row % 8) of its row, so the ring holds an
+// bytes; lane l fetches chunk (l % 8) ^ pipe_swz(row) of its row, so the ring holds an
 // XOR-swizzled layout and the 32-row MFMA operand reads spread over the LDS banks. The
 // operand reads are issued as ds_read_b128 with explicit waits: each wave waits for its
 // own DMA loads of the slab (vmcnt, counted exactly: every wave issues LPW loads per slab)
@@ -201,6 +205,15 @@ __device__ __forceinline__ void tile_of(int t, int mt, int nt, int& tm, int& tn)
     tm = first + r % gm;
     tn = r / gm;
 }
+
+// LDS swizzles. gfx950's LDS has 64 four-byte banks and serves a ds_read_b128 sixteen
+// lanes at a time: the 16 rows an MFMA operand read touches at once must land in 16
+// distinct 16-byte bank groups. With 128-byte rows (8 chunks) two rows fill the 256-byte
+// bank period, so rows of equal parity need distinct chunks: (row / 2) % 8, with the
+// parity folded into bit 2 so that any 8 consecutive rows also differ. With 64-byte rows
+// (4 chunks) four rows fill the period: rows equal mod 4 need distinct chunks.
+__device__ __forceinline__ int pipe_swz(int row) { return ((row >> 1) ^ ((row & 1) << 2)) & 7; }
+__device__ __forceinline__ int wide_swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 
 constexpr int kPBK = 64;            // K per slab
 constexpr int kPRow = kPBK * 2;     // bytes per operand row in LDS
@@ -275,11 +288,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
             const bf16_t* src;
             if (q < QA) {
                 const int row = min(m0 + q * 8 + rr, M - 1);
-                src = A + (size_t)row * K + k0 + ((cs ^ rr) << 3);
+                src = A + (size_t)row * K + k0 + ((cs ^ pipe_swz(q * 8 + rr)) << 3);
             } else {
                 int br = b_row((q - QA) * 8 + rr);
                 if (br < 0) br = 0;
-                src = B + (size_t)br * K + k0 + ((cs ^ rr) << 3);
+                src = B + (size_t)br * K + k0 + ((cs ^ pipe_swz(q * 8 + rr)) << 3);
             }
             __builtin_amdgcn_global_load_lds(
                 static_cast<const void*>(src),
@@ -301,13 +314,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int r = wm * WM + i * 32 + (lane & 31);
-            const uint32_t addr = base + (uint32_t)(r * kPRow + ((c ^ (r & 7)) << 4));
+            const uint32_t addr = base + (uint32_t)(r * kPRow + ((c ^ pipe_swz(r)) << 4));
             asm volatile("ds_read_b128 %0, %1" : "=v"(af[i]) : "v"(addr) : "memory");
         }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const int r = wn * WN + j * 32 + (lane & 31);
-            const uint32_t addr = base + (uint32_t)(BM * kPRow + r * kPRow + ((c ^ (r & 7)) << 4));
+            const uint32_t addr = base + (uint32_t)(BM * kPRow + r * kPRow + ((c ^ pipe_swz(r)) << 4));
             asm volatile("ds_read_b128 %0, %1" : "=v"(bfr[j]) : "v"(addr) : "memory");
         }
     };
@@ -394,6 +407,264 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
     }
 }
 
+// ---------------------------------------------------------------------------------
+// Wide-tile kernel: BM x BN workgroup tiles (256 x 256 in use), one workgroup per CU, its
+// WGM x WGN waves (2 x 4 in use: two per SIMD) each owning a (BM/WGM) x (BN/WGN) block of
+// 32 x 32 MFMA tiles. Relative to 128 x 128 tiles each MFMA needs half the bytes from L2
+// and, with 128 x 64 wave blocks, three quarters of the LDS reads; the second wave on
+// each SIMD issues MFMAs while the first waits on its memory instructions. (Measured on
+// the 7B gate/up shape: 4 waves with 128 x 128 blocks and 256 AGPR accumulators reach
+// 1.08 PF/s, the 2 x 4 layout 1.16 PF/s; the per-stage DMA is the largest cost beyond
+// the MFMAs themselves, about a quarter of the time, whether or not its loads hit L2.)
+//  * 32-key stages in an S-deep LDS ring filled by global_load_lds (16 bytes per lane,
+//    one 1 KB wave load covers 16 rows x 64 bytes). Lane i of a wave load lands at byte
+//    16 i of its 1 KB block, so the lane fetches the chunk that belongs there: row i / 4,
+//    logical chunk (i % 4) ^ wide_swz(row).
+//  * Per stage and wave: two 16-key steps. Step 0's MFMAs run with step 1's operand reads
+//    and the DMA of stage s + S - 1 interleaved, one memory instruction per MFMA; step 1's
+//    MFMAs run with the reads of stage s + 1's step 0, behind a bare barrier that follows
+//    this wave's own vmcnt wait for stage s + 1. That barrier also orders every wave's
+//    reads of stage s - 1 before its slot is refilled in the next stage.
+// ---------------------------------------------------------------------------------
+constexpr int kWBK = 32;            // keys per stage
+constexpr int kWRow = kWBK * 2;     // bytes per operand row per stage
+
+template <int OFF>
+__device__ __forceinline__ bf16x8_t ds_read16(uint32_t addr) {
+    bf16x8_t d;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "n"(OFF) : "memory");
+    return d;
+}
+
+// One key step's operand fragments: A rows at a + 2048 i, B rows at b + 2048 j.
+template <int TM, int TN>
+struct WideFrags {
+    bf16x8_t a[TM], b[TN];
+};
+
+template <int I, int TM, int TN>
+__device__ __forceinline__ void wide_read_one(WideFrags<TM, TN>& f, uint32_t a, uint32_t b) {
+    if constexpr (I < TM) f.a[I] = ds_read16<I * 32 * kWRow>(a);
+    else f.b[I - TM] = ds_read16<(I - TM) * 32 * kWRow>(b);
+}
+
+template <int TM, int TN, int... I>
+__device__ __forceinline__ void wide_read_all(WideFrags<TM, TN>& f, uint32_t a, uint32_t b,
+                                              std::integer_sequence<int, I...>) {
+    (wide_read_one<I>(f, a, b), ...);
+}
+
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// DMA of one stage's operand rows: per-lane byte offsets (row, swizzled chunk) of each
+// of the wave's loads from the operand base; the stage's base pointers and LDS slot are
+// uniform values computed once per stage.
+template <int LPW, int LA, int NW>
+struct WideDma {
+    uint32_t voff[LPW];
+    __device__ __forceinline__ void issue(int i, const unsigned char* sa, const unsigned char* sb,
+                                          unsigned char* slot_wave) const {
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>((i < LA ? sa : sb) + voff[i]),
+                                         (__attribute__((address_space(3))) void*)(slot_wave + i * NW * 1024), 16, 0,
+                                         0);
+    }
+};
+
+// MFMA I of a key step (tile I / TN, I % TN) on f, then (READS) operand read I of the next
+// step into g and (DMA) this wave's load I of the stage at sa / sb into slot_wave. Each
+// group is a scheduling barrier: the memory instructions go out one per MFMA, early in
+// the step (measured: issuing the loads evenly over the step is slower).
+template <int I, int TM, int TN, int LPW, bool READS, bool DMA, class Dma>
+__device__ __forceinline__ void wide_slot(f32x16_t (&acc)[TM][TN], const WideFrags<TM, TN>& f,
+                                          WideFrags<TM, TN>& g, uint32_t ga, uint32_t gb, const Dma& dma,
+                                          const unsigned char* sa, const unsigned char* sb,
+                                          unsigned char* slot_wave) {
+    constexpr int i = I / TN, j = I % TN;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+    if constexpr (READS && I < TM + TN) wide_read_one<I>(g, ga, gb);
+    if constexpr (DMA && I < LPW) dma.issue(I, sa, sb, slot_wave);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int TM, int TN, int LPW, bool READS, bool DMA, class Dma, int... I>
+__device__ __forceinline__ void wide_mma_step(f32x16_t (&acc)[TM][TN], const WideFrags<TM, TN>& f,
+                                              WideFrags<TM, TN>& g, uint32_t ga, uint32_t gb, const Dma& dma,
+                                              const unsigned char* sa, const unsigned char* sb,
+                                              unsigned char* slot_wave, std::integer_sequence<int, I...>) {
+    (wide_slot<I, TM, TN, LPW, READS, DMA>(acc, f, g, ga, gb, dma, sa, sb, slot_wave), ...);
+}
+
+template <int BM, int BN, int WGM, int WGN, int S, int EPI>
+__global__ __launch_bounds__(WGM * WGN * kWave, 1) void gemm_wide_kernel(const bf16_t* __restrict__ A,
+                                                                    const bf16_t* __restrict__ B,
+                                                                    const bf16_t* __restrict__ bias,
+                                                                    void* __restrict__ Cout, int M, int N, int K,
+                                                                    int ldc, int mt, int nt) {
+    constexpr int NW = WGM * WGN;                // waves: a WGM x WGN grid over the tile
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int STAGE = (BM + BN) * kWRow;
+    constexpr int QA = BM / 16, QB = BN / 16;   // 1 KB wave loads per operand per stage
+    constexpr int LA = QA / NW, LPW = (QA + QB) / NW;
+    constexpr int NR = TM + TN;                 // operand reads per key step
+    static_assert(QA % NW == 0 && QB % NW == 0 && S >= 2 && (S - 2) * LPW <= 63, "bad wide GEMM shape");
+    static_assert(LPW <= TM * TN && NR <= TM * TN && NR <= 15, "interleave slots");
+    static_assert(EPI != GEPI_SWIGLU || TN % 2 == 0, "SwiGLU needs paired N tiles");
+    static_assert(EPI != GEPI_PARTIAL, "no split-K in the wide kernel");
+    __shared__ __align__(1024) unsigned char smem[S * STAGE];
+
+    const int T = mt * nt;
+    const int per = (T + 7) / 8;
+    const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    if (t >= T) return;
+    int tm, tn;
+    tile_of(t, mt, nt, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = (EPI == GEPI_SWIGLU) ? tn * (BN / 2) : tn * BN;
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    auto b_row = [&](int r) -> int {
+        if (EPI == GEPI_SWIGLU) {
+            const int blk = r / 32;
+            const int col = n0 + (blk / 2) * 32 + (r % 32);
+            return (col < N) ? ((blk % 2 == 0) ? col : N + col) : -1;
+        }
+        const int n = n0 + r;
+        return (n < N) ? n : -1;
+    };
+
+    // DMA sources (the host keeps both operands under 2 GB: 32-bit byte offsets)
+    WideDma<LPW, LA, NW> dma;
+    const unsigned char* pa = reinterpret_cast<const unsigned char*>(A);
+    const unsigned char* pb = reinterpret_cast<const unsigned char*>(B);
+    auto issue_stage = [&](int stage) {
+        const unsigned char* sa = pa + stage * kWRow;
+        const unsigned char* sb = pb + stage * kWRow;
+        unsigned char* sw = smem + (stage % S) * STAGE + wave * 1024;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) dma.issue(i, sa, sb, sw);
+    };
+    {
+        const int rr = lane >> 2, cs = lane & 3;
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) {
+            const int q = wave + NW * i;
+            if (i < LA) {
+                const int row = q * 16 + rr;
+                const int grow = min(m0 + row, M - 1);
+                dma.voff[i] = (uint32_t)((grow * K + ((cs ^ wide_swz(row)) << 3)) * 2);
+            } else {
+                const int row = (q - QA) * 16 + rr;
+                int br = b_row(row);
+                if (br < 0) br = 0;
+                dma.voff[i] = (uint32_t)((br * K + ((cs ^ wide_swz(row)) << 3)) * 2);
+            }
+        }
+    }
+
+    // Operand read addresses: row (lane % 32) of each 32-row tile, chunk ks * 2 + lane / 32
+    // under the stage's swizzle.
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
+    const int r32 = lane & 31, sw = wide_swz(r32);
+    const uint32_t x0 = (uint32_t)(((lane >> 5) ^ sw) << 4), x1 = (uint32_t)(((2 + (lane >> 5)) ^ sw) << 4);
+    const uint32_t rowA = (uint32_t)((wm * WM + r32) * kWRow), rowB = (uint32_t)(BM * kWRow + (wn * WN + r32) * kWRow);
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+    WideFrags<TM, TN> f0, f1;
+    auto tie = [&](WideFrags<TM, TN>& f) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(f.a[i]));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(f.b[j]));
+    };
+
+    const int nk = K / kWBK;
+    const int pre = min(S - 1, nk);
+    for (int p = 0; p < pre; ++p) issue_stage(p);
+    vm_wait_slabs<LPW>(min(S - 2, nk - 1));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    wide_read_all(f0, lds0 + rowA + x0, lds0 + rowB + x0, std::make_integer_sequence<int, NR>{});
+
+    // Stage s: key step 0 on f0 with step 1's reads and, while stages remain, this wave's
+    // loads of stage s + S - 1 (into the slot of stage s - 1, which every wave finished
+    // reading before the previous barrier); then key step 1 on f1 with the reads of stage
+    // s + 1, behind this wave's vmcnt wait for stage s + 1 and the barrier.
+    auto run_stage = [&](int s, auto dma_on, auto next_on) {
+        constexpr bool kDma = decltype(dma_on)::value, kNext = decltype(next_on)::value;
+        const uint32_t cur = lds0 + (uint32_t)((s % S) * STAGE);
+        const int ds = s + S - 1;
+        lgkm_wait<0>();
+        tie(f0);
+        wide_mma_step<TM, TN, LPW, true, kDma>(acc, f0, f1, cur + rowA + x1, cur + rowB + x1, dma, pa + ds * kWRow,
+                                               pb + ds * kWRow, smem + (ds % S) * STAGE + wave * 1024,
+                                               std::make_integer_sequence<int, TM * TN>{});
+        lgkm_wait<0>();
+        tie(f1);
+        if constexpr (kNext) {
+            if constexpr (kDma) vm_wait<(S - 2) * LPW>();
+            else vm_wait_slabs<LPW>(min(S - 2, nk - 2 - s));
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
+        const uint32_t nxt = lds0 + (uint32_t)(((s + 1) % S) * STAGE);
+        wide_mma_step<TM, TN, LPW, kNext, false>(acc, f1, f0, nxt + rowA + x0, nxt + rowB + x0, dma, pa, pb, smem,
+                                                 std::make_integer_sequence<int, TM * TN>{});
+    };
+    int s = 0;
+    for (; s < nk - (S - 1); ++s) run_stage(s, std::true_type{}, std::true_type{});
+    for (; s < nk - 1; ++s) run_stage(s, std::false_type{}, std::true_type{});
+    run_stage(nk - 1, std::false_type{}, std::false_type{});
+
+    // Epilogue. Accumulator element e of tile (i, j): row = (e/4)*8 + (lane/32)*4 + e%4,
+    // column = lane % 32 within the 32 x 32 tile.
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + wm * WM + i * 32 + (e / 4) * 8 + (lane / 32) * 4 + (e % 4);
+            if (row >= M) continue;
+            if (EPI == GEPI_SWIGLU) {
+#pragma unroll
+                for (int j = 0; j < TN; j += 2) {
+                    const int col = n0 + ((wn * WN + j * 32) / 64) * 32 + (lane % 32);
+                    if (col < N) {
+                        const float u = round_bf16(acc[i][j][e]);
+                        const float g = round_bf16(acc[i][j + 1][e]);
+                        const float o = (g / (1.0f + expf(-g))) * u;
+                        reinterpret_cast<bf16_t*>(Cout)[(size_t)row * ldc + col] = (bf16_t)f32_to_bf16(o);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int col = n0 + wn * WN + j * 32 + (lane % 32);
+                    if (col >= N) continue;
+                    float v = acc[i][j][e];
+                    if (bias != nullptr) v += bf16_to_f32(bias[col]);
+                    if (EPI == GEPI_F32) reinterpret_cast<float*>(Cout)[(size_t)row * ldc + col] = v;
+                    else reinterpret_cast<bf16_t*>(Cout)[(size_t)row * ldc + col] = (bf16_t)f32_to_bf16(v);
+                }
+            }
+        }
+    }
+}
+
 // Split-K reduction: out[r, c] = sum over slices s = 0, 1, ... (in that order) of
 // part[s, r, c], + bias[c], as bf16 or fp32. Four columns per thread (N % 4 == 0).
 template <bool F32OUT>
@@ -436,6 +707,16 @@ static void gemm_pipe_launch(int M, int N, int K, const bf16_t* A, const bf16_t*
     const int grid = 8 * ((mt * nt + 7) / 8);
     hipLaunchKernelGGL((gemm_pipe_kernel<BM, BN, S, EPI>), dim3(grid), dim3(kGemmThreads), 0, stream, A, B, bias, C,
                        M, N, K, ldc, mt, nt, 1, K / kPBK);
+}
+
+template <int BM, int BN, int WGM, int WGN, int S, int EPI>
+static void gemm_wide_launch(int M, int N, int K, const bf16_t* A, const bf16_t* B, const bf16_t* bias, void* C,
+                             int ldc, hipStream_t stream) {
+    const int ocols = (EPI == GEPI_SWIGLU) ? BN / 2 : BN;
+    const int mt = (M + BM - 1) / BM, nt = (N + ocols - 1) / ocols;
+    const int grid = 8 * ((mt * nt + 7) / 8);
+    hipLaunchKernelGGL((gemm_wide_kernel<BM, BN, WGM, WGN, S, EPI>), dim3(grid), dim3(WGM * WGN * kWave), 0, stream, A,
+                       B, bias, C, M, N, K, ldc, mt, nt);
 }
 
 // Split-K plan for a plain (non-SwiGLU) projection with K % 64 == 0: worth it when the
@@ -486,6 +767,22 @@ static int gemm_dispatch(int M, int N, int K, const bf16_t* A, const bf16_t* B, 
         return (long)((M + bm - 1) / bm) * ((N + ocols - 1) / ocols);
     };
     const dim3 block(kGemmThreads);
+    // 256 x 256 tiles (one 8-wave workgroup per CU, 32-bit operand offsets) against the
+    // 128 x 128 kernel (two workgroups per CU): rounds of resident workgroups times the
+    // work of one round, each at its measured rate on MI355X (about 1.15 and 0.95 PF/s on
+    // the 7B prefill projections), so the wide tile wins once it wastes no more than a
+    // partial round: 512 x 1536 -> 2 x 8960 (SwiGLU) runs wide, 1344 x 2048 -> 2 x 11008
+    // does not (3 wide rounds, the last nearly empty, against 3.7 narrow ones).
+    const int tile_knob = kernel_knob(EFM_KNOB_GEMM_TILE);
+    const long b_rows = (EPI == GEPI_SWIGLU) ? 2L * N : (long)N;
+    const bool wide_ok = K % kPBK == 0 && (long)M * K * 2 < 0x7fffffffL && b_rows * K * 2 < 0x7fffffffL;
+    if (wide_ok && tile_knob != 1) {
+        const long r_wide = (tiles(256, 256) + 255) / 256, r_pipe = (tiles(128, 128) + 511) / 512;
+        if (tile_knob == 2 || 190 * r_wide < 115 * r_pipe) {
+            gemm_wide_launch<256, 256, 2, 4, 4, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+            return check_launch("gemm_bf16");
+        }
+    }
     if (K % kPBK == 0) {
         // Tile choice from a sweep of the prefill shapes on MI355X: 128 x 128 double-
         // buffered (two workgroups per CU) once there are >= 1.5 tiles per CU (>= 1 for

@@ -39,6 +39,7 @@ EFM_ATTENTION_DECODE_NOALLOC_SCRATCH_BYTES = 2359296
 EFM_KNOB_DECODE_REGISTER = 0
 EFM_KNOB_PREFILL_REGISTER = 1
 EFM_KNOB_PREFILL_SHAPE = 2
+EFM_KNOB_GEMM_TILE = 3
 
 
 class AttentionCtx(ctypes.Structure):

@@ -60,11 +60,15 @@ const char* efm_version(void);
  *                              register-staged kernels instead of the pipelined ones
  *   EFM_KNOB_PREFILL_SHAPE     4 or 8: the pipelined prefill / Sage kernels run with
  *                              4-wave (128-row) or 8-wave (256-row) workgroups
+ *   EFM_KNOB_GEMM_TILE         prefill GEMM kernel (K % 64 == 0): 1 the two-workgroup-
+ *                              per-CU 128 x 128 / 128 x 64 / 64 x 64 kernel, 2 the
+ *                              one-workgroup-per-CU 256 x 256 kernel
  * Unknown knobs or values: EFM_ERR_INVALID_ARGUMENT. Not for production callers. */
 #define EFM_KNOB_DECODE_REGISTER 0
 #define EFM_KNOB_PREFILL_REGISTER 1
 #define EFM_KNOB_PREFILL_SHAPE 2
-#define EFM_KNOB_COUNT 3
+#define EFM_KNOB_GEMM_TILE 3
+#define EFM_KNOB_COUNT 4
 int efm_testing_set_kernel_path(int32_t knob, int32_t value);
 
 /* ------------------------------------------------------------------------------------

@@ -39,5 +39,5 @@ def knob():
         C.call("efm_testing_set_kernel_path", which, int(value))
 
     yield set_knob
-    for k in (C.EFM_KNOB_DECODE_REGISTER, C.EFM_KNOB_PREFILL_REGISTER, C.EFM_KNOB_PREFILL_SHAPE):
+    for k in (C.EFM_KNOB_DECODE_REGISTER, C.EFM_KNOB_PREFILL_REGISTER, C.EFM_KNOB_PREFILL_SHAPE, C.EFM_KNOB_GEMM_TILE):
         C.call("efm_testing_set_kernel_path", k, 0)

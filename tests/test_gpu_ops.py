@@ -454,11 +454,11 @@ def test_lm_head_top1_negative_scores_edges_and_clean_workspace(gpu):
 
 @pytest.mark.parametrize("kind", ["bf16", "swiglu"])
 def test_gemm_tile_shapes_agree_bit_exact(gpu, kind):
-    """The tile shape follows M: 100 rows run 64 x 64 (SwiGLU 64 x 128), 300 rows
-    128 x 64 (SwiGLU 128 x 128), 1344 and 6144 rows 128 x 128 (many tiles per XCD: the
-    grouped tile order). Every kernel sums each output over K in the same order, so the
-    first 100 rows must agree bit for bit across all launches (and with the oracle on a
-    sample)."""
+    """The kernel and tile shape follow M: 100 rows run 64 x 64 (SwiGLU 64 x 128), 300
+    rows 128 x 64 (SwiGLU 128 x 128), 1344 rows 128 x 128 (many tiles per XCD: the
+    grouped tile order) and 6144 rows the 256 x 256 wide kernel. Every kernel sums each
+    output over K in the same order, so the first 100 rows must agree bit for bit across
+    all launches (and with the oracle on a sample)."""
     torch.manual_seed(17)
     k, n = 1024, 8192
     x = torch.randn(6144, k, dtype=torch.bfloat16, device=gpu)
@@ -482,6 +482,47 @@ def test_gemm_tile_shapes_agree_bit_exact(gpu, kind):
         assert_close_bf16(heads[0][rows], O.gate_up_swiglu(xs, w.cpu()), rtol=2e-2, atol=6.25e-2)
     else:
         assert_close_bf16(heads[0][rows], O.linear(xs, w.cpu(), b.cpu()))
+
+
+@pytest.mark.parametrize("m,k,n,kind", [
+    pytest.param(4096, 1024, 3072, "bf16", id="aligned"),
+    pytest.param(1000, 2048, 1000, "bias", id="ragged_m_n"),
+    pytest.param(777, 1536, 2400, "swiglu", id="ragged_swiglu"),
+    pytest.param(513, 3584, 4608, "f32", id="f32_bias"),
+    pytest.param(512, 1536, 8960, "swiglu", id="c2_gate_up"),
+])
+def test_gemm_wide_kernel_matches_narrow_bit_exact(gpu, knob, m, k, n, kind):
+    """The 256 x 256 wide kernel (EFM_KNOB_GEMM_TILE 2) against the 128 x 128 family
+    (knob 1) on aligned and ragged shapes and every epilogue: bit-identical outputs (both
+    sum keys 16 at a time in increasing order), and a row sample against the oracle."""
+    torch.manual_seed(m + n)
+    x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
+    nw = 2 * n if kind == "swiglu" else n
+    w = (torch.randn(nw, k, device=gpu) * 0.05).to(torch.bfloat16)
+    b = (torch.randn(n, device=gpu) * 0.05).to(torch.bfloat16) if kind in ("bias", "f32") else None
+    odt = torch.float32 if kind == "f32" else torch.bfloat16
+    outs = []
+    for path in (1, 2):
+        knob(C.EFM_KNOB_GEMM_TILE, path)
+        y = torch.full((m, n), float("nan"), dtype=odt, device=gpu)
+        if kind == "swiglu":
+            C.call("efm_fused_gate_up_swiglu", m, k, n, ptr(x), ptr(w), ptr(y), stream())
+        else:
+            cd = C.EFM_DTYPE_F32 if kind == "f32" else C.EFM_DTYPE_BF16
+            C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), cd, stream())
+        torch.cuda.synchronize()
+        outs.append(y)
+    assert not torch.isnan(outs[1]).any(), "wide kernel left outputs unwritten"
+    assert torch.equal(outs[0], outs[1]), f"{kind}: wide and narrow kernels differ"
+    rows = torch.tensor([0, m // 2, m - 1])
+    xs = x[rows].cpu()
+    if kind == "swiglu":
+        assert_close_bf16(outs[1][rows], O.gate_up_swiglu(xs, w.cpu()), rtol=2e-2, atol=6.25e-2)
+    elif kind == "f32":
+        ref = O.linear(xs, w.cpu(), b.cpu(), out_f32=True)
+        torch.testing.assert_close(outs[1][rows].cpu(), ref, rtol=1e-3, atol=1e-3)
+    else:
+        assert_close_bf16(outs[1][rows], O.linear(xs, w.cpu(), b.cpu() if b is not None else None))
 
 
 @pytest.mark.parametrize("m,k,n,kind", [
