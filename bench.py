@@ -8,10 +8,12 @@ graph-replayed decode steps). `value` = decode tokens/s over the K timed steps
 (engine HIP events around the decode loop); prefill tokens/s is reported beside it.
 
 Extra fields:
-  roofline      the dominant decode kernel (fused post-attention RMSNorm + gate/up
-                GEMV + SwiGLU, 50 % of the decode bytes) timed with HIP events around a
-                graph replay of 20 x 28 launches over all 28 layers' weights, against
-                8 TB/s HBM; `traffic` is read from the committed rocprofv3 --pmc summary.
+  roofline      the per-layer decode kernel with the longest average launch, timed with
+                HIP events around a graph replay of 20 x 28 launches over all 28 layers'
+                weights (context 640, the run's mean), against 8 TB/s HBM; `traffic` is
+                read from the committed rocprofv3 --pmc summary of that kernel.
+  per_layer_kernels  the same figures for all four per-layer decode kernels (front half:
+                norm + QKV + attention; merge + o_proj; norm + gate/up + SwiGLU; down).
   decode_loop   algorithmic bytes per decode token / measured ms per token.
   cpu_baseline  the CPU oracle (PyTorch, fp32 math on bf16 values) on this host,
                 same model and prompt: 512-token prefill, then 8 decode steps at
@@ -44,7 +46,7 @@ def decode_bytes_per_token(shape, ctx_len):
     return L * per_layer + V * H * 2 + H * 2 + H * 2 + kv
 
 ROOFLINE_KERNEL = "efm_decode_norm_gate_up_swiglu (gemv_kernel<1,1,PRO_ADD_NORM,EPI_SWIGLU>)"
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gate_up_swiglu_c2_hbm_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_c2_hbm_traffic.md")
 
 
 def gate_up_bytes(shape):
@@ -54,13 +56,15 @@ def gate_up_bytes(shape):
     return 2 * I * H * 2 + (3 * H + H + I) * 2
 
 
-def measured_traffic():
-    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), or None."""
+def measured_traffic(name="gate_up"):
+    """HBM bytes per launch of a per-layer decode kernel (front, o_proj, gate_up, down)
+    from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-kernel
+    calibrated), or None."""
+    key = f"traffic_bytes_per_launch[{name}]:"
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key):
                     return int(line.split(":", 1)[1].strip())
     except OSError:
         return None
@@ -117,9 +121,114 @@ def roofline_kernel(torch, C, shape, weights, dev, graph=True, reps=20, traffic=
             "timing": f"HIP events around one replay of a graph of {reps}x{shape.layers} launches"}
 
 
+def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20, eager=False):
+    """The four kernels of one decode layer, each timed over all layers' real weights:
+    a HIP graph of reps x layers launches of one kernel is replayed between two HIP events
+    on the replay stream (avg = kernel duration plus the graph's inter-node gap).
+      front    efm_decode_norm_qkv_attention: input RMSNorm + fused QKV GEMV + bias + KV
+               write + split attention over ctx_len cached rows (rotated cache)
+      o_proj   efm_decode_attention_merge_o_proj: split merge + o_proj GEMV
+      gate_up  efm_decode_norm_gate_up_swiglu: add-norm + gate/up GEMV + SwiGLU
+      down     efm_linear m = 1: down_proj GEMV
+    Algorithmic bytes per launch: weights (+ bias, norm weights), activations in and out,
+    the K/V rows read, and the attention partials (ceil(ctx/128) splits x heads x
+    (head_dim + 2) fp32) written by front and read by o_proj. Sorted by time, slowest
+    first. eager=True launches each kernel reps x layers times without graphs or timing
+    (the counter-collection workload) and returns None."""
+    H, I, L = shape.hidden, shape.inter, shape.layers
+    qd, kvd, hd = shape.q_dim, shape.kv_dim, shape.head_dim
+    ctx = C.make_attention_ctx(shape.heads, shape.kv_heads, hd)
+    ctx.k_already_prerotated = C.EFM_K_PREROTATED_EXCEPT_NEWEST
+    lib = C.load()
+    ws = torch.zeros(lib.efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=dev)
+    sync = torch.zeros(lib.efm_decode_qkv_attention_sync_bytes(qd, kvd), dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev).manual_seed(7)
+    per = []
+    for l in range(L):
+        p = f"model.layers.{l}."
+        w = lambda n: weights[p + n]
+        kc = torch.randn(max_kv, kvd, device=dev, generator=g).to(torch.bfloat16)
+        vc = torch.randn(max_kv, kvd, device=dev, generator=g).to(torch.bfloat16)
+        per.append(dict(
+            wqkv=torch.cat([w("self_attn.q_proj.weight"), w("self_attn.k_proj.weight"), w("self_attn.v_proj.weight")]),
+            bqkv=torch.cat([w("self_attn.q_proj.bias"), w("self_attn.k_proj.bias"), w("self_attn.v_proj.bias")]),
+            nin=w("input_layernorm.weight"), npost=w("post_attention_layernorm.weight"),
+            wo=w("self_attn.o_proj.weight"), wgu=torch.cat([w("mlp.up_proj.weight"), w("mlp.gate_proj.weight")]),
+            wd=w("mlp.down_proj.weight"), kc=kc, vc=vc))
+    d_len = torch.tensor([ctx_len], dtype=torch.int32, device=dev)
+    h = torch.randn(1, H, device=dev, generator=g).to(torch.bfloat16)
+    r_in = torch.randn(1, H, device=dev, generator=g).to(torch.bfloat16)
+    r_out = torch.empty_like(r_in)
+    o = torch.empty_like(r_in)
+    mid = torch.randn(1, I, device=dev, generator=g).to(torch.bfloat16)
+    y = torch.empty(1, H, device=dev, dtype=torch.bfloat16)
+
+    def front(x, sh):
+        C.call("efm_decode_norm_qkv_attention", ctx, H, shape.eps, h.data_ptr(), r_in.data_ptr(), r_out.data_ptr(),
+               x["nin"].data_ptr(), x["wqkv"].data_ptr(), x["bqkv"].data_ptr(), x["kc"].data_ptr(),
+               x["vc"].data_ptr(), d_len.data_ptr(), max_kv, ws.data_ptr(), ws.numel(), sync.data_ptr(),
+               sync.numel(), sh)
+
+    def oproj(x, sh):
+        C.call("efm_decode_attention_merge_o_proj", ctx, d_len.data_ptr(), max_kv, ws.data_ptr(), ws.numel(),
+               x["wo"].data_ptr(), H, o.data_ptr(), sh)
+
+    def gate_up(x, sh):
+        C.call("efm_decode_norm_gate_up_swiglu", H, I, shape.eps, o.data_ptr(), r_in.data_ptr(), r_out.data_ptr(),
+               x["npost"].data_ptr(), x["wgu"].data_ptr(), mid.data_ptr(), sh)
+
+    def down(x, sh):
+        C.call("efm_linear", 1, I, H, mid.data_ptr(), x["wd"].data_ptr(), None, y.data_ptr(), C.EFM_DTYPE_BF16, sh)
+
+    splits = -(-ctx_len // 128)
+    part = splits * shape.heads * (hd + 2) * 4
+    act = 2 * H
+    kernels = [
+        ("front", "efm_decode_norm_qkv_attention (decode_qkv_attn_kernel)", front,
+         ((qd + 2 * kvd) * (H + 1) + H) * 2 + 3 * act + 2 * (ctx_len - 1) * kvd * 2 + 2 * kvd * 2 + part),
+        ("o_proj", "efm_decode_attention_merge_o_proj (gemv_kernel, merge prologue)", oproj,
+         qd * H * 2 + part + act),
+        ("gate_up", "efm_decode_norm_gate_up_swiglu (gemv_kernel, add-norm prologue, SwiGLU epilogue)", gate_up,
+         gate_up_bytes(shape)),
+        ("down", "efm_linear m=1 (gemv_kernel)", down, I * H * 2 + 2 * I + act),
+    ]
+    stream = torch.cuda.Stream()
+    if eager:
+        for name, kname, fn, nbytes in kernels:
+            for _ in range(reps):
+                for x in per:
+                    fn(x, stream.cuda_stream)
+            stream.synchronize()
+        C.call("efm_decode_qkv_attention_status", sync.data_ptr(), stream.cuda_stream)
+        return None
+    out = []
+    for name, kname, fn, nbytes in kernels:
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream, capture_error_mode="thread_local"):
+            for _ in range(reps):
+                for x in per:
+                    fn(x, stream.cuda_stream)
+        with torch.cuda.stream(stream):
+            graph.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * L)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append({"name": name, "kernel": kname, "bytes_per_launch": int(nbytes), "avg_launch_us": round(us, 3),
+                    "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del graph
+    C.call("efm_decode_qkv_attention_status", sync.data_ptr(), stream.cuda_stream)
+    return sorted(out, key=lambda k: -k["avg_launch_us"])
+
+
 def kernel_only(torch, C, S, shape, seed):
     """Counter-collection workload: a 256 MiB device copy (calibration: 262144 KiB read,
-    262144 KiB written) then 2 x layers direct launches of the roofline kernel."""
+    262144 KiB written), then 2 x layers direct launches of each per-layer decode kernel
+    (front, o_proj, gate_up, down) at context 640."""
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     x = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).uniform_()
@@ -129,11 +238,40 @@ def kernel_only(torch, C, S, shape, seed):
     torch.cuda.synchronize()
     del x, y
     weights = S.synthetic_weights_gpu(shape, seed=seed)
-    roofline_kernel(torch, C, shape, weights, dev, graph=False, reps=2)
+    decode_layer_kernels(torch, C, shape, weights, dev, ctx_len=640, max_kv=768, reps=2, eager=True)
     torch.cuda.synchronize()
-    print(json.dumps({"kernel_only": ROOFLINE_KERNEL, "launches": 2 * shape.layers,
-                      "bytes_per_launch": gate_up_bytes(shape), "copy_calibration_bytes": 256 << 20}))
+    print(json.dumps({"kernel_only": "per-layer decode kernels", "launches_each": 2 * shape.layers,
+                      "copy_calibration_bytes": 256 << 20}))
 
+
+def gemm_only(torch, C, reps=3):
+    """Prefill GEMM counter workload: the C5 (7B, 16384-token prefill) gate/up projection
+    with its SwiGLU epilogue, [16384, 3584] x [2 x 18944, 3584]^T, reps launches through
+    efm_fused_gate_up_swiglu (the library's own kernel choice: the 256 x 256 wide kernel),
+    after one untimed launch; average time from HIP events on the launch stream."""
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    m, k, n = 16384, 3584, 18944
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(2 * n, k, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+    st = torch.cuda.current_stream()
+
+    def run():
+        C.call("efm_fused_gate_up_swiglu", m, k, n, x.data_ptr(), w.data_ptr(), y.data_ptr(), st.cuda_stream)
+
+    run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        run()
+    e1.record(st)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    flops = 2.0 * m * k * 2 * n
+    print(json.dumps({"gemm_only": "C5 gate/up + SwiGLU", "m": m, "k": k, "n": 2 * n, "launches": reps + 1,
+                      "avg_us": round(us, 1), "tflops": round(flops / us / 1e6, 1)}))
 
 
 def host_cpu_info(torch):
@@ -541,8 +679,10 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=8, help="decode steps the C2 CPU baseline times")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                     help="BASELINE configuration (default c2, the headline decode benchmark)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="prefill GEMM counter workload (C5 gate/up + SwiGLU), no model")
     ap.add_argument("--kernel-only", action="store_true",
-                    help="run only the copy calibration and the roofline kernel (for rocprofv3 --pmc passes)")
+                    help="run only the copy calibration and the four per-layer decode kernels (for rocprofv3 --pmc passes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the single-request decode path of this build runs on one MI355X; "
@@ -555,6 +695,9 @@ def main():
     import efm_capi as C
     import efm_setup as S
 
+    if args.gemm_only:
+        gemm_only(torch, C)
+        return
     if args.config != "c2":
         {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config](args)
         return
@@ -598,7 +741,14 @@ def main():
     bytes_tok = decode_bytes_per_token(shape, mean_ctx)
     loop_gbs = bytes_tok / (ms_per_token * 1e-3) / 1e9
 
-    kern = roofline_kernel(torch, C, shape, weights, dev, graph=True)
+    layer_kernels = decode_layer_kernels(torch, C, shape, weights, dev, ctx_len=int(round(mean_ctx)),
+                                         max_kv=args.prompt + args.gen)
+    dom = layer_kernels[0]
+    kern = {"kernel": dom["kernel"], "bound": "hbm", "achieved": dom["achieved_GBs"], "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": dom["frac"], "traffic": measured_traffic(dom["name"]),
+            "avg_launch_us": dom["avg_launch_us"], "bytes_per_launch": dom["bytes_per_launch"],
+            "timing": "HIP events around one replay of a graph of 20 x 28 launches on the replay stream",
+            "note": "the per-layer decode kernel with the longest average launch; all four in per_layer_kernels"}
 
     # ---- CPU baseline: the oracle on this host, bounded sample at the benchmark's context
     cpu, parity = None, None
@@ -627,6 +777,7 @@ def main():
         "decode_loop": {"bytes_per_token": int(bytes_tok), "achieved_GBs": round(loop_gbs, 1),
                         "frac_of_hbm_peak": round(loop_gbs / HBM_PEAK_GBS, 4)},
         "roofline": kern,
+        "per_layer_kernels": layer_kernels,
         "cpu_baseline": cpu,
         "tokens_head": toks[:8],
         "parity_vs_oracle": parity,
