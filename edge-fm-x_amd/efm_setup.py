@@ -73,6 +73,32 @@ def write_model_dir(path: str, shape: ModelShape, eos_token_id=None) -> str:
     return path
 
 
+def write_checkpoint(model_dir: str, weights: dict, shards: int = 1, rename=None, extra: dict | None = None) -> list:
+    """Write HF-named tensors as a safetensors checkpoint under model_dir: one
+    model.safetensors (shards == 1) or model-0000i-of-0000n.safetensors shards (tensors
+    dealt round-robin in name order). rename maps a tensor name to the name stored (a
+    Qwen2.5-VL checkpoint prefixes the language model: model.language_model.*); extra
+    tensors are stored as given (e.g. a vision tower the text model ignores). Returns the
+    file paths."""
+    from safetensors.torch import save_file
+
+    os.makedirs(model_dir, exist_ok=True)
+    named = {(rename(k) if rename else k): v.detach().cpu().contiguous() for k, v in weights.items()}
+    named.update({k: v.detach().cpu().contiguous() for k, v in (extra or {}).items()})
+    names = sorted(named)
+    if shards == 1:
+        paths = [os.path.join(model_dir, "model.safetensors")]
+        save_file(named, paths[0])
+        return paths
+    paths = []
+    for i in range(shards):
+        part = {k: named[k] for k in names[i::shards]}
+        path = os.path.join(model_dir, f"model-{i + 1:05d}-of-{shards:05d}.safetensors")
+        save_file(part, path)
+        paths.append(path)
+    return paths
+
+
 def write_compact_vocab_mapping(path: str, original_vocab_size: int, new_to_old, special_token_ids,
                                 fmt: str = "edgefm.compact_vocab.v1") -> str:
     """Write an ``edgefm.compact_vocab.v1`` mapping: compact id n is original id new_to_old[n];

@@ -33,17 +33,23 @@ std::map<std::string, SafetensorsEntry> read_safetensors_header(const std::strin
     std::string hdr(n, '\0');
     f.read(&hdr[0], (std::streamsize)n);
     if (!f) throw ModelNotLoadedError("truncated safetensors header: " + path);
-    Json j = Json::parse(hdr);
     std::map<std::string, SafetensorsEntry> out;
-    for (const auto& kv : j.as_object()) {
-        if (kv.first == "__metadata__") continue;
-        SafetensorsEntry e;
-        e.dtype = kv.second.at("dtype").as_string();
-        for (const auto& s : kv.second.at("shape").as_array()) e.shape.push_back(s.as_int());
-        const auto& off = kv.second.at("data_offsets").as_array();
-        e.begin = (size_t)off.at(0).as_int();
-        e.end = (size_t)off.at(1).as_int();
-        out[kv.first] = e;
+    try {
+        Json j = Json::parse(hdr);
+        for (const auto& kv : j.as_object()) {
+            if (kv.first == "__metadata__") continue;
+            SafetensorsEntry e;
+            e.dtype = kv.second.at("dtype").as_string();
+            for (const auto& s : kv.second.at("shape").as_array()) e.shape.push_back(s.as_int());
+            const auto& off = kv.second.at("data_offsets").as_array();
+            if (off.size() != 2 || off[0].as_int() < 0 || off[1].as_int() < off[0].as_int())
+                throw ModelNotLoadedError("bad data_offsets");
+            e.begin = (size_t)off[0].as_int();
+            e.end = (size_t)off[1].as_int();
+            out[kv.first] = e;
+        }
+    } catch (const std::exception& ex) {
+        throw ModelNotLoadedError("malformed safetensors header in " + path + ": " + ex.what());
     }
     *data_offset = 8 + n;
     return out;
@@ -65,22 +71,39 @@ WeightLoader& WeightLoader::instance() {
     return w;
 }
 
-void WeightLoader::load_weights_from_file(const std::string& model_dir, ModelStage stage, int32_t device_id) {
+std::vector<std::string> collect_safetensors_files(const std::string& model_path) {
     std::vector<std::string> files;
-    if (fs::is_regular_file(model_dir)) {
-        files.push_back(model_dir);
-    } else {
-        if (fs::exists(fs::path(model_dir) / "model.safetensors")) {
-            files.push_back((fs::path(model_dir) / "model.safetensors").string());
-        } else if (fs::is_directory(model_dir)) {
-            for (const auto& e : fs::directory_iterator(model_dir)) {
-                const std::string name = e.path().filename().string();
-                if (name.rfind("model-", 0) == 0 && e.path().extension() == ".safetensors") files.push_back(e.path());
-            }
-            std::sort(files.begin(), files.end());
+    if (fs::is_regular_file(model_path)) return {model_path};
+    const fs::path single = fs::path(model_path) / "model.safetensors";
+    if (fs::is_regular_file(single)) return {single.string()};
+    if (fs::is_directory(model_path)) {
+        for (const auto& e : fs::directory_iterator(model_path)) {
+            if (!e.is_regular_file()) continue;
+            const std::string name = e.path().filename().string();
+            if (name.rfind("model-", 0) == 0 && name.find("-of-") != std::string::npos &&
+                e.path().extension() == ".safetensors")
+                files.push_back(e.path().string());
         }
     }
-    if (files.empty()) throw ModelNotLoadedError("no safetensors weights found under " + model_dir);
+    std::sort(files.begin(), files.end());
+    if (files.empty())
+        throw ConfigurationError("No model.safetensors or model-*-of-*.safetensors found in: " + model_path);
+    return files;
+}
+
+std::string vl_language_model_name(const std::string& name) {
+    auto starts = [&](const char* p) { return name.rfind(p, 0) == 0; };
+    if (starts("model.visual.")) return "";   // the vision tower of the newer HF layout
+    if (starts("model.language_model.")) return "model." + name.substr(std::strlen("model.language_model."));
+    if (starts("model.model.")) return name.substr(std::strlen("model."));
+    if (starts("language_model.")) return name.substr(std::strlen("language_model."));
+    if (starts("model.") || starts("lm_head.")) return name;
+    return "";
+}
+
+void WeightLoader::load_weights_from_file(const std::string& model_path, ModelStage stage, int32_t device_id,
+                                          bool language_model_only) {
+    const std::vector<std::string> files = collect_safetensors_files(model_path);
     hip_check(hipSetDevice(device_id), "hipSetDevice");
     std::unordered_map<std::string, Tensor> loaded;
     for (const auto& path : files) {
@@ -95,16 +118,21 @@ void WeightLoader::load_weights_from_file(const std::string& model_dir, ModelSta
         if (map == MAP_FAILED) throw ModelNotLoadedError("mmap failed for " + path);
         for (const auto& kv : entries) {
             const auto& e = kv.second;
-            if (data_off + e.end > (size_t)st.st_size) {
+            const std::string name = language_model_only ? vl_language_model_name(kv.first) : kv.first;
+            if (name.empty()) continue;
+            if (e.begin > e.end || data_off + e.end > (size_t)st.st_size) {
                 ::munmap(map, (size_t)st.st_size);
                 throw ModelNotLoadedError("tensor " + kv.first + " out of file bounds in " + path);
             }
             Tensor t = Tensor::empty(e.shape, st_dtype(e.dtype), Device::GPU, device_id);
-            check<ModelNotLoadedError>(t.nbytes() == e.end - e.begin, "size mismatch for tensor " + kv.first);
+            if (t.nbytes() != e.end - e.begin) {
+                ::munmap(map, (size_t)st.st_size);
+                throw ModelNotLoadedError("size mismatch for tensor " + kv.first + " in " + path);
+            }
             hip_check(hipMemcpy(t.data_ptr(), static_cast<const char*>(map) + data_off + e.begin, t.nbytes(),
                                 hipMemcpyHostToDevice),
                       "upload " + kv.first);
-            loaded[kv.first] = t;
+            loaded[name] = t;
         }
         ::munmap(map, (size_t)st.st_size);
     }
@@ -340,14 +368,19 @@ std::vector<int32_t> KVManager::request_ids() const {
 // Qwen2_5
 // =================================================================================
 const Tensor& Qwen2_5::w(const std::unordered_map<std::string, Tensor>& ws, const std::string& name) const {
-    // Qwen2.5-VL checkpoints prefix the language model (engine_factory.cpp:73-98).
-    for (const std::string& p : {std::string(""), std::string("model.language_model."), std::string("language_model.")}) {
-        std::string key = name;
-        if (!p.empty()) {
-            if (name.rfind("model.", 0) != 0) continue;
-            key = p + name.substr(6);
-        }
-        auto it = ws.find(key);
+    // Registered tensors may keep a Qwen2.5-VL checkpoint's names (engine_factory.cpp:73-98):
+    // model.X is also looked up as model.language_model.X, model.model.X and
+    // language_model.model.X, lm_head.X as language_model.lm_head.X.
+    auto it = ws.find(name);
+    if (it != ws.end()) return it->second;
+    const bool under_model = name.rfind("model.", 0) == 0;
+    const std::string rest = under_model ? name.substr(6) : name;
+    const std::vector<std::string> alts =
+        under_model ? std::vector<std::string>{"model.language_model." + rest, "model.model." + rest,
+                                               "language_model.model." + rest}
+                    : std::vector<std::string>{"language_model." + name};
+    for (const auto& key : alts) {
+        it = ws.find(key);
         if (it != ws.end()) return it->second;
     }
     throw ModelNotLoadedError("missing weight tensor: " + name);
@@ -836,7 +869,8 @@ StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_pat
     const ModelConfig m = ModelConfig::from_json(cfg_.model_config());
     auto& loader = WeightLoader::instance();
     if (!loader.has_stage(ModelStage::Prefill)) {
-        loader.load_weights_from_file(cfg_.prefill_model_path(), ModelStage::Prefill, device_id_);
+        loader.load_weights_from_file(cfg_.prefill_model_path(), ModelStage::Prefill, device_id_,
+                                      cfg_.model_name() == "qwen2_5_vl");
     }
     model_ = std::make_unique<Qwen2_5>(cfg_, m, loader.get(ModelStage::Prefill), device_id_);
     // fixed KV prefixes are configuration ids: remapped like EOS ids (kv_manager.cpp:151-155)

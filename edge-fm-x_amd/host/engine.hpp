@@ -29,7 +29,13 @@ namespace edge_fm {
 class WeightLoader {
 public:
     static WeightLoader& instance();
-    void load_weights_from_file(const std::string& model_dir, ModelStage stage, int32_t device_id);
+    // Loads every tensor of the checkpoint at model_path (collect_safetensors_files) to
+    // device memory. language_model_only (Qwen2.5-VL checkpoints,
+    // src/engine/engine_factory.cpp:73-98): keep only the language model's tensors
+    // (model., language_model., lm_head. names; the vision tower is not used) under
+    // their text-model names (vl_language_model_name).
+    void load_weights_from_file(const std::string& model_path, ModelStage stage, int32_t device_id,
+                                bool language_model_only = false);
     void register_tensor(ModelStage stage, const std::string& name, const Tensor& t);
     const std::unordered_map<std::string, Tensor>& get(ModelStage stage);
     bool has_stage(ModelStage stage);
@@ -47,6 +53,16 @@ struct SafetensorsEntry {
     size_t begin = 0, end = 0;
 };
 std::map<std::string, SafetensorsEntry> read_safetensors_header(const std::string& path, size_t* data_offset);
+
+// The checkpoint files of a model path (src/engine/engine_factory.cpp:27-49): the path
+// itself when it is a file; else <dir>/model.safetensors when present; else every
+// <dir>/model-*-of-*.safetensors shard in name order. None: ConfigurationError.
+std::vector<std::string> collect_safetensors_files(const std::string& model_path);
+
+// Text-model name of a Qwen2.5-VL checkpoint tensor: model.language_model.X and
+// model.model.X -> model.X, language_model.X -> X; names of the vision tower (anything
+// not under model., language_model. or lm_head.) -> "" (not loaded).
+std::string vl_language_model_name(const std::string& name);
 
 // ---------------------------------------------------------------------------------
 // EngineConfig (src/engine/engine.h:29-89): engine_default.json merged with the user

@@ -178,7 +178,8 @@ PYBIND11_MODULE(edge_fm, m) {
     py::class_<WeightLoader, std::unique_ptr<WeightLoader, py::nodelete>>(m, "WeightLoader")
         .def_static("instance", &WeightLoader::instance, py::return_value_policy::reference)
         .def("load_weights_from_file", &WeightLoader::load_weights_from_file, py::arg("model_path"),
-             py::arg("stage"), py::arg("device_id") = 0, py::call_guard<py::gil_scoped_release>())
+             py::arg("stage"), py::arg("device_id") = 0, py::arg("language_model_only") = false,
+             py::call_guard<py::gil_scoped_release>())
         .def("register_tensor", &WeightLoader::register_tensor, py::arg("stage"), py::arg("name"), py::arg("tensor"))
         .def("get", [](WeightLoader& w, ModelStage s) {
             py::dict d;
@@ -186,6 +187,18 @@ PYBIND11_MODULE(edge_fm, m) {
             return d;
         })
         .def("clear_stage", &WeightLoader::clear_stage);
+
+    // checkpoint reading on the host (no device work): used by the loader tests
+    m.def("collect_safetensors_files", &collect_safetensors_files, py::arg("model_path"));
+    m.def("vl_language_model_name", &vl_language_model_name, py::arg("name"));
+    m.def("read_safetensors_header", [](const std::string& path) {
+        size_t data_off = 0;
+        const auto entries = read_safetensors_header(path, &data_off);
+        py::dict d;
+        for (const auto& kv : entries)
+            d[py::str(kv.first)] = py::make_tuple(kv.second.dtype, kv.second.shape, kv.second.begin, kv.second.end);
+        return py::make_tuple(d, data_off);
+    }, py::arg("path"));
 
     m.def("apply_mrope",
           [](Tensor& q, Tensor& k, const Tensor& position_ids, std::vector<int32_t> mrope_section, float rope_theta,
