@@ -117,7 +117,7 @@ def write_engine_config(path: str, model_dir: str, *, max_tokens: int = 4096, ma
                         prefix_token_ids=None, use_graph: bool = True, temperature: float = 0.0,
                         top_p: float = 1.0, seed: int = 0, lm_head_top1: bool = True, model_name: str = "",
                         operator_impl_table_path: str = "", extra_slots=None, decode_stack=None,
-                        stop_token_ids=None, compact_vocab=None) -> str:
+                        stop_token_ids=None, compact_vocab=None, decode_fused_qkv_attention=None) -> str:
     slots = [{"request_id": 0, "prefix_token_ids": list(prefix_token_ids or []), "max_tokens": max_tokens}]
     for s in extra_slots or []:
         slots.append(s)
@@ -132,6 +132,8 @@ def write_engine_config(path: str, model_dir: str, *, max_tokens: int = 4096, ma
     }
     if decode_stack is not None:
         cfg["runtime"]["decode_stack"] = bool(decode_stack)
+    if decode_fused_qkv_attention is not None:
+        cfg["runtime"]["decode_fused_qkv_attention"] = bool(decode_fused_qkv_attention)
     if compact_vocab is not None:
         cfg["compact_vocab"] = compact_vocab
     with open(path, "w") as f:

@@ -409,7 +409,7 @@ static Tensor concat_rows(const std::vector<const Tensor*>& parts, int32_t devic
 
 Qwen2_5::Qwen2_5(const EngineConfig& cfg, const ModelConfig& m, const std::unordered_map<std::string, Tensor>& ws,
                  int32_t device_id)
-    : m_(m), device_id_(device_id) {
+    : cfg_(cfg), m_(m), device_id_(device_id) {
     model_name_ = cfg.model_name();
     hw_profile_ = cfg.hw_profile();
     stack_enabled_ = cfg.decode_stack() && !m.mrope;
@@ -429,9 +429,6 @@ Qwen2_5::Qwen2_5(const EngineConfig& cfg, const ModelConfig& m, const std::unord
     AttentionOpContext actx = attn_ctx();
     attn_ = AttentionOpRegistry::instance().find_impl_by_id(resolve("attention", "prefill"));
     if (attn_ == nullptr || !attn_->supports(actx)) attn_ = AttentionOpRegistry::instance().default_impl(actx);
-    const std::string lin_id = resolve("linear", "prefill");
-    linear_ = LinearOpRegistry::instance().find_impl_by_id(lin_id);
-    if (linear_ == nullptr) throw ConfigurationError("operator table selects unknown linear impl '" + lin_id + "'");
     RMSNormOpContext nctx;
     nctx.hidden_size = (uint32_t)m.hidden;
     norm_ = NormOpRegistry::instance().find_impl_by_id(resolve("norm", "prefill"));
@@ -475,8 +472,20 @@ Qwen2_5::Qwen2_5(const EngineConfig& cfg, const ModelConfig& m, const std::unord
         L.down_w = w(ws, p + "mlp.down_proj.weight");
         L.in_norm = w(ws, p + "input_layernorm.weight");
         L.post_norm = w(ws, p + "post_attention_layernorm.weight");
+        const uint32_t H = (uint32_t)m.hidden, QD = (uint32_t)m.q_dim(), KVD = (uint32_t)m.kv_dim(),
+                       I = (uint32_t)m.inter;
+        const std::string n = "Layer_" + std::to_string(l);
+        L.qkv = std::make_unique<FusedQKVLinearLayer>(p + "self_attn", cfg, H, QD, KVD, KVD, n + "_QKVLinear");
+        L.o_proj = std::make_unique<LinearLayer>(p + "self_attn.o_proj", cfg, QD, H, n + "_OProj");
+        L.gate_up = std::make_unique<FusedGateUpLinearLayer>(p + "mlp", cfg, H, I, I, n + "_GateUp");
+        L.down = std::make_unique<LinearLayer>(p + "mlp.down_proj", cfg, I, H, n + "_DownProj");
+        L.qkv->load_weights(L.qkv_w, &L.qkv_b);
+        L.o_proj->load_weights(L.o_w, nullptr);
+        L.gate_up->load_weights(L.gu_w, nullptr);
+        L.down->load_weights(L.down_w, nullptr);
         layers_.push_back(std::move(L));
     }
+    mlp_source_ = std::make_unique<PrefillMlpSourceOp>(cfg);
     hip_check(hipDeviceSynchronize(), "fuse weights");
 
     // ---- decode scratch ----
@@ -505,18 +514,41 @@ void Qwen2_5::reserve_decode(uint32_t max_kv_len) {
         if (stack_ws_.empty() || stack_ws_.nbytes() < sb)
             stack_ws_ = Tensor::zeros({(int64_t)sb}, DType::UInt8, Device::GPU, device_id_);
     }
+    // the decode plan for this cache length (impls resolved, their scratch prepared):
+    // nothing is resolved or allocated while a decode step is captured
+    if (!plans_.count(max_kv_len)) {
+        std::vector<DecodeLayerPlan> plan;
+        for (int l = 0; l < m_.layers; ++l) {
+            Layer& Ly = layers_[l];
+            plan.push_back(resolve_decode_layer(cfg_, m_, l, max_kv_len, fused_front_enabled_, *Ly.o_proj, *Ly.down));
+            if (plan.back().gate_up.empty()) Ly.gate_up->selected_impl_id(ModelStage::Decode, 1);
+        }
+        plans_.emplace(max_kv_len, std::move(plan));
+    }
+    const auto& plan = plans_.at(max_kv_len);
     if (uses_fused_front(max_kv_len) && front_sync_ws_.empty()) {
         const size_t sb = efm_decode_qkv_attention_sync_bytes(m_.q_dim(), m_.kv_dim());
         front_sync_ws_ = Tensor::zeros({(int64_t)sb}, DType::UInt8, Device::GPU, device_id_);
     }
+    for (const auto& p : plan)
+        if (p.gate_up.empty() && dec_gu_.empty())
+            dec_gu_ = Tensor::zeros({1, 2 * (int64_t)m_.inter}, DType::BFloat16, Device::GPU, device_id_);
 }
 
-// Fused norm + QKV + attention partials (one launch per layer instead of two) for text
-// models whose cache needs at most 8 splits (the merge folds into the o_proj prologue).
+const std::vector<DecodeLayerPlan>& Qwen2_5::decode_plan(uint32_t max_kv_len) const {
+    auto it = plans_.find(max_kv_len);
+    check<InternalError>(it != plans_.end(), "decode plan not resolved for this cache length");
+    return it->second;
+}
+
+// Some layer runs the fused norm + QKV + attention partials launch (text models whose
+// cache needs at most 8 splits; the merge folds into the o_proj prologue).
 bool Qwen2_5::uses_fused_front(uint32_t max_kv_len) const {
-    if (!fused_front_enabled_ || max_kv_len > 1024 || m_.heads > 64) return false;
-    const efm_attention_ctx c = decode_ctx();
-    return efm_decode_norm_qkv_attention_supported(&c, m_.hidden, max_kv_len) == EFM_OK;
+    auto it = plans_.find(max_kv_len);
+    if (it == plans_.end()) return false;
+    for (const auto& p : it->second)
+        if (p.attention == "hip_gfx950_decode_fused_qkv_attention") return true;
+    return false;
 }
 
 bool Qwen2_5::uses_decode_stack(uint32_t max_kv_len) const {
@@ -621,13 +653,8 @@ void Qwen2_5::prefill(int32_t S, int32_t base, const int32_t* ids, const Tensor*
             norm_->fused_add_rms_norm_forward_fn()(nctx, nrm, res, Ly.in_norm, stream);
         }
         // 2b. fused QKV projection + bias
-        LinearOpContext lctx;
-        lctx.layer_role = "fused_qkv";
-        lctx.stage = ModelStage::Prefill;
-        lctx.shape = {S, DType::BFloat16, DType::BFloat16, DType::BFloat16, H, TOT};
-        lctx.has_bias = true;
         Tensor qkv = pf_qkv_.prefix_view({S, TOT});
-        linear_->forward(lctx, Ly.qkv_w, &Ly.qkv_b, nrm, qkv, stream);
+        Ly.qkv->forward_fp16_bf16(nrm, qkv, stream, ModelStage::Prefill);
         // 2c. K / V rows into cache rows [base, base + S) (qwen2_5.cpp:743-746)
         char* kc = static_cast<char*>(k_caches[l]);
         char* vc = static_cast<char*>(v_caches[l]);
@@ -647,26 +674,30 @@ void Qwen2_5::prefill(int32_t S, int32_t base, const int32_t* ids, const Tensor*
         Tensor ao = pf_attn_.prefix_view({S, QD});
         attn_->forward_prefill(actx, qv, kv_k, kv_v, ao, true, stream);
         // 2e. o_proj -> hidden, post-attention fused add + norm
-        lctx.layer_role = "attention_output";
-        lctx.shape = {S, DType::BFloat16, DType::BFloat16, DType::BFloat16, QD, H};
-        lctx.has_bias = false;
-        linear_->forward(lctx, Ly.o_w, nullptr, ao, hid, stream);
+        Ly.o_proj->forward_fp16_bf16(ao, hid, stream, ModelStage::Prefill);
         norm_->fused_add_rms_norm_forward_fn()(nctx, hid, res, Ly.post_norm, stream);
-        // 2f. MLP: gate/up GEMM with SwiGLU epilogue, down projection into the next
-        // layer's norm input (or hidden for the last layer), qwen2_5.cpp:855-875
-        Tensor mid = pf_mid_.prefix_view({S, (int64_t)m_.inter});
-        FusedGateUpActivationContext gctx;
-        gctx.stage = ModelStage::Prefill;
-        gctx.m = S;
-        gctx.hidden = H;
-        gctx.intermediate = m_.inter;
-        if (swiglu_ == nullptr || !swiglu_->run(gctx, Ly.gu_w, hid, mid, stream)) {
-            throw ConfigurationError("fused gate/up + SwiGLU unavailable for this shape");
-        }
-        lctx.layer_role = "mlp_down";
-        lctx.shape = {S, DType::BFloat16, DType::BFloat16, DType::BFloat16, (int64_t)m_.inter, H};
+        // 2f. MLP into the next layer's norm input (or hidden for the last layer),
+        // qwen2_5.cpp:855-875: the prefill MLP source op (gate/up GEMM with its SwiGLU
+        // epilogue, then down), else the layered path (GatedMlpLayer, gated_mlp.cu:19-67)
         Tensor dst = (l < m_.layers - 1) ? nrm : hid;
-        linear_->forward(lctx, Ly.down_w, nullptr, mid, dst, stream);
+        if (!mlp_source_->try_forward(l, hid, Ly.gu_w, Ly.down_w, dst, stream)) {
+            Tensor mid = pf_mid_.prefix_view({S, (int64_t)m_.inter});
+            FusedGateUpActivationContext gctx;
+            gctx.stage = ModelStage::Prefill;
+            gctx.m = S;
+            gctx.hidden = H;
+            gctx.intermediate = m_.inter;
+            if (swiglu_ == nullptr || !swiglu_->run(gctx, Ly.gu_w, hid, mid, stream)) {
+                Tensor gu = Tensor::empty({S, 2 * (int64_t)m_.inter}, DType::BFloat16, Device::GPU, device_id_);
+                Ly.gate_up->forward_fp16_bf16(hid, gu, stream, ModelStage::Prefill);
+                ActivationOpContext actx2;
+                actx2.batch_size = S;
+                actx2.hidden_size = m_.inter;
+                actx2.input_layout = ActivationInputLayout::kUpGate;
+                act_->act_and_mul(actx2, gu, mid, stream);
+            }
+            Ly.down->forward_fp16_bf16(mid, dst, stream, ModelStage::Prefill);
+        }
     }
     // 3-4. final norm + LM head on the last row (qwen2_5.cpp:883-929)
     const size_t last = (size_t)(S - 1) * H * 2;
@@ -724,80 +755,77 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
         }
         return;
     }
-    // The merge folds into the o_proj prologue when the cache needs at most 8 splits of
-    // 128 keys (max_kv_len <= 1024) and the model has at most 64 query heads.
-    fused_attn_merge_ = max_kv_len <= 1024 && m_.heads <= 64;
-    const bool front = !front_sync_ws_.empty() && uses_fused_front(max_kv_len);
+    const std::vector<DecodeLayerPlan>& plan = decode_plan(max_kv_len);
     for (int l = 0; l < m_.layers; ++l) {
-        const Layer& Ly = layers_[l];
-        if (front) {
-            // input norm (+ residual) + QKV + attention split partials in one launch; the
-            // partials merge in the o_proj prologue
+        Layer& Ly = layers_[l];
+        const DecodeLayerPlan& P = plan[l];
+        if (P.attention == "hip_gfx950_decode_fused_qkv_attention") {
+            // input norm (+ residual) + QKV + attention split partials in one launch
             efm_check(efm_decode_norm_qkv_attention(
                           &c, H, m_.eps, dec_h_.data_ptr(), (l == 0) ? nullptr : dec_res_[1].data_ptr(),
                           dec_res_[0].data_ptr(), Ly.in_norm.data_ptr(), Ly.qkv_w.data_ptr(), Ly.qkv_b.data_ptr(),
                           k_caches[l], v_caches[l], d_kv_len, max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(),
                           front_sync_ws_.data_ptr(), front_sync_ws_.nbytes(), stream),
                       "decode norm+qkv+attention");
-            efm_check(efm_decode_attention_merge_o_proj(&c, d_kv_len, max_kv_len, attn_ws_.data_ptr(),
-                                                        attn_ws_.nbytes(), Ly.o_w.data_ptr(), H, dec_a_.data_ptr(),
-                                                        stream),
-                      "decode attention merge + o_proj");
-            efm_check(efm_decode_norm_gate_up_swiglu(H, m_.inter, m_.eps, dec_a_.data_ptr(), dec_res_[0].data_ptr(),
-                                                     dec_res_[1].data_ptr(), Ly.post_norm.data_ptr(),
-                                                     Ly.gu_w.data_ptr(), dec_mid_.data_ptr(), stream),
-                      "decode norm+gate_up+swiglu");
-            efm_check(efm_linear(1, m_.inter, H, dec_mid_.data_ptr(), Ly.down_w.data_ptr(), nullptr,
-                                 dec_h_.data_ptr(), EFM_DTYPE_BF16, stream),
-                      "decode down_proj");
-            continue;
+        } else {
+            // input norm (+ residual) + QKV + bias, K/V straight into the cache slot
+            void* kdst = k_caches[l];
+            void* vdst = v_caches[l];
+            const uint32_t* slot_len = d_kv_len;
+            if (m_.mrope) {  // M-RoPE rotates K before the cache write: stage through kvtmp
+                kdst = dec_kvtmp_.data_ptr();
+                vdst = static_cast<char*>(dec_kvtmp_.data_ptr()) + (size_t)KVD * 2;
+                slot_len = static_cast<const uint32_t*>(dec_one_.data_ptr());
+            }
+            efm_check(efm_decode_norm_qkv(H, QD, KVD, m_.eps, dec_h_.data_ptr(),
+                                          (l == 0) ? nullptr : dec_res_[1].data_ptr(), dec_res_[0].data_ptr(),
+                                          Ly.in_norm.data_ptr(), Ly.qkv_w.data_ptr(), Ly.qkv_b.data_ptr(),
+                                          dec_q_.data_ptr(), kdst, vdst, slot_len, stream),
+                      "decode norm+qkv");
+            if (m_.mrope) {
+                efm_check(efm_decode_mrope_write_kv(dec_q_.data_ptr(), kdst, vdst, dec_q_.data_ptr(), k_caches[l],
+                                                    v_caches[l], m_.heads, m_.kv_heads, m_.head_dim, d_pos3,
+                                                    m_.mrope_section[0], m_.mrope_section[1], m_.mrope_section[2],
+                                                    m_.theta, 1.0f, d_kv_len, stream),
+                          "decode mrope + kv write");
+            }
+            if (P.partials_to_o_proj) {
+                efm_check(efm_decode_attention_partials(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], d_kv_len,
+                                                        max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(), stream),
+                          "decode attention partials");
+            } else {
+                efm_check(efm_attention_decode(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], dec_attn_.data_ptr(),
+                                               0, d_kv_len, max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(),
+                                               stream),
+                          "decode attention");
+            }
         }
-        // input norm (+ residual) + QKV + bias, K/V straight into the cache slot
-        void* kdst = k_caches[l];
-        void* vdst = v_caches[l];
-        const uint32_t* slot_len = d_kv_len;
-        if (m_.mrope) {  // M-RoPE rotates K before the cache write: stage through kvtmp
-            kdst = dec_kvtmp_.data_ptr();
-            vdst = static_cast<char*>(dec_kvtmp_.data_ptr()) + (size_t)KVD * 2;
-            slot_len = static_cast<const uint32_t*>(dec_one_.data_ptr());
-        }
-        efm_check(efm_decode_norm_qkv(H, QD, KVD, m_.eps, (l == 0) ? dec_h_.data_ptr() : dec_h_.data_ptr(),
-                                      (l == 0) ? nullptr : dec_res_[1].data_ptr(), dec_res_[0].data_ptr(),
-                                      Ly.in_norm.data_ptr(), Ly.qkv_w.data_ptr(), Ly.qkv_b.data_ptr(),
-                                      dec_q_.data_ptr(), kdst, vdst, slot_len, stream),
-                  "decode norm+qkv");
-        if (m_.mrope) {
-            efm_check(efm_decode_mrope_write_kv(dec_q_.data_ptr(), kdst, vdst, dec_q_.data_ptr(), k_caches[l],
-                                                v_caches[l], m_.heads, m_.kv_heads, m_.head_dim, d_pos3,
-                                                m_.mrope_section[0], m_.mrope_section[1], m_.mrope_section[2],
-                                                m_.theta, 1.0f, d_kv_len, stream),
-                      "decode mrope + kv write");
-        }
-        if (fused_attn_merge_) {
-            // split partials, merged in the o_proj prologue (two launches instead of an
-            // attention kernel with an in-kernel merge plus the o_proj)
-            efm_check(efm_decode_attention_partials(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], d_kv_len,
-                                                    max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(), stream),
-                      "decode attention partials");
+        if (P.partials_to_o_proj) {
             efm_check(efm_decode_attention_merge_o_proj(&c, d_kv_len, max_kv_len, attn_ws_.data_ptr(),
                                                         attn_ws_.nbytes(), Ly.o_w.data_ptr(), H, dec_a_.data_ptr(),
                                                         stream),
                       "decode attention merge + o_proj");
         } else {
-            efm_check(efm_attention_decode(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], dec_attn_.data_ptr(), 0,
-                                           d_kv_len, max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(), stream),
-                      "decode attention");
-            efm_check(efm_linear(1, QD, H, dec_attn_.data_ptr(), Ly.o_w.data_ptr(), nullptr, dec_a_.data_ptr(),
-                                 EFM_DTYPE_BF16, stream),
-                      "decode o_proj");
+            Ly.o_proj->forward_fp16_bf16(dec_attn_, dec_a_, stream, ModelStage::Decode);
         }
-        efm_check(efm_decode_norm_gate_up_swiglu(H, m_.inter, m_.eps, dec_a_.data_ptr(), dec_res_[0].data_ptr(),
-                                                 dec_res_[1].data_ptr(), Ly.post_norm.data_ptr(),
-                                                 Ly.gu_w.data_ptr(), dec_mid_.data_ptr(), stream),
-                  "decode norm+gate_up+swiglu");
-        efm_check(efm_linear(1, m_.inter, H, dec_mid_.data_ptr(), Ly.down_w.data_ptr(), nullptr, dec_h_.data_ptr(),
-                             EFM_DTYPE_BF16, stream),
-                  "decode down_proj");
+        if (!P.gate_up.empty()) {
+            efm_check(efm_decode_norm_gate_up_swiglu(H, m_.inter, m_.eps, dec_a_.data_ptr(), dec_res_[0].data_ptr(),
+                                                     dec_res_[1].data_ptr(), Ly.post_norm.data_ptr(),
+                                                     Ly.gu_w.data_ptr(), dec_mid_.data_ptr(), stream),
+                      "decode norm+gate_up+swiglu");
+        } else {
+            // layered: residual_out <- a + residual_in, a <- norm(.), gate/up, activation
+            hip_check(hipMemcpyAsync(dec_res_[1].data_ptr(), dec_res_[0].data_ptr(), (size_t)H * 2,
+                                     hipMemcpyDeviceToDevice, stream),
+                      "decode residual");
+            efm_check(efm_fused_add_rms_norm(1, (uint32_t)H, m_.eps, dec_a_.data_ptr(), dec_res_[1].data_ptr(),
+                                             Ly.post_norm.data_ptr(), stream),
+                      "decode post-attention norm");
+            Ly.gate_up->forward_fp16_bf16(dec_a_, dec_gu_, stream, ModelStage::Decode);
+            efm_check(efm_act_and_mul(1, m_.inter, EFM_LAYOUT_UP_GATE, dec_gu_.data_ptr(), dec_mid_.data_ptr(), stream),
+                      "decode silu_and_mul");
+        }
+        Ly.down->forward_fp16_bf16(dec_mid_, dec_h_, stream, ModelStage::Decode);
     }
     if (logits == nullptr) {
         efm_check(efm_decode_norm_lm_head_top1(H, m_.vocab, m_.eps, dec_h_.data_ptr(), dec_res_[1].data_ptr(),
@@ -812,6 +840,95 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
                              stream),
                   "decode lm head");
     }
+}
+
+// =================================================================================
+// Decode plan
+// =================================================================================
+DecodeLayerPlan resolve_decode_layer(const EngineConfig& cfg, const ModelConfig& m, int32_t layer,
+                                     uint32_t max_kv_len, bool allow_fused_front, LinearLayer& o_proj,
+                                     LinearLayer& down) {
+    const std::string model = cfg.model_name(), hw = cfg.hw_profile(), table = cfg.operator_table_path();
+    DecodeLayerPlan P;
+    // attention (AttentionLayer::resolve_impl, attention.cu:211-276)
+    AttentionOpContext ctx;
+    ctx.num_qo_heads = (uint32_t)m.heads;
+    ctx.num_kv_heads = (uint32_t)m.kv_heads;
+    ctx.head_dim = (uint32_t)m.head_dim;
+    ctx.rope_theta = m.theta;
+    ctx.dtype = DType::BFloat16;
+    ctx.pos_encoding = m.mrope ? AttentionPosEncoding::kNone : AttentionPosEncoding::kRoPELlama;
+    ctx.device_id = cfg.device_id();
+    ctx.decode_hidden = allow_fused_front ? (uint32_t)m.hidden : 0;   // the fused launch needs it
+    ctx.decode_max_kv_len = max_kv_len;
+    OperatorQuery q;
+    q.op_kind = "attention";
+    q.op_name = "attention";
+    q.stage = "decode";
+    q.shape_sig = attention_shape_sig(ctx.num_qo_heads, ctx.num_kv_heads, ctx.head_dim);
+    AttentionOp* attn = nullptr;
+    if (auto rec = OperatorImplTable::instance().resolve(model, hw, table, q)) {
+        attn = AttentionOpRegistry::instance().find_impl_by_id(rec->impl_id);
+        if (attn == nullptr)
+            throw ConfigurationError("AttentionLayer: operator_impl_table selected unknown impl '" + rec->impl_id + "'");
+        ctx.impl_params = rec->impl_params;
+        if (!attn->supports(ctx)) attn = nullptr;   // registry default instead (attention.cu:257-273)
+    }
+    if (attn == nullptr) attn = AttentionOpRegistry::instance().default_impl(ctx);
+    P.attention = attn->impl_id();
+    // o_proj, and whether the split partials merge in its prologue
+    P.o_proj = o_proj.selected_impl_id(ModelStage::Decode, 1);
+    const bool merge = P.o_proj == "hip_gfx950_decode_merge_o_proj";
+    if (P.attention == "hip_gfx950_decode_fused_qkv_attention" && !merge)
+        throw ConfigurationError("decode layer " + std::to_string(layer) + ": attention impl '" + P.attention +
+                                 "' leaves split partials, which o_proj impl '" + P.o_proj + "' cannot merge");
+    P.partials_to_o_proj = merge && P.attention != "hip_gfx950_attention";
+    // gate/up with the post-attention norm and SwiGLU fused (try_forward_decode_swiglu_fused,
+    // linear.cu:2054-2201: unknown or unsupporting record -> ConfigurationError), else,
+    // when no impl supports the shape, the layered MLP
+    FusedGateUpActivationContext g;
+    g.stage = ModelStage::Decode;
+    g.m = 1;
+    g.hidden = m.hidden;
+    g.intermediate = m.inter;
+    OperatorQuery gq;
+    gq.op_kind = "fused_gate_up_activation";
+    gq.layer_role = "fused_gate_up";
+    gq.op_name = "model.layers." + std::to_string(layer) + ".mlp";
+    gq.stage = "decode";
+    LinearLayer::LinearShapeSignature gs;
+    gs.m = 1;
+    gs.in_features = (uint32_t)m.hidden;
+    gs.out_features = 2 * (uint32_t)m.inter;
+    gq.shape_sig = gs.to_string();
+    FusedGateUpActivationOp* gop = nullptr;
+    if (auto rec = OperatorImplTable::instance().resolve(model, hw, table, gq)) {
+        gop = FusedGateUpActivationRegistry::instance().find_impl_by_id(rec->impl_id);
+        if (gop == nullptr)
+            throw ConfigurationError("FusedGateUpLinearLayer: operator_impl_table selected unknown impl '" +
+                                     rec->impl_id + "'");
+        if (!gop->supports(g))
+            throw ConfigurationError("FusedGateUpLinearLayer: operator_impl_table selected unsupported impl '" +
+                                     rec->impl_id + "'");
+    } else {
+        gop = FusedGateUpActivationRegistry::instance().default_impl(g);
+    }
+    P.gate_up = gop ? gop->impl_id() : "";
+    P.down = down.selected_impl_id(ModelStage::Decode, 1);
+    return P;
+}
+
+std::vector<DecodeLayerPlan> plan_decode(const std::string& engine_config_path, uint32_t max_kv_len) {
+    EngineConfig cfg(engine_config_path);
+    const ModelConfig m = ModelConfig::from_json(cfg.model_config());
+    std::vector<DecodeLayerPlan> out;
+    for (int l = 0; l < m.layers; ++l) {
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        LinearLayer o(p + "self_attn.o_proj", cfg, (uint32_t)m.q_dim(), (uint32_t)m.hidden);
+        LinearLayer d(p + "mlp.down_proj", cfg, (uint32_t)m.inter, (uint32_t)m.hidden);
+        out.push_back(resolve_decode_layer(cfg, m, l, max_kv_len, cfg.decode_fused_qkv_attention() && !m.mrope, o, d));
+    }
+    return out;
 }
 
 // =================================================================================

@@ -129,6 +129,38 @@ struct ModelConfig {
 };
 
 // ---------------------------------------------------------------------------------
+// Decode plan: the impls one decode layer runs, resolved from the operator table at
+// stage "decode" like the reference's AttentionLayer / LinearLayer / FusedGateUpLinearLayer
+// (src/layers/attention.cu:211-276, src/operators/linear_impl.cu:866-915):
+//   attention  AttentionOp for (op_kind attention, op_name attention, stage decode,
+//              shape_sig "num_qo_heads=..|num_kv_heads=..|head_dim=.."); a record naming an
+//              impl that does not support the shape falls back to the registry default
+//              (fused launch, split partials, generic attention, in that order)
+//   o_proj     LinearLayer impl of model.layers.<l>.self_attn.o_proj at (decode, m = 1)
+//   gate_up    FusedGateUpActivationOp at (decode, op_name model.layers.<l>.mlp), run with
+//              the post-attention norm as its prologue; "" when no impl supports the
+//              shape (norm, gate/up linear, activation as three launches)
+//   down       LinearLayer impl of model.layers.<l>.mlp.down_proj at (decode, m = 1)
+// An attention impl that leaves split partials needs the merge-in-prologue o_proj
+// (hip_gfx950_decode_merge_o_proj); the fused launch with any other o_proj is a
+// ConfigurationError, the split impl then runs with its in-kernel merge.
+// ---------------------------------------------------------------------------------
+struct DecodeLayerPlan {
+    std::string attention, o_proj, gate_up, down;
+    bool partials_to_o_proj = false;   // attention leaves split partials; o_proj merges them
+};
+
+class LinearLayer;
+// Resolve one decode layer for caches of up to max_kv_len rows. allow_fused_front: the
+// engine config permits the fused norm + QKV + attention launch.
+DecodeLayerPlan resolve_decode_layer(const EngineConfig& cfg, const ModelConfig& m, int32_t layer,
+                                     uint32_t max_kv_len, bool allow_fused_front, LinearLayer& o_proj,
+                                     LinearLayer& down);
+// The plan of every layer of the model an engine config describes, with no device work
+// (the engine resolves the same plan when it reserves its decode scratch).
+std::vector<DecodeLayerPlan> plan_decode(const std::string& engine_config_path, uint32_t max_kv_len);
+
+// ---------------------------------------------------------------------------------
 // KVManager (src/engine/tasks/token_generation/kv_manager.h:58-106): one contiguous
 // buffer per request slot, laid out [layer][K | V][max_tokens][Hkv * hd] bf16.
 // ---------------------------------------------------------------------------------
@@ -187,8 +219,10 @@ public:
     // graph capture; no-op when the stack is not used or the table exists).
     void prepare_decode_stack(uint32_t max_kv_len, void** k_caches, void** v_caches, hipStream_t stream);
     // Whether decode steps run efm_decode_norm_qkv_attention (input norm + QKV +
-    // attention partials in one launch per layer).
+    // attention partials in one launch per layer) in every layer.
     bool uses_fused_front(uint32_t max_kv_len) const;
+    // The decode plan for caches of max_kv_len rows (resolved by reserve_decode).
+    const std::vector<DecodeLayerPlan>& decode_plan(uint32_t max_kv_len) const;
     // Throws DeviceError if a decode-stack or fused QKV + attention launch since the last
     // check could not exchange its vectors in time (synchronises the stream).
     void check_decode_status(hipStream_t stream);
@@ -196,7 +230,11 @@ public:
 private:
     struct Layer {
         Tensor qkv_w, qkv_b, o_w, gu_w, down_w, in_norm, post_norm;
+        // LinearLayers over the tensors above, under the reference's prefixes
+        // (self_attn [fused_qkv], self_attn.o_proj, mlp [fused_gate_up], mlp.down_proj)
+        std::unique_ptr<LinearLayer> qkv, o_proj, gate_up, down;
     };
+    const EngineConfig& cfg_;
     ModelConfig m_;
     int32_t device_id_;
     std::string model_name_, hw_profile_, table_path_;
@@ -204,14 +242,16 @@ private:
     std::vector<Layer> layers_;
     // operator instances resolved from the implementation table
     AttentionOp* attn_ = nullptr;
-    LinearImpl* linear_ = nullptr;
     NormOp* norm_ = nullptr;
     FusedGateUpActivationOp* swiglu_ = nullptr;
     ActivationOp* act_ = nullptr;
+    std::unique_ptr<PrefillMlpSourceOp> mlp_source_;
+    // decode plans per cache length (reserve_decode)
+    std::map<uint32_t, std::vector<DecodeLayerPlan>> plans_;
+    Tensor dec_gu_;   // [1, 2 I] gate/up output of the layered decode MLP
     // decode scratch
     Tensor dec_h_, dec_res_[2], dec_q_, dec_attn_, dec_a_, dec_mid_, dec_kvtmp_, dec_one_, top1_ws_;
     Tensor attn_ws_;
-    bool fused_attn_merge_ = false;
     bool stack_enabled_ = false;   // config switch (text models only)
     Tensor stack_ws_;
     std::map<void*, Tensor> stack_tables_;   // per request slot, keyed by its layer-0 K cache

@@ -1,5 +1,7 @@
 #include "operators.hpp"
 
+#include "engine.hpp"
+
 #include <cctype>
 #include <filesystem>
 #include <map>
@@ -58,20 +60,29 @@ OperatorImplRecord OperatorImplRecord::from_json(const Json& j) {
     return r;
 }
 
+// The records used when the engine config names no table file (the role of the
+// reference's engine_default table): each op kind resolves to this library's impls, and at stage "decode" the
+// attention of a layer is the fused norm + QKV + attention launch whose split partials
+// merge in the o_proj prologue (impls that do not support a shape fall back to the
+// registry default, attention.cu:257-273).
 static std::vector<OperatorImplRecord> builtin_records() {
     std::vector<OperatorImplRecord> out;
-    const char* kinds[][2] = {{"linear", "hip_gfx950_linear"},
-                              {"attention", "hip_gfx950_attention"},
-                              {"norm", "hip_gfx950_norm"},
-                              {"activation", "hip_gfx950_silu_and_mul"},
-                              {"fused_gate_up_activation", "hip_gfx950_swiglu"}};
+    const char* recs[][4] = {{"linear", "", "", "hip_gfx950_linear"},
+                             {"linear", "attention_output", "decode", "hip_gfx950_decode_merge_o_proj"},
+                             {"attention", "", "", "hip_gfx950_attention"},
+                             {"attention", "", "decode", "hip_gfx950_decode_fused_qkv_attention"},
+                             {"norm", "", "", "hip_gfx950_norm"},
+                             {"activation", "", "", "hip_gfx950_silu_and_mul"},
+                             {"fused_gate_up_activation", "", "", "hip_gfx950_swiglu"}};
     for (const char* model : {"qwen2_5", "qwen2_5_vl"}) {
-        for (auto& k : kinds) {
+        for (auto& k : recs) {
             OperatorImplRecord r;
             r.model_name = model;
             r.hw_profile = "rocm";
             r.op_kind = k[0];
-            r.impl_id = k[1];
+            r.layer_role = k[1];
+            r.stage = k[2];
+            r.impl_id = k[3];
             out.push_back(r);
         }
     }
@@ -104,7 +115,10 @@ const std::vector<OperatorImplRecord>& OperatorImplTable::load_locked(const std:
     const std::string key = table_key(path);
     auto it = tables_.find(key);
     if (it != tables_.end()) return it->second;
-    std::vector<OperatorImplRecord> recs = builtin_records();
+    // A table file replaces the built-in records (the reference reads one table file);
+    // queries it has no record for resolve to the registry defaults.
+    std::vector<OperatorImplRecord> recs;
+    if (path.empty()) recs = builtin_records();
     if (!path.empty()) {
         Json j;
         try {
@@ -172,6 +186,11 @@ std::string resolve_impl_id(const std::string& model_name, const std::string& hw
 // ---------------------------------------------------------------------------------
 // Attention
 // ---------------------------------------------------------------------------------
+std::string attention_shape_sig(uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim) {
+    return "num_qo_heads=" + std::to_string(num_qo_heads) + "|num_kv_heads=" + std::to_string(num_kv_heads) +
+           "|head_dim=" + std::to_string(head_dim);
+}
+
 efm_attention_ctx to_c_ctx(const AttentionOpContext& c) {
     efm_attention_ctx r{};
     r.num_qo_heads = c.num_qo_heads;
@@ -212,7 +231,7 @@ struct DecodeWorkspace {
 };
 DecodeWorkspace g_decode_ws;
 
-class HipAttentionOp final : public AttentionOp {
+class HipAttentionOp : public AttentionOp {
 public:
     std::string impl_id() const override { return "hip_gfx950_attention"; }
     bool supports(const AttentionOpContext& c) const override {
@@ -243,9 +262,45 @@ public:
     }
 };
 
+// Decode-stage attention impls. Both compute the same attention as HipAttentionOp (its
+// forward_prefill / forward_decode run for direct calls); what they add is how a decode
+// layer is launched, which the engine reads from the impl id:
+//   hip_gfx950_decode_fused_qkv_attention  the input norm + QKV + split attention in one
+//       launch (efm_decode_norm_qkv_attention), partials merged in the o_proj prologue
+//   hip_gfx950_decode_split_attention      norm + QKV, then the split attention, partials
+//       merged in the o_proj prologue
+// Both need the merge to fold into o_proj: at most 8 splits (1024 cached rows) and 64
+// query heads; the fused launch also a text model (rotate-on-read cache), head_dim 128
+// and efm_decode_norm_qkv_attention_supported.
+class HipDecodeSplitAttentionOp : public HipAttentionOp {
+public:
+    std::string impl_id() const override { return "hip_gfx950_decode_split_attention"; }
+    bool supports(const AttentionOpContext& c) const override {
+        return HipAttentionOp::supports(c) && c.decode_max_kv_len > 0 && c.decode_max_kv_len <= 1024 &&
+               c.num_qo_heads <= 64;
+    }
+};
+
+class HipDecodeFusedQkvAttentionOp final : public HipDecodeSplitAttentionOp {
+public:
+    std::string impl_id() const override { return "hip_gfx950_decode_fused_qkv_attention"; }
+    bool supports(const AttentionOpContext& c) const override {
+        if (!HipDecodeSplitAttentionOp::supports(c) || c.decode_hidden == 0) return false;
+        if (c.pos_encoding != AttentionPosEncoding::kRoPELlama) return false;
+        efm_attention_ctx cc = to_c_ctx(c);
+        cc.k_already_prerotated = EFM_K_PREROTATED_EXCEPT_NEWEST;
+        return efm_decode_norm_qkv_attention_supported(&cc, (int32_t)c.decode_hidden, c.decode_max_kv_len) == EFM_OK;
+    }
+};
+
 }  // namespace
 
-AttentionOpRegistry::AttentionOpRegistry() { impls_.push_back(std::make_unique<HipAttentionOp>()); }
+// default preference: fused launch, split partials, generic attention
+AttentionOpRegistry::AttentionOpRegistry() {
+    impls_.push_back(std::make_unique<HipDecodeFusedQkvAttentionOp>());
+    impls_.push_back(std::make_unique<HipDecodeSplitAttentionOp>());
+    impls_.push_back(std::make_unique<HipAttentionOp>());
+}
 AttentionOpRegistry& AttentionOpRegistry::instance() {
     static AttentionOpRegistry r;
     return r;
@@ -342,16 +397,318 @@ ActivationOp* ActivationOpRegistry::default_impl(const ActivationOpContext& ctx)
 // ---------------------------------------------------------------------------------
 // Linear
 // ---------------------------------------------------------------------------------
-std::string linear_shape_sig(const LinearShape& s) {
-    return "m=" + std::to_string(s.m) + "|input=" + std::to_string((int)s.input) +
-           "|weight=" + std::to_string((int)s.weight) + "|output=" + std::to_string((int)s.output) +
-           "|in_features=" + std::to_string(s.in_features) + "|out_features=" + std::to_string(s.out_features);
+std::string infer_layer_role(const std::string& p) {
+    if (p.find("lm_head") != std::string::npos) return "lm_head";
+    if (p.find("qkv_fused") != std::string::npos) return "fused_qkv";
+    if (p.find("gate_up_fused") != std::string::npos) return "fused_gate_up";
+    if (p.find(".o_proj") != std::string::npos) return "attention_output";
+    if (p.find(".down_proj") != std::string::npos) return "mlp_down";
+    return "linear";
+}
+
+std::string stage_key(ModelStage stage) { return stage == ModelStage::Decode ? "decode" : "prefill"; }
+
+std::string LinearLayer::LinearShapeSignature::to_string() const {
+    return "m=" + std::to_string(m) + "|input=" + std::to_string((int)input_dtype) +
+           "|weight=" + std::to_string((int)weight_dtype) + "|output=" + std::to_string((int)output_dtype) +
+           "|in_features=" + std::to_string(in_features) + "|out_features=" + std::to_string(out_features);
 }
 
 namespace {
-// Grow-only per-device scratch for the split-K prefill GEMMs (the reference's linear impls
-// take theirs from StaticBufferManager::get_cache_buf, src/utils/memory.h:31-109). Grows
-// only outside graph capture: decode (m = 1) never needs it.
+
+bool plain_bf16(const LinearLayer::LinearOpContext& c, const LinearLayer::WeightSet& ws) {
+    const auto& s = c.shape;
+    if (ws.quant_type_ != LinearLayer::QuantType::FP16_BF16 || ws.weight_ == nullptr) return false;
+    if (s.input_dtype != DType::BFloat16 || s.weight_dtype != DType::BFloat16) return false;
+    if (s.output_dtype != DType::BFloat16 && s.output_dtype != DType::Float32) return false;
+    return s.m >= 1 && s.in_features % (s.m == 1 ? 8u : 32u) == 0;
+}
+
+// This library's GEMV (m = 1) / MFMA GEMM (m > 1). prepare() sizes the split-K scratch the
+// kernel plan for this shape uses (zero for most shapes) and allocates it once per
+// (stage, m): forward() never allocates, so a decode step can be captured into a graph.
+class HipLinearImpl : public LinearLayer::LinearImpl {
+public:
+    std::string impl_id() const override { return "hip_gfx950_linear"; }
+    bool supports(const LinearLayer::LinearOpContext& c, const LinearLayer::WeightSet& ws) const override {
+        return plain_bf16(c, ws);
+    }
+    void prepare(LinearLayer&, const LinearLayer::LinearOpContext& c, const LinearLayer::WeightSet& ws,
+                 const Tensor&, Tensor&, hipStream_t, LinearLayer::CachedDescriptors& cached) override {
+        if (cached.prepared_) return;
+        cached.workspace_bytes_ = efm_linear_workspace_bytes(c.shape.m, c.shape.in_features, c.shape.out_features);
+        if (cached.workspace_bytes_ > 0)
+            cached.workspace_ = Tensor::empty({(int64_t)cached.workspace_bytes_}, DType::UInt8, Device::GPU,
+                                              ws.weight_->device().second);
+        cached.prepared_ = true;
+    }
+    void forward(LinearLayer& owner, const LinearLayer::LinearOpContext& c, const LinearLayer::WeightSet& ws,
+                 const Tensor& in, Tensor& out, hipStream_t s, LinearLayer::CachedDescriptors& cached) override {
+        prepare(owner, c, ws, in, out, s, cached);
+        efm_check(efm_linear_ws(c.shape.m, c.shape.in_features, c.shape.out_features, in.data_ptr(),
+                                ws.weight_->data_ptr(), ws.bias_ ? ws.bias_->data_ptr() : nullptr, out.data_ptr(),
+                                c.shape.output_dtype == DType::Float32 ? EFM_DTYPE_F32 : EFM_DTYPE_BF16,
+                                cached.workspace_.empty() ? nullptr : cached.workspace_.data_ptr(),
+                                cached.workspace_bytes_, s),
+                  "linear " + c.layer_prefix);
+    }
+};
+
+// The o_proj of a decode layer whose attention left split partials: the engine runs the
+// merge in this GEMV's prologue (efm_decode_attention_merge_o_proj). Called as a plain
+// linear (a merged attention output in), it is the GEMV.
+class HipDecodeMergeOProjImpl final : public HipLinearImpl {
+public:
+    std::string impl_id() const override { return "hip_gfx950_decode_merge_o_proj"; }
+    bool supports(const LinearLayer::LinearOpContext& c, const LinearLayer::WeightSet& ws) const override {
+        return c.stage == ModelStage::Decode && c.layer_role == "attention_output" && c.shape.m == 1 &&
+               c.shape.output_dtype == DType::BFloat16 && ws.bias_ == nullptr && plain_bf16(c, ws);
+    }
+};
+
+// Prefill projections through PrefillLinearSourceOp::try_forward, the layered GEMM when
+// it declines (the reference's cutlass_prefill_linear_source_op, linear_impl.cu:708-770).
+class HipPrefillSourceOpLinearImpl final : public LinearLayer::LinearImpl {
+public:
+    std::string impl_id() const override { return "hip_gfx950_prefill_linear_source_op"; }
+    bool supports(const LinearLayer::LinearOpContext& c, const LinearLayer::WeightSet& ws) const override {
+        return c.stage == ModelStage::Prefill && (c.layer_role == "fused_qkv" || c.layer_role == "attention_output") &&
+               c.shape.output_dtype == DType::BFloat16 && plain_bf16(c, ws);
+    }
+    void prepare(LinearLayer&, const LinearLayer::LinearOpContext&, const LinearLayer::WeightSet&, const Tensor&,
+                 Tensor&, hipStream_t, LinearLayer::CachedDescriptors& cached) override {
+        cached.selected_impl_id_ = impl_id();
+    }
+    void forward(LinearLayer& owner, const LinearLayer::LinearOpContext& c, const LinearLayer::WeightSet& ws,
+                 const Tensor& in, Tensor& out, hipStream_t s, LinearLayer::CachedDescriptors& cached) override {
+        prepare(owner, c, ws, in, out, s, cached);
+        PrefillLinearSourceOp* op = owner.prefill_linear_source_op();
+        if (op != nullptr && op->try_forward(c.layer_role, 0, in, *ws.weight_, ws.bias_, out, s)) return;
+        LinearLayer::LinearImpl* fallback = LinearOpRegistry::instance().find_impl_by_id("hip_gfx950_linear");
+        check<InternalError>(fallback != nullptr, "LinearLayer: hip_gfx950_linear fallback impl is missing");
+        fallback->forward(owner, c, ws, in, out, s, cached);
+    }
+};
+
+// A shape-only weight descriptor (no storage) so that impls can be resolved and planned
+// before weights are loaded; supports() reads only dtypes and shapes.
+Tensor shape_only(std::vector<int64_t> shape, int32_t device_id) {
+    return Tensor::view(nullptr, std::move(shape), DType::BFloat16, Device::GPU, device_id);
+}
+
+}  // namespace
+
+LinearOpRegistry::LinearOpRegistry() {
+    impls_.push_back(std::make_unique<HipDecodeMergeOProjImpl>());
+    impls_.push_back(std::make_unique<HipLinearImpl>());
+    impls_.push_back(std::make_unique<HipPrefillSourceOpLinearImpl>());
+}
+LinearOpRegistry& LinearOpRegistry::instance() {
+    static LinearOpRegistry r;
+    return r;
+}
+LinearLayer::LinearImpl* LinearOpRegistry::find_impl_by_id(const std::string& id) const {
+    for (auto& i : impls_)
+        if (i->impl_id() == id) return i.get();
+    return nullptr;
+}
+LinearLayer::LinearImpl* LinearOpRegistry::default_impl(const LinearLayer::LinearOpContext& ctx,
+                                                        const LinearLayer::WeightSet& ws) const {
+    for (auto& i : impls_)
+        if (i->supports(ctx, ws)) return i.get();
+    return nullptr;
+}
+
+LinearLayer::LinearLayer(const std::string& layer_prefix, const EngineConfig& engine_config, uint32_t in_features,
+                         uint32_t out_features, std::string layer_name)
+    : LinearLayer(layer_prefix, infer_layer_role(layer_prefix), engine_config, in_features, out_features,
+                  std::move(layer_name)) {}
+
+LinearLayer::LinearLayer(const std::string& layer_prefix, std::string layer_role, const EngineConfig& engine_config,
+                         uint32_t in_features, uint32_t out_features, std::string layer_name)
+    : prefix_(layer_prefix), role_(std::move(layer_role)), name_(std::move(layer_name)),
+      model_name_(engine_config.model_name()), hw_profile_(engine_config.hw_profile()),
+      table_path_(engine_config.operator_table_path()), in_(in_features), out_(out_features),
+      source_op_(std::make_unique<PrefillLinearSourceOp>(engine_config)) {
+    weight_ = shape_only({(int64_t)out_, (int64_t)in_}, engine_config.device_id());
+    ws_.weight_ = &weight_;
+}
+
+LinearLayer::~LinearLayer() = default;
+
+void LinearLayer::load_weights(const Tensor& weight, const Tensor* bias) {
+    check<ModelNotLoadedError>(weight.shape().size() == 2 && weight.shape()[0] == out_ && weight.shape()[1] == in_,
+                               "LinearLayer " + prefix_ + ": weight must be [" + std::to_string(out_) + ", " +
+                                   std::to_string(in_) + "]");
+    check<ModelNotLoadedError>(weight.dtype() == DType::BFloat16, "LinearLayer " + prefix_ + ": weight must be bf16");
+    weight_ = weight;
+    ws_.weight_ = &weight_;
+    if (bias != nullptr) {
+        check<ModelNotLoadedError>(bias->numel() == out_ && bias->dtype() == DType::BFloat16,
+                                   "LinearLayer " + prefix_ + ": bias must be bf16 [" + std::to_string(out_) + "]");
+        bias_ = *bias;
+        ws_.bias_ = &bias_;
+    } else {
+        bias_ = Tensor();
+        ws_.bias_ = nullptr;
+    }
+    reset_operator_impl_cache();
+}
+
+const Tensor* LinearLayer::weight_tensor(ModelStage) const { return weight_.empty() ? nullptr : &weight_; }
+const Tensor* LinearLayer::bias_tensor(ModelStage) const { return bias_.empty() ? nullptr : &bias_; }
+
+void LinearLayer::reset_operator_impl_cache() {
+    cache_.clear();
+    if (source_op_) source_op_->reset_runtime_caches();
+}
+
+LinearLayer::LinearOpContext LinearLayer::make_ctx(int32_t m, DType input_dtype, DType output_dtype,
+                                                   ModelStage stage) const {
+    LinearOpContext c;
+    c.layer_prefix = prefix_;
+    c.layer_role = role_;
+    c.stage = stage;
+    c.shape.m = m;
+    c.shape.input_dtype = input_dtype;
+    c.shape.weight_dtype = weight_.dtype();
+    c.shape.output_dtype = output_dtype;
+    c.shape.in_features = in_;
+    c.shape.out_features = out_;
+    c.has_bias = ws_.bias_ != nullptr;
+    return c;
+}
+
+LinearLayer::CachedDescriptors& LinearLayer::cache_slot(ModelStage stage, int32_t m, DType output_dtype) {
+    return cache_[std::make_tuple((int)stage, m, (int)output_dtype)];
+}
+
+LinearLayer::LinearImpl* LinearLayer::resolve_impl(const LinearOpContext& ctx, const WeightSet& ws,
+                                                   CachedDescriptors& cached) const {
+    if (!cached.selected_impl_id_.empty()) {
+        if (LinearImpl* impl = LinearOpRegistry::instance().find_impl_by_id(cached.selected_impl_id_)) return impl;
+        cached.selected_impl_id_.clear();
+    }
+    OperatorQuery q;
+    q.op_kind = "linear";
+    q.layer_role = ctx.layer_role;
+    q.op_name = ctx.layer_prefix;
+    q.stage = stage_key(ctx.stage);
+    q.shape_sig = ctx.shape.to_string();
+    if (auto rec = OperatorImplTable::instance().resolve(model_name_, hw_profile_, table_path_, q)) {
+        LinearImpl* impl = LinearOpRegistry::instance().find_impl_by_id(rec->impl_id);
+        if (impl == nullptr)
+            throw ConfigurationError("LinearLayer: operator_impl_table selected unknown impl '" + rec->impl_id +
+                                     "' for layer '" + prefix_ + "'");
+        if (!impl->supports(ctx, ws))
+            throw ConfigurationError("LinearLayer: operator_impl_table selected unsupported impl '" + rec->impl_id +
+                                     "' for layer '" + prefix_ + "' (" + stage_key(ctx.stage) + ", " +
+                                     ctx.shape.to_string() + ")");
+        cached.selected_impl_id_ = impl->impl_id();
+        cached.selected_impl_params_ = rec->impl_params;
+        return impl;
+    }
+    if (LinearImpl* impl = LinearOpRegistry::instance().default_impl(ctx, ws)) {
+        cached.selected_impl_id_ = impl->impl_id();
+        cached.selected_impl_params_ = Json::object();
+        return impl;
+    }
+    throw ConfigurationError("LinearLayer: no supported implementation found for layer '" + prefix_ + "' (" +
+                             ctx.shape.to_string() + ")");
+}
+
+std::string LinearLayer::selected_impl_id(ModelStage stage, int32_t m, DType output_dtype) {
+    const LinearOpContext ctx = make_ctx(m, DType::BFloat16, output_dtype, stage);
+    return resolve_impl(ctx, ws_, cache_slot(stage, m, output_dtype))->impl_id();
+}
+
+void LinearLayer::forward_fp16_bf16(const Tensor& input, Tensor& output, hipStream_t stream, ModelStage stage) {
+    check<InvalidRequestError>(!weight_.empty(), "LinearLayer " + prefix_ + ": weights are not loaded");
+    check<InvalidRequestError>(input.shape().size() == 2 && input.shape()[1] == in_,
+                               "LinearLayer " + prefix_ + ": input must be [m, " + std::to_string(in_) + "]");
+    const int32_t m = (int32_t)input.shape()[0];
+    check<InvalidRequestError>(output.numel() == (int64_t)m * out_,
+                               "LinearLayer " + prefix_ + ": output must hold [m, " + std::to_string(out_) + "]");
+    const LinearOpContext ctx = make_ctx(m, input.dtype(), output.dtype(), stage);
+    CachedDescriptors& cached = cache_slot(stage, m, output.dtype());
+    LinearImpl* impl = resolve_impl(ctx, ws_, cached);
+    impl->forward(*this, ctx, ws_, input, output, stream, cached);
+}
+
+// ---------------------------------------------------------------------------------
+// Prefill source ops
+// ---------------------------------------------------------------------------------
+namespace {
+Tensor& scratch_for(std::map<std::tuple<int64_t, int64_t, int64_t>, Tensor>& cache, int64_t m, int64_t k, int64_t n,
+                    size_t bytes, int32_t device_id) {
+    Tensor& t = cache[std::make_tuple(m, k, n)];
+    if (bytes > 0 && (t.empty() || t.nbytes() < bytes))
+        t = Tensor::empty({(int64_t)bytes}, DType::UInt8, Device::GPU, device_id);
+    return t;
+}
+bool bf16_matrix(const Tensor& t, int64_t rows, int64_t cols) {
+    return t.dtype() == DType::BFloat16 && t.shape().size() == 2 && (rows < 0 || t.shape()[0] == rows) &&
+           (cols < 0 || t.shape()[1] == cols) && !t.empty();
+}
+}  // namespace
+
+PrefillLinearSourceOp::PrefillLinearSourceOp(const EngineConfig& config) : device_id_(config.device_id()) {}
+PrefillLinearSourceOp::~PrefillLinearSourceOp() = default;
+void PrefillLinearSourceOp::reset_runtime_caches() { scratch_.clear(); }
+
+bool PrefillLinearSourceOp::try_forward(const std::string& role, int32_t, const Tensor& input, const Tensor& weight,
+                                        const Tensor* bias, Tensor& output, hipStream_t stream) {
+    if (role != "fused_qkv" && role != "attention_output" && role != "mlp_down" && role != "linear") return false;
+    if (!bf16_matrix(input, -1, -1) || !bf16_matrix(weight, -1, input.shape()[1])) return false;
+    const int64_t m = input.shape()[0], k = input.shape()[1], n = weight.shape()[0];
+    if (m < 2 || k % 32 != 0 || output.dtype() != DType::BFloat16 || output.numel() != m * n) return false;
+    if (bias != nullptr && (bias->dtype() != DType::BFloat16 || bias->numel() != n)) return false;
+    const size_t need = efm_linear_workspace_bytes(m, k, n);
+    Tensor& ws = scratch_for(scratch_, m, k, n, need, device_id_);
+    efm_check(efm_linear_ws(m, k, n, input.data_ptr(), weight.data_ptr(), bias ? bias->data_ptr() : nullptr,
+                            output.data_ptr(), EFM_DTYPE_BF16, need ? ws.data_ptr() : nullptr, need, stream),
+              "prefill linear source op (" + role + ")");
+    return true;
+}
+
+PrefillMlpSourceOp::PrefillMlpSourceOp(const EngineConfig& config) : device_id_(config.device_id()) {}
+PrefillMlpSourceOp::~PrefillMlpSourceOp() = default;
+void PrefillMlpSourceOp::reset_runtime_caches() {
+    scratch_.clear();
+    intermediate_ = Tensor();
+}
+
+bool PrefillMlpSourceOp::try_forward(int32_t, const Tensor& input, const Tensor& gate_up_weight,
+                                     const Tensor& down_weight, Tensor& output, hipStream_t stream) {
+    if (!bf16_matrix(input, -1, -1)) return false;
+    const int64_t m = input.shape()[0], h = input.shape()[1];
+    if (m < 2 || h % 32 != 0 || !bf16_matrix(gate_up_weight, -1, h) || gate_up_weight.shape()[0] % 2 != 0)
+        return false;
+    const int64_t inter = gate_up_weight.shape()[0] / 2;
+    if (inter % 32 != 0 || !bf16_matrix(down_weight, h, inter)) return false;
+    if (output.dtype() != DType::BFloat16 || output.numel() != m * h) return false;
+    if (intermediate_.empty() || intermediate_.numel() < m * inter)
+        intermediate_ = Tensor::empty({m, inter}, DType::BFloat16, Device::GPU, device_id_);
+    const size_t need_gu = efm_fused_gate_up_swiglu_workspace_bytes(m, h, inter);
+    Tensor& ws_gu = scratch_for(scratch_, m, h, -inter, need_gu, device_id_);
+    efm_check(efm_fused_gate_up_swiglu_ws(m, h, inter, input.data_ptr(), gate_up_weight.data_ptr(),
+                                          intermediate_.data_ptr(), need_gu ? ws_gu.data_ptr() : nullptr, need_gu,
+                                          stream),
+              "prefill mlp source op (gate/up + SwiGLU)");
+    const size_t need_d = efm_linear_workspace_bytes(m, inter, h);
+    Tensor& ws_d = scratch_for(scratch_, m, inter, h, need_d, device_id_);
+    efm_check(efm_linear_ws(m, inter, h, intermediate_.data_ptr(), down_weight.data_ptr(), nullptr, output.data_ptr(),
+                            EFM_DTYPE_BF16, need_d ? ws_d.data_ptr() : nullptr, need_d, stream),
+              "prefill mlp source op (down)");
+    return true;
+}
+
+// ---------------------------------------------------------------------------------
+// Fused gate/up + SwiGLU
+// ---------------------------------------------------------------------------------
+namespace {
+// Grow-only per-device scratch for the fused gate/up kernels (the reference's impls take
+// theirs from StaticBufferManager::get_cache_buf, src/utils/memory.h:31-109).
 void* linear_scratch(size_t bytes, int32_t device_id, size_t* have) {
     static std::mutex mu;
     static std::map<int32_t, Tensor> bufs;
@@ -362,50 +719,6 @@ void* linear_scratch(size_t bytes, int32_t device_id, size_t* have) {
     return t.data_ptr();
 }
 
-class HipLinearImpl final : public LinearImpl {
-public:
-    std::string impl_id() const override { return "hip_gfx950_linear"; }
-    bool supports(const LinearOpContext& c) const override {
-        const auto& s = c.shape;
-        if (s.input != DType::BFloat16 || s.weight != DType::BFloat16) return false;
-        if (s.output != DType::BFloat16 && s.output != DType::Float32) return false;
-        return s.in_features % (s.m == 1 ? 8 : 32) == 0;
-    }
-    void forward(const LinearOpContext& c, const Tensor& w, const Tensor* bias, const Tensor& in, Tensor& out,
-                 hipStream_t s) override {
-        // The shape's own figure, not the scratch's capacity: the kernels chosen must not
-        // depend on how far earlier, longer prompts have grown the buffer.
-        const size_t need = efm_linear_workspace_bytes(c.shape.m, c.shape.in_features, c.shape.out_features);
-        size_t have = 0;
-        void* ws = need > 0 ? linear_scratch(need, w.device().second, &have) : nullptr;
-        efm_check(efm_linear_ws(c.shape.m, c.shape.in_features, c.shape.out_features, in.data_ptr(), w.data_ptr(),
-                                bias ? bias->data_ptr() : nullptr, out.data_ptr(),
-                                c.shape.output == DType::Float32 ? EFM_DTYPE_F32 : EFM_DTYPE_BF16, ws, need, s),
-                  "linear " + c.layer_prefix);
-    }
-};
-}  // namespace
-
-LinearOpRegistry::LinearOpRegistry() { impls_.push_back(std::make_unique<HipLinearImpl>()); }
-LinearOpRegistry& LinearOpRegistry::instance() {
-    static LinearOpRegistry r;
-    return r;
-}
-LinearImpl* LinearOpRegistry::find_impl_by_id(const std::string& id) const {
-    for (auto& i : impls_)
-        if (i->impl_id() == id) return i.get();
-    return nullptr;
-}
-LinearImpl* LinearOpRegistry::default_impl(const LinearOpContext& ctx) const {
-    for (auto& i : impls_)
-        if (i->supports(ctx)) return i.get();
-    throw ConfigurationError("no linear implementation supports " + linear_shape_sig(ctx.shape));
-}
-
-// ---------------------------------------------------------------------------------
-// Fused gate/up + SwiGLU
-// ---------------------------------------------------------------------------------
-namespace {
 class HipSwigluOp final : public FusedGateUpActivationOp {
 public:
     std::string impl_id() const override { return "hip_gfx950_swiglu"; }

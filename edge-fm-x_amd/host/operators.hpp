@@ -4,8 +4,10 @@
 // edgefm_hip C ABI.
 #pragma once
 
+#include <map>
 #include <memory>
 #include <mutex>
+#include <tuple>
 #include <optional>
 #include <string>
 #include <unordered_map>
@@ -67,9 +69,15 @@ struct AttentionOpContext {
     bool k_already_prerotated = false;
     int32_t device_id = 0;
     Json impl_params = Json::object();
+    // Decode planning facts (not in the reference's context; 0 = unknown): the model's
+    // hidden size and the longest cache a decode step reads. The fused decode impls
+    // support a shape only when both are known.
+    uint32_t decode_hidden = 0, decode_max_kv_len = 0;
 };
 
 efm_attention_ctx to_c_ctx(const AttentionOpContext& c);
+// "num_qo_heads=<n>|num_kv_heads=<n>|head_dim=<n>" (src/layers/attention.cu:149-153)
+std::string attention_shape_sig(uint32_t num_qo_heads, uint32_t num_kv_heads, uint32_t head_dim);
 
 class AttentionOp {
 public:
@@ -161,44 +169,183 @@ private:
 };
 
 // ---------------------------------------------------------------------------------
-// Linear (LinearLayer::LinearImpl, src/layers/linear.h:110-153; registry
-// src/operators/linear_registry.h:9-24). layer_role is one of fused_qkv,
-// attention_output, fused_gate_up, mlp_down, lm_head.
+// Linear: LinearLayer with the reference's nested interface types (WeightSet,
+// LinearShapeSignature, LinearOpContext, CachedDescriptors, LinearImpl with prepare /
+// forward: src/layers/linear.h:100-153) and LinearOpRegistry (src/operators/
+// linear_registry.h:9-24). The impl for (stage, m) is resolved once from the operator
+// table (op_kind linear, layer_role from the prefix, op_name = the prefix, stage,
+// shape_sig = LinearShapeSignature::to_string) exactly as LinearLayer::resolve_impl does
+// (src/operators/linear_impl.cu:866-915): a table record naming an unknown or unsupporting
+// impl is a ConfigurationError; without a record the registry default runs.
 // ---------------------------------------------------------------------------------
-struct LinearShape {
-    int64_t m = 0;
-    DType input = DType::BFloat16, weight = DType::BFloat16, output = DType::BFloat16;
-    int64_t in_features = 0, out_features = 0;
-};
+class EngineConfig;
+class PrefillLinearSourceOp;
 
-struct LinearOpContext {
-    std::string layer_prefix, layer_role;
-    ModelStage stage = ModelStage::Decode;
-    LinearShape shape;
-    bool has_bias = false;
-    Json impl_params = Json::object();
-};
+// "fused_qkv" (…qkv_fused), "fused_gate_up" (…gate_up_fused), "attention_output"
+// (….o_proj), "mlp_down" (….down_proj), "lm_head", else "linear"
+// (src/layers/linear.cu:41-58).
+std::string infer_layer_role(const std::string& layer_prefix);
+std::string stage_key(ModelStage stage);
 
-std::string linear_shape_sig(const LinearShape& s);
-
-class LinearImpl {
+class LinearLayer {
 public:
-    virtual ~LinearImpl() = default;
-    virtual std::string impl_id() const = 0;
-    virtual bool supports(const LinearOpContext& ctx) const = 0;
-    virtual void forward(const LinearOpContext& ctx, const Tensor& weight, const Tensor* bias, const Tensor& input,
-                         Tensor& output, hipStream_t stream) = 0;
+    enum class QuantType { FP16_BF16, INT4_GROUPWISE, INT8, FP4 };
+
+    struct WeightSet {
+        QuantType quant_type_ = QuantType::FP16_BF16;
+        const Tensor* weight_ = nullptr;           // [out_features, in_features]
+        const Tensor* bias_ = nullptr;             // [out_features] or null
+        const Tensor* scaling_factors_ = nullptr;  // quantized weights only (none supported here)
+        uint32_t group_size_ = 128;
+    };
+
+    struct LinearShapeSignature {
+        int32_t m = -1;
+        DType input_dtype = DType::BFloat16, weight_dtype = DType::BFloat16, output_dtype = DType::BFloat16;
+        uint32_t in_features = 0, out_features = 0;
+        // "m=<m>|input=<dtype>|weight=<dtype>|output=<dtype>|in_features=<k>|out_features=<n>"
+        std::string to_string() const;
+    };
+
+    struct LinearOpContext {
+        std::string layer_prefix, layer_role;
+        ModelStage stage = ModelStage::Prefill;
+        LinearShapeSignature shape;
+        bool has_bias = false;
+    };
+
+    // Per (stage, m) state an impl keeps between calls: the resolved impl and, for the
+    // MFMA GEMM, the split-K scratch its plan for this shape needs.
+    struct CachedDescriptors {
+        std::string selected_impl_id_;
+        Json selected_impl_params_ = Json::object();
+        size_t workspace_bytes_ = 0;
+        Tensor workspace_;
+        bool prepared_ = false;
+    };
+
+    class LinearImpl {
+    public:
+        virtual ~LinearImpl() = default;
+        virtual std::string impl_id() const = 0;
+        virtual bool supports(const LinearOpContext& ctx, const WeightSet& weight_set) const = 0;
+        virtual void prepare(LinearLayer& owner, const LinearOpContext& ctx, const WeightSet& weight_set,
+                             const Tensor& input, Tensor& output, hipStream_t stream, CachedDescriptors& cached) = 0;
+        virtual void forward(LinearLayer& owner, const LinearOpContext& ctx, const WeightSet& weight_set,
+                             const Tensor& input, Tensor& output, hipStream_t stream, CachedDescriptors& cached) = 0;
+    };
+
+    LinearLayer(const std::string& layer_prefix, const EngineConfig& engine_config, uint32_t in_features,
+                uint32_t out_features, std::string layer_name = "");
+    ~LinearLayer();
+    LinearLayer(const LinearLayer&) = delete;
+    LinearLayer& operator=(const LinearLayer&) = delete;
+
+    // The layer's weight [out, in] (+ bias [out]); prefill and decode share it (the
+    // engine loads one checkpoint for both stages).
+    void load_weights(const Tensor& weight, const Tensor* bias);
+    // output[m, out] = input[m, in] . W^T (+ bias) through the impl resolved for (stage, m).
+    void forward_fp16_bf16(const Tensor& input, Tensor& output, hipStream_t stream = nullptr,
+                           ModelStage stage = ModelStage::Prefill);
+    // The impl forward_fp16_bf16 runs for (stage, m, output dtype), resolved without running.
+    std::string selected_impl_id(ModelStage stage, int32_t m, DType output_dtype = DType::BFloat16);
+    LinearImpl* resolve_impl(const LinearOpContext& ctx, const WeightSet& weight_set, CachedDescriptors& cached) const;
+    void reset_operator_impl_cache();
+
+    const Tensor* weight_tensor(ModelStage stage = ModelStage::Prefill) const;
+    const Tensor* bias_tensor(ModelStage stage = ModelStage::Prefill) const;
+    const std::string& layer_prefix() const { return prefix_; }
+    const std::string& layer_role() const { return role_; }
+    const std::string& layer_name() const { return name_; }
+    uint32_t in_features() const { return in_; }
+    uint32_t out_features() const { return out_; }
+    PrefillLinearSourceOp* prefill_linear_source_op() const { return source_op_.get(); }
+
+protected:
+    // explicit role (the fused subclasses: their prefixes carry no role suffix)
+    LinearLayer(const std::string& layer_prefix, std::string layer_role, const EngineConfig& engine_config,
+                uint32_t in_features, uint32_t out_features, std::string layer_name);
+
+private:
+    LinearOpContext make_ctx(int32_t m, DType input_dtype, DType output_dtype, ModelStage stage) const;
+    CachedDescriptors& cache_slot(ModelStage stage, int32_t m, DType output_dtype);
+
+    std::string prefix_, role_, name_;
+    std::string model_name_, hw_profile_, table_path_;
+    uint32_t in_ = 0, out_ = 0;
+    Tensor weight_, bias_;
+    WeightSet ws_;
+    std::map<std::tuple<int, int32_t, int>, CachedDescriptors> cache_;
+    std::unique_ptr<PrefillLinearSourceOp> source_op_;
+};
+
+// Fused [Q; K; V] rows with [bq; bk; bv] under the attention prefix
+// (model.layers.<l>.self_attn, role fused_qkv: src/layers/linear.h FusedQKVLinearLayer).
+class FusedQKVLinearLayer : public LinearLayer {
+public:
+    FusedQKVLinearLayer(const std::string& hf_attn_prefix, const EngineConfig& engine_config, uint32_t hidden,
+                        uint32_t q_dim, uint32_t k_dim, uint32_t v_dim, std::string layer_name = "")
+        : LinearLayer(hf_attn_prefix, "fused_qkv", engine_config, hidden, q_dim + k_dim + v_dim,
+                      std::move(layer_name)) {}
+};
+
+// Fused [up; gate] rows under the MLP prefix (model.layers.<l>.mlp, role fused_gate_up:
+// src/layers/linear.h FusedGateUpLinearLayer; rows [0, I) up, [I, 2 I) gate).
+class FusedGateUpLinearLayer : public LinearLayer {
+public:
+    FusedGateUpLinearLayer(const std::string& hf_mlp_prefix, const EngineConfig& engine_config, uint32_t hidden,
+                           uint32_t gate_out_features, uint32_t up_out_features, std::string layer_name = "")
+        : LinearLayer(hf_mlp_prefix, "fused_gate_up", engine_config, hidden, gate_out_features + up_out_features,
+                      std::move(layer_name)) {}
 };
 
 class LinearOpRegistry {
 public:
     static LinearOpRegistry& instance();
-    LinearImpl* find_impl_by_id(const std::string& id) const;
-    LinearImpl* default_impl(const LinearOpContext& ctx) const;
+    LinearLayer::LinearImpl* find_impl_by_id(const std::string& id) const;
+    LinearLayer::LinearImpl* default_impl(const LinearLayer::LinearOpContext& ctx,
+                                          const LinearLayer::WeightSet& weight_set) const;
 
 private:
     LinearOpRegistry();
-    std::vector<std::unique_ptr<LinearImpl>> impls_;
+    std::vector<std::unique_ptr<LinearLayer::LinearImpl>> impls_;
+};
+
+// ---------------------------------------------------------------------------------
+// Prefill source ops (src/operators/prefill_linear_source_op.h:16-23,
+// prefill_mlp_source_op.h:13-20): try_forward runs the projection (or the whole MLP:
+// gate/up GEMM with its SwiGLU epilogue, then down) on this library's MFMA kernels and
+// returns true, or returns false, having done nothing, when the shape or dtypes are not
+// ones it handles; the caller then takes its layered path. Each keeps the scratch its
+// kernels need per shape until reset_runtime_caches().
+// ---------------------------------------------------------------------------------
+class PrefillLinearSourceOp {
+public:
+    explicit PrefillLinearSourceOp(const EngineConfig& config);
+    ~PrefillLinearSourceOp();
+    bool try_forward(const std::string& role, int32_t layer_id, const Tensor& input, const Tensor& weight,
+                     const Tensor* bias, Tensor& output, hipStream_t stream);
+    void reset_runtime_caches();
+
+private:
+    int32_t device_id_ = 0;
+    std::map<std::tuple<int64_t, int64_t, int64_t>, Tensor> scratch_;
+};
+
+class PrefillMlpSourceOp {
+public:
+    explicit PrefillMlpSourceOp(const EngineConfig& config);
+    ~PrefillMlpSourceOp();
+    // gate_up_weight [2 I, H] in the fused [up; gate] layout, down_weight [H, I];
+    // input [m, H] -> output [m, H]
+    bool try_forward(int32_t layer_id, const Tensor& input, const Tensor& gate_up_weight, const Tensor& down_weight,
+                     Tensor& output, hipStream_t stream);
+    void reset_runtime_caches();
+
+private:
+    int32_t device_id_ = 0;
+    Tensor intermediate_;   // [m_max, I], grown on demand
+    std::map<std::tuple<int64_t, int64_t, int64_t>, Tensor> scratch_;
 };
 
 // ---------------------------------------------------------------------------------

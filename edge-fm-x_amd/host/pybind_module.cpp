@@ -188,6 +188,21 @@ PYBIND11_MODULE(edge_fm, m) {
         })
         .def("clear_stage", &WeightLoader::clear_stage);
 
+    // the decode plan an engine config resolves to (operator table, no device work)
+    m.def("plan_decode", [](const std::string& path, uint32_t max_kv_len) {
+        py::list out;
+        for (const auto& p : plan_decode(path, max_kv_len)) {
+            py::dict d;
+            d["attention"] = p.attention;
+            d["o_proj"] = p.o_proj;
+            d["gate_up"] = p.gate_up;
+            d["down"] = p.down;
+            d["partials_to_o_proj"] = p.partials_to_o_proj;
+            out.append(d);
+        }
+        return out;
+    }, py::arg("engine_config_path"), py::arg("max_kv_len"));
+
     // checkpoint reading on the host (no device work): used by the loader tests
     m.def("collect_safetensors_files", &collect_safetensors_files, py::arg("model_path"));
     m.def("vl_language_model_name", &vl_language_model_name, py::arg("name"));

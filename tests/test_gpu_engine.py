@@ -340,3 +340,45 @@ def test_compact_vocab_generate_matches_unmapped_run(gpu):
         with pytest.raises(edge_fm.InvalidRequestError):
             eng.generate(edge_fm.Request(0, external[:5] + [pruned]))
         del eng
+
+
+@pytest.mark.parametrize("table", ["generic", "split", "split_o1_plain"])
+def test_decode_impls_switched_by_table_match_oracle(gpu, table):
+    """Operator-table records switch the decode attention impl (all layers) or one layer's
+    o_proj; every variant generates the oracle's tokens (teacher-forced, near-tie rule)
+    and agrees with the default plan's run at every clear step."""
+    import json
+
+    recs = {"generic": [{"op_kind": "attention", "stage": "decode", "impl_id": "hip_gfx950_attention"}],
+            "split": [{"op_kind": "attention", "stage": "decode", "impl_id": "hip_gfx950_decode_split_attention"}],
+            "split_o1_plain": [{"op_kind": "attention", "stage": "decode",
+                                "impl_id": "hip_gfx950_decode_split_attention"},
+                               {"op_kind": "linear", "op_name": "model.layers.1.self_attn.o_proj", "stage": "decode",
+                                "impl_id": "hip_gfx950_linear"}]}[table]
+    shape = TINY128
+    w = O.random_weights(_oracle_cfg(shape), seed=43, std=0.2)
+    prompt = torch.randint(0, shape.vocab, (40,), generator=torch.Generator().manual_seed(9)).to(torch.int32)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "table.json")
+        with open(path, "w") as f:
+            json.dump({"schema": "edgefm_operator_impl_table_v1", "records": recs}, f)
+        runs = {}
+        for name, tpath in (("default", ""), (table, path)):
+            eng, keep = _engine(tmp, shape, w, max_tokens=96, max_new_tokens=24, operator_impl_table_path=tpath)
+            plan = edge_fm.plan_decode(os.path.join(tmp, "engine.json"), 96)
+            req = edge_fm.Request(0, prompt.tolist())
+            req.set_ignore_stop_tokens(True)
+            runs[name] = (eng.generate(req).token_ids(), plan)
+            del eng
+    plan = runs[table][1]
+    want = {"generic": "hip_gfx950_attention"}.get(table, "hip_gfx950_decode_split_attention")
+    assert all(p["attention"] == want for p in plan)
+    assert runs["default"][1][0]["attention"] == "hip_gfx950_decode_fused_qkv_attention"
+    if table == "split_o1_plain":
+        assert plan[0]["partials_to_o_proj"] and not plan[1]["partials_to_o_proj"]
+    orc = O.Qwen2Oracle(_oracle_cfg(shape), O.fuse_weights(_oracle_cfg(shape), w), max_tokens=96)
+    for name, (toks, _) in runs.items():
+        steps = _teacher_forced(orc, prompt, toks)
+        exact = _check_against_oracle(toks, steps, tol=0.05)
+        assert exact >= 20, f"{name}: {exact}/24 exact"
+
