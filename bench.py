@@ -225,6 +225,53 @@ def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20
     return sorted(out, key=lambda k: -k["avg_launch_us"])
 
 
+def attention_layouts(torch, C, reps=20):
+    """Decode attention (efm_attention_decode with its in-call split merge) on the engine's
+    cache layout (rotated keys; the call rotates the newest row and stores it back:
+    k_already_prerotated = EFM_K_PREROTATED_EXCEPT_NEWEST) against the reference's layout
+    (un-rotated keys, RoPE applied to every key on read: k_already_prerotated = 0), at the
+    C2, C3 and C5 head layouts and mean contexts. Each figure is one replay of a graph of
+    reps x layers launches over per-layer caches (every layer its own K/V), timed with HIP
+    events on the replay stream: µs per launch, and the K/V bytes per launch over it."""
+    dev = torch.device("cuda:0")
+    lib = C.load()
+    cases = [("c2", 12, 2, 28, 640, 768), ("c3", 16, 2, 36, 1408, 1472), ("c5", 28, 4, 28, 16448, 16512)]
+    stream = torch.cuda.Stream()
+    out = []
+    for name, hq, hkv, layers, L, max_kv in cases:
+        hd = 128
+        g = torch.Generator(device=dev).manual_seed(3)
+        kcs = [torch.randn(max_kv, hkv * hd, device=dev, generator=g).to(torch.bfloat16) for _ in range(layers)]
+        vcs = [torch.randn(max_kv, hkv * hd, device=dev, generator=g).to(torch.bfloat16) for _ in range(layers)]
+        q = torch.randn(1, hq * hd, device=dev, generator=g).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        d_len = torch.tensor([L], dtype=torch.int32, device=dev)
+        row = {"config": name, "heads": f"{hq}/{hkv}/{hd}", "context": L, "layers": layers,
+               "kv_bytes_per_launch": 2 * L * hkv * hd * 2}
+        for tag, mode in (("engine_rotated_cache", C.EFM_K_PREROTATED_EXCEPT_NEWEST), ("reference_layout", 0)):
+            ctx = C.make_attention_ctx(hq, hkv, hd)
+            ctx.k_already_prerotated = mode
+            ws = torch.zeros(lib.efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=dev)
+
+            def fn(sh, ctx=ctx, ws=ws):
+                for kc, vc in zip(kcs, vcs):
+                    C.call("efm_attention_decode", ctx, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(), 0,
+                           d_len.data_ptr(), max_kv, ws.data_ptr(), ws.numel(), sh)
+
+            torch.cuda.synchronize()
+            us = _graph_time_us(torch, fn, reps, stream) / layers
+            row[tag] = {"avg_launch_us": round(us, 3),
+                        "kv_GBs": round(row["kv_bytes_per_launch"] / (us * 1e-6) / 1e9, 1)}
+            del ws
+        row["reference_over_engine"] = round(row["reference_layout"]["avg_launch_us"] /
+                                             row["engine_rotated_cache"]["avg_launch_us"], 3)
+        out.append(row)
+        del kcs, vcs
+        torch.cuda.empty_cache()
+    print(json.dumps({"metric": "decode attention µs per launch: engine rotated cache vs the reference's "
+                                "rotate-on-read layout", "unit": "us", "dtype": "bf16", "cases": out}), flush=True)
+
+
 def kernel_only(torch, C, S, shape, seed):
     """Counter-collection workload: a 256 MiB device copy (calibration: 262144 KiB read,
     262144 KiB written), then 2 x layers direct launches of each per-layer decode kernel
@@ -681,6 +728,8 @@ def main():
                     help="BASELINE configuration (default c2, the headline decode benchmark)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="prefill GEMM counter workload (C5 gate/up + SwiGLU), no model")
+    ap.add_argument("--attention-layouts", action="store_true",
+                    help="decode attention on the engine's rotated cache vs the reference's rotate-on-read layout")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the copy calibration and the four per-layer decode kernels (for rocprofv3 --pmc passes)")
     args = ap.parse_args()
@@ -697,6 +746,9 @@ def main():
 
     if args.gemm_only:
         gemm_only(torch, C)
+        return
+    if args.attention_layouts:
+        attention_layouts(torch, C)
         return
     if args.config != "c2":
         {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config](args)

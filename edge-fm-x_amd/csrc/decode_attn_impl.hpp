@@ -54,21 +54,25 @@ union BfPack {
 // and different from the previous launch, whose words a poll may still see); the last
 // attention workgroup to finish polling advances the epoch and clears `done`. Polls are
 // bounded: on time-out they raise `abort` (reported by efm_decode_qkv_attention_status)
-// and go on, so the launch always drains.
+// and go on with zeros for the words that did not arrive, so the launch always drains
+// (its outputs are then wrong, and the status call says so).
 struct FusedAttnArgs {
     const uint32_t* words;   // [q_dim + 2 kv_dim]
     uint32_t* sync;          // [0] epoch, [1] done, [2] abort
     int q_dim, kv_dim;
     uint32_t n_attn;         // attention workgroups of the launch
+    uint32_t spin_limit;     // polls before a wait gives up (kFusedSpin)
+    uint32_t tag_or;         // OR-ed into the awaited tag: 0, or 1 << 16 (test hook: no word matches)
 };
 
 constexpr uint32_t kFusedSpin = 1u << 20;
+constexpr uint32_t kFusedTestSpin = 64u;   // spin limit of the forced time-out (test hook)
 
 // Polls words addr(k) for every k set in `pending` until each carries `tag`; every round
 // issues the loads of all words still pending before checking any.
 template <int NW, class Addr>
 __device__ __forceinline__ void fused_poll(uint32_t (&w)[NW], uint32_t pending, uint32_t tag, Addr addr,
-                                           uint32_t* sync) {
+                                           uint32_t* sync, uint32_t spin_limit) {
 #pragma unroll
     for (int k = 0; k < NW; ++k) w[k] = 0u;
     uint32_t spins = 0;
@@ -84,7 +88,7 @@ __device__ __forceinline__ void fused_poll(uint32_t (&w)[NW], uint32_t pending, 
                 pending &= ~(1u << k);
             }
         if (pending == 0u) break;
-        if (++spins > kFusedSpin) {
+        if (++spins > spin_limit) {
             __hip_atomic_store(sync + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
@@ -138,7 +142,7 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
 
     // ---- 1. loads that do not depend on L: the query, the first round of K / V (rows
     //         below the allocation bound), the RoPE frequencies
-    const uint32_t tag = FUSED ? launch_tag(f.sync) : 0u;
+    const uint32_t tag = FUSED ? (launch_tag(f.sync) | f.tag_or) : 0u;
     // the group's G x 128 queries, 16 bytes per thread (staged in LDS below)
     uint4 qld = make_uint4(0, 0, 0, 0);
     if (!FUSED && tid < G * (HD / 8))
@@ -198,7 +202,7 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
         const uint32_t* nw = f.words + f.q_dim + (tid < HD ? 0 : f.kv_dim) + kvh * HD + (tid % HD);
         if (owner) pending |= 1u << NQW;
         fused_poll<NQW + 1>(w, pending, tag, [&](int k) { return k < NQW ? qw + tid + k * kAttnThreads : nw; },
-                            f.sync);
+                            f.sync, f.spin_limit);
 #pragma unroll
         for (int k = 0; k < NQW; ++k)
             if (tid + k * kAttnThreads < G * HD) qs[tid + k * kAttnThreads] = (bf16_t)(w[k] & 0xffffu);

@@ -195,6 +195,9 @@ extern "C" int efm_decode_norm_qkv_attention(const efm_attention_ctx* ctx, int32
     f.q_dim = q_dim;
     f.kv_dim = kv_dim;
     f.n_attn = (uint32_t)n_attn;
+    const bool force_timeout = kernel_knob(EFM_KNOB_FRONT_WAIT_TIMEOUT) != 0;
+    f.spin_limit = force_timeout ? kFusedTestSpin : kFusedSpin;
+    f.tag_or = force_timeout ? (1u << 16) : 0u;   // tags are 16 bits: no word matches
 
     const dim3 grid(n_attn + n_gemv), block(kGemvThreads);
     const size_t smem = (size_t)hidden * sizeof(bf16_t);
@@ -224,11 +227,22 @@ extern "C" int efm_decode_qkv_attention_status(void* sync_workspace, hipStream_t
         hipStreamSynchronize(stream) != hipSuccess)
         return set_error(EFM_ERR_DEVICE, "decode_qkv_attention_status: copy failed");
     if (flag != 0) {
-        const uint32_t zero = 0;
-        if (hipMemcpyAsync(abort_word, &zero, sizeof(zero), hipMemcpyHostToDevice, stream) != hipSuccess ||
+        // Clear the report and step the epoch once more. After a time-out the epoch can
+        // advance while a GEMV workgroup of the same launch has not read it yet; that
+        // workgroup then tags its words with the next launch's tag, and the next launch
+        // could take those stale words for its own. One more step makes the next tag
+        // one that no word written so far carries.
+        uint32_t head[3] = {0, 0, 0};
+        if (hipMemcpyAsync(head, sync_workspace, sizeof(head), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+            hipStreamSynchronize(stream) != hipSuccess)
+            return set_error(EFM_ERR_DEVICE, "decode_qkv_attention_status: copy failed");
+        head[0] += 1u;
+        head[2] = 0u;
+        if (hipMemcpyAsync(sync_workspace, head, sizeof(head), hipMemcpyHostToDevice, stream) != hipSuccess ||
             hipStreamSynchronize(stream) != hipSuccess)
             return set_error(EFM_ERR_DEVICE, "decode_qkv_attention_status: reset failed");
-        return set_error(EFM_ERR_DEVICE, "decode_norm_qkv_attention: a poll timed out (not every workgroup ran)");
+        return set_error(EFM_ERR_DEVICE, "decode_norm_qkv_attention: an attention split's wait for its inputs timed out; the outputs of "
+                         "the launches since the last status call are invalid");
     }
     return EFM_OK;
 }

@@ -40,6 +40,7 @@ EFM_KNOB_DECODE_REGISTER = 0
 EFM_KNOB_PREFILL_REGISTER = 1
 EFM_KNOB_PREFILL_SHAPE = 2
 EFM_KNOB_GEMM_TILE = 3
+EFM_KNOB_FRONT_WAIT_TIMEOUT = 4
 
 
 class AttentionCtx(ctypes.Structure):

@@ -1011,11 +1011,16 @@ StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_pat
 }
 
 StandardEngine::~StandardEngine() {
+    drop_graphs();
+    if (stream_) hipStreamDestroy(stream_);
+}
+
+void StandardEngine::drop_graphs() {
     for (auto& kv : graphs_) {
         if (kv.second.exec) hipGraphExecDestroy(kv.second.exec);
         if (kv.second.graph) hipGraphDestroy(kv.second.graph);
     }
-    if (stream_) hipStreamDestroy(stream_);
+    graphs_.clear();
 }
 
 std::vector<void*> StandardEngine::caches(int32_t request_id, bool k) {
@@ -1251,7 +1256,15 @@ Response StandardEngine::generate(const Request& request) {
         hip_check(hipEventRecord(copy.b, stream_), "event");
         hip_check(hipStreamSynchronize(stream_), "generate sync");
     }
-    model_->check_decode_status(stream_);
+    try {
+        model_->check_decode_status(stream_);
+    } catch (const DeviceError&) {
+        // A decode launch gave up a bounded wait: this response is wrong and is not
+        // returned. The launches' device state is already reset; the captured decode
+        // graphs are dropped as well, so the next call captures its launches afresh.
+        drop_graphs();
+        throw;
+    }
 
     // stop tokens truncate after the first hit, inclusive (standard_engine.cpp:1060-1068)
     const auto stop_t0 = std::chrono::steady_clock::now();

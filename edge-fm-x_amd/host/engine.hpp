@@ -300,6 +300,7 @@ private:
         hipGraphExec_t exec = nullptr;
     };
     std::map<int32_t, GraphEntry> graphs_;  // per request slot
+    void drop_graphs();
 
     // stage_events: StageEvents of the eager loop's per-step timing, or null (captured)
     void run_decode_step(int32_t request_id, void* stage_events);

@@ -63,12 +63,18 @@ const char* efm_version(void);
  *   EFM_KNOB_GEMM_TILE         prefill GEMM kernel (K % 64 == 0): 1 the two-workgroup-
  *                              per-CU 128 x 128 / 128 x 64 / 64 x 64 kernel, 2 the
  *                              one-workgroup-per-CU 256 x 256 kernel
+ *   EFM_KNOB_FRONT_WAIT_TIMEOUT 1: efm_decode_norm_qkv_attention launches whose attention
+ *                              workgroups wait for a tag that no projected word carries,
+ *                              with a 64-poll limit: every wait gives up, the launch
+ *                              drains with wrong outputs and the time-out is reported by
+ *                              efm_decode_qkv_attention_status (tests of that path)
  * Unknown knobs or values: EFM_ERR_INVALID_ARGUMENT. Not for production callers. */
 #define EFM_KNOB_DECODE_REGISTER 0
 #define EFM_KNOB_PREFILL_REGISTER 1
 #define EFM_KNOB_PREFILL_SHAPE 2
 #define EFM_KNOB_GEMM_TILE 3
-#define EFM_KNOB_COUNT 4
+#define EFM_KNOB_FRONT_WAIT_TIMEOUT 4
+#define EFM_KNOB_COUNT 5
 int efm_testing_set_kernel_path(int32_t knob, int32_t value);
 
 /* ------------------------------------------------------------------------------------
@@ -439,9 +445,12 @@ int efm_decode_norm_qkv(int32_t hidden, int32_t q_dim, int32_t kv_dim, float eps
  * efm_decode_attention_merge_o_proj. Cache slot *d_kv_len - 1 receives V and the rotated
  * K; *d_kv_len >= 1. sync_workspace: efm_decode_qkv_attention_sync_bytes(q_dim, kv_dim)
  * bytes, zero-filled once and then reused by every launch (launches sharing it must be
- * stream-ordered). A split that does not receive its inputs in time flags the workspace:
- * efm_decode_qkv_attention_status reports and clears the flag (it synchronises the
- * stream). efm_decode_norm_qkv_attention_supported tells whether a shape qualifies
+ * stream-ordered). The attention splits wait for GEMV workgroups of the same grid, which
+ * never wait themselves; with at most 128 splits every GEMV workgroup finds a slot as
+ * soon as any other workgroup on the GPU ends, so the waits end. They are bounded all the
+ * same (2^20 polls): a split that does not receive its inputs in time goes on with zeros
+ * and flags the workspace, and efm_decode_qkv_attention_status reports EFM_ERR_DEVICE and
+ * clears the flag (it synchronises the stream); launches after it compute correctly. efm_decode_norm_qkv_attention_supported tells whether a shape qualifies
  * (hidden <= 4096, at most 128 attention splits of 128 keys, contiguous cache rows);
  * otherwise call the two unfused entry points. */
 size_t efm_decode_qkv_attention_sync_bytes(int32_t q_dim, int32_t kv_dim);

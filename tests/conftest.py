@@ -39,5 +39,6 @@ def knob():
         C.call("efm_testing_set_kernel_path", which, int(value))
 
     yield set_knob
-    for k in (C.EFM_KNOB_DECODE_REGISTER, C.EFM_KNOB_PREFILL_REGISTER, C.EFM_KNOB_PREFILL_SHAPE, C.EFM_KNOB_GEMM_TILE):
+    for k in (C.EFM_KNOB_DECODE_REGISTER, C.EFM_KNOB_PREFILL_REGISTER, C.EFM_KNOB_PREFILL_SHAPE, C.EFM_KNOB_GEMM_TILE,
+              C.EFM_KNOB_FRONT_WAIT_TIMEOUT):
         C.call("efm_testing_set_kernel_path", k, 0)

@@ -382,3 +382,34 @@ def test_decode_impls_switched_by_table_match_oracle(gpu, table):
         exact = _check_against_oracle(toks, steps, tol=0.05)
         assert exact >= 20, f"{name}: {exact}/24 exact"
 
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_front_wait_timeout_raises_device_error_then_recovers(gpu, knob, use_graph):
+    """The fused front half's bounded wait forced to give up from the host
+    (EFM_KNOB_FRONT_WAIT_TIMEOUT: its attention splits wait for a tag that no word
+    carries, 64 polls; every kernel still drains): generate() raises DeviceError and
+    returns no tokens. With the knob back at 0 the same engine's next generate() returns
+    the tokens of an engine that never failed (after the error the engine drops its
+    captured decode graphs, so the graph case captures the next call afresh)."""
+    import efm_capi as C
+
+    shape = TINY128
+    w = O.random_weights(_oracle_cfg(shape), seed=44, std=0.2)
+    prompt = torch.randint(0, shape.vocab, (40,), generator=torch.Generator().manual_seed(10)).tolist()
+    with tempfile.TemporaryDirectory() as tmp:
+        eng, keep = _engine(tmp, shape, w, max_tokens=96, max_new_tokens=16, use_graph=use_graph)
+        plan = edge_fm.plan_decode(os.path.join(tmp, "engine.json"), 96)
+        assert all(p["attention"] == "hip_gfx950_decode_fused_qkv_attention" for p in plan)
+        req = edge_fm.Request(0, prompt)
+        req.set_ignore_stop_tokens(True)
+        clean = eng.generate(req).token_ids()
+        del eng
+        eng, keep = _engine(tmp, shape, w, max_tokens=96, max_new_tokens=16, use_graph=use_graph)
+        knob(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 1)
+        with pytest.raises(edge_fm.DeviceError, match="timed out"):
+            eng.generate(req)
+        knob(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 0)
+        assert eng.generate(req).token_ids() == clean
+        assert eng.generate(req).token_ids() == clean
+        del eng

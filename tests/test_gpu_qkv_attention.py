@@ -6,7 +6,9 @@ EFM_K_PREROTATED_EXCEPT_NEWEST), whose kernels are pinned to the oracle in
 test_gpu_ops.py: the residual output, every cache row (V and the rotated newest K in slot
 L-1, nothing else touched, NaN rows past L kept) and the attention split partials. Checked
 for the 1.5B, VL-3B text and 7B head layouts, at split boundaries, over many launches in a
-row on one sync workspace (the launch tag advances each time) and under HIP graph replay."""
+row on one sync workspace (the launch tag advances each time) and under HIP graph replay;
+the bounded wait forced to give up from the host is reported once and later launches
+are exact again."""
 import pytest
 import torch
 
@@ -158,6 +160,42 @@ def test_fused_graph_replay(gpu):
         for i, (ref, b) in enumerate(zip(refs, bufs)):
             _assert_same(ref, (b["r"], b["kc"], b["vc"], b["ws"]), f"replay {rep} layer {i}")
     C.call("efm_decode_qkv_attention_status", ptr(sync), stream())
+
+
+def test_forced_wait_timeout_reported_then_recovers(gpu, knob):
+    """The attention splits' bounded wait, forced to give up from the host
+    (EFM_KNOB_FRONT_WAIT_TIMEOUT: they wait for a tag that no projected word carries, with
+    a 64-poll limit, so every kernel still drains): three such launches flag the sync
+    workspace, the status call reports EFM_ERR_DEVICE once, clears the flag and steps the
+    epoch past every tag already written, and the launches after it, on the same sync
+    workspace, are bit-exact with the unfused pair again."""
+    s = SHAPES["1p5b"]
+    ctx = _ctx(s)
+    ws_bytes = C.load().efm_attention_decode_workspace_bytes(ctx, s["max_kv"])
+    sync = _sync_ws(s, gpu)
+    c = Case(s, 300, seed=5, gpu=gpu)
+    ref = _unfused(s, ctx, c, False, ws_bytes)
+    knob(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 1)
+    bad = [_fused(s, ctx, c, False, ws_bytes, sync) for _ in range(3)]
+    torch.cuda.synchronize()
+    words = sync[:12].view(torch.int32).tolist()    # epoch, done, abort
+    assert words == [3, 0, 1], f"sync header after three timed-out launches: {words}"
+    # the splits went on with zeros for the query: their partials are not the real ones
+    assert not torch.equal(_bits(bad[-1][3]), _bits(ref[3]))
+    # the GEMV half never waits: the residual and the V row are right all the same
+    assert torch.equal(_bits(bad[-1][0]), _bits(ref[0])) and torch.equal(_bits(bad[-1][2]), _bits(ref[2]))
+    with pytest.raises(C.EfmError, match="timed out") as err:
+        C.call("efm_decode_qkv_attention_status", ptr(sync), stream())
+    assert err.value.code == C.EFM_ERR_DEVICE
+    assert sync[:12].view(torch.int32).tolist() == [4, 0, 0]
+    C.call("efm_decode_qkv_attention_status", ptr(sync), stream())   # reported once
+    knob(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 0)
+    for it in range(3):
+        got = _fused(s, ctx, c, False, ws_bytes, sync)
+        torch.cuda.synchronize()
+        _assert_same(ref, got, f"launch {it} after the time-out")
+    C.call("efm_decode_qkv_attention_status", ptr(sync), stream())
+    assert sync[:12].view(torch.int32).tolist() == [7, 0, 0]
 
 
 def test_fused_supported_limits(gpu):
