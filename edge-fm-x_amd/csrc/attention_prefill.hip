@@ -259,15 +259,26 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillArgs a)
 }
 
 // ---------------------------------------------------------------------------------
-// Pipelined variant (head_dim 128, keys already rotated): one workgroup = 8 wave64s =
-// 256 query rows of one head, 32 per wave. 64-key K and V tiles stream global -> LDS
-// with global_load_lds into a 4-deep ring (no staging registers), so three tiles are
+// Pipelined variant (head_dim 128, keys already rotated): one workgroup = 4 or 8 wave64s
+// = 128 or 256 query rows of one head, 32 per wave. 64-key K and V tiles stream global ->
+// LDS with global_load_lds into an S-deep ring (no staging registers), so S - 1 tiles are
 // in flight while the matrix cores work on one; the tile layouts and operand reads are
 // described in attn_pipe.hpp (K read with ds_read_b128, the V^T operand of
-// O^T = V^T . P^T with ds_read_b64_tr_b16 from the row-major V tile). The scale is
-// applied in the exponent (exp2(s * scale - m)); the running max is only raised when a
-// row's tile max exceeds it by more than 2^8 (p <= 256 otherwise), which skips most
-// rescales of O; tiles that neither cross the diagonal nor the end are not masked.
+// O^T = V^T . P^T with ds_read_b64_tr_b16 from the row-major V tile).
+//
+// The matrix cores take the arithmetic; the vector ALU work per tile is kept to what the
+// softmax needs (one exp2 per score, a max, a bf16 pack and a row sum), because the
+// vector ALU, not the MFMA pipe, bounded the first version of this kernel:
+//  * Q is multiplied by log2(e) / sqrt(head_dim) before its bf16 rounding, so scores
+//    come out of the MFMAs in log2 units;
+//  * the running max m is folded into the MFMA accumulator start (C = -m), so
+//    p = exp2(s) needs no subtraction; m is raised only when a row's tile max exceeds it
+//    by more than 2^8 (p <= 256 otherwise), which is rare after the first tile;
+//  * row sums add the bf16-rounded p that the PV MFMAs use (v_dot2c_f32_bf16 against
+//    (1, 1)), so the normalisation matches the weights exactly;
+//  * the DMA addresses are a per-lane offset fixed for the whole loop plus a
+//    workgroup-uniform tile base (the last, partial tile clamps its rows).
+// Tiles that neither cross the diagonal nor the end are not masked.
 // ---------------------------------------------------------------------------------
 constexpr int kP2KV = 64;          // keys per tile
 constexpr int kP2HD = 128;
@@ -275,6 +286,14 @@ constexpr int kP2Row = kP2HD * 2;  // bytes per K / V row in LDS
 constexpr int kP2Tile = kP2KV * kP2Row;
 constexpr int kP2Stage = 2 * kP2Tile;
 constexpr float kP2Lazy = 8.0f;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Sum of the two bf16 halves of `w` added to acc (fp32).
+__device__ __forceinline__ float add_bf16_pair(uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
+                                           __builtin_bit_cast(bf16x2_t, 0x3f803f80u), acc, false);
+}
 
 template <int WAVES, int S>
 __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kernel(PrefillArgs a, int nqt) {
@@ -301,24 +320,45 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kerne
     const int q_last = min(a.S - 1, qt * QR + QR - 1);
     const int kv_end = a.causal ? min(a.L, q_last + diag + 1) : a.L;
     const int ntiles = (kv_end + kP2KV - 1) / kP2KV;
-    const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
-    const bf16_t* vbase = a.v + (size_t)kvh * a.v_sh;
+    const char* kbase = reinterpret_cast<const char*>(a.k + (size_t)kvh * a.k_sh);
+    const char* vbase = reinterpret_cast<const char*>(a.v + (size_t)kvh * a.v_sh);
 
-    // wave load i of a tile: 4 rows x 16 chunks; lane -> (row l / 16, physical chunk l % 16)
+    // wave load i of a tile: 4 rows x 16 chunks; lane -> (row l / 16, physical chunk l % 16).
+    // Load i is a K load for i < LPW / 2 and a V load after (q = wave + i * WAVES < 16).
+    const int pr = lane >> 4, pc = lane & 15;
+    uint32_t loff[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+        const int q = wave + i * WAVES;
+        const bool isv = i >= LPW / 2;
+        const int row = (q % (kP2Tile / 1024)) * 4 + pr;
+        const int c = isv ? (pc ^ ((row & 3) << 2)) : (pc ^ (row & 15));
+        loff[i] = (uint32_t)((row * (isv ? a.v_sn : a.k_sn) + c * 8) * 2);
+    }
+    const uint32_t dst0 = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(wave * 1024));
     auto issue = [&](int tile, int slot) {
         const int k0 = tile * kP2KV;
-        const int pr = lane >> 4, pc = lane & 15;
+        const char* kt0 = kbase + (size_t)k0 * a.k_sn * 2;
+        const char* vt0 = vbase + (size_t)k0 * a.v_sn * 2;
+        const uint32_t dst = dst0 + (uint32_t)(slot * kP2Stage);
+        auto load = [&](int i, uint32_t off) {
+            const char* src = (i >= LPW / 2 ? vt0 : kt0) + off;
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(src),
+                (__attribute__((address_space(3))) void*)(uintptr_t)(dst + (uint32_t)(i * WAVES * 1024)), 16, 0, 0);
+        };
+        if (k0 + kP2KV <= a.L) {
 #pragma unroll
-        for (int i = 0; i < LPW; ++i) {
-            const int q = wave + i * (THREADS / kWave);   // wave-load index in the stage
-            const bool isv = q >= kP2Tile / 1024;
-            const int row = (q % (kP2Tile / 1024)) * 4 + pr;
-            const int c = isv ? (pc ^ ((row & 3) << 2)) : (pc ^ (row & 15));
-            const int j = min(k0 + row, a.L - 1);
-            const bf16_t* src = (isv ? vbase + (size_t)j * a.v_sn : kbase + (size_t)j * a.k_sn) + c * 8;
-            __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                             (__attribute__((address_space(3))) void*)(smem + slot * kP2Stage + q * 1024),
-                                             16, 0, 0);
+            for (int i = 0; i < LPW; ++i) load(i, loff[i]);
+        } else {   // the last, partial tile: rows past the end read the last row
+#pragma unroll
+            for (int i = 0; i < LPW; ++i) {
+                const bool isv = i >= LPW / 2;
+                const int q = wave + i * WAVES;
+                const int row = (q % (kP2Tile / 1024)) * 4 + pr;
+                const int c = isv ? (pc ^ ((row & 3) << 2)) : (pc ^ (row & 15));
+                load(i, (uint32_t)((min(row, a.L - 1 - k0) * (isv ? a.v_sn : a.k_sn) + c * 8) * 2));
+            }
         }
     };
     // ---- Q (B operand) of this lane's row, d = ks*16 + hh*8 + e; requested before the
@@ -333,6 +373,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kerne
     }
     const int pre = min(S - 1, ntiles);
     for (int p = 0; p < pre; ++p) issue(p, p);
+    const float scale = a.sm_scale_log2;
     bf16x8_t qf[KS];
     {
         float x[KS][8];
@@ -354,6 +395,8 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kerne
         }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[ks][e] *= scale;
             Pack8 pk;
             pk.u = pack8(x[ks]);
             qf[ks] = pk.v;
@@ -365,8 +408,12 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kerne
     for (int tt = 0; tt < DT; ++tt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) oacc[tt][e] = 0.f;
+    // m_run: running row max (log2 units), -inf before the first tile; sinit = -m_run
+    // (0 before the first tile) starts every score accumulator
     float m_run = -INFINITY, l_run = 0.f;
-    const float scale = a.sm_scale_log2;
+    f32x16_t sinit;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sinit[e] = 0.f;
     const int wave_last_key = q0 + 31 + diag;   // causal: last key any row of this wave sees
 
     // lane parts of the operand addresses inside a stage (rows of the tile and the
@@ -395,7 +442,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kerne
 #pragma unroll
         for (int tt = 0; tt < DT; ++tt) va[tt] = stage + voff[tt];
 
-        // ---- S^T for keys 0..31 (s0) and 32..63 (s1) of the tile
+        // ---- S^T - m for keys 0..31 (s0) and 32..63 (s1) of the tile
         bf16x8_t kf0[KS], kf1[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) attn_pipe::read_b128<0>(kf0[ks], ka[ks]);
@@ -409,7 +456,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kerne
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kf0[ks]));
         // keys 32..63 are all masked when !two (the edge masking below sets them to -inf)
-        f32x16_t s0 = {}, s1 = {};
+        f32x16_t s0 = sinit, s1 = sinit;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf0[ks], qf[ks], s0, 0, 0, 0);
         if (two) {
@@ -448,37 +495,54 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kerne
         for (int e = 1; e < 16; ++e) mloc = fmaxf(fmaxf(mloc, s0[e]), s1[e]);
         {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
-            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scale;
+            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));   // tile max - m_run (or raw before)
         }
-        if (__any(mloc > m_run + kP2Lazy)) {
-            // a real (wave-uniform) branch: most tiles skip the rescale of O
+        // raise m when some row's tile max exceeds it by more than 2^8 (always on the
+        // first tile, where m_run = -inf); a real (wave-uniform) branch
+        if (__any(m_run == -INFINITY || mloc > kP2Lazy)) {
             asm volatile("" ::: "memory");
-            const float m_new = fmaxf(m_run, mloc);
+            const float base = (m_run == -INFINITY) ? 0.f : m_run;   // what the accumulators started from
+            const float m_new = fmaxf(m_run, base + mloc);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 on the first tile
+            const float shift = m_new - base;
             l_run *= alpha;
 #pragma unroll
             for (int tt = 0; tt < DT; ++tt)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                s0[e] -= shift;
+                s1[e] -= shift;
+                sinit[e] = -m_new;
+            }
             m_run = m_new;
         }
-        const float mref = (m_run == -INFINITY) ? 0.f : m_run;
-        float p0[16], p1[16], psum = 0.f;
+        Pack8 pb[4];
+        {
+            float p0[16], p1[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            p0[e] = __builtin_amdgcn_exp2f(fmaf(s0[e], scale, -mref));
-            p1[e] = __builtin_amdgcn_exp2f(fmaf(s1[e], scale, -mref));
-            psum += p0[e] + p1[e];
+            for (int e = 0; e < 16; ++e) {
+                p0[e] = __builtin_amdgcn_exp2f(s0[e]);
+                p1[e] = __builtin_amdgcn_exp2f(s1[e]);
+            }
+            pb[0].u = pack8(&p0[0]);
+            pb[1].u = pack8(&p0[8]);
+            pb[2].u = pack8(&p1[0]);
+            pb[3].u = pack8(&p1[8]);
+        }
+        float psum = 0.f;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            psum = add_bf16_pair(pb[b].u.x, psum);
+            psum = add_bf16_pair(pb[b].u.y, psum);
+            psum = add_bf16_pair(pb[b].u.z, psum);
+            psum = add_bf16_pair(pb[b].u.w, psum);
         }
         {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(psum), __float_as_uint(psum), false, false);
             l_run += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
         }
-        Pack8 pb[4];
-        pb[0].u = pack8(&p0[0]);
-        pb[1].u = pack8(&p0[8]);
-        pb[2].u = pack8(&p1[0]);
-        pb[3].u = pack8(&p1[8]);
 
         // ---- O^T += V^T . P^T, key block by key block (the reads of block kb + 2 are
         //      issued once block kb has landed, so at most 16 are outstanding)
@@ -533,6 +597,18 @@ int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
 // path of the pipelined one in the tests).
 static bool prefill_pipe_enabled() { return kernel_knob(EFM_KNOB_PREFILL_REGISTER) == 0; }
 
+int prefill_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 }  // namespace efm
 
 using namespace efm;
@@ -575,12 +651,11 @@ extern "C" int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q
     rope_table_fill(&a.rope, hd, ctx->rope_theta, ctx->rope_scale);
     a.sm_scale_log2 = 1.4426950408889634f / sqrtf((float)hd);
     if (hd == kP2HD && !a.rope_k && prefill_pipe_enabled()) {
-        // up to 8K rows: 4 waves (128 rows) over a 2-deep ring, two workgroups per CU
-        // (twice the workgroups, and the two drift out of phase so that one's softmax
-        // overlaps the other's matrix work); longer: 8 waves (256 rows) over a 4-deep
-        // ring, one per CU. EFM_KNOB_PREFILL_SHAPE = 4 / 8 forces one of them.
-        const int shape = kernel_knob(EFM_KNOB_PREFILL_SHAPE);
-        const bool small = shape != 0 ? shape == 4 : qo_len <= 8192;
+        // 8 waves (256 rows, 4-deep ring, one workgroup per CU) when those workgroups fill
+        // the chip; fewer rows: 4 waves (128 rows) over a 2-deep ring, two workgroups per
+        // CU (twice the workgroups). EFM_KNOB_PREFILL_SHAPE = 4 / 8 forces one of them.
+        const int knob = kernel_knob(EFM_KNOB_PREFILL_SHAPE);
+        const bool small = knob != 0 ? knob == 4 : (int)((qo_len + 255) / 256) * a.Hq < prefill_cus();
         if (small) {
             const int nqt = (int)((qo_len + 127) / 128);
             hipLaunchKernelGGL((prefill_attn_pipe_kernel<4, 2>), dim3(nqt * a.Hq), dim3(256), 0, stream, a, nqt);

@@ -321,11 +321,21 @@ __global__ __launch_bounds__(kSageThreads) void sage_attn_kernel(SageArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
-// Pipelined variant (head_dim 128): 8 wave64s = 256 query rows of one head per
-// workgroup; 64-key int8 K tiles (8 KB) and bf16 V tiles (16 KB) stream global -> LDS
-// with global_load_lds into a 4-deep ring, laid out and read as described in
+// Pipelined variant (head_dim 128): 4 or 8 wave64s = 128 or 256 query rows of one head
+// per workgroup; 64-key int8 K tiles (8 KB) and bf16 V tiles (16 KB) stream global ->
+// LDS with global_load_lds into an S-deep ring, laid out and read as described in
 // attn_pipe.hpp (int8 K operand via ds_read_b128, V^T via ds_read_b64_tr_b16). The
 // running max is only raised when a row's tile max exceeds it by more than 2^8.
+//
+// Vector ALU work per score is one FMA, one exp2 and a share of the max, the bf16 pack
+// and the row sum (the vector ALU, not the matrix cores, bounded the first version):
+//  * the int32 score accumulators start at 1.5 * 2^23 (C operand of the first MFMA), so
+//    their bits read as a float are exactly 1.5 * 2^23 + score (|score| <= 127^2 * 128 <
+//    2^22): no int -> float conversion; one FMA applies the dequantisation scale, the
+//    offset and the running max: s = t * coef - (1.5 * 2^23 * coef + m);
+//  * row sums add the bf16-rounded p that the PV MFMAs use (v_dot2c_f32_bf16);
+//  * DMA addresses are a per-lane offset fixed for the whole loop plus a
+//    workgroup-uniform tile base (the last, partial tile clamps its rows).
 // ---------------------------------------------------------------------------------
 constexpr int kSPKV = 64;
 constexpr int kSPHD = 128;
@@ -333,6 +343,15 @@ constexpr int kSPKTile = kSPKV * kSPHD;          // int8 bytes
 constexpr int kSPVTile = kSPKV * kSPHD * 2;      // bf16 bytes
 constexpr int kSPStage = kSPKTile + kSPVTile;
 constexpr float kSPLazy = 8.0f;
+constexpr float kMagic = 12582912.0f;   // 1.5 * 2^23: its float ulp is 1
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Sum of the two bf16 halves of `w` added to acc (fp32).
+__device__ __forceinline__ float add_bf16_pair(uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
+                                           __builtin_bit_cast(bf16x2_t, 0x3f803f80u), acc, false);
+}
 
 template <int WAVES, int S>
 __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(SageArgs a, int nqt) {
@@ -379,26 +398,53 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
             unpack8(u[ks][1], &xq[ks][8]);
         }
     }
-    // wave load q of a stage: K8 loads (8 rows x 8 chunks) first, then V (4 rows x 16)
+    // wave load i of a stage: K8 loads (8 rows x 8 chunks) first, then V (4 rows x 16);
+    // q = wave + i * WAVES, so whether load i is a K load is known at compile time
+    constexpr int KL = kSPKTile / 1024;   // K wave loads per stage
+    const char* kbase = reinterpret_cast<const char*>(a.k8) + (size_t)kvh * kSPHD;
+    const char* vbase = reinterpret_cast<const char*>(a.v + (size_t)kvh * a.v_sh);
+    auto load_geo = [&](int i, int& row, int& c) {
+        const int q = wave + i * WAVES;
+        if (i * WAVES < KL) {
+            row = q * 8 + (lane >> 3);
+            c = (lane & 7) ^ ((row >> 1) & 7);   // attn_pipe::k8_off
+        } else {
+            row = (q - KL) * 4 + (lane >> 4);
+            c = (lane & 15) ^ ((row & 3) << 2);   // attn_pipe::v_off
+        }
+    };
+    auto load_off = [&](int i, int row, int c) {
+        return (i * WAVES < KL) ? (uint32_t)(row * a.Hkv * kSPHD + c * 16) : (uint32_t)((row * a.v_sn + c * 8) * 2);
+    };
+    uint32_t loff[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+        int row, c;
+        load_geo(i, row, c);
+        loff[i] = load_off(i, row, c);
+    }
+    const uint32_t dst0 = __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(wave * 1024));
     auto issue = [&](int tile, int slot) {
         const int k0 = tile * kSPKV;
+        const char* kt0 = kbase + (size_t)k0 * a.Hkv * kSPHD;
+        const char* vt0 = vbase + (size_t)k0 * a.v_sn * 2;
+        const uint32_t dst = dst0 + (uint32_t)(slot * kSPStage);
+        auto load = [&](int i, uint32_t off) {
+            const char* src = (i * WAVES < KL ? kt0 : vt0) + off;
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(src),
+                (__attribute__((address_space(3))) void*)(uintptr_t)(dst + (uint32_t)(i * WAVES * 1024)), 16, 0, 0);
+        };
+        if (k0 + kSPKV <= a.L) {
 #pragma unroll
-        for (int i = 0; i < LPW; ++i) {
-            const int q = wave + i * (WAVES);
-            const void* src;
-            if (q < kSPKTile / 1024) {
-                const int row = q * 8 + (lane >> 3), pc = lane & 7;
-                const int c = pc ^ ((row >> 1) & 7);   // attn_pipe::k8_off
-                const int j = min(k0 + row, a.L - 1);
-                src = a.k8 + ((size_t)j * a.Hkv + kvh) * kSPHD + c * 16;
-            } else {
-                const int row = (q - kSPKTile / 1024) * 4 + (lane >> 4), pc = lane & 15;
-                const int c = pc ^ ((row & 3) << 2);   // attn_pipe::v_off
-                const int j = min(k0 + row, a.L - 1);
-                src = a.v + (size_t)j * a.v_sn + (size_t)kvh * a.v_sh + c * 8;
+            for (int i = 0; i < LPW; ++i) load(i, loff[i]);
+        } else {   // the last, partial tile: rows past the end read the last row
+#pragma unroll
+            for (int i = 0; i < LPW; ++i) {
+                int row, c;
+                load_geo(i, row, c);
+                load(i, load_off(i, min(row, a.L - 1 - k0), c));
             }
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(smem + slot * kSPStage + q * 1024),
-                                             16, 0, 0);
         }
     };
     const int pre = min(S - 1, ntiles);
@@ -439,6 +485,9 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
 #pragma unroll
         for (int e = 0; e < 16; ++e) oacc[tt][e] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
+    int32x16_t magic;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) magic[e] = __float_as_int(kMagic);
     const int wave_last_key = q0 + 31 + diag;
     uint32_t koff[KS8], voff[DT];
 #pragma unroll
@@ -465,8 +514,10 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
         for (int tt = 0; tt < DT; ++tt) va[tt] = stage + voff[tt];
         // sk is per 128-key block; a 64-key tile lies inside one block
         const float coef = (qscale * a.sk[(kb0 / kSageBlock) * a.Hkv + kvh]) * a.scale_log2;
+        const float m_acc = (m_run == -INFINITY) ? 0.f : m_run;
+        const float bias = fmaf(kMagic, coef, m_acc);
 
-        // ---- int32 S^T for keys 0..31 (acc0) and 32..63 (acc1) of the tile
+        // ---- int32 S^T (+ 1.5 * 2^23) for keys 0..31 (acc0) and 32..63 (acc1) of the tile
         int32x4_t kf0[KS8], kf1[KS8];
 #pragma unroll
         for (int ks = 0; ks < KS8; ++ks) attn_pipe::read_b128<0>(kf0[ks], ka[ks]);
@@ -479,7 +530,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
         }
 #pragma unroll
         for (int ks = 0; ks < KS8; ++ks) asm volatile("" : "+v"(kf0[ks]));
-        int32x16_t acc0 = {}, acc1 = {};
+        int32x16_t acc0 = magic, acc1 = magic;
 #pragma unroll
         for (int ks = 0; ks < KS8; ++ks) acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf0[ks], qf[ks], acc0, 0, 0, 0);
         if (two) {
@@ -501,11 +552,12 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
         read_v(std::integral_constant<int, 0>{});
         read_v(std::integral_constant<int, 1>{});
 
+        // s = score * coef - m_acc, in log2 units
         float s0[16], s1[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            s0[e] = (float)acc0[e];
-            s1[e] = (float)acc1[e];   // all masked below when !two
+            s0[e] = fmaf(__int_as_float(acc0[e]), coef, -bias);
+            s1[e] = fmaf(__int_as_float(acc1[e]), coef, -bias);   // all masked below when !two
         }
         if (kb0 + kSPKV > kv_end || (a.causal && kb0 + kSPKV - 1 > q0 + diag)) {
             const int lim = a.causal ? min(kv_end, qi + diag + 1) : kv_end;
@@ -521,37 +573,52 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
         for (int e = 1; e < 16; ++e) mloc = fmaxf(fmaxf(mloc, s0[e]), s1[e]);
         {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
-            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * coef;
+            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));   // tile max - m_acc
         }
-        if (__any(mloc > m_run + kSPLazy)) {
-            // a real (wave-uniform) branch: most tiles skip the rescale of O
+        // raise m when some row's tile max exceeds it by more than 2^8 (always on the
+        // first tile, where m_run = -inf); a real (wave-uniform) branch
+        if (__any(m_run == -INFINITY || mloc > kSPLazy)) {
             asm volatile("" ::: "memory");
-            const float m_new = fmaxf(m_run, mloc);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            const float m_new = fmaxf(m_run, m_acc + mloc);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 on the first tile
+            const float shift = m_new - m_acc;
             l_run *= alpha;
 #pragma unroll
             for (int tt = 0; tt < DT; ++tt)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                s0[e] -= shift;
+                s1[e] -= shift;
+            }
             m_run = m_new;
         }
-        const float mref = (m_run == -INFINITY) ? 0.f : m_run;
-        float p0[16], p1[16], psum = 0.f;
+        Pack8 pb[4];
+        {
+            float p0[16], p1[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            p0[e] = __builtin_amdgcn_exp2f(fmaf(s0[e], coef, -mref));
-            p1[e] = __builtin_amdgcn_exp2f(fmaf(s1[e], coef, -mref));
-            psum += p0[e] + p1[e];
+            for (int e = 0; e < 16; ++e) {
+                p0[e] = __builtin_amdgcn_exp2f(s0[e]);
+                p1[e] = __builtin_amdgcn_exp2f(s1[e]);
+            }
+            pb[0].u = pack8(&p0[0]);
+            pb[1].u = pack8(&p0[8]);
+            pb[2].u = pack8(&p1[0]);
+            pb[3].u = pack8(&p1[8]);
+        }
+        float psum = 0.f;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            psum = add_bf16_pair(pb[b].u.x, psum);
+            psum = add_bf16_pair(pb[b].u.y, psum);
+            psum = add_bf16_pair(pb[b].u.z, psum);
+            psum = add_bf16_pair(pb[b].u.w, psum);
         }
         {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(psum), __float_as_uint(psum), false, false);
             l_run += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
         }
-        Pack8 pb[4];
-        pb[0].u = pack8(&p0[0]);
-        pb[1].u = pack8(&p0[8]);
-        pb[2].u = pack8(&p1[0]);
-        pb[3].u = pack8(&p1[8]);
         auto pv = [&](int kb) {
 #pragma unroll
             for (int tt = 0; tt < DT; ++tt) {
@@ -597,6 +664,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
         }
 }
 
+int prefill_cus();
 int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
 
 static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -716,10 +784,10 @@ extern "C" int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, con
     a.causal = causal != 0;
     a.scale_log2 = (float)(1.4426950408889634 / sqrt((double)hd));
     if (pipe) {
-        // as the bf16 kernel: 4 waves / two workgroups per CU up to 8K rows (a 3-deep ring
-        // of 24 KB stages fits twice), 8 waves over a 4-deep ring beyond
+        // as the bf16 kernel: 8 waves over a 4-deep ring when those workgroups fill the
+        // chip, else 4 waves / two workgroups per CU (a 3-deep ring of 24 KB stages fits twice)
         const int shape = kernel_knob(EFM_KNOB_PREFILL_SHAPE);
-        const bool small = shape != 0 ? shape == 4 : qo_len <= 8192;
+        const bool small = shape != 0 ? shape == 4 : (int)((qo_len + 255) / 256) * a.Hq < prefill_cus();
         if (small) {
             const int nqt = (int)((qo_len + 127) / 128);
             hipLaunchKernelGGL((sage_attn_pipe_kernel<4, 3>), dim3(nqt * a.Hq), dim3(256), 0, stream, a, nqt);
