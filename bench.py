@@ -396,6 +396,67 @@ def c2_cpu_baseline(torch, shape, weights, prompt, gpu_tokens, n_dec=8):
     return cpu, parity
 
 
+def c3_cpu_baseline(torch, shape, weights, prompt, emb, pos, embed_id):
+    """The CPU oracle on this host for C3: the whole 1344-token multimodal prefill (the
+    same weights, vision rows, text ids and 3-D positions as the GPU run) through all
+    layers; prefill tokens/s."""
+    from oracle import efm_oracle as O
+
+    ocfg = O.QwenConfig(hidden=shape.hidden, layers=shape.layers, heads=shape.heads, kv_heads=shape.kv_heads,
+                        head_dim=shape.head_dim, inter=shape.inter, vocab=shape.vocab, eps=shape.eps,
+                        theta=shape.theta, tied=shape.tied, mrope_section=shape.mrope_section)
+    wcpu = {k: v.cpu() for k, v in weights.items()}
+    orc = O.Qwen2Oracle(ocfg, O.fuse_weights(ocfg, wcpu), max_tokens=len(prompt) + 1, cache_f32=True)
+    del wcpu
+    ids = torch.tensor(prompt, dtype=torch.int32)
+    embeds = O.embedding(ids, orc.w["embed"].to(torch.bfloat16), emb.cpu(), embed_id)
+    st = orc.new_state()
+    c0 = time.perf_counter()
+    orc.forward(st, ids, embeds=embeds, position_ids=pos.cpu())
+    pf_s = time.perf_counter() - c0
+    info = host_cpu_info(torch)
+    return {"value": round(len(prompt) / pf_s, 2), "unit": "tokens/s", "cores": info["torch_threads"], "kind": "port",
+            "sample": f"CPU oracle (PyTorch fp32 math on bf16 values), the whole {len(prompt)}-token prefill of the "
+                      f"same VL-3B-shaped weights, vision rows and M-RoPE positions; prefill tokens/s",
+            "prefill_s": round(pf_s, 2), **info}
+
+
+def c5_cpu_baseline(torch, shape, weights, ctx_len, n_dec=2):
+    """The CPU oracle on this host for C5: n_dec sampled decode steps (T 0.7, top-p 0.9,
+    the oracle's Philox sampler) of the same 7B-shaped weights over a ctx_len-row KV
+    cache. The cache holds N(0, 1) rows (one random block copied into every layer): a
+    16k-token CPU prefill would take hours and does not change a decode step's work.
+    Decode tokens/s."""
+    from oracle import efm_oracle as O
+
+    ocfg = O.QwenConfig(hidden=shape.hidden, layers=shape.layers, heads=shape.heads, kv_heads=shape.kv_heads,
+                        head_dim=shape.head_dim, inter=shape.inter, vocab=shape.vocab, eps=shape.eps,
+                        theta=shape.theta, tied=shape.tied)
+    wcpu = {k: v.cpu() for k, v in weights.items()}
+    orc = O.Qwen2Oracle(ocfg, O.fuse_weights(ocfg, wcpu), max_tokens=ctx_len + n_dec + 1, cache_f32=True)
+    del wcpu
+    st = orc.new_state()
+    g = torch.Generator().manual_seed(5)
+    kb = torch.randn(ctx_len, shape.kv_heads, shape.head_dim, generator=g).to(torch.bfloat16)
+    vb = torch.randn(ctx_len, shape.kv_heads, shape.head_dim, generator=g).to(torch.bfloat16)
+    for l in range(shape.layers):
+        st.k[l][:ctx_len] = kb
+        st.v[l][:ctx_len] = vb
+    st.length = ctx_len
+    tok, dec_s = 0, 0.0
+    for i in range(n_dec):
+        c0 = time.perf_counter()
+        logits = orc.forward(st, torch.tensor([tok], dtype=torch.int32))
+        tok, _ = O.sample_top_p(logits.numpy().astype("float32"), 0.7, 0.9, 1234, i)
+        dec_s += time.perf_counter() - c0
+    info = host_cpu_info(torch)
+    return {"value": round(n_dec / dec_s, 4), "unit": "tokens/s", "cores": info["torch_threads"], "kind": "port",
+            "sample": f"CPU oracle (PyTorch fp32 math on bf16 values), the same 7B-shaped weights (untied head); "
+                      f"{n_dec} sampled decode steps (T 0.7, top-p 0.9) at context {ctx_len + 1}-{ctx_len + n_dec} over "
+                      f"an N(0,1) KV cache; decode tokens/s",
+            **info}
+
+
 # ---------------------------------------------------------------------------------
 # Other BASELINE configurations (bench.py --config c1|c3|c4|c5). The default run (c2) is
 # the headline line above; these print one JSON line each for their own workload.
@@ -637,6 +698,7 @@ def run_c5(args):
     g = torch.Generator().manual_seed(args.seed)
     prompt = torch.randint(0, shape.vocab, (P,), generator=g).tolist()
     mets, toks, w = _engine_generate(args, shape, prompt, G, temperature=0.7, top_p=0.9, seed=1234)
+    cpu = None if args.no_cpu_baseline else c5_cpu_baseline(torch, shape, w, P)
     import efm_capi as C
     # the dominant decode kernel at this shape (272 MB of gate/up weights per launch); its
     # HBM traffic counters are profiled at the C2 shape only
@@ -662,7 +724,7 @@ def run_c5(args):
         "decode_loop": {"bytes_per_token": int(nbytes), "achieved_GBs": round(gbs, 1),
                         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)},
         "roofline": kern,
-        "tokens_head": toks[:8], "cpu_baseline": None,
+        "tokens_head": toks[:8], "cpu_baseline": cpu,
     }))
 
 
@@ -692,6 +754,7 @@ def run_c3(args):
     last = int(pos.max().item())
     mets, toks, w = _engine_generate(args, shape, prompt, G, emb=emb, embed_id=embed_id, pos=pos,
                                      last_pos=[last, last, last], model_name="qwen2_5_vl")
+    cpu = None if args.no_cpu_baseline else c3_cpu_baseline(torch, shape, w, prompt, emb, pos, embed_id)
     S_ = nv + nt
     pf_ms = sum(m["prefill_ms"] for m in mets) / len(mets)
     dec_tps = sum(m["decode_steps"] for m in mets) * 1000.0 / sum(m["decode_ms"] for m in mets)
@@ -710,7 +773,7 @@ def run_c3(args):
         "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tf / 2500.0, 4), "traffic": None,
                      "note": "whole prefill: linear %.3g + attention %.3g FLOP over the engine's prefill time" % (lin, attn)},
-        "tokens_head": toks[:8], "cpu_baseline": None,
+        "tokens_head": toks[:8], "cpu_baseline": cpu,
     }))
 
 
