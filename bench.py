@@ -12,8 +12,9 @@ Extra fields:
                 HIP events around a graph replay of 20 x 28 launches over all 28 layers'
                 weights (context 640, the run's mean), against 8 TB/s HBM; `traffic` is
                 read from the committed rocprofv3 --pmc summary of that kernel.
-  per_layer_kernels  the same figures for all four per-layer decode kernels (front half:
-                norm + QKV + attention; merge + o_proj; norm + gate/up + SwiGLU; down).
+  per_layer_kernels  the same figures for all five per-layer decode kernels of the engine's
+                default plan (norm + QKV; split attention; merge + o_proj; norm + gate/up +
+                SwiGLU; down).
   decode_loop   algorithmic bytes per decode token / measured ms per token.
   cpu_baseline  the CPU oracle (PyTorch, fp32 math on bf16 values) on this host,
                 same model and prompt: 512-token prefill, then 8 decode steps at
@@ -57,7 +58,8 @@ def gate_up_bytes(shape):
 
 
 def measured_traffic(name="gate_up"):
-    """HBM bytes per launch of a per-layer decode kernel (front, o_proj, gate_up, down)
+    """HBM bytes per launch of a per-layer decode kernel (norm_qkv, attention, o_proj,
+    gate_up, down)
     from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-kernel
     calibrated), or None."""
     key = f"traffic_bytes_per_launch[{name}]:"
@@ -122,26 +124,27 @@ def roofline_kernel(torch, C, shape, weights, dev, graph=True, reps=20, traffic=
 
 
 def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20, eager=False):
-    """The four kernels of one decode layer, each timed over all layers' real weights:
-    a HIP graph of reps x layers launches of one kernel is replayed between two HIP events
-    on the replay stream (avg = kernel duration plus the graph's inter-node gap).
-      front    efm_decode_norm_qkv_attention: input RMSNorm + fused QKV GEMV + bias + KV
-               write + split attention over ctx_len cached rows (rotated cache)
-      o_proj   efm_decode_attention_merge_o_proj: split merge + o_proj GEMV
-      gate_up  efm_decode_norm_gate_up_swiglu: add-norm + gate/up GEMV + SwiGLU
-      down     efm_linear m = 1: down_proj GEMV
+    """The five kernels of one decode layer in the engine's default plan, each timed over
+    all layers' real weights: a HIP graph of reps x layers launches of one kernel is
+    replayed between two HIP events on the replay stream (avg = kernel duration plus the
+    graph's inter-node gap).
+      norm_qkv   efm_decode_norm_qkv: add-norm + fused QKV GEMV + bias + K/V slot write
+      attention  efm_decode_attention_partials: split attention over ctx_len cached rows
+                 (rotated cache; the newest key rotated and stored back)
+      o_proj     efm_decode_attention_merge_o_proj: split merge + o_proj GEMV
+      gate_up    efm_decode_norm_gate_up_swiglu: add-norm + gate/up GEMV + SwiGLU
+      down       efm_linear m = 1: down_proj GEMV
     Algorithmic bytes per launch: weights (+ bias, norm weights), activations in and out,
-    the K/V rows read, and the attention partials (ceil(ctx/128) splits x heads x
-    (head_dim + 2) fp32) written by front and read by o_proj. Sorted by time, slowest
-    first. eager=True launches each kernel reps x layers times without graphs or timing
-    (the counter-collection workload) and returns None."""
+    the K/V rows read and written, and the attention partials (ceil(ctx/128) splits x
+    heads x (head_dim + 2) fp32) written by attention and read by o_proj. Sorted by time,
+    slowest first. eager=True launches each kernel reps x layers times without graphs or
+    timing (the counter-collection workload) and returns None."""
     H, I, L = shape.hidden, shape.inter, shape.layers
     qd, kvd, hd = shape.q_dim, shape.kv_dim, shape.head_dim
     ctx = C.make_attention_ctx(shape.heads, shape.kv_heads, hd)
     ctx.k_already_prerotated = C.EFM_K_PREROTATED_EXCEPT_NEWEST
     lib = C.load()
     ws = torch.zeros(lib.efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=dev)
-    sync = torch.zeros(lib.efm_decode_qkv_attention_sync_bytes(qd, kvd), dtype=torch.uint8, device=dev)
     g = torch.Generator(device=dev).manual_seed(7)
     per = []
     for l in range(L):
@@ -163,11 +166,16 @@ def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20
     mid = torch.randn(1, I, device=dev, generator=g).to(torch.bfloat16)
     y = torch.empty(1, H, device=dev, dtype=torch.bfloat16)
 
-    def front(x, sh):
-        C.call("efm_decode_norm_qkv_attention", ctx, H, shape.eps, h.data_ptr(), r_in.data_ptr(), r_out.data_ptr(),
-               x["nin"].data_ptr(), x["wqkv"].data_ptr(), x["bqkv"].data_ptr(), x["kc"].data_ptr(),
-               x["vc"].data_ptr(), d_len.data_ptr(), max_kv, ws.data_ptr(), ws.numel(), sync.data_ptr(),
-               sync.numel(), sh)
+    q = torch.empty(1, qd, device=dev, dtype=torch.bfloat16)
+
+    def norm_qkv(x, sh):
+        C.call("efm_decode_norm_qkv", H, qd, kvd, shape.eps, h.data_ptr(), r_in.data_ptr(), r_out.data_ptr(),
+               x["nin"].data_ptr(), x["wqkv"].data_ptr(), x["bqkv"].data_ptr(), q.data_ptr(), x["kc"].data_ptr(),
+               x["vc"].data_ptr(), d_len.data_ptr(), sh)
+
+    def attention(x, sh):
+        C.call("efm_decode_attention_partials", ctx, q.data_ptr(), x["kc"].data_ptr(), x["vc"].data_ptr(),
+               d_len.data_ptr(), max_kv, ws.data_ptr(), ws.numel(), sh)
 
     def oproj(x, sh):
         C.call("efm_decode_attention_merge_o_proj", ctx, d_len.data_ptr(), max_kv, ws.data_ptr(), ws.numel(),
@@ -184,8 +192,10 @@ def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20
     part = splits * shape.heads * (hd + 2) * 4
     act = 2 * H
     kernels = [
-        ("front", "efm_decode_norm_qkv_attention (decode_qkv_attn_kernel)", front,
-         ((qd + 2 * kvd) * (H + 1) + H) * 2 + 3 * act + 2 * (ctx_len - 1) * kvd * 2 + 2 * kvd * 2 + part),
+        ("norm_qkv", "efm_decode_norm_qkv (gemv_kernel, add-norm prologue, QKV epilogue)", norm_qkv,
+         ((qd + 2 * kvd) * (H + 1) + H) * 2 + 3 * act + qd * 2 + 2 * kvd * 2),
+        ("attention", "efm_decode_attention_partials (decode_attn_lds_kernel)", attention,
+         qd * 2 + 2 * ctx_len * kvd * 2 + kvd * 2 + part),
         ("o_proj", "efm_decode_attention_merge_o_proj (gemv_kernel, merge prologue)", oproj,
          qd * H * 2 + part + act),
         ("gate_up", "efm_decode_norm_gate_up_swiglu (gemv_kernel, add-norm prologue, SwiGLU epilogue)", gate_up,
@@ -199,7 +209,6 @@ def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20
                 for x in per:
                     fn(x, stream.cuda_stream)
             stream.synchronize()
-        C.call("efm_decode_qkv_attention_status", sync.data_ptr(), stream.cuda_stream)
         return None
     out = []
     for name, kname, fn, nbytes in kernels:
@@ -221,7 +230,6 @@ def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20
         out.append({"name": name, "kernel": kname, "bytes_per_launch": int(nbytes), "avg_launch_us": round(us, 3),
                     "achieved_GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
         del graph
-    C.call("efm_decode_qkv_attention_status", sync.data_ptr(), stream.cuda_stream)
     return sorted(out, key=lambda k: -k["avg_launch_us"])
 
 
@@ -275,7 +283,7 @@ def attention_layouts(torch, C, reps=20):
 def kernel_only(torch, C, S, shape, seed):
     """Counter-collection workload: a 256 MiB device copy (calibration: 262144 KiB read,
     262144 KiB written), then 2 x layers direct launches of each per-layer decode kernel
-    (front, o_proj, gate_up, down) at context 640."""
+    (norm_qkv, attention, o_proj, gate_up, down) at context 640."""
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     x = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).uniform_()
@@ -794,7 +802,7 @@ def main():
     ap.add_argument("--attention-layouts", action="store_true",
                     help="decode attention on the engine's rotated cache vs the reference's rotate-on-read layout")
     ap.add_argument("--kernel-only", action="store_true",
-                    help="run only the copy calibration and the four per-layer decode kernels (for rocprofv3 --pmc passes)")
+                    help="run only the copy calibration and the five per-layer decode kernels (for rocprofv3 --pmc passes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the single-request decode path of this build runs on one MI355X; "
@@ -863,7 +871,7 @@ def main():
             "unit": "GB/s", "frac": dom["frac"], "traffic": measured_traffic(dom["name"]),
             "avg_launch_us": dom["avg_launch_us"], "bytes_per_launch": dom["bytes_per_launch"],
             "timing": "HIP events around one replay of a graph of 20 x 28 launches on the replay stream",
-            "note": "the per-layer decode kernel with the longest average launch; all four in per_layer_kernels"}
+            "note": "the per-layer decode kernel with the longest average launch; all five in per_layer_kernels"}
 
     # ---- CPU baseline: the oracle on this host, bounded sample at the benchmark's context
     cpu, parity = None, None

@@ -90,9 +90,10 @@ public:
     // layer cost more than the four kernel boundaries of the per-operator path;
     // EDGE_FM_DECODE_STACK=1 / 0 overrides the config, read once when the engine is built).
     bool decode_stack() const;
-    // One launch for the input norm + QKV + attention partials of each decode layer
-    // (runtime.decode_fused_qkv_attention, default on; EDGE_FM_DECODE_FUSED_QKV_ATTENTION
-    // = 1 / 0 overrides the config).
+    // Whether the one-launch input norm + QKV + attention partials impl
+    // (hip_gfx950_decode_fused_qkv_attention) may run when an operator-table record
+    // selects it (runtime.decode_fused_qkv_attention, default on;
+    // EDGE_FM_DECODE_FUSED_QKV_ATTENTION = 1 / 0 overrides the config).
     bool decode_fused_qkv_attention() const;
     std::string operator_table_path() const;
     std::string prefill_model_path() const;

@@ -61,16 +61,18 @@ OperatorImplRecord OperatorImplRecord::from_json(const Json& j) {
 }
 
 // The records used when the engine config names no table file (the role of the
-// reference's engine_default table): each op kind resolves to this library's impls, and at stage "decode" the
-// attention of a layer is the fused norm + QKV + attention launch whose split partials
-// merge in the o_proj prologue (impls that do not support a shape fall back to the
-// registry default, attention.cu:257-273).
+// reference's engine_default table): each op kind resolves to this library's impls, and at
+// stage "decode" the attention of a layer is the split attention whose partials merge in
+// the o_proj prologue (impls that do not support a shape fall back to the registry
+// default, attention.cu:257-273). The one-launch norm + QKV + attention impl is selected
+// by a table record: on MI355X its in-kernel hand-off of the query across XCDs costs
+// more than the kernel boundary it saves.
 static std::vector<OperatorImplRecord> builtin_records() {
     std::vector<OperatorImplRecord> out;
     const char* recs[][4] = {{"linear", "", "", "hip_gfx950_linear"},
                              {"linear", "attention_output", "decode", "hip_gfx950_decode_merge_o_proj"},
                              {"attention", "", "", "hip_gfx950_attention"},
-                             {"attention", "", "decode", "hip_gfx950_decode_fused_qkv_attention"},
+                             {"attention", "", "decode", "hip_gfx950_decode_split_attention"},
                              {"norm", "", "", "hip_gfx950_norm"},
                              {"activation", "", "", "hip_gfx950_silu_and_mul"},
                              {"fused_gate_up_activation", "", "", "hip_gfx950_swiglu"}};
@@ -295,10 +297,10 @@ public:
 
 }  // namespace
 
-// default preference: fused launch, split partials, generic attention
+// default preference: split partials, fused launch, generic attention
 AttentionOpRegistry::AttentionOpRegistry() {
-    impls_.push_back(std::make_unique<HipDecodeFusedQkvAttentionOp>());
     impls_.push_back(std::make_unique<HipDecodeSplitAttentionOp>());
+    impls_.push_back(std::make_unique<HipDecodeFusedQkvAttentionOp>());
     impls_.push_back(std::make_unique<HipAttentionOp>());
 }
 AttentionOpRegistry& AttentionOpRegistry::instance() {

@@ -342,18 +342,17 @@ def test_compact_vocab_generate_matches_unmapped_run(gpu):
         del eng
 
 
-@pytest.mark.parametrize("table", ["generic", "split", "split_o1_plain"])
+@pytest.mark.parametrize("table", ["generic", "fused", "split_o1_plain"])
 def test_decode_impls_switched_by_table_match_oracle(gpu, table):
     """Operator-table records switch the decode attention impl (all layers) or one layer's
     o_proj; every variant generates the oracle's tokens (teacher-forced, near-tie rule)
     and agrees with the default plan's run at every clear step."""
     import json
 
+    fused = "hip_gfx950_decode_fused_qkv_attention"
     recs = {"generic": [{"op_kind": "attention", "stage": "decode", "impl_id": "hip_gfx950_attention"}],
-            "split": [{"op_kind": "attention", "stage": "decode", "impl_id": "hip_gfx950_decode_split_attention"}],
-            "split_o1_plain": [{"op_kind": "attention", "stage": "decode",
-                                "impl_id": "hip_gfx950_decode_split_attention"},
-                               {"op_kind": "linear", "op_name": "model.layers.1.self_attn.o_proj", "stage": "decode",
+            "fused": [{"op_kind": "attention", "stage": "decode", "impl_id": fused}],
+            "split_o1_plain": [{"op_kind": "linear", "op_name": "model.layers.1.self_attn.o_proj", "stage": "decode",
                                 "impl_id": "hip_gfx950_linear"}]}[table]
     shape = TINY128
     w = O.random_weights(_oracle_cfg(shape), seed=43, std=0.2)
@@ -371,9 +370,10 @@ def test_decode_impls_switched_by_table_match_oracle(gpu, table):
             runs[name] = (eng.generate(req).token_ids(), plan)
             del eng
     plan = runs[table][1]
-    want = {"generic": "hip_gfx950_attention"}.get(table, "hip_gfx950_decode_split_attention")
+    want = {"generic": "hip_gfx950_attention", "fused": fused}.get(
+        table, "hip_gfx950_decode_split_attention")
     assert all(p["attention"] == want for p in plan)
-    assert runs["default"][1][0]["attention"] == "hip_gfx950_decode_fused_qkv_attention"
+    assert all(p["attention"] == "hip_gfx950_decode_split_attention" for p in runs["default"][1])
     if table == "split_o1_plain":
         assert plan[0]["partials_to_o_proj"] and not plan[1]["partials_to_o_proj"]
     orc = O.Qwen2Oracle(_oracle_cfg(shape), O.fuse_weights(_oracle_cfg(shape), w), max_tokens=96)
@@ -386,26 +386,33 @@ def test_decode_impls_switched_by_table_match_oracle(gpu, table):
 
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_front_wait_timeout_raises_device_error_then_recovers(gpu, knob, use_graph):
-    """The fused front half's bounded wait forced to give up from the host
+    """The fused front half (selected by a table record)'s bounded wait forced to give up from the host
     (EFM_KNOB_FRONT_WAIT_TIMEOUT: its attention splits wait for a tag that no word
     carries, 64 polls; every kernel still drains): generate() raises DeviceError and
     returns no tokens. With the knob back at 0 the same engine's next generate() returns
     the tokens of an engine that never failed (after the error the engine drops its
     captured decode graphs, so the graph case captures the next call afresh)."""
+    import json
     import efm_capi as C
 
     shape = TINY128
     w = O.random_weights(_oracle_cfg(shape), seed=44, std=0.2)
     prompt = torch.randint(0, shape.vocab, (40,), generator=torch.Generator().manual_seed(10)).tolist()
     with tempfile.TemporaryDirectory() as tmp:
-        eng, keep = _engine(tmp, shape, w, max_tokens=96, max_new_tokens=16, use_graph=use_graph)
+        table = os.path.join(tmp, "table.json")
+        with open(table, "w") as f:
+            json.dump({"schema": "edgefm_operator_impl_table_v1",
+                       "records": [{"op_kind": "attention", "stage": "decode",
+                                    "impl_id": "hip_gfx950_decode_fused_qkv_attention"}]}, f)
+        cfg = dict(max_tokens=96, max_new_tokens=16, use_graph=use_graph, operator_impl_table_path=table)
+        eng, keep = _engine(tmp, shape, w, **cfg)
         plan = edge_fm.plan_decode(os.path.join(tmp, "engine.json"), 96)
         assert all(p["attention"] == "hip_gfx950_decode_fused_qkv_attention" for p in plan)
         req = edge_fm.Request(0, prompt)
         req.set_ignore_stop_tokens(True)
         clean = eng.generate(req).token_ids()
         del eng
-        eng, keep = _engine(tmp, shape, w, max_tokens=96, max_new_tokens=16, use_graph=use_graph)
+        eng, keep = _engine(tmp, shape, w, **cfg)
         knob(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 1)
         with pytest.raises(edge_fm.DeviceError, match="timed out"):
             eng.generate(req)

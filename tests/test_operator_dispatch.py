@@ -56,20 +56,24 @@ def _plan(tmp_path, shape, records=None, max_kv=96, name="t", **cfg):
 
 
 def test_default_plan_follows_the_shape(tmp_path):
+    # split attention, partials merged in the o_proj prologue
     p = _plan(tmp_path, TEXT128, name="a")
-    assert [l["attention"] for l in p] == [FUSED, FUSED]
+    assert [l["attention"] for l in p] == [SPLIT, SPLIT]
     assert all(l["o_proj"] == MERGE and l["partials_to_o_proj"] and l["gate_up"] == "hip_gfx950_swiglu"
                and l["down"] == LINEAR for l in p)
-    # head_dim 64: no fused launch, split partials merged in o_proj
     assert [l["attention"] for l in _plan(tmp_path, TEXT64, name="b")] == [SPLIT, SPLIT]
-    # M-RoPE rotates before the cache write: no fused launch
     assert [l["attention"] for l in _plan(tmp_path, VL128, name="c")] == [SPLIT, SPLIT]
     # more than 8 splits of 128 rows cannot merge in o_proj: generic attention, plain GEMV o_proj
     p = _plan(tmp_path, TEXT128, max_kv=4096, name="d")
     assert all(l["attention"] == GENERIC and not l["partials_to_o_proj"] for l in p)
-    # the engine config can forbid the fused launch
-    p = _plan(tmp_path, TEXT128, name="e", decode_fused_qkv_attention=False)
+    # a record selects the one-launch impl; the engine config can forbid it
+    fused = [_record(op_kind="attention", stage="decode", impl_id=FUSED)]
+    assert [l["attention"] for l in _plan(tmp_path, TEXT128, fused, name="e")] == [FUSED, FUSED]
+    p = _plan(tmp_path, TEXT128, fused, name="e2", decode_fused_qkv_attention=False)
     assert [l["attention"] for l in p] == [SPLIT, SPLIT]
+    # head_dim 64 and M-RoPE (rotation before the cache write) cannot run it: registry default
+    assert [l["attention"] for l in _plan(tmp_path, TEXT64, fused, name="e3")] == [SPLIT, SPLIT]
+    assert [l["attention"] for l in _plan(tmp_path, VL128, fused, name="e4")] == [SPLIT, SPLIT]
 
 
 def test_shipped_table_resolves_like_the_builtin_records(tmp_path):
@@ -92,12 +96,12 @@ def test_table_record_switches_decode_attention(tmp_path):
     assert all(l["attention"] == SPLIT and l["partials_to_o_proj"] for l in p)
     # a record for another head shape does not apply
     p = _plan(tmp_path, TEXT128, [_record(op_kind="attention", stage="decode",
-                                          shape_sig="num_qo_heads=28|num_kv_heads=4|head_dim=128", impl_id=GENERIC)],
+                                          shape_sig="num_qo_heads=28|num_kv_heads=4|head_dim=128", impl_id=FUSED)],
               name="h")
-    assert [l["attention"] for l in p] == [FUSED, FUSED]
+    assert [l["attention"] for l in p] == [SPLIT, SPLIT]
     # a prefill-stage record does not touch decode
     p = _plan(tmp_path, TEXT128, [_record(op_kind="attention", stage="prefill", impl_id=GENERIC)], name="i")
-    assert [l["attention"] for l in p] == [FUSED, FUSED]
+    assert [l["attention"] for l in p] == [SPLIT, SPLIT]
     # an impl that does not support the shape falls back to the registry default
     p = _plan(tmp_path, TEXT64, [_record(op_kind="attention", stage="decode", impl_id=FUSED)], name="j")
     assert [l["attention"] for l in p] == [SPLIT, SPLIT]
@@ -110,8 +114,9 @@ def test_per_layer_linear_records(tmp_path):
     assert p[0]["o_proj"] == MERGE and p[0]["partials_to_o_proj"]
     assert p[1]["o_proj"] == LINEAR and not p[1]["partials_to_o_proj"], "layer 1 merges in-kernel, plain o_proj"
     # the fused launch needs its partials merged in o_proj
+    fused = _record(op_kind="attention", stage="decode", impl_id=FUSED)
     with pytest.raises(edge_fm.ConfigurationError, match="cannot merge"):
-        _plan(tmp_path, TEXT128, [o1], name="l")
+        _plan(tmp_path, TEXT128, [fused, o1], name="l")
     # shape_sig of the m = 1 down projection selects the same impl explicitly
     down = _record(op_kind="linear", layer_role="mlp_down", stage="decode",
                    shape_sig="m=1|input=2|weight=2|output=2|in_features=512|out_features=256", impl_id=LINEAR)
