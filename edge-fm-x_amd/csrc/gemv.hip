@@ -223,7 +223,16 @@ extern "C" int efm_decode_attention_merge_o_proj(const efm_attention_ctx* ctx, c
     a.group = (int)(ctx->num_qo_heads / ctx->num_kv_heads);
     a.attn_len = d_kv_len;
     a.attn_max_len = max_kv_len;
-    return gemv_launch<PRO_ATTN_MERGE, EPI_BF16>(gemv_pick(q_dim, hidden, 1, 1024, false), a, stream);
+    // Every workgroup merges all split partials before its first dot product: with one
+    // wave per row (K split 1), two rows per wave group halve the workgroups and with
+    // them the repeated merges (C2: 6.10 -> 5.89 us; four rows: 6.69 us).
+    GemvCfg g = gemv_pick(q_dim, hidden, 1, 1024, false);
+    if (g.KS == 1 && g.R == 1) {
+        g.R = 2;
+        g.nrb = (hidden + 4 * g.R - 1) / (4 * g.R);
+        g.grid = std::min(g.nrb, 1024);
+    }
+    return gemv_launch<PRO_ATTN_MERGE, EPI_BF16>(g, a, stream);
 }
 
 extern "C" int efm_decode_norm_lm_head_top1(int32_t hidden, int64_t vocab, float eps, const void* h,
