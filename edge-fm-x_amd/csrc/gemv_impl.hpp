@@ -30,11 +30,18 @@ namespace efm {
 enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ADD_NORM = 2, PRO_ATTN_MERGE = 3 };
 enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_TOP1 = 4, EPI_QKV_TAG = 5 };
 
-// Weight-stream load used by the GEMV main loop (non-temporal: weights are read once
-// per decode step and must not evict the activation working set).
-#ifndef EFM_WEIGHT_LOAD
-#define EFM_WEIGHT_LOAD load_stream16
-#endif
+// Weight-stream load of the GEMV main loop: a non-temporal 16-byte buffer load (weights
+// are read once per decode step and must not evict the activation working set). Offsets
+// at or past the resource's num_records read as zero without a memory access, so tails
+// (rows past N, chunks past K, unused load slots) need no branch: every wave issues the
+// same straight-line loads, and the compiler counts them exactly when it waits for the
+// prologue's loads issued before them.
+__device__ __forceinline__ uint4 gemv_wload(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2 /* nt */);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+constexpr uint32_t kWloadSkip = 0x80000000u;   // past every num_records the GEMV builds
 
 constexpr int kGemvThreads = 256;
 constexpr int kNJMax = 6;
@@ -75,16 +82,130 @@ struct GemvArgs {
 constexpr int kMergeMaxSplits = 8;
 constexpr int kMergeMaxHeads = 64;
 
+constexpr int kPlainPre = 4;   // PLAIN input chunks per thread loaded ahead of the weights
+constexpr int kNormPre = 2;    // NORM / ADD_NORM chunks per thread loaded ahead (K <= 4096)
+
+// The prologue's own loads (input vector, residual, norm weight), issued before the first
+// weight loads of the workgroup: loads return in issue order, so issued after the weight
+// stream they would wait for all of it, and the norm's reduction would start only then.
 template <int PRO>
-__device__ __forceinline__ void gemv_prologue(const GemvArgs& a, bf16_t* xs, float* red, int blk) {
+struct ProLoads {
+    static constexpr int N = (PRO == PRO_PLAIN) ? kPlainPre : (PRO == PRO_ATTN_MERGE ? 0 : kNormPre);
+    uint4 x[N > 0 ? N : 1], r[PRO == PRO_ADD_NORM ? N : 1], w[(PRO == PRO_NORM || PRO == PRO_ADD_NORM) ? N : 1];
+};
+
+// Branch-free like the weight loads (chunks past K read as zero), so that the compiler
+// waits for each of them by its exact position in the wave's load sequence.
+template <int PRO>
+__device__ __forceinline__ void gemv_prologue_load(const GemvArgs& a, ProLoads<PRO>& p) {
+    if constexpr (PRO != PRO_ATTN_MERGE) {
+        const int nbytes = a.K * 2;
+        auto rsrc = [&](const bf16_t* v) {
+            return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(v), (short)0, nbytes, 0x00020000);
+        };
+        auto ld = [&](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+            typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+            return make_uint4(v[0], v[1], v[2], v[3]);
+        };
+        const __amdgpu_buffer_rsrc_t rx = rsrc(a.x);
+#pragma unroll
+        for (int i = 0; i < ProLoads<PRO>::N; ++i) {
+            const uint32_t off = (uint32_t)(threadIdx.x + i * kGemvThreads) * 16u;
+            p.x[i] = ld(rx, off);
+            if constexpr (PRO == PRO_ADD_NORM) p.r[i] = ld(rsrc(a.r_in), off);
+            if constexpr (PRO == PRO_NORM || PRO == PRO_ADD_NORM) p.w[i] = ld(rsrc(a.norm_w), off);
+        }
+    }
+}
+
+template <int PRO>
+__device__ __forceinline__ void gemv_prologue(const GemvArgs& a, const ProLoads<PRO>& pl, bf16_t* xs, float* red,
+                                              int blk) {
     const int C = a.K >> 3;
     const uint4* x4 = reinterpret_cast<const uint4*>(a.x);
     uint4* xs4 = reinterpret_cast<uint4*>(xs);
-    if (PRO == PRO_PLAIN) {
-        for (int c = threadIdx.x; c < C; c += kGemvThreads) xs4[c] = x4[c];
+    if constexpr (PRO == PRO_PLAIN) {
+#pragma unroll
+        for (int i = 0; i < kPlainPre; ++i) {
+            const int c = threadIdx.x + i * kGemvThreads;
+            if (c < C) xs4[c] = pl.x[i];
+        }
+        for (int c = threadIdx.x + kPlainPre * kGemvThreads; c < C; c += kGemvThreads) xs4[c] = x4[c];
         return;
     }
-    if (PRO == PRO_ATTN_MERGE && a.K <= 2 * 4 * kGemvThreads && a.split_cap <= kMergeMaxSplits) {
+    if constexpr (PRO != PRO_ATTN_MERGE) {
+        // Chunks past K hold zeros: they add nothing to the sum of squares. Chunks beyond the
+        // preloaded ones (K > 4096) are loaded here, behind the weights, and read again for
+        // the normalisation instead of being kept in registers.
+        auto pre_sum = [&](int i, float (&v)[8]) {
+            unpack8(pl.x[i], v);
+            if (PRO == PRO_ADD_NORM) {
+                float r[8];
+                unpack8(pl.r[i], r);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] += r[e];
+            }
+        };
+        auto late_sum = [&](int c, float (&v)[8]) {
+            unpack8(reinterpret_cast<const uint4*>(a.x)[c], v);
+            if (PRO == PRO_ADD_NORM) {
+                float r[8];
+                unpack8(reinterpret_cast<const uint4*>(a.r_in)[c], r);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] += r[e];
+            }
+        };
+        float s[kNormPre][8];
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < kNormPre; ++i) {
+            pre_sum(i, s[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(s[i][e], s[i][e], ss);
+        }
+        // the residual stream's new value, once (after every use of the preloaded chunks: a
+        // store in a branch would blur the compiler's count of the loads in flight)
+        const bool store_r = blk == 0 && a.r_out != nullptr;
+        if (store_r) {
+#pragma unroll
+            for (int i = 0; i < kNormPre; ++i) {
+                const int c = threadIdx.x + i * kGemvThreads;
+                if (c < C) reinterpret_cast<uint4*>(a.r_out)[c] = pack8(s[i]);
+            }
+        }
+        for (int c = threadIdx.x + kNormPre * kGemvThreads; c < C; c += kGemvThreads) {
+            float v[8];
+            late_sum(c, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+            if (store_r) reinterpret_cast<uint4*>(a.r_out)[c] = pack8(v);
+        }
+        const float tot = block_sum<kGemvThreads>(ss, red);
+        const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+#pragma unroll
+        for (int i = 0; i < kNormPre; ++i) {
+            const int c = threadIdx.x + i * kGemvThreads;
+            if (c < C) {
+                float w[8], o[8];
+                unpack8(pl.w[i], w);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = (s[i][e] * inv) * w[e];
+                xs4[c] = pack8(o);
+            }
+        }
+        for (int c = threadIdx.x + kNormPre * kGemvThreads; c < C; c += kGemvThreads) {
+            float v[8], w[8], o[8];
+            late_sum(c, v);
+            unpack8(reinterpret_cast<const uint4*>(a.norm_w)[c], w);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (v[e] * inv) * w[e];
+            xs4[c] = pack8(o);
+        }
+        return;
+    }
+    if constexpr (PRO == PRO_ATTN_MERGE) {
+    if (a.K <= 2 * 4 * kGemvThreads && a.split_cap <= kMergeMaxSplits) {
         // Same merge as below with every load issued up front (the cache length, each head's
         // split statistics and this thread's partial outputs for every split slot; slots
         // beyond the live split count get weight 0): one memory round trip instead of two.
@@ -160,7 +281,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, bf16_t* xs, flo
         }
         return;
     }
-    if (PRO == PRO_ATTN_MERGE) {
+    {
         // x[h*hd + d] = bf16( sum_s w[h][s] * o_part[kvh][s][g][d] ),
         // w[h][s] = exp2(m_s - M) / sum_s exp2(m_s - M) l_s  (log-sum-exp merge of the splits)
         __shared__ float sw[kMergeMaxHeads * kMergeMaxSplits];
@@ -209,40 +330,6 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, bf16_t* xs, flo
         }
         return;
     }
-    float s[kProMax][8];
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < kProMax; ++i) {
-        const int c = threadIdx.x + i * kGemvThreads;
-        if (c < C) {
-            uint4 hv = x4[c];
-            unpack8(hv, s[i]);
-            if (PRO == PRO_ADD_NORM) {
-                float r[8];
-                unpack8(reinterpret_cast<const uint4*>(a.r_in)[c], r);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) s[i][e] += r[e];
-            }
-            if (blk == 0 && a.r_out != nullptr) {
-                reinterpret_cast<uint4*>(a.r_out)[c] = (PRO == PRO_ADD_NORM) ? pack8(s[i]) : hv;
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ss = fmaf(s[i][e], s[i][e], ss);
-        }
-    }
-    const float tot = block_sum<kGemvThreads>(ss, red);
-    const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
-    const uint4* w4 = reinterpret_cast<const uint4*>(a.norm_w);
-#pragma unroll
-    for (int i = 0; i < kProMax; ++i) {
-        const int c = threadIdx.x + i * kGemvThreads;
-        if (c < C) {
-            float w[8], o[8];
-            unpack8(w4[c], w);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = (s[i][e] * inv) * w[e];
-            xs4[c] = pack8(o);
-        }
     }
 }
 
@@ -288,31 +375,40 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
     best.v = -INFINITY;
     best.i = 0x7fffffff;
 
+    // Weight loads of row block rb, segment seg: one buffer resource per block and part
+    // (uniform across the workgroup) covering the block's rows below N.
     uint4 wr[R][P][kNJMax];
+    const int grpu = __builtin_amdgcn_readfirstlane(grp);
+    const int kwu = __builtin_amdgcn_readfirstlane(kw);
     auto issue = [&](int rb, int seg) {
+        const int row0 = rb * RB;
+        const int rows = max(0, min(RB, a.N - row0));
+        const int nrec = __builtin_amdgcn_readfirstlane(rows * a.K * 2);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int n = rb * RB + grp * R + r;
+        for (int p = 0; p < P; ++p) {
+            const bf16_t* base = a.W + (size_t)phys_row<EPI>(row0, p, a.N) * (size_t)a.K;
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, nrec, 0x00020000);
 #pragma unroll
-            for (int p = 0; p < P; ++p) {
-                const bf16_t* row = a.W + (size_t)phys_row<EPI>(n, p, a.N) * (size_t)a.K;
+            for (int r = 0; r < R; ++r) {
+                const uint32_t roff = (uint32_t)((grpu * R + r) * a.K) * 2u;
 #pragma unroll
                 for (int j = 0; j < kNJMax; ++j) {
-                    const int c = seg * segC + kw * kWave + lane + j * kWave * KS;
-                    if (j < nj && n < a.N && c < C) {
-                        wr[r][p][j] = EFM_WEIGHT_LOAD(row + (size_t)c * 8);
-                    } else {
-                        wr[r][p][j] = make_uint4(0u, 0u, 0u, 0u);
-                    }
+                    const int c = seg * segC + kwu * kWave + lane + j * kWave * KS;
+                    const uint32_t off = (j < nj && c < C) ? roff + (uint32_t)c * 16u : kWloadSkip;
+                    wr[r][p][j] = gemv_wload(rs, off);
                 }
             }
         }
     };
 
     const uint32_t tag = (EPI == EPI_QKV_TAG) ? launch_tag(a.epoch) : 0u;
+    ProLoads<PRO> pl;
+    gemv_prologue_load<PRO>(a, pl);
     int rb = blk;
-    if (rb < nrb) issue(rb, 0);
-    gemv_prologue<PRO>(a, xs, red, blk);
+    issue(rb, 0);   // unconditional (a block past the end reads zeros): see gemv_wload
+    __builtin_amdgcn_sched_barrier(0);   // every load goes out before the prologue's first wait
+    gemv_prologue<PRO>(a, pl, xs, red, blk);
     __syncthreads();
     const uint4* xs4 = reinterpret_cast<const uint4*>(xs);
 
