@@ -91,13 +91,56 @@ constexpr int kNormPre = 2;    // NORM / ADD_NORM chunks per thread loaded ahead
 template <int PRO>
 struct ProLoads {
     static constexpr int N = (PRO == PRO_PLAIN) ? kPlainPre : (PRO == PRO_ATTN_MERGE ? 0 : kNormPre);
+    static constexpr int MS = (PRO == PRO_ATTN_MERGE) ? kMergeMaxSplits : 1;
     uint4 x[N > 0 ? N : 1], r[PRO == PRO_ADD_NORM ? N : 1], w[(PRO == PRO_NORM || PRO == PRO_ADD_NORM) ? N : 1];
+    float2 ml[MS];      // ATTN_MERGE: this thread's head's split statistics (m, l)
+    float4 op[2][MS];   // ATTN_MERGE: this thread's 2 x 4 output elements of every split
 };
+
+// The one-round-trip attention merge (prologue of merge + o_proj) covers these shapes.
+__device__ __forceinline__ bool merge_fast(const GemvArgs& a) {
+    return a.K <= 2 * 4 * kGemvThreads && a.split_cap <= kMergeMaxSplits;
+}
 
 // Branch-free like the weight loads (chunks past K read as zero), so that the compiler
 // waits for each of them by its exact position in the wave's load sequence.
 template <int PRO>
 __device__ __forceinline__ void gemv_prologue_load(const GemvArgs& a, ProLoads<PRO>& p) {
+    if constexpr (PRO == PRO_ATTN_MERGE) {
+        // every split slot of this thread's elements (slots past split_cap, threads past
+        // the heads / elements and shapes outside merge_fast read zeros)
+        typedef float f32x2_t __attribute__((ext_vector_type(2)));
+        typedef float f32x4_t __attribute__((ext_vector_type(4)));
+        const bool fast = merge_fast(a);
+        const int hd = a.head_dim, G = a.group, cap = a.split_cap;
+        const int Hq = a.K / hd, Hkv = Hq / G;
+        const int ml_bytes = fast ? Hkv * cap * G * 8 : 0, op_bytes = fast ? Hkv * cap * G * hd * 4 : 0;
+        const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.ml_part), (short)0, __builtin_amdgcn_readfirstlane(ml_bytes), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rop = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.o_part), (short)0, __builtin_amdgcn_readfirstlane(op_bytes), 0x00020000);
+        {
+            const int h = threadIdx.x;
+#pragma unroll
+            for (int j = 0; j < kMergeMaxSplits; ++j) {
+                const uint32_t off = (h < Hq && j < cap) ? (uint32_t)((((h / G) * cap + j) * G + (h % G)) * 8) : kWloadSkip;
+                const f32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rml, off, 0, 0);
+                p.ml[j] = make_float2(v[0], v[1]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int c = threadIdx.x + q * kGemvThreads;
+            const int n0 = c * 4, h = n0 / hd, d0 = n0 % hd;
+            const uint32_t base = (uint32_t)((((h / G) * cap * G + (h % G)) * hd + d0) * 4);
+#pragma unroll
+            for (int j = 0; j < kMergeMaxSplits; ++j) {
+                const uint32_t off = (c < (a.K >> 2) && j < cap) ? base + (uint32_t)(j * G * hd * 4) : kWloadSkip;
+                const f32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rop, off, 0, 0);
+                p.op[q][j] = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
+    }
     if constexpr (PRO != PRO_ATTN_MERGE) {
         const int nbytes = a.K * 2;
         auto rsrc = [&](const bf16_t* v) {
@@ -205,36 +248,17 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, const ProLoads<
         return;
     }
     if constexpr (PRO == PRO_ATTN_MERGE) {
-    if (a.K <= 2 * 4 * kGemvThreads && a.split_cap <= kMergeMaxSplits) {
-        // Same merge as below with every load issued up front (the cache length, each head's
-        // split statistics and this thread's partial outputs for every split slot; slots
-        // beyond the live split count get weight 0): one memory round trip instead of two.
+    if (merge_fast(a)) {
+        // Same merge as below with every load issued up front, ahead of the weight stream
+        // (gemv_prologue_load: each head's split statistics and this thread's partial
+        // outputs for every split slot; slots beyond the live split count get weight 0):
+        // one memory round trip, under the weights' instead of after them.
         __shared__ float swf[kMergeMaxHeads * kMergeMaxSplits];
-        const int hd = a.head_dim, G = a.group, cap = a.split_cap;
+        const int hd = a.head_dim;
         const int Hq = a.K / hd;
         const uint32_t L = min(a.attn_len[0], a.attn_max_len);
-        float2 ml[kMergeMaxSplits];
-        if ((int)threadIdx.x < Hq) {
-            const int h = threadIdx.x;
-#pragma unroll
-            for (int j = 0; j < kMergeMaxSplits; ++j) {
-                const size_t idx = ((size_t)(h / G) * cap + j) * G + (h % G);
-                ml[j] = (j < cap) ? *reinterpret_cast<const float2*>(a.ml_part + idx * 2) : make_float2(0.f, 0.f);
-            }
-        }
-        float4 op[2][kMergeMaxSplits];
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int c = threadIdx.x + q * kGemvThreads;
-            if (c < (a.K >> 2)) {
-                const int n0 = c * 4, h = n0 / hd, d0 = n0 % hd;
-                const float* base = a.o_part + ((size_t)(h / G) * cap * G + (h % G)) * hd + d0;
-#pragma unroll
-                for (int j = 0; j < kMergeMaxSplits; ++j)
-                    op[q][j] = (j < cap) ? *reinterpret_cast<const float4*>(base + (size_t)j * G * hd)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-        }
+        const float2 (&ml)[kMergeMaxSplits] = pl.ml;
+        const float4 (&op)[2][kMergeMaxSplits] = pl.op;
         const int kps = a.keys_per_split;
         const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
         if ((int)threadIdx.x < Hq) {
