@@ -136,7 +136,7 @@ extern "C" int efm_decode_norm_qkv_attention(const efm_attention_ctx* ctx, int32
     // GEMV workgroup publishes words
     const int cap = decode_split_cap(Hkv, max_kv_len);
     const int n_attn = Hkv * cap;
-    const GemvCfg g = gemv_pick_config(hidden, N, 1, 1024, false);
+    const GemvCfg g = gemv_pick_config(hidden, N, 1, 1024, false, true);
     if (g.R != 1 || g.KS > 2)
         return set_error(EFM_ERR_UNSUPPORTED, "decode_norm_qkv_attention: GEMV shape R=%d KS=%d", g.R, g.KS);
     const int n_gemv = std::max(1, std::min(g.nrb, 2 * num_cus() - n_attn));

@@ -19,12 +19,17 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a, int nj, 
 // ----------------------------------------------------------------------------------
 namespace efm {
 
-// Launch geometry for K inputs and N logical rows (P physical rows each), chosen from
-// a sweep on MI355X: one row per wave (R = 1) except for very tall matrices (the LM
-// head, R = 4); the K split KS keeps each lane at <= 6 16-byte chunks per row;
-// about 4 workgroups per CU (2 for the top-1 reduction) walking row blocks grid-stride
-// amortise the per-workgroup prologue (the RMSNorm of the input vector).
-static GemvCfg gemv_pick(int K, int N, int P, int max_grid, bool tall) {
+// Launch geometry for K inputs and N logical rows (P physical rows each), from a sweep of
+// the Qwen2.5 1.5B and 7B decode shapes on MI355X (graph replays over 28 weight copies):
+//  * the K split KS keeps each lane at <= 6 16-byte chunks per row and segment;
+//  * rows per wave group R: 4 for very tall matrices (the LM head), 2 with one wave per
+//    single row (1.5B q/k/v 4.52 -> 3.97 us), else 1 (single_row: always 1);
+//  * grid: 768 workgroups for single rows split over 2 or 4 waves (7B q/k/v 8.92 -> 8.27,
+//    o_proj 6.72 -> 6.27, down 24.15 -> 23.67; 1.5B down 7.39 -> 7.01 us); paired up /
+//    gate rows: 512 with one wave per row pair (1.5B 10.84 -> 10.43 us), 4096 with two (7B
+//    41.95 -> 41.04 us); otherwise the caller's cap (about 4 workgroups per CU, 2 for the
+//    top-1 reduction). Workgroups walk row blocks grid-stride.
+static GemvCfg gemv_pick(int K, int N, int P, int max_grid, bool tall, bool single_row = false) {
     GemvCfg g;
     const int C = K / 8;
     g.KS = (C <= 256) ? 1 : (C <= 512 ? 2 : 4);
@@ -35,18 +40,19 @@ static GemvCfg gemv_pick(int K, int N, int P, int max_grid, bool tall) {
     const int groups = 4 / g.KS;
     g.R = 1;
     if (tall && (int64_t)N >= 65536) g.R = 4;
-    else if (P == 1 && g.KS == 4 && (int64_t)N * K >= (64 << 20)) g.R = 2;  // very large K x N (7B down)
-    // two-wave K split (7B q/o rows): six workgroups per CU measured 4-7 % faster
-    if (P == 1 && g.KS == 2 && !tall) max_grid = std::max(max_grid, 1536);
-    // four-wave K split, one row per workgroup (1.5B down_proj: 1536 rows): one row block
-    // per workgroup measured 0.6 % faster per decode step than four workgroups per CU
-    if (P == 1 && g.KS == 4 && g.R == 1 && !tall) max_grid = std::max(max_grid, 2048);
+    else if (!tall && !single_row && P == 1 && g.KS == 1) g.R = 2;
+    if (!tall) {
+        if (P == 1 && g.KS >= 2) max_grid = 768;
+        else if (P == 2) max_grid = (g.KS == 1) ? 512 : 4096;
+    }
     g.nrb = (N + groups * g.R - 1) / (groups * g.R);
     g.grid = std::min(g.nrb, max_grid);
     return g;
 }
 
-GemvCfg gemv_pick_config(int K, int N, int P, int max_grid, bool tall) { return gemv_pick(K, N, P, max_grid, tall); }
+GemvCfg gemv_pick_config(int K, int N, int P, int max_grid, bool tall, bool single_row) {
+    return gemv_pick(K, N, P, max_grid, tall, single_row);
+}
 
 template <int PRO, int EPI>
 static int gemv_launch(const GemvCfg& g, const GemvArgs& a, hipStream_t stream) {
@@ -223,15 +229,9 @@ extern "C" int efm_decode_attention_merge_o_proj(const efm_attention_ctx* ctx, c
     a.group = (int)(ctx->num_qo_heads / ctx->num_kv_heads);
     a.attn_len = d_kv_len;
     a.attn_max_len = max_kv_len;
-    // Every workgroup merges all split partials before its first dot product: with one
-    // wave per row (K split 1), two rows per wave group halve the workgroups and with
-    // them the repeated merges (C2: 6.10 -> 5.89 us; four rows: 6.69 us).
-    GemvCfg g = gemv_pick(q_dim, hidden, 1, 1024, false);
-    if (g.KS == 1 && g.R == 1) {
-        g.R = 2;
-        g.nrb = (hidden + 4 * g.R - 1) / (4 * g.R);
-        g.grid = std::min(g.nrb, 1024);
-    }
+    // every workgroup repeats the split merge: two rows per wave group (gemv_pick's choice
+    // with one wave per row) halve the workgroups and the repeats
+    const GemvCfg g = gemv_pick(q_dim, hidden, 1, 1024, false);
     return gemv_launch<PRO_ATTN_MERGE, EPI_BF16>(g, a, stream);
 }
 

@@ -566,6 +566,6 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
 struct GemvCfg {
     int R, KS, nj, nseg, grid, nrb;
 };
-GemvCfg gemv_pick_config(int K, int N, int P, int max_grid, bool tall);
+GemvCfg gemv_pick_config(int K, int N, int P, int max_grid, bool tall, bool single_row);
 
 }  // namespace efm
