@@ -349,10 +349,15 @@ __global__ __launch_bounds__(kAttnThreads, ROTK ? 1 : 2) void decode_attn_kernel
     }
 }
 
-// LDS-staged kernel (head_dim 128, rotated cache); body in decode_attn_impl.hpp.
+// LDS-staged kernels (head_dim 128, rotated cache); bodies in decode_attn_impl.hpp.
 template <int G, bool MERGE>
 __global__ __launch_bounds__(kAttnThreads, 2) void decode_attn_lds_kernel(DecodeArgs a) {
     decode_attn_lds_body<G, MERGE, false>(a, blockIdx.x, blockIdx.y, FusedAttnArgs{});
+}
+
+template <int G, bool MERGE>
+__global__ __launch_bounds__(kWideThreads, 1) void decode_attn_wide_kernel(DecodeArgs a) {
+    decode_attn_wide_body<G, MERGE>(a, blockIdx.x, blockIdx.y);
 }
 
 // Split merge of efm_attention_decode: one workgroup per query head, 256 threads =
@@ -450,18 +455,38 @@ __global__ __launch_bounds__(kAttnThreads) void decode_merge_kernel(DecodeArgs a
 }
 
 // Split geometry: 128 keys (one 32-key tile per wave, one LDS round) per workgroup, so
-// that every K/V load of a workgroup is in flight at once, until the grid reaches 512
-// workgroups (two per CU); past that the keys per split grow in whole 128-key rounds (a
-// partial round leaves waves idle: at 16k keys and 4 KV heads, 256 keys per split
-// measured 11.8 us against 12.6 us for 160). Split b covers keys [b * kps, (b + 1) * kps)
-// whatever the current length, so its first loads need not wait for *d_kv_len.
+// that every K/V load of a workgroup is in flight at once, while the grid stays within
+// 512 workgroups (two per CU). Longer contexts take splits of up to kWideMaxTiles tiles
+// for the 8-wave kernel, one workgroup per CU (kChipCUs on MI355X) and every tile in
+// flight at once: at 16k keys and 4 KV heads, 58 splits of 288 keys instead of 65 of 256
+// loaded in two serial 128-key rounds. Past that, splits grow in whole 128-key rounds.
+// Split b covers keys [b * kps, (b + 1) * kps) whatever the current length, so its first
+// loads need not wait for *d_kv_len. Every launch that shares split partials (attention,
+// merge, merge + o_proj, the fused front half) takes its plan from here.
 constexpr int kKeysPerSplit = 128;
+constexpr int kChipCUs = 256;
 
 int decode_keys_per_split(int num_kv_heads, uint32_t max_kv_len) {
     const uint32_t bound = std::max<uint32_t>(max_kv_len, 1u);
-    const uint32_t by_chip = (uint32_t)std::max(1, kMaxSplits / std::max(1, num_kv_heads));
+    const uint32_t heads = (uint32_t)std::max(1, num_kv_heads);
+    const uint32_t by_chip = std::max<uint32_t>(1u, (uint32_t)kMaxSplits / heads);
+    if ((bound + kKeysPerSplit - 1) / kKeysPerSplit <= by_chip) return kKeysPerSplit;
+    const uint32_t per_cu = std::max<uint32_t>(1u, (uint32_t)kChipCUs / heads);
+    const uint32_t wide = kTileKeys * ((bound + kTileKeys * per_cu - 1) / (kTileKeys * per_cu));
+    if (wide <= (uint32_t)(kWideMaxTiles * kTileKeys)) return (int)wide;
     const uint32_t rounds = (bound + kKeysPerSplit * by_chip - 1) / (kKeysPerSplit * by_chip);
-    return (int)(std::max<uint32_t>(1u, rounds) * kKeysPerSplit);
+    return (int)(rounds * kKeysPerSplit);
+}
+
+// The LDS-staged kernels load K / V rows with buffer loads: 32-bit byte offsets from the
+// head's first row.
+static bool decode_lds_offsets_fit(const DecodeArgs& a) {
+    return (int64_t)a.row_bound * a.k_sn * 2 < 0x7fffffffLL && (int64_t)a.row_bound * a.v_sn * 2 < 0x7fffffffLL;
+}
+
+// The 8-wave kernel takes splits of 5 to kWideMaxTiles tiles.
+static bool decode_wide_fits(const DecodeArgs& a) {
+    return a.keys_per_split > kKeysPerSplit && a.keys_per_split <= kWideMaxTiles * kTileKeys;
 }
 
 int decode_split_cap(int num_kv_heads, uint32_t max_kv_len) {
@@ -571,10 +596,14 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
     dim3 grid(a.split_cap, ctx->num_kv_heads), block(kAttnThreads);
     // one split: that workgroup writes the output; more: partials, then the merge kernel
     const bool direct = merge && a.split_cap == 1;
-    if (hd == 128 && !rotk && kernel_knob(EFM_KNOB_DECODE_REGISTER) == 0) {
+    if (hd == 128 && !rotk && decode_lds_offsets_fit(a) && kernel_knob(EFM_KNOB_DECODE_REGISTER) == 0) {
+        const bool wide = decode_wide_fits(a);
+        const dim3 wblock(kWideThreads);
 #define EFM_DEC_LDS_CASE(GV)                                                                                   \
         if (G == GV) {                                                                                         \
-            if (direct) hipLaunchKernelGGL((decode_attn_lds_kernel<GV, true>), grid, block, 0, stream, a);     \
+            if (wide && direct) hipLaunchKernelGGL((decode_attn_wide_kernel<GV, true>), grid, wblock, 0, stream, a); \
+            else if (wide) hipLaunchKernelGGL((decode_attn_wide_kernel<GV, false>), grid, wblock, 0, stream, a);  \
+            else if (direct) hipLaunchKernelGGL((decode_attn_lds_kernel<GV, true>), grid, block, 0, stream, a); \
             else hipLaunchKernelGGL((decode_attn_lds_kernel<GV, false>), grid, block, 0, stream, a);           \
             if (merge && !direct)                                                                              \
                 hipLaunchKernelGGL((decode_merge_kernel<128>), dim3(ctx->num_qo_heads), block, 0, stream, a, G); \

@@ -66,6 +66,7 @@ struct FusedAttnArgs {
 };
 
 constexpr uint32_t kFusedSpin = 1u << 20;
+constexpr uint32_t kWloadSkipAttn = 0x80000000u;   // past every buffer resource the attention builds
 constexpr uint32_t kFusedTestSpin = 64u;   // spin limit of the forced time-out (test hook)
 
 // Polls words addr(k) for every k set in `pending` until each carries `tag`; every round
@@ -103,6 +104,24 @@ __device__ __forceinline__ void fused_attn_done(const FusedAttnArgs& f) {
         __hip_atomic_store(f.sync + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         (void)__hip_atomic_fetch_add(f.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+// Context length for the decode kernels, read through the scalar cache after the first
+// tile loads have gone out: a plain load there would be a vector load (the tile loads may
+// write memory, as far as the compiler knows), and its wait would cover every tile.
+__device__ __forceinline__ uint32_t decode_len(const DecodeArgs& a) {
+    if (a.d_kv_len == nullptr) return a.kv_len;
+    uint32_t v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(a.d_kv_len) : "memory");
+    return min(v, a.max_kv_len);
+}
+
+// Workgroup barrier for LDS data only: __syncthreads() also waits for every outstanding
+// global load (its fence counts the K / V tiles still streaming into LDS).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 // LDS-staged variant for head_dim 128 with a rotated cache (ROTK = false): each round
@@ -148,27 +167,41 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
     if (!FUSED && tid < G * (HD / 8))
         qld = *reinterpret_cast<const uint4*>(a.q + (size_t)(kvh * G + tid / (HD / 8)) * a.q_sh + (tid % (HD / 8)) * 8);
     const int lim = min(a.row_bound, start + kps) - 1;   // last row this split may read
+    // uniform copies read before the first tile loads: read after them, a kernel argument
+    // or the length would come through a vector load that waits for every tile load
+    const int k_sn = __builtin_amdgcn_readfirstlane(a.k_sn), v_sn = __builtin_amdgcn_readfirstlane(a.v_sn);
+    // Tile loads are buffer loads straight into LDS (byte offsets below 2 GB: host-checked),
+    // which the compiler counts exactly, so the prologue's waits for its own loads (issued
+    // first) do not wait for the tiles.
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t*>(kbase), (short)0, __builtin_amdgcn_readfirstlane(a.row_bound * k_sn * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t*>(vbase), (short)0, __builtin_amdgcn_readfirstlane(a.row_bound * v_sn * 2), 0x00020000);
+    const int wu = __builtin_amdgcn_readfirstlane(wave);
     auto issue = [&](int r) {
         const int k0 = start + r * RK;
         const int pr = lane >> 4, pc = lane & 15;
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
-            const int q = wave + i * kAttnWaves;               // wave-load index: K 0..31, V 32..63
-            const bool isv = q >= TILE / 1024;
-            const int row = (q % (TILE / 1024)) * 4 + pr;
+            const int q = wu + i * kAttnWaves;                 // wave-load index: K 0..31, V 32..63
+            constexpr int HL = TILE / 1024 / kAttnWaves;          // loads per wave per operand
+            const bool isv = i >= HL;                              // = q >= TILE / 1024 (wu < 4)
+            const int row = (wu + (i % HL) * kAttnWaves) * 4 + pr;
             const int c = isv ? (pc ^ ((row & 3) << 2)) : (pc ^ (row & 15));
             const int j = min(k0 + row, lim);
-            const bf16_t* src = (isv ? vbase + (size_t)j * a.v_sn : kbase + (size_t)j * a.k_sn) + c * 8;
-            __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                             (__attribute__((address_space(3))) void*)(smem + q * 1024), 16, 0, 0);
+            const uint32_t off = (uint32_t)(j * (isv ? v_sn : k_sn) + c * 8) * 2u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(isv ? rv : rk,
+                                                     (__attribute__((address_space(3))) void*)(smem + q * 1024), 16,
+                                                     off, 0, 0, 0);
         }
     };
-    issue(0);
     const float freq = (a.rope_q && tid < 2 * HALF) ? a.rope.inv_freq[tid % HALF] : 0.f;
+    const int q_pos_off = __builtin_amdgcn_readfirstlane(a.q_pos_off);
+    const int k_pos_off = __builtin_amdgcn_readfirstlane(a.k_pos_off);
+    issue(0);
 
     // ---- 2. the context length and this split's key range [start, end)
-    uint32_t L = a.kv_len;
-    if (a.d_kv_len != nullptr) L = min(a.d_kv_len[0], a.max_kv_len);
+    const uint32_t L = decode_len(a);
     const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
     if (b >= nsplit) {
         attn_pipe::vm_wait<0>();   // no LDS write may outlive the workgroup
@@ -180,13 +213,13 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
 
     // ---- 3. RoPE at the query position and at the newest key's position
     if (a.rope_q && tid < 2 * HALF) {
-        const int pos = (int)L - 1 + (tid < HALF ? a.q_pos_off : a.k_pos_off);
+        const int pos = (int)L - 1 + (tid < HALF ? q_pos_off : k_pos_off);
         float sn, cs;
         sincos_reduced((float)pos * freq, &sn, &cs);
         cs_qk[tid / HALF][tid % HALF] = make_float2(cs, sn);
     }
     if (!FUSED && tid < G * (HD / 8)) *reinterpret_cast<uint4*>(&qs[tid * 8]) = qld;
-    __syncthreads();
+    lds_barrier();
     // FUSED: wait for this step's query words (and, in the split that owns row L - 1,
     // the newest K / V row: thread t < 128 takes K[t], t >= 128 takes V[t - 128])
     const bool owner = FUSED && L > 0 && (int)L - 1 >= start && (int)L - 1 < end;
@@ -207,7 +240,7 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
         for (int k = 0; k < NQW; ++k)
             if (tid + k * kAttnThreads < G * HD) qs[tid + k * kAttnThreads] = (bf16_t)(w[k] & 0xffffu);
         newest = w[NQW] & 0xffffu;
-        __syncthreads();
+        lds_barrier();
     }
     // rotate (pairs d, d + 64 at the query position) and scale by log2(e) / sqrt(hd), one
     // element per thread and step (independent LDS reads, no serial chain), then every
@@ -230,7 +263,7 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
     bf16x8_t qf[KS];
     {
         const bool qv = ql < G;
@@ -452,6 +485,328 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
     // FUSED: counted in only now (the returning atomic stays off the critical path); every
     // word this workgroup needed arrived long before
     if (FUSED && tid == 0) fused_attn_done(f);
+}
+
+// Wide variant for long contexts (head_dim 128, rotated cache, unfused launches): one
+// 8-wave workgroup per CU holds every 32-key tile of its split in LDS (up to
+// kWideMaxTiles: 288 keys, 144 KB), all requested at the start; wave w computes the tiles
+// w and w + 8. Eight waves per CU keep more K/V loads in flight than the 4-wave kernel's
+// two workgroups, whose 256-key splits at 16k keys had to load their second 128-key
+// round after the first. The loads are buffer loads straight into LDS: a wave's
+// missing second tile reads past the resource (no memory access) into a shared sink, so
+// every wave issues the same number of loads and the compiler waits for the query,
+// length and RoPE loads issued before them without waiting for the tiles.
+constexpr int kWideWaves = 8;
+constexpr int kWideThreads = kWideWaves * kWave;
+constexpr int kWideMaxTiles = 9;
+constexpr int kWideTileBytes = 2 * kTileKeys * attn_pipe::kRow;   // K and V of one tile
+
+__device__ __forceinline__ void wide_lds_load(__amdgpu_buffer_rsrc_t rs, uint32_t lds_addr, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(uintptr_t)lds_addr, 16, off,
+                                             0, 0, 0);
+}
+
+template <int G, bool MERGE>
+__device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b, int kvh) {
+    constexpr int HD = 128, HALF = 64, KS = 8, DT = 4, W = kWideWaves, NT = kWideThreads;
+    constexpr int KB = kTileKeys * attn_pipe::kRow;            // bytes of K (or V) of a tile
+    constexpr int LPT = 2 * KB / 1024;                         // 1 KB wave loads per tile
+    static_assert((W * G * HD + 2 * W * 32 + W * G + 2 * G) * 4 <= kWideMaxTiles * kWideTileBytes,
+                  "merge buffers must fit the tiles");
+    __shared__ __align__(1024) unsigned char smem[kWideMaxTiles * kWideTileBytes];   // tiles; then the merge
+    __shared__ __align__(1024) unsigned char sink[1024];      // destination of the skipped loads
+    __shared__ float2 cs_qk[2][HALF];
+    __shared__ __align__(16) bf16_t qs[G * HD];
+    __shared__ __align__(16) bf16_t qr[G * HD];
+
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave, lane = tid % kWave;
+    const int ql = lane % 32, hh = lane / 32;
+    const int kps = a.keys_per_split;
+    const int start = b * kps;
+    const int ntiles = kps / kTileKeys;                        // <= kWideMaxTiles (host-checked)
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
+
+    // ---- 1. the query and the RoPE frequencies, then every tile of the split (rows below
+    //         the allocation bound; the length is not known yet)
+    uint4 qld = make_uint4(0, 0, 0, 0);
+    if (tid < G * (HD / 8))
+        qld = *reinterpret_cast<const uint4*>(a.q + (size_t)(kvh * G + tid / (HD / 8)) * a.q_sh + (tid % (HD / 8)) * 8);
+    const float freq = (a.rope_q && tid < 2 * HALF) ? a.rope.inv_freq[tid % HALF] : 0.f;
+    const int q_pos_off = __builtin_amdgcn_readfirstlane(a.q_pos_off);
+    const int k_pos_off = __builtin_amdgcn_readfirstlane(a.k_pos_off);
+    {
+        const int lim = min(a.row_bound, start + kps) - 1;   // last row this split may read
+        const int nrec = __builtin_amdgcn_readfirstlane(a.row_bound * a.k_sn * 2);
+        const int nrecv = __builtin_amdgcn_readfirstlane(a.row_bound * a.v_sn * 2);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<bf16_t*>(a.k + (size_t)kvh * a.k_sh), (short)0, nrec, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<bf16_t*>(a.v + (size_t)kvh * a.v_sh), (short)0, nrecv, 0x00020000);
+        const int pr = lane >> 4, pc = lane & 15;
+        const int wu = __builtin_amdgcn_readfirstlane(wave);
+        // A missing tile's loads keep their place in the sequence (masks, not branches: the
+        // compiler counts loads only along straight-line code) but read nothing.
+        const uint32_t smem_a = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
+        const uint32_t sink_a = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)sink);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int t = wu + i * W;
+            const uint32_t live = (uint32_t)__builtin_amdgcn_readfirstlane(t < ntiles ? -1 : 0);   // all ones or 0
+            const uint32_t slot = ((smem_a + (uint32_t)(t * kWideTileBytes)) & live) | (sink_a & ~live);
+            const uint32_t qstep = 1024u & live;
+            const int k0 = start + t * kTileKeys;
+#pragma unroll
+            for (int q = 0; q < LPT; ++q) {
+                const bool isv = q >= KB / 1024;                 // loads 0..7: K rows, 8..15: V rows
+                const int row = (q % (KB / 1024)) * 4 + pr;       // row of the tile
+                const int c = isv ? (pc ^ ((row & 3) << 2)) : (pc ^ (row & 15));
+                const int j = min(k0 + row, lim);
+                const uint32_t off = ((uint32_t)(j * (isv ? a.v_sn : a.k_sn) + c * 8) * 2u & live) | (kWloadSkipAttn & ~live);
+                wide_lds_load(isv ? rv : rk, slot + (uint32_t)q * qstep, off);
+            }
+        }
+    }
+
+    // ---- 2. the context length and this split's key range [start, end)
+    const uint32_t L = decode_len(a);
+    const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
+    if (b >= nsplit) {
+        attn_pipe::vm_wait<0>();   // no LDS write may outlive the workgroup
+        return;
+    }
+    const int end = min((int)L, start + kps);
+
+    // ---- 3. RoPE at the query position and at the newest key's position; the queries
+    //         rotated and scaled by log2(e) / sqrt(hd) into the MFMA operand
+    if (a.rope_q && tid < 2 * HALF) {
+        const int pos = (int)L - 1 + (tid < HALF ? q_pos_off : k_pos_off);
+        float sn, cs;
+        sincos_reduced((float)pos * freq, &sn, &cs);
+        cs_qk[tid / HALF][tid % HALF] = make_float2(cs, sn);
+    }
+    if (tid < G * (HD / 8)) *reinterpret_cast<uint4*>(&qs[tid * 8]) = qld;
+    lds_barrier();
+    {
+        const float qscale = kLog2e / sqrtf((float)HD);
+#pragma unroll
+        for (int k = 0; k < (G * HD + NT - 1) / NT; ++k) {
+            const int i = tid + k * NT;
+            if (i < G * HD) {
+                const int d = i % HD;
+                const float x = bf16_to_f32(qs[i]);
+                float r = x;
+                if (a.rope_q) {
+                    const float y = bf16_to_f32(qs[i ^ HALF]);
+                    const float2 c2 = cs_qk[0][d % HALF];
+                    r = (d < HALF) ? x * c2.x - y * c2.y : x * c2.x + y * c2.y;
+                }
+                qr[i] = (bf16_t)f32_to_bf16(r * qscale);
+            }
+        }
+    }
+    lds_barrier();
+    bf16x8_t qf[KS];
+    {
+        const bool qv = ql < G;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            BfPack pk;
+            pk.u = qv ? *reinterpret_cast<const uint4*>(&qr[ql * HD + ks * 16 + hh * 8]) : make_uint4(0, 0, 0, 0);
+            qf[ks] = pk.v;
+        }
+    }
+    const int fix_row = (a.rope_q && a.fix_last && L > 0) ? (int)L - 1 : -1;
+    const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
+
+    f32x16_t oacc[DT];
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[tt][e] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    typedef short s4_t __attribute__((ext_vector_type(4)));
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int t = wave + i * W;
+        const int t0 = start + t * kTileKeys;
+        if (i == 0) attn_pipe::vm_wait<LPT>();   // tile i = 0 landed (the second may fly)
+        else attn_pipe::vm_wait<0>();
+        asm volatile("" ::: "memory");
+        if (t >= ntiles || t0 >= end) continue;
+        unsigned char* tile = smem + t * kWideTileBytes;
+        const uint32_t sb = lds0 + (uint32_t)(t * kWideTileBytes);
+        if (t0 + kTileKeys > end) {
+            // zero the V rows past the length (P is 0 there, but the rows may hold NaN)
+            for (int x = lane; x < (t0 + kTileKeys - end) * 16; x += kWave) {
+                const int row = end - t0 + x / 16;
+                *reinterpret_cast<uint4*>(tile + KB + row * attn_pipe::kRow + (x % 16) * 16) = make_uint4(0, 0, 0, 0);
+            }
+        }
+        bf16x8_t kf[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) attn_pipe::read_b128<0>(kf[ks], sb + attn_pipe::k_off(ql, ks * 2 + hh));
+        s4_t vf[2][DT][2];
+        auto read_v = [&](auto kbc) {
+            constexpr int kb = decltype(kbc)::value;
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt) {
+                const uint32_t va = sb + (uint32_t)KB + attn_pipe::v_tr_lane_off(lane, tt);
+                attn_pipe::read_tr16<(kb * 16) * attn_pipe::kRow>(vf[kb][tt][0], va);
+                attn_pipe::read_tr16<(kb * 16 + 8) * attn_pipe::kRow>(vf[kb][tt][1], va);
+            }
+        };
+        read_v(std::integral_constant<int, 0>{});
+        asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");   // the K reads (issued first) are done
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kf[ks]));
+        if (t0 + ql == fix_row && fix_row < end) {
+            // the newest key: rotate at its position, use it and store it back rotated
+            bf16_t* kw = const_cast<bf16_t*>(kbase) + (size_t)fix_row * a.k_sn + hh * 8;
+#pragma unroll
+            for (int ks = 0; ks < KS / 2; ++ks) {
+                BfPack u0, u1;
+                u0.v = kf[ks];
+                u1.v = kf[ks + KS / 2];
+                float x0[8], x1[8];
+                unpack8(u0.u, x0);
+                unpack8(u1.u, x1);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float2 c2 = cs_qk[1][ks * 16 + hh * 8 + e];
+                    const float y0 = x0[e] * c2.x - x1[e] * c2.y;
+                    const float y1 = x1[e] * c2.x + x0[e] * c2.y;
+                    x0[e] = y0;
+                    x1[e] = y1;
+                }
+                u0.u = pack8(x0);
+                u1.u = pack8(x1);
+                kf[ks] = u0.v;
+                kf[ks + KS / 2] = u1.v;
+                *reinterpret_cast<uint4*>(kw + ks * 16) = u0.u;
+                *reinterpret_cast<uint4*>(kw + (ks + KS / 2) * 16) = u1.u;
+            }
+        }
+        f32x16_t s = {};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
+        read_v(std::integral_constant<int, 1>{});
+        // element e: key = t0 + (e/4)*8 + hh*4 + e%4, head = ql
+        if (t0 + kTileKeys > end) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int j = t0 + (e / 4) * 8 + hh * 4 + (e % 4);
+                s[e] = (j < end) ? s[e] : -INFINITY;
+            }
+        }
+        float mloc = fmaxf(s[0], s[1]);
+#pragma unroll
+        for (int e = 2; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const float m_new = fmaxf(m_run, mloc);   // finite: the tile holds a valid key
+        float p[16], psum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            p[e] = __builtin_amdgcn_exp2f(s[e] - m_new);
+            psum += p[e];
+        }
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(psum), __float_as_uint(psum), false, false);
+            psum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        if (i == 0) {
+            l_run = psum;
+        } else {
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run = l_run * alpha + psum;
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+        }
+        m_run = m_new;
+        BfPack pb[2];
+        pb[0].u = pack8(&p[0]);
+        pb[1].u = pack8(&p[8]);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt) {
+                if (tt == 0) {
+                    if (kb == 0) asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");
+                    else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                }
+                asm volatile("" : "+v"(vf[kb][tt][0]), "+v"(vf[kb][tt][1]));
+                union {
+                    s4_t h[2];
+                    bf16x8_t v;
+                } vv;
+                vv.h[0] = vf[kb][tt][0];
+                vv.h[1] = vf[kb][tt][1];
+                oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv.v, pb[kb].v, oacc[tt], 0, 0, 0);
+            }
+    }
+
+    // ---- merge the 8 waves through LDS (every tile load has landed: the waits above)
+    __syncthreads();
+    float* om = reinterpret_cast<float*>(smem);                  // [W][32]
+    float* ol = om + W * 32;                                     // [W][32]
+    float* ob = ol + W * 32;                                     // [W][G][HD]
+    float* sw = ob + W * G * HD;                                 // [W][G]
+    float* md = sw + W * G;                                      // [G][2]: M, den
+    if (hh == 0) {
+        om[wave * 32 + ql] = m_run;
+        ol[wave * 32 + ql] = l_run;
+    }
+    if (ql < G) {
+#pragma unroll
+        for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+            for (int eb = 0; eb < 4; ++eb)
+                *reinterpret_cast<float4*>(&ob[(wave * G + ql) * HD + tt * 32 + eb * 8 + hh * 4]) =
+                    make_float4(oacc[tt][eb * 4 + 0], oacc[tt][eb * 4 + 1], oacc[tt][eb * 4 + 2], oacc[tt][eb * 4 + 3]);
+    }
+    __syncthreads();
+    if (tid < G) {
+        const int g = tid;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, om[w * 32 + g]);
+        float den = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float mw = om[w * 32 + g];
+            const float sc = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+            sw[w * G + g] = sc;
+            den = fmaf(sc, ol[w * 32 + g], den);
+        }
+        md[g * 2 + 0] = M;
+        md[g * 2 + 1] = den;
+    }
+    __syncthreads();
+    float* o_part = a.o_part + ((size_t)kvh * a.split_cap + b) * G * HD;
+    float* ml_part = a.ml_part + ((size_t)kvh * a.split_cap + b) * G * 2;
+    constexpr int NO = (G * HD + NT - 1) / NT;
+#pragma unroll
+    for (int k = 0; k < NO; ++k) {
+        const int i = tid + k * NT;
+        if (i >= G * HD) break;
+        const int g = i / HD, d = i % HD;
+        float num = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) num = fmaf(sw[w * G + g], ob[(w * G + g) * HD + d], num);
+        if (MERGE) {
+            const float den = md[g * 2 + 1];
+            a.o[(size_t)(kvh * G + g) * HD + d] = (bf16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
+        } else {
+            o_part[i] = num;
+            if (d == 0) *reinterpret_cast<float2*>(&ml_part[g * 2]) = make_float2(md[g * 2 + 0], md[g * 2 + 1]);
+        }
+    }
 }
 
 }  // namespace efm

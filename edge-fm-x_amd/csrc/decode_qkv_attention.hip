@@ -79,6 +79,8 @@ static int fused_supported(const efm_attention_ctx* ctx, int32_t hidden, uint32_
         return set_error(EFM_ERR_UNSUPPORTED, "decode_norm_qkv_attention: hidden %d (multiple of 8, <= %d)", hidden,
                          kFusedMaxHidden);
     if (max_kv_len == 0) return set_error(EFM_ERR_INVALID_ARGUMENT, "decode_norm_qkv_attention: max_kv_len is 0");
+    if ((int64_t)max_kv_len * kvd * 2 >= 0x7fffffffLL)
+        return set_error(EFM_ERR_UNSUPPORTED, "decode_norm_qkv_attention: K / V caches past 2 GB per layer");
     const int kps = decode_keys_per_split(Hkv, max_kv_len);
     const int n_attn = Hkv * decode_split_cap(Hkv, max_kv_len);
     if (kps != kAttnWaves * kTileKeys || n_attn > kFusedMaxAttn)
