@@ -360,21 +360,24 @@ __global__ __launch_bounds__(kWideThreads, 1) void decode_attn_wide_kernel(Decod
     decode_attn_wide_body<G, MERGE>(a, blockIdx.x, blockIdx.y);
 }
 
-// Split merge of efm_attention_decode: one workgroup per query head, 256 threads =
-// HD/4 float4 columns x NPART split lanes. The partial loads of the first chunk are
-// issued before the (m, l) pairs are reduced into the normalised split weights
+// Split merge of efm_attention_decode: kMergeSlices workgroups per query head (blockIdx.y
+// takes a quarter of the head's columns, so a workgroup reads a quarter of the partials),
+// 256 threads = NCOL float4 columns x NPART split lanes. The partial loads of the first
+// chunk are issued before the (m, l) pairs are reduced into the normalised split weights
 // w_s = exp2(m_s - M) / sum_s exp2(m_s - M) l_s; each lane accumulates its splits in
 // order and the lanes are summed in a fixed order.
+constexpr int kMergeSlices = 4;
+
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void decode_merge_kernel(DecodeArgs a, int G) {
-    constexpr int NCOL = HD / 4;
+    constexpr int NCOL = HD / 4 / kMergeSlices;
     constexpr int NPART = kAttnThreads / NCOL;
-    constexpr int CH = 16;  // loads in flight per thread: up to 128 splits (hd 128) in one round trip
+    constexpr int CH = 128 / NPART;  // loads in flight per thread: up to 128 splits in one round trip
     __shared__ float sw[kMaxSplits];
     __shared__ float4 red[NPART][NCOL];
     const int tid = threadIdx.x;
     const int h = blockIdx.x, kvh = h / G, g = h % G;
-    const int col = tid % NCOL, part = tid / NCOL;
+    const int col = blockIdx.y * NCOL + tid % NCOL, part = tid / NCOL;
     uint32_t L = a.kv_len;
     if (a.d_kv_len != nullptr) L = min(a.d_kv_len[0], a.max_kv_len);
     const int kps = a.keys_per_split;
@@ -435,16 +438,17 @@ __global__ __launch_bounds__(kAttnThreads) void decode_merge_kernel(DecodeArgs a
             }
         }
     }
-    red[part][col] = acc;
+    const int lc = tid % NCOL;
+    red[part][lc] = acc;
     __syncthreads();
     if (part == 0) {
-        float4 t = red[0][col];
+        float4 t = red[0][lc];
 #pragma unroll
         for (int p = 1; p < NPART; ++p) {
-            t.x += red[p][col].x;
-            t.y += red[p][col].y;
-            t.z += red[p][col].z;
-            t.w += red[p][col].w;
+            t.x += red[p][lc].x;
+            t.y += red[p][lc].y;
+            t.z += red[p][lc].z;
+            t.w += red[p][lc].w;
         }
         bf16_t* o = a.o + (size_t)h * HD + col * 4;
         o[0] = (bf16_t)f32_to_bf16(t.x);
@@ -606,7 +610,7 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
             else if (direct) hipLaunchKernelGGL((decode_attn_lds_kernel<GV, true>), grid, block, 0, stream, a); \
             else hipLaunchKernelGGL((decode_attn_lds_kernel<GV, false>), grid, block, 0, stream, a);           \
             if (merge && !direct)                                                                              \
-                hipLaunchKernelGGL((decode_merge_kernel<128>), dim3(ctx->num_qo_heads), block, 0, stream, a, G); \
+                hipLaunchKernelGGL((decode_merge_kernel<128>), dim3(ctx->num_qo_heads, kMergeSlices), block, 0, stream, a, G); \
             return check_launch("attention_decode");                                                           \
         }
         EFM_DEC_LDS_CASE(1) EFM_DEC_LDS_CASE(2) EFM_DEC_LDS_CASE(3) EFM_DEC_LDS_CASE(4)
@@ -620,7 +624,7 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
         else if (rotk) hipLaunchKernelGGL((decode_attn_kernel<HDV, GV, false, true>), grid, block, 0, stream, a);     \
         else hipLaunchKernelGGL((decode_attn_kernel<HDV, GV, false, false>), grid, block, 0, stream, a);              \
         if (merge && !direct)                                                                                  \
-            hipLaunchKernelGGL((decode_merge_kernel<HDV>), dim3(ctx->num_qo_heads), block, 0, stream, a, G);    \
+            hipLaunchKernelGGL((decode_merge_kernel<HDV>), dim3(ctx->num_qo_heads, kMergeSlices), block, 0, stream, a, G);    \
         return check_launch("attention_decode");                                                               \
     }
     EFM_DEC_CASE(128, 1) EFM_DEC_CASE(128, 2) EFM_DEC_CASE(128, 3) EFM_DEC_CASE(128, 4)
