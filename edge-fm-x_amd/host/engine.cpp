@@ -1019,6 +1019,8 @@ void StandardEngine::drop_graphs() {
     for (auto& kv : graphs_) {
         if (kv.second.exec) hipGraphExecDestroy(kv.second.exec);
         if (kv.second.graph) hipGraphDestroy(kv.second.graph);
+        if (kv.second.exec_n) hipGraphExecDestroy(kv.second.exec_n);
+        if (kv.second.graph_n) hipGraphDestroy(kv.second.graph_n);
     }
     graphs_.clear();
 }
@@ -1222,23 +1224,30 @@ Response StandardEngine::generate(const Request& request) {
         RoctxRange decode_range("EDGEFM_GENERATION");
         if (cfg_.use_graph()) {
             GraphEntry& g = graphs_[req.request_id];
-            if (g.exec == nullptr) {
+            // every step reads its position and writes its token through device state, so
+            // n consecutive captures of one step replay as n steps
+            auto capture = [&](int32_t n, hipGraph_t* graph, hipGraphExec_t* exec) {
                 RoctxRange capture_range("EDGEFM_DECODE_PREPARE");
                 hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
                 try {
-                    run_decode_step(req.request_id, nullptr);
+                    for (int32_t i = 0; i < n; ++i) run_decode_step(req.request_id, nullptr);
                 } catch (...) {
                     hipGraph_t tmp = nullptr;
                     hipStreamEndCapture(stream_, &tmp);
                     if (tmp) hipGraphDestroy(tmp);
                     throw;
                 }
-                hip_check(hipStreamEndCapture(stream_, &g.graph), "end capture");
-                hip_check(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0), "graph instantiate");
-            }
+                hip_check(hipStreamEndCapture(stream_, graph), "end capture");
+                hip_check(hipGraphInstantiate(exec, *graph, nullptr, nullptr, 0), "graph instantiate");
+            };
+            if (g.exec == nullptr) capture(1, &g.graph, &g.exec);
+            if (steps >= kGraphSteps && g.exec_n == nullptr) capture(kGraphSteps, &g.graph_n, &g.exec_n);
             decode_prepare_host_ms = host_ms_since(dprep_t0);
             RoctxRange replay_range("EDGEFM_DECODE_GRAPH_REPLAY");
-            for (int32_t i = 0; i < steps; ++i) hip_check(hipGraphLaunch(g.exec, stream_), "graph launch");
+            int32_t done = 0;
+            for (; done + kGraphSteps <= steps; done += kGraphSteps)
+                hip_check(hipGraphLaunch(g.exec_n, stream_), "graph launch");
+            for (; done < steps; ++done) hip_check(hipGraphLaunch(g.exec, stream_), "graph launch");
         } else {
             for (int32_t i = 0; i < steps; ++i) run_decode_step(req.request_id, &stage);
         }

@@ -296,9 +296,14 @@ private:
     Tensor ids_dev_;
     Tensor logits_;
     Tensor sample_ws_;
+    // One decode step, and kGraphSteps consecutive steps in one graph (fewer graph launches:
+    // each costs a few us of command-processor time between the steps it separates).
+    static constexpr int32_t kGraphSteps = 8;
     struct GraphEntry {
         hipGraph_t graph = nullptr;
         hipGraphExec_t exec = nullptr;
+        hipGraph_t graph_n = nullptr;
+        hipGraphExec_t exec_n = nullptr;
     };
     std::map<int32_t, GraphEntry> graphs_;  // per request slot
     void drop_graphs();
