@@ -1136,6 +1136,24 @@ def test_decode_attention_lds_kernel_matches_register_kernel(gpu, knob, hq, hkv,
     the register kernel (EFM_KNOB_DECODE_REGISTER) on the same cache, through both the merged
     entry point and the partials + fused o_proj merge, and store the same rotated newest
     row. Rows past the length hold NaN."""
+    _lds_vs_register(gpu, knob, hq, hkv, kv_len, max_kv)
+
+
+@pytest.mark.parametrize("hq,hkv,kv_len,max_kv", [
+    pytest.param(64, 64, 1057, 1100, id="288keys-partial-last-split"),
+    pytest.param(64, 64, 1, 1100, id="288keys-one-row"),
+    pytest.param(128, 64, 900, 1100, id="288keys-g2"),
+    pytest.param(448, 64, 1100, 1100, id="288keys-g7-full"),
+    pytest.param(256, 256, 257, 300, id="256keys-8-tiles"),
+])
+def test_decode_attention_wide_kernel_matches_register_kernel(gpu, knob, hq, hkv, kv_len, max_kv):
+    """Plans past 512 splits of 128 keys run the 8-wave kernel (splits of 256-288 keys, every
+    tile in LDS; wave 0 takes a ninth tile): same checks as the 4-wave kernel, including a
+    split whose last tiles lie past the length and waves without a tile."""
+    _lds_vs_register(gpu, knob, hq, hkv, kv_len, max_kv)
+
+
+def _lds_vs_register(gpu, knob, hq, hkv, kv_len, max_kv):
     torch.manual_seed(kv_len + hq)
     hd = 128
     q = torch.randn(1, hq * hd, dtype=torch.bfloat16, device=gpu)
