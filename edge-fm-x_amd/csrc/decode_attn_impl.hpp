@@ -490,7 +490,8 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
 // Wide variant for long contexts (head_dim 128, rotated cache, unfused launches): one
 // 8-wave workgroup per CU holds every 32-key tile of its split in LDS (up to
 // kWideMaxTiles: 288 keys, 144 KB), all requested at the start; wave w computes the tiles
-// w and w + 8. Eight waves per CU keep more K/V loads in flight than the 4-wave kernel's
+// w and w + 8 (a split need not be whole tiles: rows past its end read as zeros and are
+// masked). Eight waves per CU keep more K/V loads in flight than the 4-wave kernel's
 // two workgroups, whose 256-key splits at 16k keys had to load their second 128-key
 // round after the first. The loads are buffer loads straight into LDS: a wave's
 // missing second tile reads past the resource (no memory access) into a shared sink, so
@@ -524,7 +525,7 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
     const int ql = lane % 32, hh = lane / 32;
     const int kps = a.keys_per_split;
     const int start = b * kps;
-    const int ntiles = kps / kTileKeys;                        // <= kWideMaxTiles (host-checked)
+    const int ntiles = (kps + kTileKeys - 1) / kTileKeys;      // <= kWideMaxTiles (host-checked)
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
 
     // ---- 1. the query and the RoPE frequencies, then every tile of the split (rows below
@@ -561,8 +562,10 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
                 const bool isv = q >= KB / 1024;                 // loads 0..7: K rows, 8..15: V rows
                 const int row = (q % (KB / 1024)) * 4 + pr;       // row of the tile
                 const int c = isv ? (pc ^ ((row & 3) << 2)) : (pc ^ (row & 15));
-                const int j = min(k0 + row, lim);
-                const uint32_t off = ((uint32_t)(j * (isv ? a.v_sn : a.k_sn) + c * 8) * 2u & live) | (kWloadSkipAttn & ~live);
+                // rows past the split's last readable row read nothing (zeros)
+                const uint32_t rowm = live & (k0 + row <= lim ? ~0u : 0u);
+                const uint32_t off = ((uint32_t)((k0 + row) * (isv ? a.v_sn : a.k_sn) + c * 8) * 2u & rowm) |
+                                     (kWloadSkipAttn & ~rowm);
                 wide_lds_load(isv ? rv : rk, slot + (uint32_t)q * qstep, off);
             }
         }
