@@ -125,8 +125,8 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // LDS-staged variant for head_dim 128 with a rotated cache (ROTK = false): each round
-// stages 128 keys of K and V with global_load_lds (1 KB wave loads: 4 rows x 256 bytes,
-// so every load instruction reads whole 256-byte row pieces), in the layouts of
+// stages 128 keys of K and V with buffer loads straight into LDS (1 KB wave loads: 4 rows x
+// 256 bytes, so every load instruction reads whole 256-byte row pieces), in the layouts of
 // attn_pipe.hpp. Wave w then takes the keys [32 w, 32 w + 32) of the round: the K operand
 // of S^T = K . Q^T comes from ds_read_b128, the V^T operand of O^T = V^T . P^T from
 // ds_read_b64_tr_b16 (no transpose through registers). Rows past the length are masked
