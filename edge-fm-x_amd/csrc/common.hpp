@@ -30,6 +30,23 @@ __device__ __forceinline__ float round_bf16(float f) {
     return bf16_to_f32(f32_to_bf16(f));
 }
 
+// silu(g) = g / (1 + e^-g), the activation's own formula, in about a third of the
+// instructions of expf and an IEEE division: e^-g = 2^(-g log2 e) on v_exp_f32, then
+// q = g * rcp(d) and one residual step q + (g - d q) rcp(d), which rounds like the
+// division. The residual is formed as -(d q - g) so that g = -0 keeps its sign. Where the
+// step is not finite (g = +inf, -inf, NaN, or e^-g overflowing for g < -88.7) q is the
+// quotient: +inf, NaN, NaN, -0, as g / (1 + e^-g) gives. For g in (-88.7, -87.3) the
+// reciprocal is below the normal range and the result, under 1e-36 in magnitude, may
+// differ from the division's. Every SwiGLU epilogue uses this one form, so the decode
+// GEMVs, the prefill GEMMs and the standalone activation agree bit for bit.
+__device__ __forceinline__ float silu_f32(float g) {
+    const float d = 1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+    const float r = __builtin_amdgcn_rcpf(d);
+    const float q = g * r;
+    const float s = __builtin_fmaf(-__builtin_fmaf(d, q, -g), r, q);
+    return __builtin_isfinite(s) ? s : q;
+}
+
 // Low and high bf16 halves of a packed 32-bit word, as fp32.
 __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

@@ -524,7 +524,7 @@ __device__ __forceinline__ void stk_gemv(const StackArgs& a, int j, unsigned cha
                 const int n = 6 * k + i - ge0;
                 const float u = round_bf16(sum_slots(n * m.npH, m.npH));
                 const float g = round_bf16(sum_slots(m.c2 + n * m.npH, m.npH));
-                const float sg = g / (1.0f + expf(-g));
+                const float sg = silu_f32(g);
                 wv[i / 2] |= f32_to_bf16(sg * u) << (16 * (i & 1));
             }
             rec_store(a.rec_mid, k, tag, wv[0], wv[1], wv[2]);

@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kRowThreads) void act_and_mul_kernel(const bf16_t* 
         unpack8(up4[c], u);
         unpack8(gate4[c], g);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = (g[e] / (1.0f + expf(-g[e]))) * u[e];
+        for (int e = 0; e < 8; ++e) o[e] = silu_f32(g[e]) * u[e];
         o4[c] = pack8(o);
     }
 }

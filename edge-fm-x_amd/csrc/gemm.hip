@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_bf16_kernel(const bf16_t* _
                     if (col < N) {
                         const float u = round_bf16(acc[i][j][e]);
                         const float g = round_bf16(acc[i][j + 1][e]);
-                        const float o = (g / (1.0f + expf(-g))) * u;
+                        const float o = silu_f32(g) * u;
                         reinterpret_cast<bf16_t*>(Cout)[(size_t)row * ldc + col] = (bf16_t)f32_to_bf16(o);
                     }
                 }
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_pipe_kernel(const bf16_t* _
                     if (col < N) {
                         const float u = round_bf16(acc[i][j][e]);
                         const float g = round_bf16(acc[i][j + 1][e]);
-                        const float o = (g / (1.0f + expf(-g))) * u;
+                        const float o = silu_f32(g) * u;
                         reinterpret_cast<bf16_t*>(Cout)[(size_t)row * ldc + col] = (bf16_t)f32_to_bf16(o);
                     }
                 }
@@ -646,7 +646,7 @@ __global__ __launch_bounds__(WGM * WGN * kWave, 1) void gemm_wide_kernel(const b
                     if (col < N) {
                         const float u = round_bf16(acc[i][j][e]);
                         const float g = round_bf16(acc[i][j + 1][e]);
-                        const float o = (g / (1.0f + expf(-g))) * u;
+                        const float o = silu_f32(g) * u;
                         reinterpret_cast<bf16_t*>(Cout)[(size_t)row * ldc + col] = (bf16_t)f32_to_bf16(o);
                     }
                 }

@@ -521,7 +521,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
                 } else if (EPI == EPI_SWIGLU) {
                     const float u = round_bf16(acc[r][0]);
                     const float g = round_bf16(acc[r][P - 1]);
-                    const float sg = g / (1.0f + expf(-g));
+                    const float sg = silu_f32(g);
                     reinterpret_cast<bf16_t*>(a.y)[n] = (bf16_t)f32_to_bf16(sg * u);
                 } else if (EPI == EPI_TOP1) {
                     ArgMax c;
