@@ -447,7 +447,12 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
             }
         }
     };
-    const int pre = min(S - 1, ntiles);
+    // With a 4-slot ring the tiles go in pairs: one barrier per two tiles (after this wave's
+    // loads of both have landed), then the next pair is loaded into the slots of the
+    // previous pair, which every wave has finished. Smaller rings keep one barrier per tile,
+    // with S - 1 tiles in flight.
+    constexpr bool PAIR = (S == 4);
+    const int pre = PAIR ? min(2, ntiles) : min(S - 1, ntiles);
     for (int p = 0; p < pre; ++p) issue(p, p);
 
     __shared__ float s_qmax[WAVES];
@@ -497,11 +502,22 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void sage_attn_pipe_kernel(S
     typedef short s4_t __attribute__((ext_vector_type(4)));
 
     for (int kt = 0; kt < ntiles; ++kt) {
-        attn_pipe::vm_wait_tiles<LPW>(min(S - 2, ntiles - 1 - kt));
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        if (kt + S - 1 < ntiles) issue(kt + S - 1, (kt + S - 1) % S);
+        if constexpr (PAIR) {
+            if (kt % 2 == 0) {
+                attn_pipe::vm_wait<0>();
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                if (kt + 2 < ntiles) issue(kt + 2, (kt + 2) % S);
+                if (kt + 3 < ntiles) issue(kt + 3, (kt + 3) % S);
+            }
+        } else {
+            attn_pipe::vm_wait_tiles<LPW>(min(S - 2, ntiles - 1 - kt));
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (kt + S - 1 < ntiles) issue(kt + S - 1, (kt + S - 1) % S);
+        }
         if (q0 >= a.S) continue;
         const int kb0 = kt * kSPKV;
         if (a.causal && kb0 > wave_last_key) continue;   // the whole tile is above this wave's rows
