@@ -669,10 +669,20 @@ extern "C" int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q
     if (hd == kP2HD && !a.rope_k && prefill_pipe_enabled()) {
         // 8 waves (256 rows, 4-deep ring, one workgroup per CU) when those workgroups fill
         // the chip; fewer rows: 4 waves (128 rows) over a 2-deep ring, two workgroups per
-        // CU (twice the workgroups). EFM_KNOB_PREFILL_SHAPE = 4 / 8 forces one of them.
+        // CU (twice the workgroups); when even those would occupy at most a quarter of the
+        // CUs: 2 waves (64 rows, 2-deep ring, four times the workgroups; measured at 12/2
+        // heads, S 512: 18.0 us against 22.4 with 4 waves, while at 112 or more 4-wave
+        // workgroups the 4-wave kernel is faster). EFM_KNOB_PREFILL_SHAPE = 2 / 4 / 8
+        // forces one of them.
         const int knob = kernel_knob(EFM_KNOB_PREFILL_SHAPE);
-        const bool small = knob != 0 ? knob == 4 : (int)((qo_len + 255) / 256) * a.Hq < prefill_cus();
-        if (small) {
+        const int cus = prefill_cus();
+        const int shape = knob != 0 ? knob
+                          : (int)((qo_len + 255) / 256) * a.Hq >= cus ? 8
+                          : (int)((qo_len + 127) / 128) * a.Hq * 4 > cus ? 4 : 2;
+        if (shape == 2) {
+            const int nqt = (int)((qo_len + 63) / 64);
+            hipLaunchKernelGGL((prefill_attn_pipe_kernel<2, 2>), dim3(nqt * a.Hq), dim3(128), 0, stream, a, nqt);
+        } else if (shape == 4) {
             const int nqt = (int)((qo_len + 127) / 128);
             hipLaunchKernelGGL((prefill_attn_pipe_kernel<4, 2>), dim3(nqt * a.Hq), dim3(256), 0, stream, a, nqt);
         } else {

@@ -803,7 +803,7 @@ extern "C" int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, con
         // as the bf16 kernel: 8 waves over a 4-deep ring when those workgroups fill the
         // chip, else 4 waves / two workgroups per CU (a 3-deep ring of 24 KB stages fits twice)
         const int shape = kernel_knob(EFM_KNOB_PREFILL_SHAPE);
-        const bool small = shape != 0 ? shape == 4 : (int)((qo_len + 255) / 256) * a.Hq < prefill_cus();
+        const bool small = shape != 0 ? shape <= 4 : (int)((qo_len + 255) / 256) * a.Hq < prefill_cus();
         if (small) {
             const int nqt = (int)((qo_len + 127) / 128);
             hipLaunchKernelGGL((sage_attn_pipe_kernel<4, 3>), dim3(nqt * a.Hq), dim3(256), 0, stream, a, nqt);

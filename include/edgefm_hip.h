@@ -59,7 +59,9 @@ const char* efm_version(void);
  *   EFM_KNOB_PREFILL_REGISTER  1: prefill and Sage attention (head_dim 128) run the
  *                              register-staged kernels instead of the pipelined ones
  *   EFM_KNOB_PREFILL_SHAPE     4 or 8: the pipelined prefill / Sage kernels run with
- *                              4-wave (128-row) or 8-wave (256-row) workgroups
+ *                              4-wave (128-row) or 8-wave (256-row) workgroups; 2: the
+ *                              prefill kernel runs 2-wave (64-row) workgroups (the Sage
+ *                              kernel treats 2 as 4)
  *   EFM_KNOB_GEMM_TILE         prefill GEMM kernel (K % 64 == 0): 1 the two-workgroup-
  *                              per-CU 128 x 128 / 128 x 64 / 64 x 64 kernel, 2 the
  *                              one-workgroup-per-CU 256 x 256 kernel

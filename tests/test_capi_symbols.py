@@ -70,6 +70,7 @@ def test_testing_kernel_path_setter_validates():
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_DECODE_REGISTER, 1) == C.EFM_OK
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_DECODE_REGISTER, 0) == C.EFM_OK
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_PREFILL_SHAPE, 8) == C.EFM_OK
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_PREFILL_SHAPE, 2) == C.EFM_OK
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_PREFILL_SHAPE, 0) == C.EFM_OK
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_PREFILL_SHAPE, 5) == C.EFM_ERR_INVALID_ARGUMENT
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_PREFILL_REGISTER, 2) == C.EFM_ERR_INVALID_ARGUMENT

@@ -906,12 +906,12 @@ PIPE_CASES = [
 ]
 
 
-@pytest.mark.parametrize("shape", ["4", "8"])
+@pytest.mark.parametrize("shape", ["2", "4", "8"])
 @pytest.mark.parametrize("hq,hkv,S,L,causal,mode", PIPE_CASES)
 def test_attention_prefill_pipelined_matches_oracle(gpu, knob, shape, hq, hkv, S, L, causal, mode):
     """head_dim 128 with keys already rotated (pos NONE, or RoPE on q only with
-    k_already_prerotated) runs the global_load_lds ring kernel, in both workgroup shapes
-    (4 waves over a 2-deep ring, 8 waves over a 4-deep ring)."""
+    k_already_prerotated) runs the global_load_lds ring kernel, in every workgroup shape
+    (2 or 4 waves over a 2-deep ring, 8 waves over a 4-deep ring)."""
     knob(C.EFM_KNOB_PREFILL_SHAPE, int(shape))
     torch.manual_seed(S + L)
     hd = 128
