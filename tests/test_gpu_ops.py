@@ -934,10 +934,10 @@ def test_attention_prefill_pipelined_matches_oracle(gpu, knob, shape, hq, hkv, S
     assert_close_bf16(o.reshape(S, hq, hd), ref, rtol=2e-2, atol=2e-2, what=f"pipelined S={S} L={L} {mode}")
 
 
-@pytest.mark.parametrize("shape", ["4", "8"])
+@pytest.mark.parametrize("shape", ["2", "4", "8"])
 def test_attention_prefill_pipelined_matches_register_kernel_c4(gpu, knob, shape):
-    """BASELINE C4 shape (28/4 heads, S = 4096, causal): the pipelined kernel (both
-    workgroup shapes) against the register-staged one (EFM_KNOB_PREFILL_REGISTER)."""
+    """BASELINE C4 shape (28/4 heads, S = 4096, causal): the pipelined kernel (every
+    workgroup shape) against the register-staged one (EFM_KNOB_PREFILL_REGISTER)."""
     knob(C.EFM_KNOB_PREFILL_SHAPE, int(shape))
     torch.manual_seed(44)
     hq, hkv, hd, S = 28, 4, 128, 4096
