@@ -360,6 +360,337 @@ __global__ __launch_bounds__(kWideThreads, 1) void decode_attn_wide_kernel(Decod
     decode_attn_wide_body<G, MERGE>(a, blockIdx.x, blockIdx.y);
 }
 
+// ---- one-wave splits (short and mid contexts) ----
+// A launch of few workgroups is bound by what each workgroup loads and by its serial
+// chain, not by the chip's bandwidth: an MI355X graph node costs 1.6 us with nothing in
+// it, 1.8 us when each workgroup loads 8 KB of cold memory, 2.2 us at 16 KB and 3.0 us at
+// 64 KB. So short contexts take one wave64 per workgroup and one split of T (1 or 2)
+// 32-key tiles: every K / V byte of the split is requested up front (buffer loads straight
+// into LDS), the wave computes S^T = K . Q^T and O^T = V^T . P^T on the matrix cores with
+// an online softmax over its tiles, and writes one partial (or, with one split, the
+// output). No barrier and no wave merge: the splits meet in decode_merge_kernel.
+//
+// LDS rows are 16-byte chunks, swizzled so that the K-operand reads (ds_read_b128, rows
+// of 16 lanes at one chunk) and the V^T reads (ds_read_b64_tr_b16, 4 rows x 32 columns
+// per 32 lanes) hit distinct banks of gfx950's 64: head_dim 128 (256-byte rows) uses the
+// attn_pipe layouts; head_dim 64 (128-byte rows) puts chunk c of K row r at
+// c ^ ((r >> 1) & 7) and of V row r at c ^ (((r >> 1) & 1) << 2).
+constexpr int kTileMaxT = 2;       // tiles per split
+constexpr int kTileMaxWG = 256;    // workgroups of a launch (one per CU)
+
+template <int HD>
+struct TileLayout {
+    static constexpr int ROW = HD * 2;            // bytes per K / V row
+    static constexpr int CPR = ROW / 16;          // 16-byte chunks per row
+    static constexpr int TB = kTileKeys * ROW;    // bytes of K (or V) per tile
+    static constexpr int RPL = 1024 / ROW;        // rows per 1 KB wave load
+    static constexpr int LPK = TB / 1024;         // wave loads per K (or V) tile
+    __device__ static int kswz(int r) { return HD == 128 ? (r & 15) : ((r >> 1) & 7); }
+    __device__ static int vswz(int r) { return HD == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2); }
+    __device__ static uint32_t k_off(int r, int c) { return (uint32_t)(r * ROW + ((c ^ kswz(r)) << 4)); }
+    __device__ static uint32_t v_off(int r, int c) { return (uint32_t)(r * ROW + ((c ^ vswz(r)) << 4)); }
+    // V^T operand of d tile tt: lane j = 4 e + q of 16-lane group g reads key 4 (g / 2) + e,
+    // d = 32 tt + 16 (g % 2) + 4 q (attn_pipe.hpp describes the transposing read)
+    __device__ static uint32_t v_tr_lane_off(int lane, int tt) {
+        const int g = lane >> 4, j = lane & 15;
+        const int r = (g >> 1) * 4 + (j >> 2);
+        const int d = tt * 32 + 16 * (g & 1) + 4 * (j & 3);
+        return v_off(r, d >> 3) + (uint32_t)((d & 7) << 1);
+    }
+};
+
+// ROTK = true: every key is rotated on read at its position (the reference's un-rotated
+// cache); its cos / sin are computed while the tiles load. ROTK = false: keys are used as
+// stored (rotated cache, or no RoPE), and with a.fix_last row L - 1 is rotated, used and
+// stored back by the lane that holds it.
+template <int HD, int G, int T, bool ROTK>
+__global__ __launch_bounds__(kWave) void decode_attn_tile_kernel(DecodeArgs a) {
+    using Lay = TileLayout<HD>;
+    constexpr int HALF = HD / 2, KS = HD / 16, DT = HD / 32;
+    constexpr int TB = Lay::TB, LPK = Lay::LPK;
+    static_assert(G <= 32 && T >= 1 && T <= kTileMaxT, "tile kernel shape");
+    __shared__ __align__(1024) unsigned char smem[T * 2 * TB];   // per tile: K | V
+    __shared__ __align__(16) float2 cs_qk[2][HALF];              // cos/sin at q's / key L-1's position
+    __shared__ float sfreq[ROTK ? HALF : 1];
+
+    const int lane = threadIdx.x, ql = lane % 32, hh = lane / 32;
+    const int kvh = blockIdx.y, b = blockIdx.x;
+    const int kps = a.keys_per_split;   // T * 32 (host plan)
+    const int start = b * kps;
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
+
+    // ---- 1. loads that do not depend on L: the query fragments (B operand: lane = head
+    //         column ql, d = 16 ks + 8 hh + e), the RoPE frequency, every tile of the split
+    // (lanes past the group read head G - 1 and zero it below: a load under a lane
+    // condition becomes a branch, after which the compiler waits for it before the tiles)
+    uint4 qraw[KS];
+    {
+        const bf16_t* qp = a.q + (size_t)(kvh * G + min(ql, G - 1)) * a.q_sh + hh * 8;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qraw[ks] = *reinterpret_cast<const uint4*>(qp + ks * 16);
+    }
+    const float freq = (a.rope_q && lane < HALF) ? a.rope.inv_freq[lane] : 0.f;
+    const int q_pos_off = __builtin_amdgcn_readfirstlane(a.q_pos_off);
+    const int k_pos_off = __builtin_amdgcn_readfirstlane(a.k_pos_off);
+    {
+        const int k_sn = __builtin_amdgcn_readfirstlane(a.k_sn), v_sn = __builtin_amdgcn_readfirstlane(a.v_sn);
+        const int lim = min(a.row_bound, start + kps) - 1;   // last row this split may read
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<bf16_t*>(a.k + (size_t)kvh * a.k_sh), (short)0,
+            __builtin_amdgcn_readfirstlane(a.row_bound * k_sn * 2), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<bf16_t*>(a.v + (size_t)kvh * a.v_sh), (short)0,
+            __builtin_amdgcn_readfirstlane(a.row_bound * v_sn * 2), 0x00020000);
+        const int rin = lane / Lay::CPR, slot = lane % Lay::CPR;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+#pragma unroll
+            for (int q = 0; q < 2 * LPK; ++q) {
+                const bool isv = q >= LPK;
+                const int row = (q % LPK) * Lay::RPL + rin;   // row of the tile
+                const int key = start + t * kTileKeys + row;
+                const int c = slot ^ (isv ? Lay::vswz(row) : Lay::kswz(row));
+                // rows past the split's last readable row read nothing (zeros)
+                const uint32_t off = (key <= lim) ? (uint32_t)(key * (isv ? v_sn : k_sn) + c * 8) * 2u : kWloadSkipAttn;
+                wide_lds_load(isv ? rv : rk, lds0 + (uint32_t)(t * 2 * TB + q * 1024), off);
+            }
+        }
+    }
+
+    // ---- 2. the context length and this split's key range [start, end)
+    const uint32_t L = decode_len(a);
+    const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
+    if (b >= nsplit) {
+        attn_pipe::vm_wait<0>();   // no LDS write may outlive the workgroup
+        return;
+    }
+    const int end = min((int)L, start + kps);
+
+    // ---- 3. RoPE at the query position and at the newest key's position; the queries
+    //         rotated in registers (pair d, d + HD/2 sits in chunks ks, ks + KS/2 of the
+    //         same lane) and scaled by log2(e) / sqrt(hd) into the MFMA operand
+    if (a.rope_q) {
+#pragma unroll
+        for (int i = lane; i < 2 * HALF; i += kWave) {
+            const float f = __shfl(freq, i % HALF, kWave);
+            const int pos = (int)L - 1 + (i < HALF ? q_pos_off : k_pos_off);
+            float sn, cs;
+            sincos_reduced((float)pos * f, &sn, &cs);
+            cs_qk[i / HALF][i % HALF] = make_float2(cs, sn);
+        }
+        if (ROTK && lane < HALF) sfreq[lane] = freq;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // one wave: LDS order is issue order
+    }
+    bf16x8_t qf[KS];
+    {
+        float x[KS][8];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) unpack8(qraw[ks], x[ks]);
+        if (a.rope_q) {
+#pragma unroll
+            for (int ks = 0; ks < KS / 2; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float2 c2 = cs_qk[0][ks * 16 + hh * 8 + e];
+                    const float x0 = x[ks][e], x1 = x[ks + KS / 2][e];
+                    x[ks][e] = x0 * c2.x - x1 * c2.y;
+                    x[ks + KS / 2][e] = x1 * c2.x + x0 * c2.y;
+                }
+        }
+        const float qscale = kLog2e / sqrtf((float)HD);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[ks][e] *= qscale;
+            BfPack pk;
+            pk.u = pack8(x[ks]);
+            if (ql >= G) pk.u = make_uint4(0, 0, 0, 0);   // head columns past the group
+            qf[ks] = pk.v;
+        }
+    }
+    const int fix_row = (!ROTK && a.rope_q && a.fix_last && L > 0) ? (int)L - 1 : -1;
+    const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
+
+    f32x16_t oacc[DT];
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[tt][e] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    typedef short s4_t __attribute__((ext_vector_type(4)));
+
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int t0 = start + t * kTileKeys;
+        // ROTK: cos / sin of this lane's key (t0 + ql) for its d = 16 ks + 8 hh + e, ks <
+        // KS / 2, computed before the wait so that they overlap the tile loads
+        float2 ck[ROTK ? KS / 2 : 1][8];
+        if (ROTK) {
+            const float pos = (float)(t0 + ql + k_pos_off);
+#pragma unroll
+            for (int ks = 0; ks < KS / 2; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float sn, cs;
+                    sincos_reduced(pos * sfreq[ks * 16 + hh * 8 + e], &sn, &cs);
+                    ck[ks][e] = make_float2(cs, sn);
+                }
+        }
+        if (t == 0 && T > 1) attn_pipe::vm_wait<(T - 1) * 2 * LPK>();   // tile 0 landed
+        else attn_pipe::vm_wait<0>();
+        asm volatile("" ::: "memory");
+        if (t0 >= end) continue;
+        unsigned char* tile = smem + t * 2 * TB;
+        const uint32_t sb = lds0 + (uint32_t)(t * 2 * TB);
+        if (t0 + kTileKeys > end) {
+            // zero the V rows past the length (P is 0 there, but the rows may hold NaN)
+            for (int x = lane; x < (t0 + kTileKeys - end) * Lay::CPR; x += kWave) {
+                const int row = end - t0 + x / Lay::CPR;
+                *reinterpret_cast<uint4*>(tile + TB + row * Lay::ROW + (x % Lay::CPR) * 16) = make_uint4(0, 0, 0, 0);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+        bf16x8_t kf[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) attn_pipe::read_b128<0>(kf[ks], sb + Lay::k_off(ql, ks * 2 + hh));
+        s4_t vf[2][DT][2];
+        auto read_v = [&](auto kbc) {
+            constexpr int kb = decltype(kbc)::value;
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt) {
+                const uint32_t va = sb + (uint32_t)TB + Lay::v_tr_lane_off(lane, tt);
+                attn_pipe::read_tr16<(kb * 16) * Lay::ROW>(vf[kb][tt][0], va);
+                attn_pipe::read_tr16<(kb * 16 + 8) * Lay::ROW>(vf[kb][tt][1], va);
+            }
+        };
+        read_v(std::integral_constant<int, 0>{});
+        asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(2 * DT) : "memory");   // the K reads (issued first) are done
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kf[ks]));
+        if (ROTK || (t0 + ql == fix_row && fix_row < end)) {
+            // rotate this lane's key: every key (ROTK) or the newest one, which is then
+            // stored back rotated
+#pragma unroll
+            for (int ks = 0; ks < KS / 2; ++ks) {
+                BfPack u0, u1;
+                u0.v = kf[ks];
+                u1.v = kf[ks + KS / 2];
+                float x0[8], x1[8];
+                unpack8(u0.u, x0);
+                unpack8(u1.u, x1);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float2 c2 = ROTK ? ck[ks][e] : cs_qk[1][ks * 16 + hh * 8 + e];
+                    const float y0 = x0[e] * c2.x - x1[e] * c2.y;
+                    const float y1 = x1[e] * c2.x + x0[e] * c2.y;
+                    x0[e] = y0;
+                    x1[e] = y1;
+                }
+                u0.u = pack8(x0);
+                u1.u = pack8(x1);
+                kf[ks] = u0.v;
+                kf[ks + KS / 2] = u1.v;
+                if (!ROTK) {
+                    bf16_t* kw = const_cast<bf16_t*>(kbase) + (size_t)fix_row * a.k_sn + hh * 8;
+                    *reinterpret_cast<uint4*>(kw + ks * 16) = u0.u;
+                    *reinterpret_cast<uint4*>(kw + (ks + KS / 2) * 16) = u1.u;
+                }
+            }
+        }
+        f32x16_t s = {};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
+        read_v(std::integral_constant<int, 1>{});
+        // element e: key = t0 + (e/4)*8 + hh*4 + e%4, head = ql
+        if (t0 + kTileKeys > end) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int j = t0 + (e / 4) * 8 + hh * 4 + (e % 4);
+                s[e] = (j < end) ? s[e] : -INFINITY;
+            }
+        }
+        float mloc = fmaxf(s[0], s[1]);
+#pragma unroll
+        for (int e = 2; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+            mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const float m_new = fmaxf(m_run, mloc);   // finite: the tile holds a valid key
+        float p[16], psum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            p[e] = __builtin_amdgcn_exp2f(s[e] - m_new);
+            psum += p[e];
+        }
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(psum), __float_as_uint(psum), false, false);
+            psum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        if (t == 0) {
+            l_run = psum;
+        } else {
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run = l_run * alpha + psum;
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) oacc[tt][e] *= alpha;
+        }
+        m_run = m_new;
+        BfPack pb[2];
+        pb[0].u = pack8(&p[0]);
+        pb[1].u = pack8(&p[8]);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt) {
+                if (tt == 0) {
+                    if (kb == 0) asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(2 * DT) : "memory");
+                    else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                }
+                asm volatile("" : "+v"(vf[kb][tt][0]), "+v"(vf[kb][tt][1]));
+                union {
+                    s4_t h[2];
+                    bf16x8_t v;
+                } vv;
+                vv.h[0] = vf[kb][tt][0];   // A slots 0-3: keys 16 kb + 4 hh + 0..3
+                vv.h[1] = vf[kb][tt][1];   // A slots 4-7: keys 16 kb + 8 + 4 hh + 0..3
+                oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv.v, pb[kb].v, oacc[tt], 0, 0, 0);
+            }
+    }
+
+    // ---- 4. the split's partial (o unnormalised, m, l), or with one split the output;
+    //         lane (ql, hh) holds d = 32 tt + 8 eb + 4 hh + 0..3 of head ql
+    if (ql < G) {
+        if (a.split_cap == 1) {
+            const float inv = (l_run > 0.f) ? 1.f / l_run : 0.f;
+            bf16_t* o = a.o + (size_t)(kvh * G + ql) * HD;
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                for (int eb = 0; eb < 4; ++eb) {
+                    uint2 pk;
+                    pk.x = pack_bf16x2(oacc[tt][eb * 4 + 0] * inv, oacc[tt][eb * 4 + 1] * inv);
+                    pk.y = pack_bf16x2(oacc[tt][eb * 4 + 2] * inv, oacc[tt][eb * 4 + 3] * inv);
+                    *reinterpret_cast<uint2*>(o + tt * 32 + eb * 8 + hh * 4) = pk;
+                }
+        } else {
+            float* op = a.o_part + (((size_t)kvh * a.split_cap + b) * G + ql) * HD;
+#pragma unroll
+            for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+                for (int eb = 0; eb < 4; ++eb)
+                    *reinterpret_cast<float4*>(op + tt * 32 + eb * 8 + hh * 4) =
+                        make_float4(oacc[tt][eb * 4 + 0], oacc[tt][eb * 4 + 1], oacc[tt][eb * 4 + 2],
+                                    oacc[tt][eb * 4 + 3]);
+            if (hh == 0)
+                *reinterpret_cast<float2*>(a.ml_part + (((size_t)kvh * a.split_cap + b) * G + ql) * 2) =
+                    make_float2(m_run, l_run);
+        }
+    }
+}
+
 // Split merge of efm_attention_decode: kMergeSlices workgroups per query head (blockIdx.y
 // takes a quarter of the head's columns, so a workgroup reads a quarter of the partials),
 // 256 threads = NCOL float4 columns x NPART split lanes. The partial loads of the first
@@ -500,6 +831,19 @@ int decode_split_cap(int num_kv_heads, uint32_t max_kv_len) {
     return (int)((bound + kps - 1) / kps);
 }
 
+// One-wave split plan of efm_attention_decode (decode_attn_tile_kernel): splits of T
+// tiles, the fewest T <= kTileMaxT that keeps the launch within kTileMaxWG workgroups over
+// all KV heads; 0 when none does (the 4- and 8-wave plans above take those lengths). The
+// partials entry points keep the 4-wave plan: their consumers (the o_proj merge, the
+// fused front half) merge at most a few 128-key splits.
+static int tile_keys_per_split(int num_kv_heads, uint32_t max_kv_len) {
+    const uint32_t tiles = (std::max<uint32_t>(max_kv_len, 1u) + kTileKeys - 1) / kTileKeys;
+    const uint32_t heads = (uint32_t)std::max(1, num_kv_heads);
+    for (int t = 1; t <= kTileMaxT; ++t)
+        if ((tiles + t - 1) / t * heads <= (uint32_t)kTileMaxWG) return t * kTileKeys;
+    return 0;
+}
+
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct DecodeWs {
@@ -509,7 +853,10 @@ struct DecodeWs {
 
 static DecodeWs decode_ws(const efm_attention_ctx* c, uint32_t max_kv_len) {
     const int G = c->num_qo_heads / c->num_kv_heads;
-    const int cap = decode_split_cap(c->num_kv_heads, max_kv_len);
+    const uint32_t bound = std::max<uint32_t>(max_kv_len, 1u);
+    int cap = decode_split_cap(c->num_kv_heads, bound);
+    if (const int tk = tile_keys_per_split((int)c->num_kv_heads, bound))
+        cap = std::max(cap, (int)((bound + tk - 1) / tk));
     DecodeWs w;
     w.o_bytes = align256((size_t)c->num_kv_heads * cap * G * c->head_dim * sizeof(float));
     w.ml_bytes = align256((size_t)c->num_kv_heads * cap * G * 2 * sizeof(float));
@@ -597,6 +944,33 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
     a.o_part = reinterpret_cast<float*>(wsb);
     a.ml_part = reinterpret_cast<float*>(wsb + ws.o_bytes);
     a.counter = reinterpret_cast<uint32_t*>(wsb + ws.o_bytes + ws.ml_bytes);
+
+    // Merged calls on short and mid contexts: one-wave splits, then the merge kernel (or,
+    // with one split, the output written by that wave).
+    const int tile_kps = tile_keys_per_split((int)ctx->num_kv_heads, a.row_bound);
+    if (merge && tile_kps > 0 && decode_lds_offsets_fit(a) && kernel_knob(EFM_KNOB_DECODE_TILE) == 0) {
+        a.keys_per_split = tile_kps;
+        a.split_cap = (a.row_bound + tile_kps - 1) / tile_kps;
+        const dim3 tgrid(a.split_cap, ctx->num_kv_heads), tblock(kWave);
+        const int T = tile_kps / kTileKeys;
+#define EFM_DEC_TILE_CASE(HDV, GV)                                                                             \
+        if (hd == HDV && G == GV) {                                                                            \
+            if (rotk && T == 1) hipLaunchKernelGGL((decode_attn_tile_kernel<HDV, GV, 1, true>), tgrid, tblock, 0, stream, a);  \
+            else if (rotk) hipLaunchKernelGGL((decode_attn_tile_kernel<HDV, GV, 2, true>), tgrid, tblock, 0, stream, a);      \
+            else if (T == 1) hipLaunchKernelGGL((decode_attn_tile_kernel<HDV, GV, 1, false>), tgrid, tblock, 0, stream, a);  \
+            else hipLaunchKernelGGL((decode_attn_tile_kernel<HDV, GV, 2, false>), tgrid, tblock, 0, stream, a);              \
+            if (a.split_cap > 1)                                                                               \
+                hipLaunchKernelGGL((decode_merge_kernel<HDV>), dim3(ctx->num_qo_heads, kMergeSlices), dim3(kAttnThreads), 0, \
+                                   stream, a, G);                                                              \
+            return check_launch("attention_decode");                                                           \
+        }
+        EFM_DEC_TILE_CASE(128, 1) EFM_DEC_TILE_CASE(128, 2) EFM_DEC_TILE_CASE(128, 3) EFM_DEC_TILE_CASE(128, 4)
+        EFM_DEC_TILE_CASE(128, 6) EFM_DEC_TILE_CASE(128, 7) EFM_DEC_TILE_CASE(128, 8)
+        EFM_DEC_TILE_CASE(64, 1) EFM_DEC_TILE_CASE(64, 2) EFM_DEC_TILE_CASE(64, 3) EFM_DEC_TILE_CASE(64, 4)
+        EFM_DEC_TILE_CASE(64, 6) EFM_DEC_TILE_CASE(64, 7) EFM_DEC_TILE_CASE(64, 8)
+#undef EFM_DEC_TILE_CASE
+        return set_error(EFM_ERR_UNSUPPORTED, "attention_decode: hd=%d G=%d", hd, G);
+    }
 
     dim3 grid(a.split_cap, ctx->num_kv_heads), block(kAttnThreads);
     // one split: that workgroup writes the output; more: partials, then the merge kernel

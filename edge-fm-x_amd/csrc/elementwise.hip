@@ -577,3 +577,25 @@ extern "C" int efm_finalize_decode_token_indexed(const int32_t* sampled_token, i
                        d_kv_len, capacity);
     return check_launch("finalize_decode_token_indexed");
 }
+
+// dst[*d_index] <- src (row_bytes bytes) when *d_index < max_rows: a per-step copy whose
+// destination row is read on the device, so one captured decode graph stores every step.
+__global__ __launch_bounds__(256) void store_row_indexed_kernel(const uint4* src, uint4* dst, int64_t n16,
+                                                                const uint32_t* d_index, uint32_t max_rows) {
+    const uint32_t r = d_index[0];
+    if (r >= max_rows) return;
+    uint4* d = dst + (size_t)r * (size_t)n16;
+    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256ll) d[i] = src[i];
+}
+
+extern "C" int efm_store_row_indexed(const void* src, void* dst, int64_t row_bytes, const uint32_t* d_index,
+                                     uint32_t max_rows, hipStream_t stream) {
+    if (!src || !dst || !d_index) return set_error(EFM_ERR_INVALID_ARGUMENT, "store_row_indexed: null pointer");
+    if (row_bytes <= 0 || row_bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "store_row_indexed: rows must be 16-byte multiples, 16-byte aligned");
+    const int64_t n16 = row_bytes / 16;
+    const int grid = (int)std::min<int64_t>(1024, (n16 + 255) / 256);
+    hipLaunchKernelGGL(store_row_indexed_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const uint4*>(src),
+                       static_cast<uint4*>(dst), n16, d_index, max_rows);
+    return check_launch("store_row_indexed");
+}

@@ -176,6 +176,59 @@ extern "C" int efm_decode_norm_qkv(int32_t hidden, int32_t q_dim, int32_t kv_dim
     return gemv_launch<PRO_ADD_NORM, EPI_QKV>(g, a, stream);
 }
 
+namespace efm {
+int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
+}
+
+extern "C" int efm_decode_norm_qkv_rope(const efm_attention_ctx* ctx, int32_t hidden, float eps, const void* h,
+                                        const void* residual_in, void* residual_out, const void* norm_w,
+                                        const void* w_qkv, const void* b_qkv, void* q_out, void* k_cache,
+                                        void* v_cache, const uint32_t* d_kv_len, hipStream_t stream) {
+    int rc = validate_attention_ctx(ctx, "decode_norm_qkv_rope");
+    if (rc) return rc;
+    const int hd = (int)ctx->head_dim, Hq = (int)ctx->num_qo_heads, Hkv = (int)ctx->num_kv_heads;
+    const int q_dim = Hq * hd, kv_dim = Hkv * hd, N = q_dim + 2 * kv_dim;
+    if (ctx->pos_encoding != EFM_POS_ROPE_LLAMA)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "decode_norm_qkv_rope: ctx must name EFM_POS_ROPE_LLAMA");
+    if ((ctx->q_stride_n != 0 && ctx->q_stride_n != (uint32_t)q_dim) ||
+        (ctx->q_stride_h != 0 && ctx->q_stride_h != (uint32_t)hd) ||
+        (ctx->k_stride_n != 0 && ctx->k_stride_n != (uint32_t)kv_dim) ||
+        (ctx->k_stride_h != 0 && ctx->k_stride_h != (uint32_t)hd) ||
+        (ctx->kv_stride_n != 0 && ctx->kv_stride_n != (uint32_t)kv_dim) ||
+        (ctx->kv_stride_h != 0 && ctx->kv_stride_h != (uint32_t)hd))
+        return set_error(EFM_ERR_UNSUPPORTED, "decode_norm_qkv_rope: q and the K / V cache rows must be contiguous");
+    rc = gemv_check(hidden, N, w_qkv, h, q_out, true);
+    if (rc) return rc;
+    if (norm_w == nullptr || residual_out == nullptr || k_cache == nullptr || v_cache == nullptr ||
+        d_kv_len == nullptr)
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "decode_norm_qkv_rope: null pointer");
+    if (residual_out == h || (residual_in != nullptr && residual_out == residual_in))
+        return set_error(EFM_ERR_INVALID_ARGUMENT, "decode_norm_qkv_rope: residual_out must not alias its inputs");
+    GemvArgs a = gemv_args(hidden, N / 2, w_qkv, h);
+    a.r_in = static_cast<const bf16_t*>(residual_in);
+    a.r_out = static_cast<bf16_t*>(residual_out);
+    a.norm_w = static_cast<const bf16_t*>(norm_w);
+    a.eps = eps;
+    a.bias = static_cast<const bf16_t*>(b_qkv);
+    a.y = q_out;
+    a.q_dim = q_dim;
+    a.kv_dim = kv_dim;
+    a.k_cache = static_cast<bf16_t*>(k_cache);
+    a.v_cache = static_cast<bf16_t*>(v_cache);
+    a.d_kv_len = d_kv_len;
+    a.rope_half = hd / 2;
+    a.q_pos_off = (int)ctx->q_rope_pos_offset;
+    a.k_pos_off = (int)ctx->k_rope_pos_offset;
+    rope_table_fill(&a.rope, hd, ctx->rope_theta, ctx->rope_scale);
+    // one logical row = the pair (d, d + hd/2) of a head: a row block (4 / KS logical rows)
+    // must not straddle two heads
+    const GemvCfg g = gemv_pick(hidden, N / 2, 2, 1024, false);
+    if ((hd / 2) % (4 / g.KS * g.R) != 0)
+        return set_error(EFM_ERR_UNSUPPORTED, "decode_norm_qkv_rope: head_dim %d with hidden %d", hd, hidden);
+    if (residual_in == nullptr) return gemv_launch<PRO_NORM, EPI_QKV_ROPE>(g, a, stream);
+    return gemv_launch<PRO_ADD_NORM, EPI_QKV_ROPE>(g, a, stream);
+}
+
 extern "C" int efm_decode_norm_gate_up_swiglu(int32_t hidden, int32_t inter, float eps, const void* a_in,
                                               const void* residual_in, void* residual_out, const void* norm_w,
                                               const void* w_up_gate, void* out, hipStream_t stream) {

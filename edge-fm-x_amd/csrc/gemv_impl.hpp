@@ -18,9 +18,10 @@
 //  * Workgroups walk row blocks grid-stride; the next block's loads are issued before
 //    the current block's cross-lane reductions and epilogue.
 //  * Epilogues: bf16 store (+bias), fp32 store, QKV split with K/V written straight
-//    into the KV-cache slot (optionally also published as tagged words), SwiGLU over
-//    paired up/gate rows, and greedy top-1 with a last-workgroup grid reduction (no
-//    second launch, self-resetting counter).
+//    into the KV-cache slot (optionally also published as tagged words, or with q and k
+//    rotated: the rows d and d + hd/2 of a head are the two parts of one logical row),
+//    SwiGLU over paired up/gate rows, and greedy top-1 with a last-workgroup grid
+//    reduction (no second launch, self-resetting counter).
 #pragma once
 
 #include "common.hpp"
@@ -28,7 +29,7 @@
 namespace efm {
 
 enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ADD_NORM = 2, PRO_ATTN_MERGE = 3 };
-enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_TOP1 = 4, EPI_QKV_TAG = 5 };
+enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_TOP1 = 4, EPI_QKV_TAG = 5, EPI_QKV_ROPE = 6 };
 
 // Weight-stream load of the GEMV main loop: a non-temporal 16-byte buffer load (weights
 // are read once per decode step and must not evict the activation working set). Offsets
@@ -76,6 +77,11 @@ struct GemvArgs {
     // (bf16 bits | launch tag << 16) for the attention workgroups of the same launch
     uint32_t* tag_words;
     const uint32_t* epoch;      // launch counter the tag derives from (launch_tag)
+    // QKV_ROPE: logical row n = (head n / rope_half, pair d = n % rope_half) computes the
+    // rows d and d + rope_half of that head; q and k heads are rotated at position
+    // *d_kv_len - 1 (+ q_pos_off / k_pos_off) by inv_freq[d]
+    int rope_half, q_pos_off, k_pos_off;
+    RopeTable rope;
 };
 
 
@@ -368,17 +374,33 @@ __device__ __forceinline__ unsigned long long top1_key(ArgMax c) {
     return ((unsigned long long)bits << 32) | (unsigned long long)(~(uint32_t)c.i);
 }
 
-// Physical weight row of logical row n, part p (SwiGLU: p=0 up row n, p=1 gate row N+n).
+// Physical weight row of logical row n, part p (SwiGLU: p=0 up row n, p=1 gate row N+n;
+// QKV_ROPE: rows d and d + half of head n / half, d = n % half).
 template <int EPI>
-__device__ __forceinline__ int phys_row(int n, int p, int N) {
+__device__ __forceinline__ int phys_row(int n, int p, int N, int half) {
+    if (EPI == EPI_QKV_ROPE) return (n / half) * 2 * half + p * half + n % half;
     return (EPI == EPI_SWIGLU && p == 1) ? (N + n) : n;
+}
+
+// QKV_ROPE: cos / sin of logical row n (the pair d = n % half of its head) at position
+// L - 1 + the q or k offset. The row is the same for every lane of a wave (one row per
+// wave group), so the frequency comes through a scalar load, not a per-lane load of the
+// kernel-argument table.
+__device__ __forceinline__ float2 qkv_rope_cs(const GemvArgs& a, int n, uint32_t L) {
+    n = __builtin_amdgcn_readfirstlane(n);
+    const int half = a.rope_half, d = n % half;
+    const int n0 = (n / half) * 2 * half + d;
+    const int pos = (int)L - 1 + (n0 < a.q_dim ? a.q_pos_off : a.k_pos_off);
+    float sn, cs;
+    sincosf((float)pos * a.rope.inv_freq[d], &sn, &cs);
+    return make_float2(cs, sn);
 }
 
 // Body of the GEMV kernel for workgroup `blk` of `nblk` (grid-stride over row blocks),
 // shared by gemv_kernel and the fused QKV + attention kernel.
 template <int R, int KS, int PRO, int EPI>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, int blk, int nblk) {
-    constexpr int P = (EPI == EPI_SWIGLU) ? 2 : 1;
+    constexpr int P = (EPI == EPI_SWIGLU || EPI == EPI_QKV_ROPE) ? 2 : 1;
     constexpr int G = 4 / KS;          // row groups per block
     constexpr int RB = G * R;          // logical rows per block
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -410,7 +432,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
         const int nrec = __builtin_amdgcn_readfirstlane(rows * a.K * 2);
 #pragma unroll
         for (int p = 0; p < P; ++p) {
-            const bf16_t* base = a.W + (size_t)phys_row<EPI>(row0, p, a.N) * (size_t)a.K;
+            const bf16_t* base = a.W + (size_t)phys_row<EPI>(row0, p, a.N, a.rope_half) * (size_t)a.K;
             const __amdgpu_buffer_rsrc_t rs =
                 __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, nrec, 0x00020000);
 #pragma unroll
@@ -432,6 +454,15 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
     int rb = blk;
     issue(rb, 0);   // unconditional (a block past the end reads zeros): see gemv_wload
     __builtin_amdgcn_sched_barrier(0);   // every load goes out before the prologue's first wait
+    // QKV_ROPE: the first row block's cos / sin while the weights stream (the epilogue
+    // recomputes them for any later block of a grid-stride walk)
+    float2 rcs[R];
+    uint32_t rope_len = 0;
+    if constexpr (EPI == EPI_QKV_ROPE) {
+        rope_len = a.d_kv_len[0];
+#pragma unroll
+        for (int r = 0; r < R; ++r) rcs[r] = qkv_rope_cs(a, blk * RB + grp * R + r, rope_len);
+    }
     gemv_prologue<PRO>(a, pl, xs, red, blk);
     __syncthreads();
     const uint4* xs4 = reinterpret_cast<const uint4*>(xs);
@@ -491,6 +522,39 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
             for (int r = 0; r < R; ++r) {
                 const int n = rb * RB + grp * R + r;
                 if (n >= a.N) continue;
+                if (EPI == EPI_QKV_ROPE) {
+                    // bf16(x . W + b) for rows d and d + half of the head, then q and k
+                    // rotated as the reference rotates them on read; K / V into the slot
+                    const int half = a.rope_half;
+                    const int d = n % half;
+                    const int n0 = (n / half) * 2 * half + d, n1 = n0 + half;
+                    float v0 = acc[r][0], v1 = acc[r][P - 1];
+                    if (a.bias != nullptr) {
+                        v0 += bf16_to_f32(a.bias[n0]);
+                        v1 += bf16_to_f32(a.bias[n1]);
+                    }
+                    float x0 = round_bf16(v0), x1 = round_bf16(v1);
+                    const uint32_t L = rope_len;
+                    if (n0 < a.q_dim + a.kv_dim) {
+                        const float2 c2 = (rb == blk) ? rcs[r] : qkv_rope_cs(a, n, L);
+                        const float cs = c2.x, sn = c2.y;
+                        const float y0 = x0 * cs - x1 * sn, y1 = x1 * cs + x0 * sn;
+                        x0 = y0;
+                        x1 = y1;
+                    }
+                    const bf16_t b0 = (bf16_t)f32_to_bf16(x0), b1 = (bf16_t)f32_to_bf16(x1);
+                    if (n0 < a.q_dim) {
+                        reinterpret_cast<bf16_t*>(a.y)[n0] = b0;
+                        reinterpret_cast<bf16_t*>(a.y)[n1] = b1;
+                    } else if (L > 0) {
+                        const size_t slot = (size_t)(L - 1) * (size_t)a.kv_dim;
+                        const int m0 = n0 - a.q_dim;
+                        bf16_t* dst = (m0 < a.kv_dim) ? a.k_cache + slot + m0 : a.v_cache + slot + (m0 - a.kv_dim);
+                        dst[0] = b0;
+                        dst[half] = b1;
+                    }
+                    continue;
+                }
                 float v = acc[r][0];
                 if (a.bias != nullptr) v += bf16_to_f32(a.bias[n]);
                 if (EPI == EPI_BF16) {

@@ -41,6 +41,7 @@ EFM_KNOB_PREFILL_REGISTER = 1
 EFM_KNOB_PREFILL_SHAPE = 2
 EFM_KNOB_GEMM_TILE = 3
 EFM_KNOB_FRONT_WAIT_TIMEOUT = 4
+EFM_KNOB_DECODE_TILE = 5
 
 
 class AttentionCtx(ctypes.Structure):
@@ -137,6 +138,10 @@ SIGNATURES = {
     "efm_increment_int32_triplet": (c_int32, [c_void_p, c_void_p]),
     "efm_decode_norm_qkv": (c_int32, [c_int32, c_int32, c_int32, c_float, c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "efm_store_row_indexed": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p, c_uint32, c_void_p]),
+    "efm_decode_norm_qkv_rope": (c_int32, [POINTER(AttentionCtx), c_int32, c_float, c_void_p, c_void_p, c_void_p,
+                                           c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                           c_void_p]),
     "efm_decode_qkv_attention_sync_bytes": (c_size_t, [c_int32, c_int32]),
     "efm_decode_norm_qkv_attention_supported": (c_int32, [POINTER(AttentionCtx), c_int32, c_uint32]),
     "efm_decode_norm_qkv_attention": (c_int32, [POINTER(AttentionCtx), c_int32, c_float, c_void_p, c_void_p, c_void_p,

@@ -117,7 +117,8 @@ def write_engine_config(path: str, model_dir: str, *, max_tokens: int = 4096, ma
                         prefix_token_ids=None, use_graph: bool = True, temperature: float = 0.0,
                         top_p: float = 1.0, seed: int = 0, lm_head_top1: bool = True, model_name: str = "",
                         operator_impl_table_path: str = "", extra_slots=None, decode_stack=None,
-                        stop_token_ids=None, compact_vocab=None, decode_fused_qkv_attention=None) -> str:
+                        stop_token_ids=None, compact_vocab=None, decode_fused_qkv_attention=None,
+                        debug_logits: bool = False) -> str:
     slots = [{"request_id": 0, "prefix_token_ids": list(prefix_token_ids or []), "max_tokens": max_tokens}]
     for s in extra_slots or []:
         slots.append(s)
@@ -136,6 +137,8 @@ def write_engine_config(path: str, model_dir: str, *, max_tokens: int = 4096, ma
         cfg["runtime"]["decode_fused_qkv_attention"] = bool(decode_fused_qkv_attention)
     if compact_vocab is not None:
         cfg["compact_vocab"] = compact_vocab
+    if debug_logits:
+        cfg["runtime"]["debug_logits"] = True
     with open(path, "w") as f:
         json.dump(cfg, f)
     return path

@@ -213,6 +213,9 @@ bool EngineConfig::use_graph() const {
 bool EngineConfig::lm_head_top1() const {
     return json_.contains("runtime") ? json_.at("runtime").get_bool("lm_head_top1", true) : true;
 }
+bool EngineConfig::debug_logits() const {
+    return json_.contains("runtime") ? json_.at("runtime").get_bool("debug_logits", false) : false;
+}
 bool EngineConfig::decode_fused_qkv_attention() const {
     const char* env = std::getenv("EDGE_FM_DECODE_FUSED_QKV_ATTENTION");
     if (env != nullptr && env[0] != '\0') return std::string(env) != "0";
@@ -600,8 +603,18 @@ efm_attention_ctx Qwen2_5::decode_ctx() const {
     efm_attention_ctx c = to_c_ctx(attn_ctx());
     // text models: the cache holds keys rotated at their positions (prefill rotates
     // them before the cache write); this step's key, written un-rotated by the QKV
-    // projection, is rotated by the attention call that first reads it
+    // projection of the fused front half / the decode stack, is rotated by the attention
+    // call that first reads it
     if (!m_.mrope) c.k_already_prerotated = EFM_K_PREROTATED_EXCEPT_NEWEST;
+    return c;
+}
+
+efm_attention_ctx Qwen2_5::decode_attn_ctx_rotated() const {
+    // every key in the cache and q already rotated (efm_decode_norm_qkv_rope, or the
+    // M-RoPE write): the attention itself applies no positional encoding
+    efm_attention_ctx c = to_c_ctx(attn_ctx());
+    c.pos_encoding = EFM_POS_NONE;
+    c.k_already_prerotated = 0;
     return c;
 }
 
@@ -756,6 +769,7 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
         return;
     }
     const std::vector<DecodeLayerPlan>& plan = decode_plan(max_kv_len);
+    const efm_attention_ctx cr = decode_attn_ctx_rotated();
     for (int l = 0; l < m_.layers; ++l) {
         Layer& Ly = layers_[l];
         const DecodeLayerPlan& P = plan[l];
@@ -777,11 +791,22 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
                 vdst = static_cast<char*>(dec_kvtmp_.data_ptr()) + (size_t)KVD * 2;
                 slot_len = static_cast<const uint32_t*>(dec_one_.data_ptr());
             }
-            efm_check(efm_decode_norm_qkv(H, QD, KVD, m_.eps, dec_h_.data_ptr(),
-                                          (l == 0) ? nullptr : dec_res_[1].data_ptr(), dec_res_[0].data_ptr(),
-                                          Ly.in_norm.data_ptr(), Ly.qkv_w.data_ptr(), Ly.qkv_b.data_ptr(),
-                                          dec_q_.data_ptr(), kdst, vdst, slot_len, stream),
-                      "decode norm+qkv");
+            if (m_.mrope) {
+                efm_check(efm_decode_norm_qkv(H, QD, KVD, m_.eps, dec_h_.data_ptr(),
+                                              (l == 0) ? nullptr : dec_res_[1].data_ptr(), dec_res_[0].data_ptr(),
+                                              Ly.in_norm.data_ptr(), Ly.qkv_w.data_ptr(), Ly.qkv_b.data_ptr(),
+                                              dec_q_.data_ptr(), kdst, vdst, slot_len, stream),
+                          "decode norm+qkv");
+            } else {
+                // q and this step's key rotated in the projection's epilogue (the key
+                // straight into the cache slot)
+                const efm_attention_ctx cq = to_c_ctx(attn_ctx());
+                efm_check(efm_decode_norm_qkv_rope(&cq, H, m_.eps, dec_h_.data_ptr(),
+                                                   (l == 0) ? nullptr : dec_res_[1].data_ptr(), dec_res_[0].data_ptr(),
+                                                   Ly.in_norm.data_ptr(), Ly.qkv_w.data_ptr(), Ly.qkv_b.data_ptr(),
+                                                   dec_q_.data_ptr(), kdst, vdst, slot_len, stream),
+                          "decode norm+qkv+rope");
+            }
             if (m_.mrope) {
                 efm_check(efm_decode_mrope_write_kv(dec_q_.data_ptr(), kdst, vdst, dec_q_.data_ptr(), k_caches[l],
                                                     v_caches[l], m_.heads, m_.kv_heads, m_.head_dim, d_pos3,
@@ -790,11 +815,11 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
                           "decode mrope + kv write");
             }
             if (P.partials_to_o_proj) {
-                efm_check(efm_decode_attention_partials(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], d_kv_len,
+                efm_check(efm_decode_attention_partials(&cr, dec_q_.data_ptr(), k_caches[l], v_caches[l], d_kv_len,
                                                         max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(), stream),
                           "decode attention partials");
             } else {
-                efm_check(efm_attention_decode(&c, dec_q_.data_ptr(), k_caches[l], v_caches[l], dec_attn_.data_ptr(),
+                efm_check(efm_attention_decode(&cr, dec_q_.data_ptr(), k_caches[l], v_caches[l], dec_attn_.data_ptr(),
                                                0, d_kv_len, max_kv_len, attn_ws_.data_ptr(), attn_ws_.nbytes(),
                                                stream),
                           "decode attention");
@@ -1004,6 +1029,10 @@ StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_pat
     }
     response_dev_ = Tensor::zeros({(int64_t)max_resp}, DType::Int32, Device::GPU, device_id_);
     logits_ = Tensor::zeros({m.vocab}, DType::Float32, Device::GPU, device_id_);
+    // per-token logits record: one row per response slot, allocated once so that captured
+    // decode graphs keep a valid destination
+    if (cfg_.debug_logits())
+        logits_hist_ = Tensor::zeros({(int64_t)max_resp, m.vocab}, DType::Float32, Device::GPU, device_id_);
     sample_ws_ = Tensor::zeros({(int64_t)std::max(efm_sampler_greedy_workspace_bytes(1, m.vocab),
                                                    efm_sampler_top_p_workspace_bytes(m.vocab))},
                                DType::UInt8, Device::GPU, device_id_);
@@ -1054,6 +1083,14 @@ void StandardEngine::warmup() {
 void StandardEngine::sample_logits(uint32_t) {
     int32_t* tok = static_cast<int32_t*>(state_.data_ptr()) + 2;
     const float T = cfg_.temperature();
+    if (!logits_hist_.empty()) {
+        // row = response index of the token about to be sampled (device step counter)
+        const int64_t V = model_->config().vocab;
+        efm_check(efm_store_row_indexed(logits_.data_ptr(), logits_hist_.data_ptr(), V * 4,
+                                        static_cast<const uint32_t*>(state_.data_ptr()) + 1,
+                                        (uint32_t)logits_hist_.shape()[0], stream_),
+                  "logits record");
+    }
     if (T < 1e-6f) {
         efm_check(efm_sampler_greedy(1, model_->config().vocab, static_cast<float*>(logits_.data_ptr()), tok,
                                      sample_ws_.data_ptr(), sample_ws_.nbytes(), stream_),
@@ -1078,7 +1115,7 @@ void StandardEngine::run_decode_step(int32_t request_id, void* stage_events) {
     const int32_t* pos3 = st + 3;
     KVSlot& slot = kv_->slot(request_id);
     auto kc = caches(request_id, true), vc = caches(request_id, false);
-    const bool greedy_fused = cfg_.temperature() < 1e-6f && cfg_.lm_head_top1();
+    const bool greedy_fused = cfg_.temperature() < 1e-6f && cfg_.lm_head_top1() && !cfg_.debug_logits();
     if (se) se->record(stream_);
     {
         RoctxRange r(se ? "EDGEFM_DECODE_MODEL" : nullptr);
@@ -1194,7 +1231,7 @@ Response StandardEngine::generate(const Request& request) {
 
     EventTimer pf_model;  // pf.a .. pf_model.b: model; pf_model.b .. pf.b: sampler + finalize
     hip_check(hipEventRecord(pf.a, stream_), "event");
-    const bool greedy_fused = cfg_.temperature() < 1e-6f && cfg_.lm_head_top1();
+    const bool greedy_fused = cfg_.temperature() < 1e-6f && cfg_.lm_head_top1() && !cfg_.debug_logits();
     {
         RoctxRange prefill_range("EDGEFM_PREFILL");
         {
@@ -1254,6 +1291,7 @@ Response StandardEngine::generate(const Request& request) {
     }
     hip_check(hipEventRecord(dc.b, stream_), "event");
 
+    last_n_gen_ = n_gen;
     std::vector<int32_t> host((size_t)n_gen);
     EventTimer copy;
     {
@@ -1340,6 +1378,21 @@ Response StandardEngine::generate(const Request& request) {
 
 EdgeFM::EdgeFM(const std::string& config_path) : engine_(std::make_unique<StandardEngine>(config_path)) {}
 Response EdgeFM::generate(const Request& request) const { return engine_->generate(request); }
+std::vector<float> EdgeFM::last_logits(int32_t* rows, int32_t* vocab) const { return engine_->last_logits(rows, vocab); }
+
+std::vector<float> StandardEngine::last_logits(int32_t* rows, int32_t* vocab) const {
+    if (logits_hist_.empty())
+        throw ConfigurationError("EdgeFM.last_logits: the engine config does not set runtime.debug_logits");
+    const int64_t V = model_->config().vocab;
+    const int32_t n = std::min<int32_t>(last_n_gen_, (int32_t)logits_hist_.shape()[0]);
+    std::vector<float> out((size_t)n * (size_t)V);
+    if (n > 0)
+        hip_check(hipMemcpy(out.data(), logits_hist_.data_ptr(), out.size() * sizeof(float), hipMemcpyDeviceToHost),
+                  "logits record D2H");
+    *rows = n;
+    *vocab = (int32_t)V;
+    return out;
+}
 std::unordered_map<std::string, double> EdgeFM::last_generate_metrics() const { return engine_->last_generate_metrics(); }
 
 }  // namespace edge_fm

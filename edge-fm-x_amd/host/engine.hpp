@@ -85,6 +85,10 @@ public:
     std::string hw_profile() const;
     bool use_graph() const;
     bool lm_head_top1() const;
+    // runtime.debug_logits: every generated token's fp32 logits are kept on the device
+    // (logits path instead of the fused LM-head top-1) and returned by
+    // EdgeFM::last_logits() (test and debugging aid; off by default)
+    bool debug_logits() const;
     // Whole decode step of a text model in one persistent launch (efm_decode_stack;
     // runtime.decode_stack, default off: on MI355X its six cross-workgroup hand-offs per
     // layer cost more than the four kernel boundaries of the per-operator path;
@@ -265,6 +269,7 @@ private:
     const Tensor& w(const std::unordered_map<std::string, Tensor>& ws, const std::string& name) const;
     void ensure_prefill_capacity(int32_t S);
     efm_attention_ctx decode_ctx() const;
+    efm_attention_ctx decode_attn_ctx_rotated() const;
     AttentionOpContext attn_ctx() const;
 };
 
@@ -281,6 +286,9 @@ public:
     const EngineConfig& engine_config() const { return cfg_; }
     const CompactVocab& compact_vocab() const { return compact_vocab_; }
     void warmup();
+    // fp32 logits of every token of the last generate() call ([rows, vocab], row-major),
+    // with runtime.debug_logits set; ConfigurationError otherwise
+    std::vector<float> last_logits(int32_t* rows, int32_t* vocab) const;
 
 private:
     EngineConfig cfg_;
@@ -295,6 +303,8 @@ private:
     Tensor response_dev_;
     Tensor ids_dev_;
     Tensor logits_;
+    Tensor logits_hist_;     // runtime.debug_logits: [response slots, vocab] fp32
+    int32_t last_n_gen_ = 0;
     Tensor sample_ws_;
     // One decode step, and kGraphSteps consecutive steps in one graph (fewer graph launches:
     // each costs a few us of command-processor time between the steps it separates).
@@ -319,6 +329,7 @@ public:
     explicit EdgeFM(const std::string& config_path);
     Response generate(const Request& request) const;
     std::unordered_map<std::string, double> last_generate_metrics() const;
+    std::vector<float> last_logits(int32_t* rows, int32_t* vocab) const;
     const StandardEngine& engine() const { return *engine_; }
 
 private:

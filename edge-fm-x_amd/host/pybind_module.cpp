@@ -2,6 +2,7 @@
 // 313-1735) for the MI355X runtime — DType / Device / ModelStage, Tensor (zero-copy
 // views of device memory, DLPack export as kDLROCM), Request / Response, EdgeFM with
 // generate() and last_generate_metrics(), the WeightLoader singleton and apply_mrope.
+#include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
@@ -146,6 +147,15 @@ PYBIND11_MODULE(edge_fm, m) {
         .def(py::init<const std::string&>(), py::arg("config_path"), py::call_guard<py::gil_scoped_release>())
         .def("generate", &EdgeFM::generate, py::arg("request"), py::call_guard<py::gil_scoped_release>())
         .def("last_generate_metrics", &EdgeFM::last_generate_metrics)
+        .def("last_logits",
+             [](const EdgeFM& e) {
+                 int32_t rows = 0, vocab = 0;
+                 std::vector<float> v = e.last_logits(&rows, &vocab);
+                 py::array_t<float> a({(py::ssize_t)rows, (py::ssize_t)vocab});
+                 std::copy(v.begin(), v.end(), a.mutable_data());
+                 return a;
+             },
+             "fp32 logits [tokens, vocab] of every token of the last generate() (runtime.debug_logits)")
         .def("model_config", [](const EdgeFM& e) {
             const ModelConfig& c = e.engine().model_config();
             py::dict d;

@@ -70,13 +70,17 @@ const char* efm_version(void);
  *                              with a 64-poll limit: every wait gives up, the launch
  *                              drains with wrong outputs and the time-out is reported by
  *                              efm_decode_qkv_attention_status (tests of that path)
+ *   EFM_KNOB_DECODE_TILE       1: efm_attention_decode leaves the one-wave split kernel
+ *                              of short and mid contexts aside and runs the 4-wave /
+ *                              8-wave / register kernels those lengths had before it
  * Unknown knobs or values: EFM_ERR_INVALID_ARGUMENT. Not for production callers. */
 #define EFM_KNOB_DECODE_REGISTER 0
 #define EFM_KNOB_PREFILL_REGISTER 1
 #define EFM_KNOB_PREFILL_SHAPE 2
 #define EFM_KNOB_GEMM_TILE 3
 #define EFM_KNOB_FRONT_WAIT_TIMEOUT 4
-#define EFM_KNOB_COUNT 5
+#define EFM_KNOB_DECODE_TILE 5
+#define EFM_KNOB_COUNT 6
 int efm_testing_set_kernel_path(int32_t knob, int32_t value);
 
 /* ------------------------------------------------------------------------------------
@@ -417,6 +421,14 @@ int efm_decode_mrope_write_kv(const void* q_src, const void* k_src, const void* 
 int efm_finalize_decode_token_indexed(const int32_t* sampled_token, int32_t* response_base, uint32_t* d_step,
                                       uint32_t* d_kv_len, uint32_t capacity, hipStream_t stream);
 
+/* dst[*d_index * row_bytes ...] <- src[0 .. row_bytes) when *d_index < max_rows, else
+ * nothing (device-side row index, so a captured decode graph stores each step's row).
+ * row_bytes a multiple of 16, src / dst 16-byte aligned. The engine's per-step logits
+ * record (runtime.debug_logits) uses it, in the role of the reference's debug bindings
+ * that hand intermediate tensors to its tests (src/python/pybind_debug.cpp:486-1580). */
+int efm_store_row_indexed(const void* src, void* dst, int64_t row_bytes, const uint32_t* d_index, uint32_t max_rows,
+                          hipStream_t stream);
+
 /* ------------------------------------------------------------------------------------
  * Fused decode-step kernels. Each one replaces a short sequence of the reference's
  * per-token operator calls inside Qwen2_5::forward_impl (src/models/qwen2_5/
@@ -434,6 +446,22 @@ int efm_decode_norm_qkv(int32_t hidden, int32_t q_dim, int32_t kv_dim, float eps
                         const void* residual_in, void* residual_out, const void* norm_w,
                         const void* w_qkv, const void* b_qkv, void* q_out, void* k_cache,
                         void* v_cache, const uint32_t* d_kv_len, hipStream_t stream);
+
+/* efm_decode_norm_qkv with RoPE-Llama applied in the projection's epilogue, for caches
+ * that hold rotated keys: with L = *d_kv_len, q_out <- bf16(rot(bf16(q), L - 1 +
+ * q_rope_pos_offset)) and the cache slot L - 1 receives bf16(rot(bf16(k), L - 1 +
+ * k_rope_pos_offset)) and V; rot turns the pair (d, d + hd/2) by pos * inv_freq[d]
+ * (inv_freq as in efm_rope_llama_inplace, cos / sin in fp32). The head geometry and the
+ * RoPE parameters come from ctx (pos_encoding EFM_POS_ROPE_LLAMA, contiguous q and cache
+ * rows). A following efm_attention_decode with pos_encoding EFM_POS_NONE on that cache
+ * computes the reference's RoPE-on-read attention (qwen2_5.cpp:600-790 with
+ * attention.cu:135-139): q . k_j after both rotations. Replaces the FusedQKVLinearLayer
+ * projection of the decode step plus the RoPE that FlashInferAttentionOp::forward_decode
+ * (attention_op.cu:1565-1604) applies to q and to the newest key. */
+int efm_decode_norm_qkv_rope(const efm_attention_ctx* ctx, int32_t hidden, float eps, const void* h,
+                             const void* residual_in, void* residual_out, const void* norm_w,
+                             const void* w_qkv, const void* b_qkv, void* q_out, void* k_cache,
+                             void* v_cache, const uint32_t* d_kv_len, hipStream_t stream);
 
 /* Fused front half of a decode layer: efm_decode_norm_qkv followed by
  * efm_decode_attention_partials, in one launch, with bit-identical results. Replaces the

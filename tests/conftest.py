@@ -40,5 +40,5 @@ def knob():
 
     yield set_knob
     for k in (C.EFM_KNOB_DECODE_REGISTER, C.EFM_KNOB_PREFILL_REGISTER, C.EFM_KNOB_PREFILL_SHAPE, C.EFM_KNOB_GEMM_TILE,
-              C.EFM_KNOB_FRONT_WAIT_TIMEOUT):
+              C.EFM_KNOB_FRONT_WAIT_TIMEOUT, C.EFM_KNOB_DECODE_TILE):
         C.call("efm_testing_set_kernel_path", k, 0)

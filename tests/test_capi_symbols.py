@@ -80,5 +80,8 @@ def test_testing_kernel_path_setter_validates():
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 1) == C.EFM_OK
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 0) == C.EFM_OK
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 2) == C.EFM_ERR_INVALID_ARGUMENT
-    assert lib.efm_testing_set_kernel_path(5, 0) == C.EFM_ERR_INVALID_ARGUMENT
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_DECODE_TILE, 1) == C.EFM_OK
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_DECODE_TILE, 0) == C.EFM_OK
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_DECODE_TILE, 2) == C.EFM_ERR_INVALID_ARGUMENT
+    assert lib.efm_testing_set_kernel_path(6, 0) == C.EFM_ERR_INVALID_ARGUMENT
     assert lib.efm_testing_set_kernel_path(99, 0) == C.EFM_ERR_INVALID_ARGUMENT

@@ -10,11 +10,14 @@ GPU's tokens.
     (t, h, w) grid with 3-D M-RoPE positions plus 64 text tokens, a short greedy decode
     from position last + 1.
 
-Greedy steps: a token may differ from the oracle's argmax only where the oracle's top-1
-minus the GPU token's logit is below 0.05 (a bf16 near tie), and every step whose oracle
-top-2 margin is at least 0.05 must match. Sampled steps: the token must be the oracle
-sampler's choice (same seed, draw counter = response index) unless the decision lies
-within 10 % of a boundary (relative mass). Each test prints its per-step margins.
+The engine records every step's fp32 logits (runtime.debug_logits). Each token must be
+exactly the argmax (greedy) or the oracle sampler's draw (top-p: same seed, draw counter =
+response index) on the engine's own logits; the production configuration (fused LM-head
+top-1 for greedy) must give the same tokens; a rerun must repeat tokens and logits bit for
+bit; the engine's logits must follow the oracle's, teacher-forced on the GPU's tokens,
+within stated bounds (in units of the step's logit std); and greedy steps whose oracle
+top-2 margin lies far outside that noise must give the oracle's token. Each test prints
+its per-step figures.
 
 Weights are generated on the GPU from a seed (S.synthetic_weights_gpu: N(0, std), norm
 weights ones) and copied to the host for the oracle. Mirrors
@@ -24,6 +27,7 @@ import os
 import tempfile
 import time
 
+import numpy as np
 import pytest
 import torch
 
@@ -32,6 +36,20 @@ import efm_setup as S
 from oracle import efm_oracle as O
 
 pytestmark = pytest.mark.gpu
+
+# Accepted |engine logit - oracle logit| in units of the step's logit std: (max over the
+# vocabulary, mean over the vocabulary); for greedy configs also the oracle top-2 margin
+# (in logit stds) above which the token must be the oracle's, and how many such steps the
+# run must hold. Measured on MI355X (max / mean): C2 0.169 / 0.029, 7B 0.294 / 0.043,
+# VL-3B 0.255 / 0.044. The bounds sit about 1.5x above; an error in any operator moves
+# the mean by an order of magnitude. The clear-step margin is >= 5 standard deviations
+# of the noise on the difference of two logits (about 1.8 x the mean error): below it a
+# flip is bf16 noise. On the VL-3B shape that noise is the model's own: nudging 1 % of
+# the oracle's attention outputs by one bf16 ulp moves its logits by up to 0.2 (0.03 on
+# average), as much as the whole engine-oracle difference.
+C2_TOL = (0.3, 0.05, 0.3, 4)
+B7_TOL = (0.45, 0.07)
+VL_TOL = (0.4, 0.07, 0.45, 0)
 
 
 def _cfg(shape):
@@ -54,43 +72,85 @@ def _oracle_from_gpu(shape, wdev, max_tokens):
 
 
 def _run_engine(tmp, shape, wdev, req, **cfg):
+    """Runs the request on an engine that records every step's fp32 logits
+    (runtime.debug_logits) twice (tokens and logits must repeat bit for bit), then once
+    on the production configuration (greedy: the fused LM-head top-1), whose tokens must
+    be the same. Returns (tokens, logits [steps, vocab])."""
     S.register_weights(wdev)
     mdir = S.write_model_dir(os.path.join(tmp, "model"), shape)
+    req.set_ignore_stop_tokens(True)
+    ecfg = S.write_engine_config(os.path.join(tmp, "engine_dbg.json"), mdir, debug_logits=True, **cfg)
+    eng = edge_fm.EdgeFM(ecfg)
+    toks = eng.generate(req).token_ids()
+    lg = eng.last_logits()
+    again = eng.generate(req).token_ids()
+    lg_again = eng.last_logits()
+    del eng
+    assert toks == again, "the same request must give the same tokens"
+    assert (lg == lg_again).all(), "the same request must give the same logits bit for bit"
     ecfg = S.write_engine_config(os.path.join(tmp, "engine.json"), mdir, **cfg)
     eng = edge_fm.EdgeFM(ecfg)
-    req.set_ignore_stop_tokens(True)
-    toks = eng.generate(req).token_ids()
-    again = eng.generate(req).token_ids()
+    prod = eng.generate(req).token_ids()
     del eng
     torch.cuda.synchronize()
-    return toks, again
+    assert prod == toks, "the production configuration (fused LM-head top-1) must give the recorded tokens"
+    return toks, lg
 
 
-def _greedy_steps(orc, prompt, toks, embeds=None, pos=None, decode_pos=None):
-    """(gpu token, oracle argmax, top-2 margin, top-1 minus gpu-token logit) per step."""
+def _oracle_logits(orc, prompt, toks, embeds=None, pos=None, decode_pos=None):
+    """The oracle's fp32 logits for every step, teacher-forced on the GPU's tokens."""
     st = orc.new_state()
     logits = orc.forward(st, prompt, embeds=embeds, position_ids=pos)
     out = []
     for i, tok in enumerate(toks):
-        ref = int(O.argmax_lowest(logits.unsqueeze(0))[0])
-        top2 = torch.topk(logits.double(), 2).values
-        out.append((tok, ref, float(top2[0] - top2[1]), float(logits[ref] - logits[tok])))
+        out.append(logits.numpy().astype(np.float32))
         if i + 1 < len(toks):
             p = None if decode_pos is None else decode_pos(i)
             logits = orc.forward(st, torch.tensor([tok], dtype=torch.int32), position_ids=p)
+    return np.stack(out)
+
+
+def _logit_errors(tag, lg_gpu, lg_orc):
+    """Per step: max and mean |engine logit - oracle logit| relative to the spread (std)
+    of the oracle's logits of that step."""
+    out = []
+    for g, o in zip(lg_gpu, lg_orc):
+        d = np.abs(g.astype(np.float64) - o.astype(np.float64))
+        sd = float(o.astype(np.float64).std())
+        out.append((float(d.max()) / sd, float(d.mean()) / sd, float(d.max()), float(d.mean())))
+    _log(f"{tag}: |logit - oracle| / logit std per step: max {max(e[0] for e in out):.4f}, "
+         f"mean {max(e[1] for e in out):.5f} (absolute: max {max(e[2] for e in out):.4f}, "
+         f"mean {np.mean([e[3] for e in out]):.5f})")
     return out
 
 
-def _check_greedy(steps, tag, min_clear):
-    _log(f"{tag} per-step (gpu, oracle, top-2 margin, gap): " +
-         " ".join(f"{t}/{r}/{m:.3f}/{g:.3f}" for t, r, m, g in steps))
-    for i, (tok, ref, margin, gap) in enumerate(steps):
-        if tok != ref:
-            assert gap < 0.05, f"{tag} step {i}: gpu {tok} vs oracle {ref}, logit gap {gap:.4f}"
-            assert margin < 0.05, f"{tag} step {i}: clear step (margin {margin:.4f}) differs"
-    clear = sum(1 for _, _, m, _ in steps if m >= 0.05)
-    exact = sum(1 for t, r, _, _ in steps if t == r)
-    _log(f"{tag}: {exact}/{len(steps)} exact, {clear} clear steps (margin >= 0.05), all clear steps match")
+def _check_logits(tag, errs, tol_max, tol_mean):
+    worst_max, worst_mean = max(e[0] for e in errs), max(e[1] for e in errs)
+    assert worst_mean <= tol_mean, f"{tag}: mean logit error {worst_mean:.5f} logit std (> {tol_mean})"
+    assert worst_max <= tol_max, f"{tag}: max logit error {worst_max:.4f} logit std (> {tol_max})"
+
+
+def _check_greedy(tag, toks, lg_gpu, lg_orc, tol_max, tol_mean, clear_sd, min_clear):
+    """Every token is the argmax (lowest index on ties) of the engine's own logits; the
+    engine's logits follow the oracle's (errors in units of the step's logit std, bounded
+    by tol_max / tol_mean); and wherever the oracle's top-2 margin exceeds clear_sd logit
+    stds the token is the oracle's argmax."""
+    errs = _logit_errors(tag, lg_gpu, lg_orc)
+    report, clear = [], 0
+    for i, tok in enumerate(toks):
+        g, o = lg_gpu[i], lg_orc[i]
+        assert tok == int(O.argmax_lowest(torch.from_numpy(g).unsqueeze(0))[0]), \
+            f"{tag} step {i}: token {tok} is not the argmax of the engine's logits"
+        ref = int(O.argmax_lowest(torch.from_numpy(o).unsqueeze(0))[0])
+        top2 = np.sort(o.astype(np.float64))[-2:]
+        margin = float(top2[1] - top2[0]) / float(o.astype(np.float64).std())
+        report.append(f"{tok}/{ref}/{margin:.3f}/{errs[i][0]:.3f}")
+        if margin > clear_sd:
+            clear += 1
+            assert tok == ref, f"{tag} step {i}: clear step (oracle margin {margin:.4f} std) gives {tok}, oracle {ref}"
+    _log(f"{tag} per-step (gpu, oracle, oracle top-2 margin / std, max |logit - oracle| / std): " + " ".join(report))
+    _log(f"{tag}: {clear} clear steps (margin > {clear_sd} std) all match")
+    _check_logits(tag, errs, tol_max, tol_mean)
     assert clear >= min_clear, f"{tag}: only {clear} steps with a clear oracle margin"
 
 
@@ -101,15 +161,14 @@ def test_c2_headline_512_prompt_32_greedy_tokens(gpu):
     wdev = S.synthetic_weights_gpu(shape, seed=3, std=0.02)
     prompt = torch.randint(0, shape.vocab, (P,), generator=torch.Generator().manual_seed(11)).to(torch.int32)
     with tempfile.TemporaryDirectory() as tmp:
-        toks, again = _run_engine(tmp, shape, wdev, edge_fm.Request(0, prompt.tolist()), max_tokens=P + G,
-                                  max_new_tokens=G, use_graph=True)
-    assert len(toks) == G and toks == again
+        toks, lg = _run_engine(tmp, shape, wdev, edge_fm.Request(0, prompt.tolist()), max_tokens=P + G,
+                               max_new_tokens=G, use_graph=True)
+    assert len(toks) == G
     _log("C2: oracle")
     orc = _oracle_from_gpu(shape, wdev, P + G)
     del wdev
     torch.cuda.empty_cache()
-    steps = _greedy_steps(orc, prompt, toks)
-    _check_greedy(steps, "C2 1.5B 512+32", min_clear=8)
+    _check_greedy("C2 1.5B 512+32", toks, lg, _oracle_logits(orc, prompt, toks), *C2_TOL)
 
 
 def test_7b_shape_untied_head_top_p_sampling(gpu):
@@ -127,34 +186,26 @@ def test_7b_shape_untied_head_top_p_sampling(gpu):
         torch.bfloat16)
     prompt = torch.randint(0, shape.vocab, (P,), generator=torch.Generator().manual_seed(12)).to(torch.int32)
     with tempfile.TemporaryDirectory() as tmp:
-        toks, again = _run_engine(tmp, shape, wdev, edge_fm.Request(0, prompt.tolist()), max_tokens=P + G,
-                                  max_new_tokens=G, use_graph=True, temperature=T, top_p=TOP_P, seed=SEED)
-    assert len(toks) == G and toks == again, "same seed must give the same tokens"
+        toks, lg = _run_engine(tmp, shape, wdev, edge_fm.Request(0, prompt.tolist()), max_tokens=P + G,
+                               max_new_tokens=G, use_graph=True, temperature=T, top_p=TOP_P, seed=SEED)
+    assert len(toks) == G
     _log("7B: oracle")
     orc = _oracle_from_gpu(shape, wdev, P + G)
     del wdev
     torch.cuda.empty_cache()
-    st = orc.new_state()
-    logits = orc.forward(st, prompt)
-    exact, report, nuclei = 0, [], []
+    lg_orc = _oracle_logits(orc, prompt, toks)
+    errs = _logit_errors("7B", lg, lg_orc)
+    report, nuclei = [], []
     for i, tok in enumerate(toks):
-        lg = logits.numpy().astype("float32")
-        ref, info = O.sample_top_p(lg, T, TOP_P, SEED, i)
-        margin = O.sample_margin(lg, T, TOP_P, SEED, i)
+        # the draw: exactly the oracle sampler's on the engine's own logits (same seed,
+        # counter = response index), with no allowance
+        ref, info = O.sample_top_p(lg[i], T, TOP_P, SEED, i)
+        assert tok == ref, f"7B step {i}: engine drew {tok}, the oracle sampler on the engine's logits draws {ref}"
         nuclei.append(info["nucleus"])
-        report.append(f"{tok}/{ref}/{margin:.4f}/{info['nucleus']}")
-        if tok == ref:
-            exact += 1
-        else:
-            assert margin < 0.1, f"7B step {i}: gpu {tok} vs oracle {ref}, margin {margin:.4f}"
-        if i + 1 < G:
-            logits = orc.forward(st, torch.tensor([tok], dtype=torch.int32))
-    _log("7B per-step (gpu, oracle, boundary margin, nucleus size): " + " ".join(report))
-    _log(f"7B: {exact}/{G} sampled tokens equal the oracle sampler's")
+        report.append(f"{tok}/{info['nucleus']}/{errs[i][0]:.3f}")
+    _log("7B per-step (token, nucleus size, max |logit - oracle| / std): " + " ".join(report))
     assert max(nuclei) > 1, "nucleus never held more than one token: the test would not exercise sampling"
-    # Measured: the differing draws all sit within 0.5 % of a boundary (bf16 noise in the
-    # 28-layer hidden state moves the 7B logits by a few hundredths).
-    assert exact >= G // 2
+    _check_logits("7B", errs, *B7_TOL)
 
 
 def test_vl3b_shape_1280_vision_rows_mrope(gpu):
@@ -184,9 +235,9 @@ def test_vl3b_shape_1280_vision_rows_mrope(gpu):
                           edge_fm.Tensor(pos_g.data_ptr(), [3, len(ids)], edge_fm.DType.Int32, edge_fm.Device.GPU, 0,
                                          False))
     with tempfile.TemporaryDirectory() as tmp:
-        toks, again = _run_engine(tmp, shape, wdev, req, max_tokens=nv + nt + G, max_new_tokens=G, use_graph=True,
-                                  model_name="qwen2_5_vl")
-    assert len(toks) == G and toks == again
+        toks, lg = _run_engine(tmp, shape, wdev, req, max_tokens=nv + nt + G, max_new_tokens=G, use_graph=True,
+                               model_name="qwen2_5_vl")
+    assert len(toks) == G
     _log("VL-3B: oracle")
     orc = _oracle_from_gpu(shape, wdev, nv + nt + G)
     emb = O.embedding(torch.tensor(ids, dtype=torch.int32), orc.w["embed"].to(torch.bfloat16), vis, embed_id)
@@ -196,5 +247,5 @@ def test_vl3b_shape_1280_vision_rows_mrope(gpu):
     def dpos(i):
         return torch.full((3, 1), last + 1 + i, dtype=torch.int32)
 
-    steps = _greedy_steps(orc, torch.tensor(ids, dtype=torch.int32), toks, embeds=emb, pos=pos, decode_pos=dpos)
-    _check_greedy(steps, "VL-3B 1280 vision + 64 text", min_clear=4)
+    lg_orc = _oracle_logits(orc, torch.tensor(ids, dtype=torch.int32), toks, embeds=emb, pos=pos, decode_pos=dpos)
+    _check_greedy("VL-3B 1280 vision + 64 text", toks, lg, lg_orc, *VL_TOL)

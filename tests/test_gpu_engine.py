@@ -8,6 +8,7 @@ tests/test_oracle.py)."""
 import os
 import tempfile
 
+import numpy as np
 import pytest
 import torch
 
@@ -218,37 +219,41 @@ def test_qwen25_1p5b_shape_greedy_matches_oracle(gpu):
 
 @pytest.mark.parametrize("use_graph", [True, False])
 def test_tiny_top_p_sampling_matches_oracle(gpu, use_graph):
-    """temperature 0.8 / top-p 0.9: every token is the oracle sampler's choice on the
-    oracle's logits (teacher-forced on the GPU's tokens) with the draw counter = the
-    token's response index; a mismatch is accepted only where the decision lies within
-    10 % (relative mass) of a boundary, the reach of bf16 logit noise at T = 0.8."""
+    """temperature 0.8 / top-p 0.9. The engine records every step's fp32 logits
+    (runtime.debug_logits): every token must be exactly the oracle sampler's draw on the
+    engine's own logits (same seed, draw counter = the token's response index), and those
+    logits must follow the oracle's (teacher-forced on the GPU's tokens) within bf16
+    noise. A wrong draw counter, a wrong logits buffer or a sampler change cannot hide."""
     T, P, SEED = 0.8, 0.9, 5
     w = O.random_weights(_oracle_cfg(TINY), seed=31, std=0.2)
     prompt = torch.randint(0, TINY.vocab, (32,), generator=torch.Generator().manual_seed(8)).to(torch.int32)
     with tempfile.TemporaryDirectory() as tmp:
         eng, keep = _engine(tmp, TINY, w, max_tokens=128, max_new_tokens=32, use_graph=use_graph, temperature=T,
-                            top_p=P, seed=SEED)
+                            top_p=P, seed=SEED, debug_logits=True)
         req = edge_fm.Request(0, prompt.tolist())
         req.set_ignore_stop_tokens(True)
         toks = eng.generate(req).token_ids()
+        lg_gpu = eng.last_logits()
         again = eng.generate(req).token_ids()
+        lg_again = eng.last_logits()
         del eng
     assert toks == again, "same seed must give the same tokens"
-    assert len(toks) == 32
+    assert (lg_gpu == lg_again).all(), "the same request must give the same logits bit for bit"
+    assert len(toks) == 32 and lg_gpu.shape == (32, TINY.vocab)
     orc = O.Qwen2Oracle(_oracle_cfg(TINY), O.fuse_weights(_oracle_cfg(TINY), w), max_tokens=128)
     st = orc.new_state()
     logits = orc.forward(st, prompt)
-    exact = 0
+    worst_max = worst_mean = 0.0
     for i, tok in enumerate(toks):
-        lg = logits.numpy().astype("float32")
-        ref, _ = O.sample_top_p(lg, T, P, SEED, i)
-        if tok == ref:
-            exact += 1
-        else:
-            margin = O.sample_margin(lg, T, P, SEED, i)
-            assert margin < 0.1, f"step {i}: gpu {tok} vs oracle {ref}, margin {margin:.4f}"
+        ref, _ = O.sample_top_p(lg_gpu[i], T, P, SEED, i)
+        assert tok == ref, f"step {i}: engine drew {tok}, the oracle sampler on the engine's logits draws {ref}"
+        o = logits.numpy().astype(np.float64)
+        d = np.abs(lg_gpu[i].astype(np.float64) - o)
+        worst_max, worst_mean = max(worst_max, d.max() / o.std()), max(worst_mean, d.mean() / o.std())
         logits = orc.forward(st, torch.tensor([tok], dtype=torch.int32))
-    assert exact >= 24
+    print(f"tiny top-p: |logit - oracle| / logit std: max {worst_max:.4f}, mean {worst_mean:.5f}")
+    # measured 0.435 / 0.081 (std-0.2 weights: larger activations, larger bf16 noise)
+    assert worst_max < 0.65 and worst_mean < 0.12, f"engine logits off the oracle's: {worst_max:.4f} / {worst_mean:.5f}"
 
 
 def test_top_p_sampling_seeds_differ_and_config_checks(gpu):

@@ -146,6 +146,60 @@ def test_attention_decode_prerotated_except_newest(gpu, hq, hkv, hd, kv_len, mer
     assert_close_bf16(got[kv_len - 1], k_rot[kv_len - 1], rtol=1e-2, atol=1e-2, what="newest row stored rotated")
 
 
+@pytest.mark.parametrize("hq,hkv,hd", HEAD_CASES)
+@pytest.mark.parametrize("kv_len,max_kv", [(1, 64), (31, 31), (33, 700), (640, 768), (1025, 1100), (3000, 3000),
+                                           (5000, 5000)])
+@pytest.mark.parametrize("layout", ["rope_on_read", "rotated_except_newest", "no_rope"])
+def test_attention_decode_one_wave_splits(gpu, knob, hq, hkv, hd, kv_len, max_kv, layout):
+    """The one-wave split kernel of short and mid contexts (32- and 64-key splits, a
+    partial last tile, a single split that writes the output itself) against the oracle
+    and against the kernels those lengths ran before it (EFM_KNOB_DECODE_TILE), over the
+    three cache layouts: un-rotated keys rotated on read (the reference's), rotated keys
+    with this step's row still un-rotated (the engine's), and no RoPE (M-RoPE models).
+    Rows >= L hold NaN."""
+    torch.manual_seed(kv_len * 7 + hd)
+    q = torch.randn(1, hq, hd, dtype=torch.bfloat16)
+    k = torch.randn(kv_len, hkv, hd, dtype=torch.bfloat16)
+    v = torch.randn(kv_len, hkv, hd, dtype=torch.bfloat16)
+    rope = layout != "no_rope"
+    ref = O.attention_decode(q, k, v, kv_len, O.AttnCtx(hq, hkv, hd, rope=rope))
+    kstore = k
+    if layout == "rotated_except_newest":
+        kstore = O.rope_llama(k, torch.arange(kv_len), 1.0e6).to(torch.bfloat16)
+        kstore[kv_len - 1] = k[kv_len - 1]
+    ctx = C.make_attention_ctx(hq, hkv, hd, rope=rope)
+    if layout == "rotated_except_newest":
+        ctx.k_already_prerotated = C.EFM_K_PREROTATED_EXCEPT_NEWEST
+    d_len = torch.tensor([kv_len], dtype=torch.int32, device=gpu)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=gpu)
+    qg = q.to(gpu)
+    outs, caches = [], []
+    for tile_off in (0, 1):
+        knob(C.EFM_KNOB_DECODE_TILE, tile_off)
+        kc = torch.full((max_kv, hkv, hd), float("nan"), dtype=torch.bfloat16)
+        vc = torch.full((max_kv, hkv, hd), float("nan"), dtype=torch.bfloat16)
+        kc[:kv_len] = kstore
+        vc[:kv_len] = v
+        kc, vc = kc.to(gpu), vc.to(gpu)
+        o = torch.empty_like(qg)
+        C.call("efm_attention_decode", ctx, ptr(qg), ptr(kc), ptr(vc), ptr(o), 0, ptr(d_len), max_kv, ptr(ws),
+               ws.numel(), stream())
+        torch.cuda.synchronize()
+        outs.append(o)
+        caches.append(kc.cpu())
+    what = f"{layout} hq={hq} hkv={hkv} hd={hd} L={kv_len}"
+    assert torch.isfinite(outs[0].float()).all(), what
+    assert_close_bf16(outs[0], ref, what="one-wave splits vs oracle, " + what)
+    assert_close_bf16(outs[0], outs[1], what="one-wave splits vs previous kernels, " + what)
+    if layout == "rotated_except_newest":
+        # the newest row is stored back rotated the same way by both paths; no other row moves
+        assert torch.equal(caches[0][: kv_len - 1], kstore[: kv_len - 1])
+        assert torch.isnan(caches[0][kv_len:].float()).all()
+        assert torch.equal(caches[0][kv_len - 1], caches[1][kv_len - 1])
+    else:
+        assert torch.equal(caches[0][:kv_len], kstore), "the call must not write the cache"
+
+
 def test_attention_decode_partials_ignore_stale_rows(gpu):
     """Rows >= L of the cache hold NaN / Inf; the partials + merge path must give the
     same result as a cache that ends at L."""
@@ -299,8 +353,9 @@ def test_act_and_mul(gpu, layout, batch, inter):
     C.call("efm_act_and_mul", batch, inter, layout, ptr(xg), ptr(out), stream())
     torch.cuda.synchronize()
     ref = O.act_and_mul(x, up_first=(layout == C.EFM_LAYOUT_UP_GATE))
-    # tests/operators/test_fused_gate_up_activation.py:75-79 (2e-2 / 6.25e-2)
-    assert_close_bf16(out, ref, rtol=2e-2, atol=6.25e-2)
+    # the north star's per-operator bound (2e-2 / 2e-2; the reference's own test allows
+    # atol 6.25e-2, tests/operators/test_fused_gate_up_activation.py:75-79)
+    assert_close_bf16(out, ref, rtol=2e-2, atol=2e-2)
 
 
 @pytest.mark.parametrize("up", [1.0, 0.7421875, -1.3984375, 3.0])
@@ -392,7 +447,7 @@ def test_gemm_large_shapes_row_sample_vs_oracle(gpu, m, k, n, bias, kind):
     rows = torch.tensor([0, m // 2, m - 1])
     xs = x[rows].cpu()
     if kind == "swiglu":
-        assert_close_bf16(y[rows], O.gate_up_swiglu(xs, w.cpu()), rtol=2e-2, atol=6.25e-2)
+        assert_close_bf16(y[rows], O.gate_up_swiglu(xs, w.cpu()), rtol=2e-2, atol=2e-2)
     elif kind == "f32":
         torch.testing.assert_close(y[rows].cpu(), O.linear(xs, w.cpu(), out_f32=True), rtol=1e-4, atol=1e-4)
     else:
@@ -409,7 +464,7 @@ def test_fused_gate_up_swiglu(gpu, hidden, inter, m):
     xg, wg = x.to(gpu), w.to(gpu)
     C.call("efm_fused_gate_up_swiglu", m, hidden, inter, ptr(xg), ptr(wg), ptr(out), stream())
     torch.cuda.synchronize()
-    assert_close_bf16(out, O.gate_up_swiglu(x, w), rtol=2e-2, atol=6.25e-2)
+    assert_close_bf16(out, O.gate_up_swiglu(x, w), rtol=2e-2, atol=2e-2)
 
 
 def _top1_ref_ok(logits: torch.Tensor, tok: int) -> bool:
@@ -504,7 +559,7 @@ def test_gemm_tile_shapes_agree_bit_exact(gpu, kind):
     rows = torch.tensor([0, 57, 99])
     xs = x[rows].cpu()
     if kind == "swiglu":
-        assert_close_bf16(heads[0][rows], O.gate_up_swiglu(xs, w.cpu()), rtol=2e-2, atol=6.25e-2)
+        assert_close_bf16(heads[0][rows], O.gate_up_swiglu(xs, w.cpu()), rtol=2e-2, atol=2e-2)
     else:
         assert_close_bf16(heads[0][rows], O.linear(xs, w.cpu(), b.cpu()))
 
@@ -542,7 +597,7 @@ def test_gemm_wide_kernel_matches_narrow_bit_exact(gpu, knob, m, k, n, kind):
     rows = torch.tensor([0, m // 2, m - 1])
     xs = x[rows].cpu()
     if kind == "swiglu":
-        assert_close_bf16(outs[1][rows], O.gate_up_swiglu(xs, w.cpu()), rtol=2e-2, atol=6.25e-2)
+        assert_close_bf16(outs[1][rows], O.gate_up_swiglu(xs, w.cpu()), rtol=2e-2, atol=2e-2)
     elif kind == "f32":
         ref = O.linear(xs, w.cpu(), b.cpu(), out_f32=True)
         torch.testing.assert_close(outs[1][rows].cpu(), ref, rtol=1e-3, atol=1e-3)
@@ -725,7 +780,7 @@ def test_gate_up_swiglu_ws_is_fused_kernel(gpu, m, hidden, inter):
     diff = (two.float() - fused.float()).abs()
     assert float(diff.max()) <= float(fused.float().abs().max()) * 2 ** -6
     rows = torch.tensor([0, m - 1])
-    assert_close_bf16(out[rows], O.gate_up_swiglu(x[rows].cpu(), w.cpu()), rtol=2e-2, atol=6.25e-2)
+    assert_close_bf16(out[rows], O.gate_up_swiglu(x[rows].cpu(), w.cpu()), rtol=2e-2, atol=2e-2)
 
 
 def test_sampler_greedy_ties(gpu):
@@ -811,6 +866,122 @@ def test_decode_norm_qkv_matches_unfused(gpu, hidden, hq, hkv, hd, layer0):
     assert kc[:12].abs().sum() == 0 and kc[13:].abs().sum() == 0
 
 
+@pytest.mark.parametrize("hidden,hq,hkv,hd", [(1536, 12, 2, 128), (896, 14, 2, 64), (3584, 28, 4, 128)])
+@pytest.mark.parametrize("layer0", [True, False])
+@pytest.mark.parametrize("pos_off", [0, 5])
+def test_decode_norm_qkv_rope_matches_oracle(gpu, hidden, hq, hkv, hd, layer0, pos_off):
+    """efm_decode_norm_qkv_rope: the projection of efm_decode_norm_qkv with q and the new
+    key rotated at position L - 1 (+ offset) in the epilogue: q_out and the K slot equal
+    the oracle's rope_llama of the bf16 projection (one bf16 rounding), V and the residual
+    are exact; no other cache row is written. Then decode attention with pos NONE over
+    that cache equals the oracle's RoPE-on-read attention over the un-rotated keys."""
+    torch.manual_seed(1 + hd)
+    eps, theta, L = 1e-6, 1.0e6, 300
+    qd, kvd = hq * hd, hkv * hd
+    h = torch.randn(1, hidden, dtype=torch.bfloat16)
+    r = torch.randn(1, hidden, dtype=torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(hidden)).to(torch.bfloat16)
+    W = (torch.randn(qd + 2 * kvd, hidden) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(qd + 2 * kvd) * 0.02).to(torch.bfloat16)
+    k_prev = torch.randn(L - 1, hkv, hd, dtype=torch.bfloat16)
+    v_prev = torch.randn(L - 1, hkv, hd, dtype=torch.bfloat16)
+    rows = L + 20
+    kc = torch.zeros(rows, kvd, dtype=torch.bfloat16)
+    vc = torch.zeros(rows, kvd, dtype=torch.bfloat16)
+    kc[: L - 1] = O.rope_llama(k_prev, torch.arange(L - 1) + pos_off, theta).to(torch.bfloat16).reshape(L - 1, kvd)
+    vc[: L - 1] = v_prev.reshape(L - 1, kvd)
+    kc, vc = kc.to(gpu), vc.to(gpu)
+    d_len = torch.tensor([L], dtype=torch.int32, device=gpu)
+    q_out = torch.empty(1, qd, dtype=torch.bfloat16, device=gpu)
+    r_out = torch.empty(1, hidden, dtype=torch.bfloat16, device=gpu)
+    ctx = C.make_attention_ctx(hq, hkv, hd, rope_theta=theta, q_rope_pos_offset=pos_off, k_rope_pos_offset=pos_off)
+    hg, rg, nwg, Wg, bg = h.to(gpu), r.to(gpu), nw.to(gpu), W.to(gpu), b.to(gpu)
+    C.call("efm_decode_norm_qkv_rope", ctx, hidden, eps, ptr(hg), None if layer0 else ptr(rg), ptr(r_out), ptr(nwg),
+           ptr(Wg), ptr(bg), ptr(q_out), ptr(kc), ptr(vc), ptr(d_len), stream())
+    torch.cuda.synchronize()
+    if layer0:
+        n, res = O.rms_norm(h, nw, eps), h
+    else:
+        n, res = O.fused_add_rms_norm(h, r, nw, eps)
+    qkv = O.linear(n, W, b)
+    pos = torch.tensor([L - 1 + pos_off])
+    q_ref = O.rope_llama(qkv[:, :qd].reshape(1, hq, hd), pos, theta).to(torch.bfloat16).reshape(1, qd)
+    k_new = qkv[:, qd:qd + kvd].reshape(1, hkv, hd)
+    k_ref = O.rope_llama(k_new, pos, theta).to(torch.bfloat16).reshape(1, kvd)
+    assert torch.equal(r_out.cpu(), res)
+    assert_close_bf16(q_out, q_ref, what="rotated q")
+    assert_close_bf16(kc[L - 1:L], k_ref, what="rotated k slot")
+    assert_close_bf16(vc[L - 1:L], qkv[:, qd + kvd:], what="v slot")
+    assert kc[L:].abs().sum() == 0 and vc[L:].abs().sum() == 0
+    # attention over the rotated cache without RoPE == RoPE-on-read over un-rotated keys
+    k_all = torch.cat([k_prev, k_new.to(torch.bfloat16)])
+    v_all = torch.cat([v_prev, qkv[:, qd + kvd:].reshape(1, hkv, hd)])
+    ref = O.attention_decode(qkv[:, :qd].reshape(1, hq, hd), k_all, v_all, L,
+                             O.AttnCtx(hq, hkv, hd, rope_theta=theta, q_rope_pos_offset=pos_off,
+                                       k_rope_pos_offset=pos_off))
+    actx = C.make_attention_ctx(hq, hkv, hd, rope=False)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(actx, rows), dtype=torch.uint8, device=gpu)
+    o = torch.empty(1, hq, hd, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_attention_decode", actx, ptr(q_out), ptr(kc), ptr(vc), ptr(o), 0, ptr(d_len), rows, ptr(ws),
+           ws.numel(), stream())
+    torch.cuda.synchronize()
+    assert_close_bf16(o, ref, what="attention over the rotated cache")
+
+
+def test_decode_front_half_7b_16k_engine_chain(gpu):
+    """The decode front half of one Qwen2.5-7B-shaped layer at C5's context, through the
+    C-ABI chain the engine runs: norm + QKV with q and the new key rotated in the epilogue
+    (slot 16447), decode attention over 16,448 rotated cache rows (28/4 heads: the 8-wave
+    kernel, 58 splits of 288 keys of a 16,512-row cache, then the split merge kernel), and
+    the o_proj GEMV; against the oracle's layer with RoPE on read over the un-rotated keys
+    (Appendix-A rounding points)."""
+    torch.manual_seed(21)
+    hidden, hq, hkv, hd, eps, theta = 3584, 28, 4, 128, 1e-6, 1.0e6
+    L, max_kv = 16448, 16512
+    qd, kvd = hq * hd, hkv * hd
+    h = torch.randn(1, hidden, dtype=torch.bfloat16)
+    r = torch.randn(1, hidden, dtype=torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(hidden)).to(torch.bfloat16)
+    W = (torch.randn(qd + 2 * kvd, hidden) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(qd + 2 * kvd) * 0.02).to(torch.bfloat16)
+    Wo = (torch.randn(hidden, qd) * 0.02).to(torch.bfloat16)
+    k_prev = torch.randn(L - 1, hkv, hd, dtype=torch.bfloat16)
+    v_prev = torch.randn(L - 1, hkv, hd, dtype=torch.bfloat16)
+    kc = torch.full((max_kv, kvd), float("nan"), dtype=torch.bfloat16)
+    vc = torch.full((max_kv, kvd), float("nan"), dtype=torch.bfloat16)
+    kc[: L - 1] = O.rope_llama(k_prev, torch.arange(L - 1), theta).to(torch.bfloat16).reshape(L - 1, kvd)
+    vc[: L - 1] = v_prev.reshape(L - 1, kvd)
+    kc, vc = kc.to(gpu), vc.to(gpu)
+    d_len = torch.tensor([L], dtype=torch.int32, device=gpu)
+    hg, rg, nwg, Wg, bg, Wog = (t.to(gpu) for t in (h, r, nw, W, b, Wo))
+    q = torch.empty(1, qd, dtype=torch.bfloat16, device=gpu)
+    r_out = torch.empty(1, hidden, dtype=torch.bfloat16, device=gpu)
+    attn = torch.empty(1, qd, dtype=torch.bfloat16, device=gpu)
+    a = torch.empty(1, hidden, dtype=torch.bfloat16, device=gpu)
+    cq = C.make_attention_ctx(hq, hkv, hd, rope_theta=theta)
+    ca = C.make_attention_ctx(hq, hkv, hd, rope=False)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ca, max_kv), dtype=torch.uint8, device=gpu)
+    C.call("efm_decode_norm_qkv_rope", cq, hidden, eps, ptr(hg), ptr(rg), ptr(r_out), ptr(nwg), ptr(Wg), ptr(bg),
+           ptr(q), ptr(kc), ptr(vc), ptr(d_len), stream())
+    C.call("efm_attention_decode", ca, ptr(q), ptr(kc), ptr(vc), ptr(attn), 0, ptr(d_len), max_kv, ptr(ws), ws.numel(),
+           stream())
+    C.call("efm_linear", 1, qd, hidden, ptr(attn), ptr(Wog), None, ptr(a), C.EFM_DTYPE_BF16, stream())
+    torch.cuda.synchronize()
+    n, res = O.fused_add_rms_norm(h, r, nw, eps)
+    qkv = O.linear(n, W, b)
+    k_all = torch.cat([k_prev, qkv[:, qd:qd + kvd].reshape(1, hkv, hd)])
+    v_all = torch.cat([v_prev, qkv[:, qd + kvd:].reshape(1, hkv, hd)])
+    o_ref = O.attention_decode(qkv[:, :qd].reshape(1, hq, hd), k_all, v_all, L,
+                               O.AttnCtx(hq, hkv, hd, rope_theta=theta)).reshape(1, qd)
+    a_ref = O.linear(o_ref, Wo)
+    assert torch.equal(r_out.cpu(), res)
+    assert torch.isfinite(attn.float()).all()
+    assert_close_bf16(attn, o_ref, what="attention over 16,448 rows")
+    assert_close_bf16(a, a_ref, what="o_proj of the attention output")
+    assert torch.isnan(kc[L:].float()).all(), "rows past the newest must not be written"
+    assert_close_bf16(vc[L - 1:L], qkv[:, qd + kvd:], what="v slot")
+
+
 @pytest.mark.parametrize("hidden,inter", [(1536, 8960), (896, 4864), (3584, 18944)])
 def test_decode_norm_gate_up_swiglu_matches_unfused(gpu, hidden, inter):
     torch.manual_seed(0)
@@ -827,7 +998,7 @@ def test_decode_norm_gate_up_swiglu_matches_unfused(gpu, hidden, inter):
     torch.cuda.synchronize()
     n2, res = O.fused_add_rms_norm(a, r, nw, eps)
     assert torch.equal(r_out.cpu(), res)
-    assert_close_bf16(out, O.gate_up_swiglu(n2, W), rtol=2e-2, atol=6.25e-2)
+    assert_close_bf16(out, O.gate_up_swiglu(n2, W), rtol=2e-2, atol=2e-2)
 
 
 @pytest.mark.parametrize("hidden,vocab", [(1536, 151936), (896, 151936)])

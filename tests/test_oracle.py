@@ -336,6 +336,31 @@ def test_sage_quant_blocks_bounds_and_rounding():
     assert float(s[0, 0]) == 1.0 and q.flatten().tolist() == [127, 0, 2, -2, 2]
 
 
+def test_sage_kmean_closed_form():
+    """sage_kmean is the per-(KV head, channel) mean over tokens: a float64 numpy mean
+    over axis 0 rounded once to fp32, exactly; a hand-worked case; the smoothed keys have a
+    zero token mean. A sum without the division, a mean over the wrong axis or an fp32
+    accumulation fails one of these."""
+    torch.manual_seed(4)
+    k = (torch.randn(333, 4, 128) * 3 + 1.5).to(torch.bfloat16)
+    m = O.sage_kmean(k)
+    ref = np.mean(k.float().numpy().astype(np.float64), axis=0).astype(np.float32)
+    assert m.shape == (4, 128) and m.dtype == torch.float32
+    assert np.array_equal(m.numpy(), ref)
+    # tokens 1, 2, 4 of one channel: 7/3 rounded to fp32; a constant channel keeps its value
+    t = torch.zeros(3, 1, 2, dtype=torch.bfloat16)
+    t[:, 0, 0] = torch.tensor([1.0, 2.0, 4.0])
+    t[:, 0, 1] = -0.75
+    mt = O.sage_kmean(t)
+    assert float(mt[0, 0]) == float(np.float32(7.0 / 3.0)) and float(mt[0, 1]) == -0.75
+    # fp32 accumulation of 2^24 + 1 + 1 + ... would lose the ones; float64 keeps them
+    big = torch.ones(4097, 1, 1, dtype=torch.bfloat16)
+    big[0] = 2.0 ** 24
+    assert float(O.sage_kmean(big)[0, 0]) == float(np.float32((2.0 ** 24 + 4096) / 4097))
+    ks = k.float() - m[None]
+    assert float(ks.double().mean(0).abs().max()) < 1e-5
+
+
 def test_sage_k_smoothing_is_softmax_invariant():
     """Adding a per-channel constant to K does not change the (exact) attention, which is
     what makes subtracting the K mean legal; the oracle's result barely moves."""
