@@ -128,9 +128,10 @@ def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20
     all layers' real weights: a HIP graph of reps x layers launches of one kernel is
     replayed between two HIP events on the replay stream (avg = kernel duration plus the
     graph's inter-node gap).
-      norm_qkv   efm_decode_norm_qkv: add-norm + fused QKV GEMV + bias + K/V slot write
+      norm_qkv   efm_decode_norm_qkv_rope: add-norm + fused QKV GEMV + bias, q and the new
+                 key rotated in the epilogue, K/V slot write
       attention  efm_decode_attention_partials: split attention over ctx_len cached rows
-                 (rotated cache; the newest key rotated and stored back)
+                 (rotated cache, no positional encoding in the attention)
       o_proj     efm_decode_attention_merge_o_proj: split merge + o_proj GEMV
       gate_up    efm_decode_norm_gate_up_swiglu: add-norm + gate/up GEMV + SwiGLU
       down       efm_linear m = 1: down_proj GEMV
@@ -141,8 +142,8 @@ def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20
     timing (the counter-collection workload) and returns None."""
     H, I, L = shape.hidden, shape.inter, shape.layers
     qd, kvd, hd = shape.q_dim, shape.kv_dim, shape.head_dim
-    ctx = C.make_attention_ctx(shape.heads, shape.kv_heads, hd)
-    ctx.k_already_prerotated = C.EFM_K_PREROTATED_EXCEPT_NEWEST
+    ctx = C.make_attention_ctx(shape.heads, shape.kv_heads, hd, rope=False)
+    ctx_q = C.make_attention_ctx(shape.heads, shape.kv_heads, hd, rope_theta=shape.theta)
     lib = C.load()
     ws = torch.zeros(lib.efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=dev)
     g = torch.Generator(device=dev).manual_seed(7)
@@ -169,7 +170,7 @@ def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20
     q = torch.empty(1, qd, device=dev, dtype=torch.bfloat16)
 
     def norm_qkv(x, sh):
-        C.call("efm_decode_norm_qkv", H, qd, kvd, shape.eps, h.data_ptr(), r_in.data_ptr(), r_out.data_ptr(),
+        C.call("efm_decode_norm_qkv_rope", ctx_q, H, shape.eps, h.data_ptr(), r_in.data_ptr(), r_out.data_ptr(),
                x["nin"].data_ptr(), x["wqkv"].data_ptr(), x["bqkv"].data_ptr(), q.data_ptr(), x["kc"].data_ptr(),
                x["vc"].data_ptr(), d_len.data_ptr(), sh)
 
@@ -192,7 +193,7 @@ def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20
     part = splits * shape.heads * (hd + 2) * 4
     act = 2 * H
     kernels = [
-        ("norm_qkv", "efm_decode_norm_qkv (gemv_kernel, add-norm prologue, QKV epilogue)", norm_qkv,
+        ("norm_qkv", "efm_decode_norm_qkv_rope (gemv_kernel, add-norm prologue, QKV + RoPE epilogue)", norm_qkv,
          ((qd + 2 * kvd) * (H + 1) + H) * 2 + 3 * act + qd * 2 + 2 * kvd * 2),
         ("attention", "efm_decode_attention_partials (decode_attn_lds_kernel)", attention,
          qd * 2 + 2 * ctx_len * kvd * 2 + kvd * 2 + part),
@@ -553,9 +554,9 @@ def run_c1(args):
     hd 64, inter 4864), KV cache of 1024 N(0,1) positions, input hidden N(0,1). 16 copies
     of the layer (weights + cache, 485 MB) are rotated so the 256 MB Infinity Cache does
     not serve the weights. The cache follows the engine's convention: rows hold keys
-    rotated at their positions (the prefill rotates them before the cache write), and
-    this step's key, written un-rotated by the QKV projection, is rotated by the attention
-    call (k_already_prerotated = EFM_K_PREROTATED_EXCEPT_NEWEST)."""
+    rotated at their positions (the prefill rotates them before the cache write), the QKV
+    projection rotates q and this step's key in its epilogue (efm_decode_norm_qkv_rope),
+    and the attention applies no positional encoding."""
     import torch
     import efm_capi as C
     import efm_setup as S
@@ -582,8 +583,8 @@ def run_c1(args):
     h = torch.randn(1, H, device=dev, generator=g).to(torch.bfloat16)
     res_in = torch.randn(1, H, device=dev, generator=g).to(torch.bfloat16)
     d_len = torch.tensor([max_kv], dtype=torch.int32, device=dev)
-    ctx = C.make_attention_ctx(sh.heads, sh.kv_heads, hd)
-    ctx.k_already_prerotated = C.EFM_K_PREROTATED_EXCEPT_NEWEST
+    ctx = C.make_attention_ctx(sh.heads, sh.kv_heads, hd, rope=False)
+    ctx_q = C.make_attention_ctx(sh.heads, sh.kv_heads, hd, rope_theta=sh.theta)
     ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=dev)
     r0 = torch.empty(1, H, device=dev, dtype=torch.bfloat16)
     r1 = torch.empty_like(r0)
@@ -602,7 +603,7 @@ def run_c1(args):
         # write, attention split partials, merge + o_proj, norm + gate/up + SwiGLU, down
         L = layers[state["i"] % ncopy]
         state["i"] += 1
-        C.call("efm_decode_norm_qkv", H, QD, KVD, sh.eps, h.data_ptr(), res_in.data_ptr(), r0.data_ptr(),
+        C.call("efm_decode_norm_qkv_rope", ctx_q, H, sh.eps, h.data_ptr(), res_in.data_ptr(), r0.data_ptr(),
                L["in_norm"].data_ptr(), L["w_qkv"].data_ptr(), L["b_qkv"].data_ptr(), q.data_ptr(), L["k"].data_ptr(),
                L["v"].data_ptr(), d_len.data_ptr(), stream_handle)
         if fused_merge:

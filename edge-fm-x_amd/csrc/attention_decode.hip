@@ -1014,9 +1014,10 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
 // The split partials live in `scratch`, a file-scope device array that every GPU the
 // library runs on holds until the process ends. In host code `scratch` names a host-side
 // stand-in, never the device memory: the device address comes from hipGetSymbolAddress,
-// fetched once per device (with that device current) on the entry point's first call
-// there, and only that address is passed to kernels. Nothing in the partials needs to
-// start at zero: every split writes its own slots before the merge reads them.
+// fetched once per device (with that device current) by efm_init, or by the entry point's
+// first call on that device when it is not being captured into a graph, and only that
+// address is passed to kernels. Nothing in the partials needs to start at zero: every
+// split writes its own slots before the merge reads them.
 constexpr size_t kNoAllocScratchBytes = EFM_ATTENTION_DECODE_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
@@ -1024,7 +1025,9 @@ constexpr int kNoAllocMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static void* g_scratch_dev[kNoAllocMaxDevices];
 
-static int noalloc_scratch(void** out) {
+// capture_stream: the call's stream; a first lookup while that stream is being captured
+// is refused (the runtime call may load code objects), so capture needs efm_init first.
+static int noalloc_scratch(void** out, hipStream_t capture_stream, bool check_capture) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return set_error(EFM_ERR_DEVICE, "attention_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
@@ -1032,6 +1035,13 @@ static int noalloc_scratch(void** out) {
         return set_error(EFM_ERR_UNSUPPORTED, "attention_decode_noalloc: device %d beyond %d", dev, kNoAllocMaxDevices);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch_dev[dev] == nullptr) {
+        if (check_capture) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(capture_stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+                return set_error(EFM_ERR_INVALID_ARGUMENT,
+                                 "attention_decode_noalloc: first call on device %d inside a graph capture; call "
+                                 "efm_init on this device before capturing", dev);
+        }
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || p == nullptr)
@@ -1053,12 +1063,17 @@ static int decode_noalloc(const efm_attention_ctx* ctx, const void* q, const voi
                          "attention_decode_noalloc: this shape needs %zu bytes of split scratch; the library holds %zu "
                          "(use efm_attention_decode with a workspace)", need, kNoAllocScratchBytes);
     void* ptr = nullptr;
-    rc = noalloc_scratch(&ptr);
+    rc = noalloc_scratch(&ptr, stream, true);
     if (rc) return rc;
     return decode_launch(ctx, q, k, v, o, kv_len, d_kv_len, max_kv_len, ptr, kNoAllocScratchBytes, true, stream);
 }
 
 }  // namespace efm
+
+extern "C" int efm_init(void) {
+    void* ptr = nullptr;
+    return efm::noalloc_scratch(&ptr, nullptr, false);
+}
 
 extern "C" int efm_attention_decode_noalloc(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v,
                                             void* o, uint32_t kv_len, const uint32_t* d_kv_len, uint32_t max_kv_len,

@@ -392,7 +392,7 @@ __device__ __forceinline__ float2 qkv_rope_cs(const GemvArgs& a, int n, uint32_t
     const int n0 = (n / half) * 2 * half + d;
     const int pos = (int)L - 1 + (n0 < a.q_dim ? a.q_pos_off : a.k_pos_off);
     float sn, cs;
-    sincosf((float)pos * a.rope.inv_freq[d], &sn, &cs);
+    sincos_reduced((float)pos * a.rope.inv_freq[d], &sn, &cs);
     return make_float2(cs, sn);
 }
 
@@ -449,21 +449,23 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
     };
 
     const uint32_t tag = (EPI == EPI_QKV_TAG) ? launch_tag(a.epoch) : 0u;
+    // QKV_ROPE: the cache length is read first, so that its round trip runs under the
+    // prologue's and the weights' instead of after them
+    uint32_t rope_len = 0;
+    if constexpr (EPI == EPI_QKV_ROPE) rope_len = a.d_kv_len[0];
     ProLoads<PRO> pl;
     gemv_prologue_load<PRO>(a, pl);
     int rb = blk;
     issue(rb, 0);   // unconditional (a block past the end reads zeros): see gemv_wload
     __builtin_amdgcn_sched_barrier(0);   // every load goes out before the prologue's first wait
+    gemv_prologue<PRO>(a, pl, xs, red, blk);
     // QKV_ROPE: the first row block's cos / sin while the weights stream (the epilogue
     // recomputes them for any later block of a grid-stride walk)
     float2 rcs[R];
-    uint32_t rope_len = 0;
     if constexpr (EPI == EPI_QKV_ROPE) {
-        rope_len = a.d_kv_len[0];
 #pragma unroll
         for (int r = 0; r < R; ++r) rcs[r] = qkv_rope_cs(a, blk * RB + grp * R + r, rope_len);
     }
-    gemv_prologue<PRO>(a, pl, xs, red, blk);
     __syncthreads();
     const uint4* xs4 = reinterpret_cast<const uint4*>(xs);
 

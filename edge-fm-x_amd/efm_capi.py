@@ -78,6 +78,7 @@ def make_attention_ctx(num_qo_heads, num_kv_heads, head_dim, *, rope=True, rope_
 SIGNATURES = {
     "efm_last_error": (c_char_p, []),
     "efm_version": (c_char_p, []),
+    "efm_init": (c_int32, []),
     "efm_attention_decode_workspace_bytes": (c_size_t, [POINTER(AttentionCtx), c_uint32]),
     "efm_attention_decode_noalloc": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
                                                c_void_p, c_uint32, c_void_p]),

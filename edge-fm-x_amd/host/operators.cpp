@@ -426,9 +426,44 @@ bool plain_bf16(const LinearLayer::LinearOpContext& c, const LinearLayer::Weight
     return s.m >= 1 && s.in_features % (s.m == 1 ? 8u : 32u) == 0;
 }
 
-// This library's GEMV (m = 1) / MFMA GEMM (m > 1). prepare() sizes the split-K scratch the
-// kernel plan for this shape uses (zero for most shapes) and allocates it once per
-// (stage, m): forward() never allocates, so a decode step can be captured into a graph.
+}  // namespace
+
+// One grow-only split-K scratch per device, shared by every prefill projection (linear
+// impls, the prefill source ops, the fused gate/up op), in the role of the reference's
+// StaticBufferManager::get_cache_buf (src/utils/memory.h:31-109): all of them run in
+// stream order, so one buffer sized to the largest need serves every prompt length. It
+// only grows: the device is synchronised first, so no launch still reads the old one.
+// Decode GEMVs (m = 1) need none, so captured decode graphs never hold it.
+namespace {
+struct SharedLinearScratch {
+    std::mutex mu;
+    std::map<int32_t, Tensor> bufs;
+} g_linear_scratch;
+}  // namespace
+
+void* linear_scratch(size_t bytes, int32_t device_id, size_t* have) {
+    std::lock_guard<std::mutex> lock(g_linear_scratch.mu);
+    Tensor& t = g_linear_scratch.bufs[device_id];
+    if (bytes > 0 && (t.empty() || t.nbytes() < bytes)) {
+        if (!t.empty()) hip_check(hipDeviceSynchronize(), "linear scratch grow");
+        t = Tensor();
+        t = Tensor::empty({(int64_t)bytes}, DType::UInt8, Device::GPU, device_id);
+    }
+    *have = t.empty() ? 0 : t.nbytes();
+    return t.empty() ? nullptr : t.data_ptr();
+}
+
+size_t linear_scratch_bytes(int32_t device_id) {
+    std::lock_guard<std::mutex> lock(g_linear_scratch.mu);
+    auto it = g_linear_scratch.bufs.find(device_id);
+    return (it == g_linear_scratch.bufs.end() || it->second.empty()) ? 0 : it->second.nbytes();
+}
+
+namespace {
+// This library's GEMV (m = 1) / MFMA GEMM (m > 1). prepare() records the split-K scratch
+// the kernel plan for this shape uses (zero for most shapes, and always for m = 1);
+// forward() takes it from the shared device scratch, which only grows when a new shape
+// needs more (never at m = 1, so a decode step can be captured into a graph).
 class HipLinearImpl : public LinearLayer::LinearImpl {
 public:
     std::string impl_id() const override { return "hip_gfx950_linear"; }
@@ -439,19 +474,19 @@ public:
                  const Tensor&, Tensor&, hipStream_t, LinearLayer::CachedDescriptors& cached) override {
         if (cached.prepared_) return;
         cached.workspace_bytes_ = efm_linear_workspace_bytes(c.shape.m, c.shape.in_features, c.shape.out_features);
-        if (cached.workspace_bytes_ > 0)
-            cached.workspace_ = Tensor::empty({(int64_t)cached.workspace_bytes_}, DType::UInt8, Device::GPU,
-                                              ws.weight_->device().second);
         cached.prepared_ = true;
     }
     void forward(LinearLayer& owner, const LinearLayer::LinearOpContext& c, const LinearLayer::WeightSet& ws,
                  const Tensor& in, Tensor& out, hipStream_t s, LinearLayer::CachedDescriptors& cached) override {
         prepare(owner, c, ws, in, out, s, cached);
+        size_t have = 0;
+        void* scratch = cached.workspace_bytes_ > 0
+                            ? linear_scratch(cached.workspace_bytes_, ws.weight_->device().second, &have)
+                            : nullptr;
         efm_check(efm_linear_ws(c.shape.m, c.shape.in_features, c.shape.out_features, in.data_ptr(),
                                 ws.weight_->data_ptr(), ws.bias_ ? ws.bias_->data_ptr() : nullptr, out.data_ptr(),
-                                c.shape.output_dtype == DType::Float32 ? EFM_DTYPE_F32 : EFM_DTYPE_BF16,
-                                cached.workspace_.empty() ? nullptr : cached.workspace_.data_ptr(),
-                                cached.workspace_bytes_, s),
+                                c.shape.output_dtype == DType::Float32 ? EFM_DTYPE_F32 : EFM_DTYPE_BF16, scratch,
+                                have, s),
                   "linear " + c.layer_prefix);
     }
 };
@@ -641,13 +676,6 @@ void LinearLayer::forward_fp16_bf16(const Tensor& input, Tensor& output, hipStre
 // Prefill source ops
 // ---------------------------------------------------------------------------------
 namespace {
-Tensor& scratch_for(std::map<std::tuple<int64_t, int64_t, int64_t>, Tensor>& cache, int64_t m, int64_t k, int64_t n,
-                    size_t bytes, int32_t device_id) {
-    Tensor& t = cache[std::make_tuple(m, k, n)];
-    if (bytes > 0 && (t.empty() || t.nbytes() < bytes))
-        t = Tensor::empty({(int64_t)bytes}, DType::UInt8, Device::GPU, device_id);
-    return t;
-}
 bool bf16_matrix(const Tensor& t, int64_t rows, int64_t cols) {
     return t.dtype() == DType::BFloat16 && t.shape().size() == 2 && (rows < 0 || t.shape()[0] == rows) &&
            (cols < 0 || t.shape()[1] == cols) && !t.empty();
@@ -656,7 +684,7 @@ bool bf16_matrix(const Tensor& t, int64_t rows, int64_t cols) {
 
 PrefillLinearSourceOp::PrefillLinearSourceOp(const EngineConfig& config) : device_id_(config.device_id()) {}
 PrefillLinearSourceOp::~PrefillLinearSourceOp() = default;
-void PrefillLinearSourceOp::reset_runtime_caches() { scratch_.clear(); }
+void PrefillLinearSourceOp::reset_runtime_caches() {}
 
 bool PrefillLinearSourceOp::try_forward(const std::string& role, int32_t, const Tensor& input, const Tensor& weight,
                                         const Tensor* bias, Tensor& output, hipStream_t stream) {
@@ -666,19 +694,17 @@ bool PrefillLinearSourceOp::try_forward(const std::string& role, int32_t, const 
     if (m < 2 || k % 32 != 0 || output.dtype() != DType::BFloat16 || output.numel() != m * n) return false;
     if (bias != nullptr && (bias->dtype() != DType::BFloat16 || bias->numel() != n)) return false;
     const size_t need = efm_linear_workspace_bytes(m, k, n);
-    Tensor& ws = scratch_for(scratch_, m, k, n, need, device_id_);
+    size_t have = 0;
+    void* ws = need > 0 ? linear_scratch(need, device_id_, &have) : nullptr;
     efm_check(efm_linear_ws(m, k, n, input.data_ptr(), weight.data_ptr(), bias ? bias->data_ptr() : nullptr,
-                            output.data_ptr(), EFM_DTYPE_BF16, need ? ws.data_ptr() : nullptr, need, stream),
+                            output.data_ptr(), EFM_DTYPE_BF16, ws, have, stream),
               "prefill linear source op (" + role + ")");
     return true;
 }
 
 PrefillMlpSourceOp::PrefillMlpSourceOp(const EngineConfig& config) : device_id_(config.device_id()) {}
 PrefillMlpSourceOp::~PrefillMlpSourceOp() = default;
-void PrefillMlpSourceOp::reset_runtime_caches() {
-    scratch_.clear();
-    intermediate_ = Tensor();
-}
+void PrefillMlpSourceOp::reset_runtime_caches() { intermediate_ = Tensor(); }
 
 bool PrefillMlpSourceOp::try_forward(int32_t, const Tensor& input, const Tensor& gate_up_weight,
                                      const Tensor& down_weight, Tensor& output, hipStream_t stream) {
@@ -689,18 +715,22 @@ bool PrefillMlpSourceOp::try_forward(int32_t, const Tensor& input, const Tensor&
     const int64_t inter = gate_up_weight.shape()[0] / 2;
     if (inter % 32 != 0 || !bf16_matrix(down_weight, h, inter)) return false;
     if (output.dtype() != DType::BFloat16 || output.numel() != m * h) return false;
-    if (intermediate_.empty() || intermediate_.numel() < m * inter)
+    if (intermediate_.empty() || intermediate_.numel() < m * inter) {
+        if (!intermediate_.empty()) hip_check(hipDeviceSynchronize(), "prefill mlp intermediate grow");
+        intermediate_ = Tensor();
         intermediate_ = Tensor::empty({m, inter}, DType::BFloat16, Device::GPU, device_id_);
+    }
+    // both launches share the scratch (stream order): grown once, to the larger need
     const size_t need_gu = efm_fused_gate_up_swiglu_workspace_bytes(m, h, inter);
-    Tensor& ws_gu = scratch_for(scratch_, m, h, -inter, need_gu, device_id_);
+    const size_t need_d = efm_linear_workspace_bytes(m, inter, h);
+    size_t have = 0;
+    void* ws = (need_gu | need_d) ? linear_scratch(std::max(need_gu, need_d), device_id_, &have) : nullptr;
     efm_check(efm_fused_gate_up_swiglu_ws(m, h, inter, input.data_ptr(), gate_up_weight.data_ptr(),
-                                          intermediate_.data_ptr(), need_gu ? ws_gu.data_ptr() : nullptr, need_gu,
+                                          intermediate_.data_ptr(), need_gu ? ws : nullptr, need_gu ? have : 0,
                                           stream),
               "prefill mlp source op (gate/up + SwiGLU)");
-    const size_t need_d = efm_linear_workspace_bytes(m, inter, h);
-    Tensor& ws_d = scratch_for(scratch_, m, inter, h, need_d, device_id_);
     efm_check(efm_linear_ws(m, inter, h, intermediate_.data_ptr(), down_weight.data_ptr(), nullptr, output.data_ptr(),
-                            EFM_DTYPE_BF16, need_d ? ws_d.data_ptr() : nullptr, need_d, stream),
+                            EFM_DTYPE_BF16, need_d ? ws : nullptr, need_d ? have : 0, stream),
               "prefill mlp source op (down)");
     return true;
 }
@@ -709,18 +739,6 @@ bool PrefillMlpSourceOp::try_forward(int32_t, const Tensor& input, const Tensor&
 // Fused gate/up + SwiGLU
 // ---------------------------------------------------------------------------------
 namespace {
-// Grow-only per-device scratch for the fused gate/up kernels (the reference's impls take
-// theirs from StaticBufferManager::get_cache_buf, src/utils/memory.h:31-109).
-void* linear_scratch(size_t bytes, int32_t device_id, size_t* have) {
-    static std::mutex mu;
-    static std::map<int32_t, Tensor> bufs;
-    std::lock_guard<std::mutex> lock(mu);
-    Tensor& t = bufs[device_id];
-    if (t.empty() || t.nbytes() < bytes) t = Tensor::empty({(int64_t)bytes}, DType::UInt8, Device::GPU, device_id);
-    *have = t.nbytes();
-    return t.data_ptr();
-}
-
 class HipSwigluOp final : public FusedGateUpActivationOp {
 public:
     std::string impl_id() const override { return "hip_gfx950_swiglu"; }

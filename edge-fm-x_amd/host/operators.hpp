@@ -329,7 +329,6 @@ public:
 
 private:
     int32_t device_id_ = 0;
-    std::map<std::tuple<int64_t, int64_t, int64_t>, Tensor> scratch_;
 };
 
 class PrefillMlpSourceOp {
@@ -345,8 +344,12 @@ public:
 private:
     int32_t device_id_ = 0;
     Tensor intermediate_;   // [m_max, I], grown on demand
-    std::map<std::tuple<int64_t, int64_t, int64_t>, Tensor> scratch_;
 };
+
+// The split-K scratch shared by every prefill projection on a device (grow-only; see
+// operators.cpp): a pointer to at least `bytes` (have = its size), and its current size.
+void* linear_scratch(size_t bytes, int32_t device_id, size_t* have);
+size_t linear_scratch_bytes(int32_t device_id);
 
 // ---------------------------------------------------------------------------------
 // Fused gate/up + SwiGLU (src/operators/fused_gate_up_activation_op.h:14-74). The

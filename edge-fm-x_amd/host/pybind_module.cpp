@@ -143,6 +143,9 @@ PYBIND11_MODULE(edge_fm, m) {
 
     py::class_<Response>(m, "Response").def("token_ids", [](const Response& r) { return r.token_ids; });
 
+    m.def("linear_scratch_bytes", &linear_scratch_bytes, py::arg("device_id") = 0,
+          "bytes of the split-K scratch shared by the prefill projections on a device (grow-only)");
+
     py::class_<EdgeFM>(m, "EdgeFM")
         .def(py::init<const std::string&>(), py::arg("config_path"), py::call_guard<py::gil_scoped_release>())
         .def("generate", &EdgeFM::generate, py::arg("request"), py::call_guard<py::gil_scoped_release>())

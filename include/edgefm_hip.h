@@ -51,6 +51,13 @@ const char* efm_last_error(void);
 /* Library version string. */
 const char* efm_version(void);
 
+/* Per-device set-up of the current device (no counterpart in the reference, which sets
+ * its buffers up inside its engine): looks up the device address of the library-held
+ * array that efm_attention_decode_noalloc uses. Call it once per device, with that device
+ * current, before capturing efm_attention_decode_noalloc into a graph; outside capture
+ * the entry point's first call does the same by itself. Allocates nothing. */
+int efm_init(void);
+
 /* Test hook (no counterpart in the reference): process-wide choice between kernels that
  * compute the same operator, so that tests can compare a fast kernel with the simpler
  * one it replaces on the same inputs. value 0 restores the library's own choice.
@@ -137,8 +144,10 @@ int efm_attention_decode(const efm_attention_ctx* ctx, const void* q, const void
  * EFM_ATTENTION_DECODE_NOALLOC_SCRATCH_BYTES; that covers every shape whose
  * efm_attention_decode_workspace_bytes fits in it (all head_dim <= 128, group <= 8 shapes
  * with up to 512 KV heads, any length). Larger needs: EFM_ERR_UNSUPPORTED, nothing
- * launched. The call allocates nothing (its first call on a device looks up the array's
- * address). Every call on one GPU shares the array: calls that overlap on one GPU (on
+ * launched. The call allocates nothing. The array's device address is looked up once per
+ * device, by efm_init or by the first call there; a first call made while its stream is
+ * being captured into a graph is refused (EFM_ERR_INVALID_ARGUMENT: call efm_init before
+ * capturing). Every call on one GPU shares the array: calls that overlap on one GPU (on
  * different streams, or from several threads without stream order) race. */
 #define EFM_ATTENTION_DECODE_NOALLOC_SCRATCH_BYTES 2359296
 int efm_attention_decode_noalloc(const efm_attention_ctx* ctx, const void* q, const void* k, const void* v,

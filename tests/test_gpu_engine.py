@@ -256,6 +256,46 @@ def test_tiny_top_p_sampling_matches_oracle(gpu, use_graph):
     assert worst_max < 0.65 and worst_mean < 0.12, f"engine logits off the oracle's: {worst_max:.4f} / {worst_mean:.5f}"
 
 
+def test_prefill_split_k_scratch_is_shared_and_bounded(gpu):
+    """Prefill at several prompt lengths on 1.5B-width layers (whose split-K GEMMs need
+    scratch at these lengths): every projection takes its split-K scratch from one
+    grow-only buffer per device, so its size only grows, ends at the largest single need of
+    the lengths run (or what earlier work had already grown it to), and a second pass over
+    the same lengths leaves it unchanged; the tokens do not depend on the order."""
+    import efm_capi as C
+
+    shape = S.ModelShape(hidden=1536, layers=2, heads=12, kv_heads=2, head_dim=128, inter=8960, vocab=1000)
+    cfg = _oracle_cfg(shape)
+    w = O.random_weights(cfg, seed=41, std=0.02)
+    lib = C.load()
+    H, I, qd, kvd = shape.hidden, shape.inter, shape.q_dim, shape.kv_dim
+    lengths = [900, 300, 1200, 64, 700]
+    need = max(max(lib.efm_linear_workspace_bytes(m, H, qd + 2 * kvd), lib.efm_linear_workspace_bytes(m, qd, H),
+                   lib.efm_linear_workspace_bytes(m, I, H), lib.efm_fused_gate_up_swiglu_workspace_bytes(m, H, I))
+               for m in lengths)
+    assert need > 0, "these shapes must exercise the split-K scratch"
+    before = edge_fm.linear_scratch_bytes(0)
+    g = torch.Generator().manual_seed(9)
+    prompts = {L: torch.randint(0, shape.vocab, (L,), generator=g).tolist() for L in lengths}
+    sizes, toks = [], {}
+    with tempfile.TemporaryDirectory() as tmp:
+        eng, keep = _engine(tmp, shape, w, max_tokens=1300, max_new_tokens=2)
+        for rep in range(2):
+            for L in lengths:
+                req = edge_fm.Request(0, prompts[L])
+                req.set_ignore_stop_tokens(True)
+                t = eng.generate(req).token_ids()
+                if rep == 0:
+                    toks[L] = t
+                else:
+                    assert t == toks[L], f"prompt {L}: tokens changed on the second pass"
+                sizes.append(edge_fm.linear_scratch_bytes(0))
+        del eng
+    assert sizes == sorted(sizes), f"the scratch must only grow: {sizes}"
+    assert sizes[-1] == max(before, need), f"scratch {sizes[-1]} bytes, largest need {need} (before {before})"
+    assert sizes[len(lengths) - 1] == sizes[-1], "the second pass must not grow the scratch"
+
+
 def test_top_p_sampling_seeds_differ_and_config_checks(gpu):
     w = O.random_weights(_oracle_cfg(TINY), seed=32, std=0.2)
     prompt = list(range(10, 40))

@@ -55,6 +55,43 @@ def test_noalloc_matches_workspace_entry_point(gpu, seq):
             assert_close_bf16(got.reshape(1, hq, hd), exp, what=f"call {i} vs oracle")
 
 
+@pytest.mark.gpu
+def test_noalloc_captured_in_a_graph_matches_workspace_entry_point(gpu):
+    """After efm_init, noalloc calls of two shapes (the C2 heads over a 768-row cache with
+    a device-side length, then the 0.5B heads) are captured into one graph and replayed
+    three times, with eager work and synchronisations between the replays and the length
+    changed on the device; every replay equals efm_attention_decode's eager result bit for
+    bit."""
+    assert C.load().efm_init() == C.EFM_OK
+    torch.manual_seed(5)
+    shapes = [(12, 2, 128, 768), (14, 2, 64, 1100)]
+    bufs = []
+    for hq, hkv, hd, rows in shapes:
+        q = torch.randn(1, hq, hd, dtype=torch.bfloat16, device=gpu)
+        k = torch.randn(rows, hkv, hd, dtype=torch.bfloat16, device=gpu)
+        v = torch.randn(rows, hkv, hd, dtype=torch.bfloat16, device=gpu)
+        d_len = torch.tensor([rows // 2], dtype=torch.int32, device=gpu)
+        bufs.append((C.make_attention_ctx(hq, hkv, hd), q, k, v, d_len, rows, torch.empty_like(q)))
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+        for ctx, q, k, v, d_len, rows, o in bufs:
+            C.call("efm_attention_decode_noalloc", ctx, ptr(q), ptr(k), ptr(v), ptr(o), 0, ptr(d_len), rows,
+                   s.cuda_stream)
+    for rep, length_frac in enumerate((0.5, 0.9, 0.25)):
+        for ctx, q, k, v, d_len, rows, o in bufs:
+            d_len.fill_(max(1, int(rows * length_frac)))
+            o.fill_(float("nan"))
+        torch.randn(1 << 20, device=gpu).sum()   # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (ctx, q, k, v, d_len, rows, o) in enumerate(bufs):
+            ref = _with_workspace(ctx, q, k, v, 0, d_len, rows)
+            torch.cuda.synchronize()
+            assert torch.equal(o, ref), f"replay {rep}, call {i}: captured noalloc differs from efm_attention_decode"
+
+
 def test_noalloc_rejects_shapes_beyond_its_array():
     """A shape whose split partials need more than the library's array is refused on the
     host before anything is launched (no GPU needed)."""
