@@ -326,7 +326,8 @@ ModelConfig ModelConfig::from_json(const Json& j0) {
 // =================================================================================
 // KVManager
 // =================================================================================
-KVManager::KVManager(const std::vector<KVSlotConfig>& slots, const ModelConfig& m, int32_t device_id) : m_(m) {
+KVManager::KVManager(const std::vector<KVSlotConfig>& slots, const ModelConfig& m, int32_t device_id)
+    : m_(m), device_id_(device_id) {
     std::set<int32_t> seen;
     for (const auto& s : slots) {
         check<ConfigurationError>(seen.insert(s.request_id).second, "duplicate kvcache request_id");
@@ -367,6 +368,58 @@ std::vector<int32_t> KVManager::request_ids() const {
     return out;
 }
 
+namespace {
+std::vector<KVSlotConfig> remapped_slots(const EngineConfig& cfg) {
+    const CompactVocab vocab(cfg);
+    std::vector<KVSlotConfig> slots = cfg.kv_slots();
+    check<ConfigurationError>(!slots.empty(), "kvcache.requests array must not be empty");
+    for (auto& s : slots)
+        s.prefix_token_ids = vocab.remap_required_token_ids(s.prefix_token_ids, "kvcache.requests[].prefix_token_ids");
+    return slots;
+}
+}  // namespace
+
+KVManager::KVManager(const EngineConfig& cfg)
+    : KVManager(remapped_slots(cfg), ModelConfig::from_json(cfg.model_config()), cfg.device_id()) {}
+
+const KVSlot& KVManager::find(int32_t request_id) const {
+    for (const auto& s : slots_)
+        if (s.cfg.request_id == request_id) return s;
+    throw InvalidRequestError("Invalid request_id: " + std::to_string(request_id));
+}
+
+std::vector<void*> KVManager::get_read_kvcache(int32_t request_id) const {
+    const KVSlot& s = find(request_id);
+    const size_t layer_bytes = 2 * (size_t)s.cfg.max_tokens * (size_t)m_.kv_dim() * 2;
+    std::vector<void*> out((size_t)m_.layers);
+    for (int l = 0; l < m_.layers; ++l) out[l] = static_cast<char*>(s.buffer.data_ptr()) + (size_t)l * layer_bytes;
+    return out;
+}
+
+std::vector<void*> KVManager::get_write_kvcache(int32_t request_id) const {
+    const KVSlot& s = find(request_id);
+    std::vector<void*> out = get_read_kvcache(request_id);
+    const size_t prefix_bytes = (size_t)s.prefix_size * (size_t)m_.kv_dim() * 2;
+    for (auto& p : out) p = static_cast<char*>(p) + prefix_bytes;
+    return out;
+}
+
+KVManagerStatus KVManager::get_status() const {
+    KVManagerStatus st;
+    st.device = Device::GPU;
+    st.device_id = device_id_;
+    for (const auto& s : slots_) {
+        KVSlotStatus k;
+        k.request_id = s.cfg.request_id;
+        k.prefix_token_ids = s.cfg.prefix_token_ids;
+        k.prefix_size = (size_t)s.prefix_size;
+        k.max_tokens = s.cfg.max_tokens;
+        k.allocated_size = s.buffer.nbytes();
+        st.slots.push_back(std::move(k));
+    }
+    return st;
+}
+
 // =================================================================================
 // Qwen2_5
 // =================================================================================
@@ -389,7 +442,7 @@ const Tensor& Qwen2_5::w(const std::unordered_map<std::string, Tensor>& ws, cons
     throw ModelNotLoadedError("missing weight tensor: " + name);
 }
 
-static Tensor concat_rows(const std::vector<const Tensor*>& parts, int32_t device_id, hipStream_t s) {
+Tensor concat_rows(const std::vector<const Tensor*>& parts, int32_t device_id, hipStream_t s) {
     int64_t rows = 0, cols = -1;
     for (auto* p : parts) {
         check<ModelNotLoadedError>(p->dtype() == DType::BFloat16, "weights must be bf16");

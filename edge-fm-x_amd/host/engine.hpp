@@ -176,19 +176,46 @@ struct KVSlot {
     bool prefix_ready = false;
 };
 
+struct KVSlotStatus {
+    int32_t request_id = 0;
+    std::vector<int32_t> prefix_token_ids;
+    size_t prefix_size = 0;
+    int32_t max_tokens = 0;
+    size_t allocated_size = 0;   // bytes over all layers
+};
+struct KVManagerStatus {
+    std::vector<KVSlotStatus> slots;
+    Device device = Device::GPU;
+    int32_t device_id = 0;
+};
+
 class KVManager {
 public:
     KVManager(const std::vector<KVSlotConfig>& slots, const ModelConfig& m, int32_t device_id);
+    // The slots of the config's kvcache.requests (prefix ids remapped through the config's
+    // compact vocabulary, kv_manager.cpp:45-190).
+    explicit KVManager(const EngineConfig& engine_config);
     KVSlot& slot(int32_t request_id);
     bool is_request_valid(int32_t request_id) const;
     void* k_cache(int32_t request_id, int layer);
     void* v_cache(int32_t request_id, int layer);
     std::vector<int32_t> request_ids() const;
+    // Per layer: the start of the layer's [K | V] block, and that start advanced past the
+    // fixed prefix's K rows (the first row a request writes), kv_manager.cpp:248-262.
+    std::vector<void*> get_read_kvcache(int32_t request_id) const;
+    std::vector<void*> get_write_kvcache(int32_t request_id) const;
+    KVManagerStatus get_status() const;
 
 private:
+    const KVSlot& find(int32_t request_id) const;
     ModelConfig m_;
+    int32_t device_id_ = 0;
     std::vector<KVSlot> slots_;
 };
+
+// Rows of `parts` stacked into one new bf16 device tensor (2-D parts share their column
+// count), copied on `stream`.
+Tensor concat_rows(const std::vector<const Tensor*>& parts, int32_t device_id, hipStream_t stream);
 
 // ---------------------------------------------------------------------------------
 // Qwen2.5 model (src/models/qwen2_5/qwen2_5.cpp:84-980)

@@ -294,9 +294,21 @@ public:
 class FusedGateUpLinearLayer : public LinearLayer {
 public:
     FusedGateUpLinearLayer(const std::string& hf_mlp_prefix, const EngineConfig& engine_config, uint32_t hidden,
-                           uint32_t gate_out_features, uint32_t up_out_features, std::string layer_name = "")
-        : LinearLayer(hf_mlp_prefix, "fused_gate_up", engine_config, hidden, gate_out_features + up_out_features,
-                      std::move(layer_name)) {}
+                           uint32_t gate_out_features, uint32_t up_out_features, std::string layer_name = "");
+    // output [m, I] = silu(x . Wgate^T) * (x . Wup^T) in one fused launch, through the
+    // fused gate/up + SwiGLU op resolved for (stage, the layer prefix, m) from the operator
+    // table (linear.cu:2054-2223: a record naming an unknown or unsupporting impl is a
+    // ConfigurationError). Returns false, having done nothing, when the shapes are not
+    // decode [1, H] -> [1, I] (prefill: m >= 64) or no impl supports them.
+    bool try_forward_decode_swiglu_fused(const Tensor& input, Tensor& output, hipStream_t stream);
+    bool try_forward_prefill_swiglu_fused(const Tensor& input, Tensor& output, hipStream_t stream);
+    uint32_t gate_out_features() const { return gate_out_; }
+    uint32_t up_out_features() const { return up_out_; }
+
+private:
+    bool try_forward_swiglu_fused_impl(const Tensor& input, Tensor& output, ModelStage stage, hipStream_t stream);
+    uint32_t gate_out_ = 0, up_out_ = 0;
+    std::string model_name_, hw_profile_, table_path_;
 };
 
 class LinearOpRegistry {

@@ -1,7 +1,8 @@
 // Python module `edge_fm`: the reference's pybind surface (src/python/pybind_debug.cpp:
 // 313-1735) for the MI355X runtime — DType / Device / ModelStage, Tensor (zero-copy
-// views of device memory, DLPack export as kDLROCM), Request / Response, EdgeFM with
-// generate() and last_generate_metrics(), the WeightLoader singleton and apply_mrope.
+// views of device memory, DLPack export as kDLROCM, copying DLPack import), Request /
+// Response, EdgeFM with generate() and last_generate_metrics(), the WeightLoader
+// singleton, apply_mrope, and the layer tier (pybind_layers.cpp).
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
@@ -63,7 +64,60 @@ py::capsule to_dlpack(const Tensor& t) {
     });
 }
 
+DType from_dl(const DLDataType& t) {
+    if (t.lanes == 1) {
+        if (t.code == kDLFloat && t.bits == 32) return DType::Float32;
+        if (t.code == kDLFloat && t.bits == 16) return DType::Float16;
+        if (t.code == kDLBfloat && t.bits == 16) return DType::BFloat16;
+        if (t.code == kDLInt && t.bits == 32) return DType::Int32;
+        if (t.code == kDLInt && t.bits == 64) return DType::Int64;
+        if (t.code == kDLUInt && t.bits == 8) return DType::UInt8;
+        if (t.code == kDLInt && t.bits == 8) return DType::Int8;
+    }
+    throw InvalidArgumentError("from_dlpack: unsupported dtype (code " + std::to_string(t.code) + ", bits " +
+                               std::to_string(t.bits) + ")");
+}
+
+// A new tensor holding a copy of a DLPack capsule's data (Tensor.from_dlpack,
+// pybind_debug.cpp:437-449: the data is copied, the capsule may be released afterwards).
+// Row-major contiguous data only; a GPU source is copied after the device is idle, so
+// work queued on any stream of the producer has finished.
+Tensor from_dlpack(py::capsule cap) {
+    PyObject* obj = cap.ptr();
+    if (!PyCapsule_IsValid(obj, "dltensor"))
+        throw InvalidArgumentError("from_dlpack: expected an unconsumed 'dltensor' capsule");
+    auto* mt = static_cast<DLManagedTensor*>(PyCapsule_GetPointer(obj, "dltensor"));
+    const DLTensor& d = mt->dl_tensor;
+    std::vector<int64_t> shape(d.shape, d.shape + d.ndim);
+    if (d.strides != nullptr) {
+        int64_t expect = 1;
+        for (int i = d.ndim - 1; i >= 0; --i) {
+            if (shape[i] != 1 && d.strides[i] != expect)
+                throw InvalidArgumentError("from_dlpack: tensor must be contiguous and row-major");
+            expect *= shape[i];
+        }
+    }
+    const DType dt = from_dl(d.dtype);
+    const bool gpu = d.device.device_type == kDLROCM || d.device.device_type == kDLCUDA;
+    if (!gpu && d.device.device_type != kDLCPU) throw InvalidArgumentError("from_dlpack: unsupported device type");
+    const Device dev = gpu ? Device::GPU : Device::CPU;
+    const int32_t id = gpu ? d.device.device_id : 0;
+    const void* src = static_cast<const char*>(d.data) + d.byte_offset;
+    if (gpu) {
+        hip_check(hipSetDevice(id), "hipSetDevice");
+        hip_check(hipDeviceSynchronize(), "from_dlpack sync");
+    }
+    Tensor t = Tensor::clone_from(src, shape, dt, dev, id, dev, id, nullptr);
+    PyCapsule_SetName(obj, "used_dltensor");
+    if (mt->deleter) mt->deleter(mt);
+    return t;
+}
+
 }  // namespace
+
+namespace edge_fm {
+void bind_layers(py::module_& m);   // pybind_layers.cpp
+}
 
 PYBIND11_MODULE(edge_fm, m) {
     m.doc() = "EdgeFM single-request transformer runtime for AMD Instinct MI355X (gfx950)";
@@ -99,6 +153,13 @@ PYBIND11_MODULE(edge_fm, m) {
              }),
              py::arg("data_ptr"), py::arg("shape"), py::arg("dtype"), py::arg("device") = Device::GPU,
              py::arg("device_id") = 0, py::arg("owned") = false)
+        .def_static("view",
+                    [](uintptr_t ptr, std::vector<int64_t> shape, DType dtype, Device device, int32_t device_id) {
+                        return Tensor::view(reinterpret_cast<void*>(ptr), std::move(shape), dtype, device, device_id);
+                    },
+                    py::arg("data_ptr"), py::arg("shape"), py::arg("dtype"), py::arg("device"),
+                    py::arg("device_id") = 0)
+        .def_static("from_dlpack", &from_dlpack, py::arg("capsule"))
         .def("to_dlpack", &to_dlpack)
         .def("empty", [](const Tensor& t) { return t.empty(); })
         .def("dtype", &Tensor::dtype)
@@ -243,6 +304,8 @@ PYBIND11_MODULE(edge_fm, m) {
           },
           py::arg("q"), py::arg("k"), py::arg("position_ids"), py::arg("mrope_section"), py::arg("rope_theta"),
           py::arg("rope_scale") = 1.0f);
+
+    bind_layers(m);
 
     m.attr("__version__") = efm_version();
 }
