@@ -897,6 +897,7 @@ def main():
                    "head_dim": shape.head_dim, "intermediate": shape.inter, "vocab": shape.vocab,
                    "prompt": args.prompt, "generated": args.gen, "hip_graph": True},
         "prefill_tokens_per_s": round(prefill_tps, 1),
+        "prefill_graph_replays": int(sum(m.get("prefill_graph_replayed", 0.0) for m in mets)),
         "decode_ms_per_token": round(ms_per_token, 4),
         "decode_loop": {"bytes_per_token": int(bytes_tok), "achieved_GBs": round(loop_gbs, 1),
                         "frac_of_hbm_peak": round(loop_gbs / HBM_PEAK_GBS, 4)},

@@ -295,8 +295,17 @@ __device__ __forceinline__ float add_bf16_pair(uint32_t w, float acc) {
                                            __builtin_bit_cast(bf16x2_t, 0x3f803f80u), acc, false);
 }
 
+// Waves per SIMD the register allocation aims for: 8 / WAVES, but never more than the
+// LDS ring lets reside (S stages of kP2Stage bytes out of 160 KB per CU, four SIMDs).
+constexpr int pipe_waves_per_eu(int waves, int stages) {
+    const int by_lds = (160 * 1024 / (stages * kP2Stage)) * waves / 4;
+    const int want = 8 / waves;
+    return by_lds < 1 ? 1 : (by_lds < want ? by_lds : want);
+}
+
 template <int WAVES, int S>
-__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_attn_pipe_kernel(PrefillArgs a, int nqt) {
+__global__ __launch_bounds__(WAVES * 64, pipe_waves_per_eu(WAVES, S)) void prefill_attn_pipe_kernel(PrefillArgs a,
+                                                                                                   int nqt) {
     constexpr int THREADS = WAVES * 64;
     constexpr int QR = WAVES * 32;                         // query rows per workgroup
     constexpr int LPW = kP2Stage / 1024 / WAVES;           // 1 KB wave loads per wave per tile

@@ -671,8 +671,13 @@ efm_attention_ctx Qwen2_5::decode_attn_ctx_rotated() const {
     return c;
 }
 
+uint64_t Qwen2_5::prefill_buffers_epoch() const {
+    return pf_epoch_ + mlp_source_->generation() + linear_scratch_generation(device_id_);
+}
+
 void Qwen2_5::ensure_prefill_capacity(int32_t S) {
     if (S <= pf_cap_) return;
+    ++pf_epoch_;
     const int64_t n = std::max<int64_t>(S, 64);
     const int64_t H = m_.hidden;
     pf_hidden_ = Tensor::empty({n, H}, DType::BFloat16, Device::GPU, device_id_);
@@ -1094,8 +1099,19 @@ StandardEngine::StandardEngine(const std::string& config_path) : cfg_(config_pat
 
 StandardEngine::~StandardEngine() {
     drop_graphs();
+    drop_prefill_graphs();
     if (stream_) hipStreamDestroy(stream_);
 }
+
+void StandardEngine::drop_prefill_graphs() {
+    for (auto& kv : pf_graphs_) {
+        if (kv.second.exec) hipGraphExecDestroy(kv.second.exec);
+        if (kv.second.graph) hipGraphDestroy(kv.second.graph);
+    }
+    pf_graphs_.clear();
+}
+
+uint64_t StandardEngine::prefill_epoch() const { return pf_input_epoch_ + model_->prefill_buffers_epoch(); }
 
 void StandardEngine::drop_graphs() {
     for (auto& kv : graphs_) {
@@ -1120,7 +1136,10 @@ void StandardEngine::warmup() {
         KVSlot& s = kv_->slot(rid);
         if (s.prefix_size == 0 || s.prefix_ready) continue;
         const int32_t n = s.prefix_size;
-        if (ids_dev_.empty() || ids_dev_.numel() < n) ids_dev_ = Tensor::empty({n}, DType::Int32, Device::GPU, device_id_);
+        if (ids_dev_.empty() || ids_dev_.numel() < n) {
+            ids_dev_ = Tensor::empty({n}, DType::Int32, Device::GPU, device_id_);
+            ++pf_input_epoch_;
+        }
         hip_check(hipMemcpyAsync(ids_dev_.data_ptr(), s.cfg.prefix_token_ids.data(), (size_t)n * 4,
                                  hipMemcpyHostToDevice, stream_),
                   "prefix ids");
@@ -1226,7 +1245,10 @@ Response StandardEngine::generate(const Request& request) {
     // max_generated = min(max_new_tokens, max_tokens - len(ids) + 1) (scheduler.cpp:123-134)
     const int32_t n_gen = std::max(1, std::min(cfg_.max_new_tokens(), slot.cfg.max_tokens - n_ids + 1));
 
-    if (ids_dev_.empty() || ids_dev_.numel() < S) ids_dev_ = Tensor::empty({S}, DType::Int32, Device::GPU, device_id_);
+    if (ids_dev_.empty() || ids_dev_.numel() < S) {
+        ids_dev_ = Tensor::empty({S}, DType::Int32, Device::GPU, device_id_);
+        ++pf_input_epoch_;
+    }
     hip_check(hipMemcpyAsync(ids_dev_.data_ptr(), req.token_ids.data() + base, (size_t)S * 4, hipMemcpyHostToDevice,
                              stream_),
               "token ids H2D");
@@ -1283,25 +1305,95 @@ Response StandardEngine::generate(const Request& request) {
     prepare_range.reset();
 
     EventTimer pf_model;  // pf.a .. pf_model.b: model; pf_model.b .. pf.b: sampler + finalize
-    hip_check(hipEventRecord(pf.a, stream_), "event");
     const bool greedy_fused = cfg_.temperature() < 1e-6f && cfg_.lm_head_top1() && !cfg_.debug_logits();
-    {
-        RoctxRange prefill_range("EDGEFM_PREFILL");
-        {
-            RoctxRange model_range("EDGEFM_PREFILL_MODEL");
-            model_->prefill(S, base, static_cast<int32_t*>(ids_dev_.data_ptr()), emb.empty() ? nullptr : &emb,
-                            req.embed_token_id, pos.empty() ? nullptr : static_cast<int32_t*>(pos.data_ptr()),
-                            kc.data(), vc.data(), st + 2,
-                            greedy_fused ? nullptr : static_cast<float*>(logits_.data_ptr()), stream_);
+    // graph mode: custom embeddings and M-RoPE positions go to persistent buffers that a
+    // captured prefill reads (stream-ordered copies ahead of the replay)
+    if (cfg_.use_graph()) {
+        if (!emb.empty()) {
+            if (pf_emb_dev_.empty() || pf_emb_dev_.nbytes() < emb.nbytes()) {
+                pf_emb_dev_ = Tensor::empty({(int64_t)emb.numel()}, DType::BFloat16, Device::GPU, device_id_);
+                ++pf_input_epoch_;
+            }
+            hip_check(hipMemcpyAsync(pf_emb_dev_.data_ptr(), emb.data_ptr(), emb.nbytes(), hipMemcpyDeviceToDevice,
+                                     stream_),
+                      "stage embeddings");
+            emb = pf_emb_dev_.prefix_view(emb.shape());
         }
-        hip_check(hipEventRecord(pf_model.b, stream_), "event");
-        RoctxRange sampler_range("EDGEFM_PREFILL_SAMPLER");
+        if (!pos.empty()) {
+            if (pf_pos_dev_.empty() || pf_pos_dev_.nbytes() < pos.nbytes()) {
+                pf_pos_dev_ = Tensor::empty({(int64_t)pos.numel()}, DType::Int32, Device::GPU, device_id_);
+                ++pf_input_epoch_;
+            }
+            hip_check(hipMemcpyAsync(pf_pos_dev_.data_ptr(), pos.data_ptr(), pos.nbytes(), hipMemcpyDeviceToDevice,
+                                     stream_),
+                      "stage position ids");
+            pos = pf_pos_dev_.prefix_view(pos.shape());
+        }
+    }
+    auto prefill_work = [&]() {
+        model_->prefill(S, base, static_cast<int32_t*>(ids_dev_.data_ptr()), emb.empty() ? nullptr : &emb,
+                        req.embed_token_id, pos.empty() ? nullptr : static_cast<int32_t*>(pos.data_ptr()), kc.data(),
+                        vc.data(), st + 2, greedy_fused ? nullptr : static_cast<float*>(logits_.data_ptr()), stream_);
+    };
+    auto finalize_work = [&]() {
         if (!greedy_fused) sample_logits(0);
         efm_check(efm_finalize_decode_token_indexed(st + 2, static_cast<int32_t*>(response_dev_.data_ptr()),
                                                     reinterpret_cast<uint32_t*>(st + 1),
                                                     reinterpret_cast<uint32_t*>(st), (uint32_t)response_dev_.numel(),
                                                     stream_),
                   "finalize prefill token");
+    };
+    bool prefill_replayed = false;
+    if (cfg_.use_graph()) {
+        const PrefillKey key{req.request_id, S, base, emb.empty() ? 0 : emb.shape()[0],
+                             emb.empty() ? -1 : req.embed_token_id};
+        const uint64_t epoch = prefill_epoch();
+        auto it = pf_graphs_.find(key);
+        if (it != pf_graphs_.end() && it->second.epoch != epoch) {
+            hipGraphExecDestroy(it->second.exec);
+            hipGraphDestroy(it->second.graph);
+            pf_graphs_.erase(it);
+            it = pf_graphs_.end();
+        }
+        if (it == pf_graphs_.end() && pf_seen_.count(key)) {
+            if (pf_graphs_.size() >= kMaxPrefillGraphs) drop_prefill_graphs();
+            RoctxRange capture_range("EDGEFM_PREFILL_CAPTURE");
+            PrefillGraph g;
+            hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin prefill capture");
+            try {
+                prefill_work();
+                finalize_work();
+            } catch (...) {
+                hipGraph_t tmp = nullptr;
+                hipStreamEndCapture(stream_, &tmp);
+                if (tmp) hipGraphDestroy(tmp);
+                throw;
+            }
+            hip_check(hipStreamEndCapture(stream_, &g.graph), "end prefill capture");
+            hip_check(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0), "prefill graph instantiate");
+            g.epoch = epoch;
+            it = pf_graphs_.emplace(key, g).first;
+        }
+        if (it != pf_graphs_.end()) {
+            RoctxRange replay_range("EDGEFM_PREFILL_GRAPH_REPLAY");
+            hip_check(hipEventRecord(pf.a, stream_), "event");
+            hip_check(hipGraphLaunch(it->second.exec, stream_), "prefill graph launch");
+            hip_check(hipEventRecord(pf_model.b, stream_), "event");
+            prefill_replayed = true;
+        } else {
+            pf_seen_.insert(key);
+        }
+    }
+    if (!prefill_replayed) {
+        hip_check(hipEventRecord(pf.a, stream_), "event");
+        RoctxRange prefill_range("EDGEFM_PREFILL");
+        {
+            RoctxRange model_range("EDGEFM_PREFILL_MODEL");
+            prefill_work();
+        }
+        hip_check(hipEventRecord(pf_model.b, stream_), "event");
+        RoctxRange sampler_range("EDGEFM_PREFILL_SAMPLER");
+        finalize_work();
     }
     hip_check(hipEventRecord(pf.b, stream_), "event");
 
@@ -1415,6 +1507,7 @@ Response StandardEngine::generate(const Request& request) {
     metrics_["executed_generated_tokens_total"] = n_gen;
     metrics_["returned_generated_tokens_total"] = returned;
     metrics_["cuda_graph_enabled"] = cfg_.use_graph() ? 1.0 : 0.0;
+    metrics_["prefill_graph_replayed"] = prefill_replayed ? 1.0 : 0.0;
     metrics_["lm_head_top1_enabled"] = greedy_fused ? 1.0 : 0.0;
     metrics_["lm_head_top1_decode_steps"] = greedy_fused ? steps : 0.0;
     metrics_["response_tokens_capacity"] = (double)response_dev_.numel();

@@ -8,6 +8,7 @@
 #pragma once
 
 #include <map>
+#include <set>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -244,6 +245,11 @@ public:
     // a decode step is captured into a graph: capture cannot allocate).
     void reserve_decode(uint32_t max_kv_len);
 
+    // Changes whenever a buffer that prefill reads or writes is replaced (its grow-only
+    // scratch, the MLP intermediate, the shared split-K scratch): a captured prefill is
+    // valid only while this is unchanged.
+    uint64_t prefill_buffers_epoch() const;
+
     // Whether decode steps with caches of max_kv_len rows run every layer in one
     // persistent launch (efm_decode_stack) instead of the per-operator kernels.
     bool uses_decode_stack(uint32_t max_kv_len) const;
@@ -291,6 +297,7 @@ private:
     Tensor front_sync_ws_;
     // prefill scratch (grow-only)
     int32_t pf_cap_ = 0;
+    uint64_t pf_epoch_ = 0;
     Tensor pf_hidden_, pf_res_, pf_norm_, pf_qkv_, pf_attn_, pf_mid_;
 
     const Tensor& w(const std::unordered_map<std::string, Tensor>& ws, const std::string& name) const;
@@ -344,6 +351,26 @@ private:
     };
     std::map<int32_t, GraphEntry> graphs_;  // per request slot
     void drop_graphs();
+
+    // Prefill graphs (standard_engine.cpp:568-800): one per (request slot, prefilled rows,
+    // cache base row, custom embedding rows, embed_token_id), captured the second time a
+    // key is prefilled (the first, eager, run sizes every buffer the capture then reads)
+    // and replayed after that. The request's ids, custom embeddings and M-RoPE positions
+    // are staged into the persistent buffers below first, so a replay reads this call's
+    // inputs. A graph is dropped when a buffer it uses has been replaced since capture.
+    using PrefillKey = std::tuple<int32_t, int32_t, int32_t, int64_t, int32_t>;
+    struct PrefillGraph {
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        uint64_t epoch = 0;
+    };
+    static constexpr size_t kMaxPrefillGraphs = 32;
+    std::map<PrefillKey, PrefillGraph> pf_graphs_;
+    std::set<PrefillKey> pf_seen_;
+    Tensor pf_emb_dev_, pf_pos_dev_;
+    uint64_t pf_input_epoch_ = 0;
+    uint64_t prefill_epoch() const;
+    void drop_prefill_graphs();
 
     // stage_events: StageEvents of the eager loop's per-step timing, or null (captured)
     void run_decode_step(int32_t request_id, void* stage_events);

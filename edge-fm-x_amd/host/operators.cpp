@@ -438,6 +438,7 @@ namespace {
 struct SharedLinearScratch {
     std::mutex mu;
     std::map<int32_t, Tensor> bufs;
+    std::map<int32_t, uint64_t> generation;   // bumped whenever a device's buffer is replaced
 } g_linear_scratch;
 }  // namespace
 
@@ -448,9 +449,15 @@ void* linear_scratch(size_t bytes, int32_t device_id, size_t* have) {
         if (!t.empty()) hip_check(hipDeviceSynchronize(), "linear scratch grow");
         t = Tensor();
         t = Tensor::empty({(int64_t)bytes}, DType::UInt8, Device::GPU, device_id);
+        ++g_linear_scratch.generation[device_id];
     }
     *have = t.empty() ? 0 : t.nbytes();
     return t.empty() ? nullptr : t.data_ptr();
+}
+
+uint64_t linear_scratch_generation(int32_t device_id) {
+    std::lock_guard<std::mutex> lock(g_linear_scratch.mu);
+    return g_linear_scratch.generation[device_id];
 }
 
 size_t linear_scratch_bytes(int32_t device_id) {
@@ -704,7 +711,10 @@ bool PrefillLinearSourceOp::try_forward(const std::string& role, int32_t, const 
 
 PrefillMlpSourceOp::PrefillMlpSourceOp(const EngineConfig& config) : device_id_(config.device_id()) {}
 PrefillMlpSourceOp::~PrefillMlpSourceOp() = default;
-void PrefillMlpSourceOp::reset_runtime_caches() { intermediate_ = Tensor(); }
+void PrefillMlpSourceOp::reset_runtime_caches() {
+    intermediate_ = Tensor();
+    ++generation_;
+}
 
 bool PrefillMlpSourceOp::try_forward(int32_t, const Tensor& input, const Tensor& gate_up_weight,
                                      const Tensor& down_weight, Tensor& output, hipStream_t stream) {
@@ -719,6 +729,7 @@ bool PrefillMlpSourceOp::try_forward(int32_t, const Tensor& input, const Tensor&
         if (!intermediate_.empty()) hip_check(hipDeviceSynchronize(), "prefill mlp intermediate grow");
         intermediate_ = Tensor();
         intermediate_ = Tensor::empty({m, inter}, DType::BFloat16, Device::GPU, device_id_);
+        ++generation_;
     }
     // both launches share the scratch (stream order): grown once, to the larger need
     const size_t need_gu = efm_fused_gate_up_swiglu_workspace_bytes(m, h, inter);

@@ -352,16 +352,23 @@ public:
     bool try_forward(int32_t layer_id, const Tensor& input, const Tensor& gate_up_weight, const Tensor& down_weight,
                      Tensor& output, hipStream_t stream);
     void reset_runtime_caches();
+    // Changes whenever the intermediate buffer is replaced (captured work that used the
+    // old one must be captured again).
+    uint64_t generation() const { return generation_; }
 
 private:
     int32_t device_id_ = 0;
     Tensor intermediate_;   // [m_max, I], grown on demand
+    uint64_t generation_ = 0;
 };
 
 // The split-K scratch shared by every prefill projection on a device (grow-only; see
 // operators.cpp): a pointer to at least `bytes` (have = its size), and its current size.
 void* linear_scratch(size_t bytes, int32_t device_id, size_t* have);
 size_t linear_scratch_bytes(int32_t device_id);
+// Number of times the device's scratch has been replaced (captured work that used the
+// old buffer must be captured again).
+uint64_t linear_scratch_generation(int32_t device_id);
 
 // ---------------------------------------------------------------------------------
 // Fused gate/up + SwiGLU (src/operators/fused_gate_up_activation_op.h:14-74). The
