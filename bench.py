@@ -123,6 +123,12 @@ def roofline_kernel(torch, C, shape, weights, dev, graph=True, reps=20, traffic=
             "timing": f"HIP events around one replay of a graph of {reps}x{shape.layers} launches"}
 
 
+def engine_row_bound(rows, capacity):
+    """The row bound the engine's decode launches use for steps attending `rows` rows: the
+    128-row bucket holding it, at most the slot capacity (StandardEngine::decode_row_bound)."""
+    return min(capacity, (max(rows, 1) + 127) // 128 * 128)
+
+
 def decode_layer_kernels(torch, C, shape, weights, dev, ctx_len, max_kv, reps=20, eager=False):
     """The five kernels of one decode layer in the engine's default plan, each timed over
     all layers' real weights: a HIP graph of reps x layers launches of one kernel is
@@ -294,7 +300,8 @@ def kernel_only(torch, C, S, shape, seed):
     torch.cuda.synchronize()
     del x, y
     weights = S.synthetic_weights_gpu(shape, seed=seed)
-    decode_layer_kernels(torch, C, shape, weights, dev, ctx_len=640, max_kv=768, reps=2, eager=True)
+    decode_layer_kernels(torch, C, shape, weights, dev, ctx_len=640, max_kv=engine_row_bound(640, 768), reps=2,
+                         eager=True)
     torch.cuda.synchronize()
     print(json.dumps({"kernel_only": "per-layer decode kernels", "launches_each": 2 * shape.layers,
                       "copy_calibration_bytes": 256 << 20}))
@@ -865,8 +872,9 @@ def main():
     bytes_tok = decode_bytes_per_token(shape, mean_ctx)
     loop_gbs = bytes_tok / (ms_per_token * 1e-3) / 1e9
 
-    layer_kernels = decode_layer_kernels(torch, C, shape, weights, dev, ctx_len=int(round(mean_ctx)),
-                                         max_kv=args.prompt + args.gen)
+    ctx_mean = int(round(mean_ctx))
+    layer_kernels = decode_layer_kernels(torch, C, shape, weights, dev, ctx_len=ctx_mean,
+                                         max_kv=engine_row_bound(ctx_mean, args.prompt + args.gen))
     dom = layer_kernels[0]
     kern = {"kernel": dom["kernel"], "bound": "hbm", "achieved": dom["achieved_GBs"], "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": dom["frac"], "traffic": measured_traffic(dom["name"]),

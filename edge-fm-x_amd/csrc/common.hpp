@@ -13,6 +13,9 @@
 namespace efm {
 
 constexpr int kWave = 64;
+// Split-KV decode partials that the o_proj GEMV's merge prologue holds (one register
+// slot per split): caches of up to 8 x 128 rows.
+constexpr int kMergeMaxSplits = 8;
 
 typedef uint16_t bf16_t;
 

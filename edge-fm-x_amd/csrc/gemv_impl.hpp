@@ -85,7 +85,6 @@ struct GemvArgs {
 };
 
 
-constexpr int kMergeMaxSplits = 8;
 constexpr int kMergeMaxHeads = 64;
 
 constexpr int kPlainPre = 4;   // PLAIN input chunks per thread loaded ahead of the weights

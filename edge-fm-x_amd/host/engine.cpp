@@ -1178,7 +1178,12 @@ void StandardEngine::sample_logits(uint32_t) {
               "top-p sampler");
 }
 
-void StandardEngine::run_decode_step(int32_t request_id, void* stage_events) {
+uint32_t StandardEngine::decode_row_bound(uint32_t rows, uint32_t capacity) {
+    const uint32_t b = (std::max<uint32_t>(rows, 1u) + kDecodeBoundRows - 1) / kDecodeBoundRows * kDecodeBoundRows;
+    return std::min(b, capacity);
+}
+
+void StandardEngine::run_decode_step(int32_t request_id, void* stage_events, uint32_t row_bound) {
     StageEvents* se = static_cast<StageEvents*>(stage_events);
     int32_t* st = static_cast<int32_t*>(state_.data_ptr());
     uint32_t* d_kv_len = reinterpret_cast<uint32_t*>(st + 0);
@@ -1191,7 +1196,8 @@ void StandardEngine::run_decode_step(int32_t request_id, void* stage_events) {
     if (se) se->record(stream_);
     {
         RoctxRange r(se ? "EDGEFM_DECODE_MODEL" : nullptr);
-        model_->decode_step(tok, d_kv_len, (uint32_t)slot.cfg.max_tokens, pos3, kc.data(), vc.data(),
+        check<InternalError>(row_bound >= 1 && row_bound <= (uint32_t)slot.cfg.max_tokens, "decode row bound");
+        model_->decode_step(tok, d_kv_len, row_bound, pos3, kc.data(), vc.data(),
                             greedy_fused ? nullptr : static_cast<float*>(logits_.data_ptr()), stream_);
     }
     if (se) se->record(stream_);
@@ -1404,15 +1410,25 @@ Response StandardEngine::generate(const Request& request) {
     const int32_t steps = n_gen - 1;
     if (steps > 0) {
         RoctxRange decode_range("EDGEFM_GENERATION");
+        // decode step i attends base + S + i + 1 rows; its launches read below a 128-row bound:
+        // that of the last step of its kGraphSteps group (a graph's steps share one bound), or
+        // its own past the last whole group. Eager decoding uses the same bounds, so both
+        // run the same kernels.
+        const uint32_t cap = (uint32_t)slot.cfg.max_tokens;
+        auto bound_at = [&](int32_t step_end) { return decode_row_bound((uint32_t)(base + S + step_end), cap); };
+        const int32_t grouped = steps / kGraphSteps * kGraphSteps;
+        auto step_bound = [&](int32_t i) {
+            return i < grouped ? bound_at((i / kGraphSteps + 1) * kGraphSteps) : bound_at(i + 1);
+        };
         if (cfg_.use_graph()) {
-            GraphEntry& g = graphs_[req.request_id];
             // every step reads its position and writes its token through device state, so
             // n consecutive captures of one step replay as n steps
-            auto capture = [&](int32_t n, hipGraph_t* graph, hipGraphExec_t* exec) {
+            auto capture = [&](int32_t n, uint32_t bound, hipGraph_t* graph, hipGraphExec_t* exec) {
                 RoctxRange capture_range("EDGEFM_DECODE_PREPARE");
+                model_->reserve_decode(bound);
                 hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
                 try {
-                    for (int32_t i = 0; i < n; ++i) run_decode_step(req.request_id, nullptr);
+                    for (int32_t i = 0; i < n; ++i) run_decode_step(req.request_id, nullptr, bound);
                 } catch (...) {
                     hipGraph_t tmp = nullptr;
                     hipStreamEndCapture(stream_, &tmp);
@@ -1422,16 +1438,31 @@ Response StandardEngine::generate(const Request& request) {
                 hip_check(hipStreamEndCapture(stream_, graph), "end capture");
                 hip_check(hipGraphInstantiate(exec, *graph, nullptr, nullptr, 0), "graph instantiate");
             };
-            if (g.exec == nullptr) capture(1, &g.graph, &g.exec);
-            if (steps >= kGraphSteps && g.exec_n == nullptr) capture(kGraphSteps, &g.graph_n, &g.exec_n);
+            // the launch sequence (graph of kGraphSteps steps or of one, and its bound); every
+            // graph it needs is captured before the first replay
+            std::vector<std::pair<hipGraphExec_t*, uint32_t>> seq;
+            int32_t done = 0;
+            for (; done + kGraphSteps <= steps; done += kGraphSteps) {
+                const uint32_t bound = step_bound(done);
+                GraphEntry& g = graphs_[{req.request_id, bound}];
+                if (g.exec_n == nullptr) capture(kGraphSteps, bound, &g.graph_n, &g.exec_n);
+                seq.push_back({&g.exec_n, bound});
+            }
+            for (; done < steps; ++done) {
+                const uint32_t bound = step_bound(done);
+                GraphEntry& g = graphs_[{req.request_id, bound}];
+                if (g.exec == nullptr) capture(1, bound, &g.graph, &g.exec);
+                seq.push_back({&g.exec, bound});
+            }
             decode_prepare_host_ms = host_ms_since(dprep_t0);
             RoctxRange replay_range("EDGEFM_DECODE_GRAPH_REPLAY");
-            int32_t done = 0;
-            for (; done + kGraphSteps <= steps; done += kGraphSteps)
-                hip_check(hipGraphLaunch(g.exec_n, stream_), "graph launch");
-            for (; done < steps; ++done) hip_check(hipGraphLaunch(g.exec, stream_), "graph launch");
+            for (const auto& e : seq) hip_check(hipGraphLaunch(*e.first, stream_), "graph launch");
         } else {
-            for (int32_t i = 0; i < steps; ++i) run_decode_step(req.request_id, &stage);
+            for (int32_t i = 0; i < steps; ++i) {
+                const uint32_t bound = step_bound(i);
+                model_->reserve_decode(bound);
+                run_decode_step(req.request_id, &stage, bound);
+            }
         }
     }
     hip_check(hipEventRecord(dc.b, stream_), "event");

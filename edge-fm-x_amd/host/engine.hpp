@@ -349,8 +349,17 @@ private:
         hipGraph_t graph_n = nullptr;
         hipGraphExec_t exec_n = nullptr;
     };
-    std::map<int32_t, GraphEntry> graphs_;  // per request slot
+    // per (request slot, row bound): a decode step reads cache rows below the bound that
+    // its launches were built for, so graphs are captured per 128-row bucket of the
+    // lengths their steps reach (decode_row_bound)
+    std::map<std::pair<int32_t, uint32_t>, GraphEntry> graphs_;
     void drop_graphs();
+    // Row bound of decode steps whose longest attended length is `rows`: the 128-row
+    // bucket holding it (the split plan's unit), at most the slot's capacity. Split b
+    // requests rows [128 b, 128 b + 128) below the bound before the device-side length is
+    // read, so a bound near the length keeps those reads to live rows.
+    static constexpr uint32_t kDecodeBoundRows = 128;
+    static uint32_t decode_row_bound(uint32_t rows, uint32_t capacity);
 
     // Prefill graphs (standard_engine.cpp:568-800): one per (request slot, prefilled rows,
     // cache base row, custom embedding rows, embed_token_id), captured the second time a
@@ -373,7 +382,7 @@ private:
     void drop_prefill_graphs();
 
     // stage_events: StageEvents of the eager loop's per-step timing, or null (captured)
-    void run_decode_step(int32_t request_id, void* stage_events);
+    void run_decode_step(int32_t request_id, void* stage_events, uint32_t row_bound);
     void sample_logits(uint32_t step_index);
     std::vector<void*> caches(int32_t request_id, bool k);
 };

@@ -119,3 +119,22 @@ def test_prefill_graph_vl_embeddings_and_positions_change():
             etoks, elogits, _ = _run(ee, r)
             assert m["prefill_graph_replayed"] == (0.0 if i == 0 else 1.0)
             assert toks == etoks and np.array_equal(logits, elogits), f"call {i}"
+
+
+@pytest.mark.parametrize("prompt_len,gen,max_tokens", [(100, 200, 400), (1000, 60, 1100)])
+def test_decode_graphs_per_row_bucket_equal_eager(prompt_len, gen, max_tokens):
+    """Decode graphs are captured per 128-row bucket of the lengths their steps reach
+    (StandardEngine::decode_row_bound): generations that cross buckets inside an 8-step
+    graph, and (1000 + 60 rows) cross from the 8-split plan whose merge folds into o_proj
+    (<= 1024 rows) to the generic attention, must equal the eager engine's tokens and fp32
+    logits bit for bit."""
+    w = O.random_weights(_cfg(TINY), seed=24, std=0.2)
+    ids = torch.randint(0, TINY.vocab, (prompt_len,), generator=torch.Generator().manual_seed(9)).tolist()
+    with tempfile.TemporaryDirectory() as tmp:
+        (ge, _k1), (ee, _k2) = _engines(tmp, TINY, w, max_tokens=max_tokens, max_new_tokens=gen)
+        etoks, elogits, _ = _run(ee, _req(ids))
+        for rep in range(2):
+            toks, logits, m = _run(ge, _req(ids))
+            assert len(toks) == gen and m["decode_steps"] == gen - 1
+            assert toks == etoks, f"rep {rep}: tokens differ from the eager engine"
+            assert np.array_equal(logits, elogits), f"rep {rep}: logits differ from the eager engine"

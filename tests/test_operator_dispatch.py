@@ -63,7 +63,12 @@ def test_default_plan_follows_the_shape(tmp_path):
                and l["down"] == LINEAR for l in p)
     assert [l["attention"] for l in _plan(tmp_path, TEXT64, name="b")] == [SPLIT, SPLIT]
     assert [l["attention"] for l in _plan(tmp_path, VL128, name="c")] == [SPLIT, SPLIT]
-    # more than 8 splits of 128 rows cannot merge in o_proj: generic attention, plain GEMV o_proj
+    # more than 8 splits of 128 rows cannot merge in o_proj: generic attention, plain GEMV
+    # o_proj (splits of 160-256 rows that would keep 8 were measured slower than this)
+    p = _plan(tmp_path, TEXT128, max_kv=1024, name="d0")
+    assert all(l["attention"] == SPLIT and l["partials_to_o_proj"] for l in p)
+    p = _plan(tmp_path, TEXT128, max_kv=1025, name="d1")
+    assert all(l["attention"] == GENERIC and not l["partials_to_o_proj"] for l in p)
     p = _plan(tmp_path, TEXT128, max_kv=4096, name="d")
     assert all(l["attention"] == GENERIC and not l["partials_to_o_proj"] for l in p)
     # a record selects the one-launch impl; the engine config can forbid it
