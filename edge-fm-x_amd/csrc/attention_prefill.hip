@@ -678,16 +678,14 @@ extern "C" int efm_attention_prefill(const efm_attention_ctx* ctx, const void* q
     if (hd == kP2HD && !a.rope_k && prefill_pipe_enabled()) {
         // 8 waves (256 rows, 4-deep ring, one workgroup per CU) when those workgroups fill
         // the chip; fewer rows: 4 waves (128 rows) over a 2-deep ring, two workgroups per
-        // CU (twice the workgroups); when even those would occupy at most a quarter of the
-        // CUs: 2 waves (64 rows, 2-deep ring, four times the workgroups; measured at 12/2
-        // heads, S 512: 18.0 us against 22.4 with 4 waves, while at 112 or more 4-wave
-        // workgroups the 4-wave kernel is faster). EFM_KNOB_PREFILL_SHAPE = 2 / 4 / 8
-        // forces one of them.
+        // CU (twice the workgroups). Measured (causal, no prefix): 12/2 heads S 256 / 512 /
+        // 2048: 10.7 / 15.9 / 46.0 us with 4 waves against 11.4 / 18.2 / 62.8 with the
+        // 2-wave (64-row) kernel and 12.5 / 19.2 / 58.7 with 8 waves; 16/2 S 1344: 31.2
+        // against 42.9 / 38.7; 28/4 S 4096: 151.4 against 237.4 / 146.2. The 2-wave kernel
+        // stays for EFM_KNOB_PREFILL_SHAPE = 2 (2 / 4 / 8 force a shape).
         const int knob = kernel_knob(EFM_KNOB_PREFILL_SHAPE);
         const int cus = prefill_cus();
-        const int shape = knob != 0 ? knob
-                          : (int)((qo_len + 255) / 256) * a.Hq >= cus ? 8
-                          : (int)((qo_len + 127) / 128) * a.Hq * 4 > cus ? 4 : 2;
+        const int shape = knob != 0 ? knob : (int)((qo_len + 255) / 256) * a.Hq >= cus ? 8 : 4;
         if (shape == 2) {
             const int nqt = (int)((qo_len + 63) / 64);
             hipLaunchKernelGGL((prefill_attn_pipe_kernel<2, 2>), dim3(nqt * a.Hq), dim3(128), 0, stream, a, nqt);

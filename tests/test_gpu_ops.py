@@ -1074,6 +1074,7 @@ PIPE_CASES = [
     pytest.param(28, 4, 1000, 1000, 1, "none", id="7b_s1000"),
     pytest.param(16, 2, 1344, 1344, 1, "none", id="vl3b_s1344"),
     pytest.param(12, 2, 255, 1025, 0, "prerot", id="noncausal_prefix"),
+    pytest.param(12, 2, 512, 512, 1, "none", id="1p5b_s512"),
 ]
 
 
