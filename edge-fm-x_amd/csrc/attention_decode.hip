@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kAttnThreads, ROTK ? 1 : 2) void decode_attn_kernel
     const int ql = lane % 32, hh = lane / 32;
     const int kvh = blockIdx.y;
     const int b = blockIdx.x;
-    const int kps = a.keys_per_split;   // a multiple of 32 keys (>= 128), fixed per launch
+    const int kps = a.keys_per_split;   // >= 128 keys, fixed per launch
     const int start = b * kps;
 
     const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
@@ -355,9 +355,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void decode_attn_lds_kernel(Decode
     decode_attn_lds_body<G, MERGE, false>(a, blockIdx.x, blockIdx.y, FusedAttnArgs{});
 }
 
-template <int G, bool MERGE>
+template <int G, bool MERGE, bool ROTK>
 __global__ __launch_bounds__(kWideThreads, 1) void decode_attn_wide_kernel(DecodeArgs a) {
-    decode_attn_wide_body<G, MERGE>(a, blockIdx.x, blockIdx.y);
+    decode_attn_wide_body<G, MERGE, ROTK>(a, blockIdx.x, blockIdx.y);
 }
 
 // ---- one-wave splits (short and mid contexts) ----
@@ -807,6 +807,10 @@ int decode_keys_per_split(int num_kv_heads, uint32_t max_kv_len) {
     const uint32_t heads = (uint32_t)std::max(1, num_kv_heads);
     const uint32_t by_chip = std::max<uint32_t>(1u, (uint32_t)kMaxSplits / heads);
     if ((bound + kKeysPerSplit - 1) / kKeysPerSplit <= by_chip) return kKeysPerSplit;
+    // one 8-wave workgroup per CU in whole 32-key tiles: a tile's 16 load requests take
+    // the address unit's time whether or not its rows exist, so whole tiles on fewer CUs
+    // beat partial ones on every CU (16512 rows x 4 KV heads: 58 splits of 288 rows
+    // 11.0 us; 60 of 276 11.4; 64 of 260 11.6)
     const uint32_t per_cu = std::max<uint32_t>(1u, (uint32_t)kChipCUs / heads);
     const uint32_t wide = kTileKeys * ((bound + kTileKeys * per_cu - 1) / (kTileKeys * per_cu));
     if (wide <= (uint32_t)(kWideMaxTiles * kTileKeys)) return (int)wide;
@@ -975,13 +979,17 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
     dim3 grid(a.split_cap, ctx->num_kv_heads), block(kAttnThreads);
     // one split: that workgroup writes the output; more: partials, then the merge kernel
     const bool direct = merge && a.split_cap == 1;
-    if (hd == 128 && !rotk && decode_lds_offsets_fit(a) && kernel_knob(EFM_KNOB_DECODE_REGISTER) == 0) {
-        const bool wide = decode_wide_fits(a);
+    // The reference's un-rotated cache (rotk) takes the 8-wave kernel where its splits fit
+    // it, else the register-staged kernel; the 4-wave LDS kernel reads rotated keys only.
+    const bool wide = decode_wide_fits(a);
+    if (hd == 128 && (!rotk || wide) && decode_lds_offsets_fit(a) && kernel_knob(EFM_KNOB_DECODE_REGISTER) == 0) {
         const dim3 wblock(kWideThreads);
 #define EFM_DEC_LDS_CASE(GV)                                                                                   \
         if (G == GV) {                                                                                         \
-            if (wide && direct) hipLaunchKernelGGL((decode_attn_wide_kernel<GV, true>), grid, wblock, 0, stream, a); \
-            else if (wide) hipLaunchKernelGGL((decode_attn_wide_kernel<GV, false>), grid, wblock, 0, stream, a);  \
+            if (wide && direct && rotk) hipLaunchKernelGGL((decode_attn_wide_kernel<GV, true, true>), grid, wblock, 0, stream, a); \
+            else if (wide && rotk) hipLaunchKernelGGL((decode_attn_wide_kernel<GV, false, true>), grid, wblock, 0, stream, a); \
+            else if (wide && direct) hipLaunchKernelGGL((decode_attn_wide_kernel<GV, true, false>), grid, wblock, 0, stream, a); \
+            else if (wide) hipLaunchKernelGGL((decode_attn_wide_kernel<GV, false, false>), grid, wblock, 0, stream, a); \
             else if (direct) hipLaunchKernelGGL((decode_attn_lds_kernel<GV, true>), grid, block, 0, stream, a); \
             else hipLaunchKernelGGL((decode_attn_lds_kernel<GV, false>), grid, block, 0, stream, a);           \
             if (merge && !direct)                                                                              \

@@ -487,16 +487,19 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
     if (FUSED && tid == 0) fused_attn_done(f);
 }
 
-// Wide variant for long contexts (head_dim 128, rotated cache, unfused launches): one
+// Wide variant for long contexts (head_dim 128, unfused launches): one
 // 8-wave workgroup per CU holds every 32-key tile of its split in LDS (up to
 // kWideMaxTiles: 288 keys, 144 KB), all requested at the start; wave w computes the tiles
 // w and w + 8 (a split need not be whole tiles: rows past its end read as zeros and are
 // masked). Eight waves per CU keep more K/V loads in flight than the 4-wave kernel's
 // two workgroups, whose 256-key splits at 16k keys had to load their second 128-key
-// round after the first. The loads are buffer loads straight into LDS: a wave's
-// missing second tile reads past the resource (no memory access) into a shared sink, so
-// every wave issues the same number of loads and the compiler waits for the query,
-// length and RoPE loads issued before them without waiting for the tiles.
+// round after the first. The loads are buffer loads straight into LDS, issued before the
+// length is known; rows past the split's last readable row read past the resource (no
+// memory access) and land as zeros.
+// ROTK = true: every key is rotated on read at its position (the reference's un-rotated
+// cache); each wave computes its tile's cos / sin before waiting for the tile, under the
+// load phase. ROTK = false: keys are used as stored, and with a.fix_last row L - 1 is
+// rotated, used and stored back by the lane that holds it.
 constexpr int kWideWaves = 8;
 constexpr int kWideThreads = kWideWaves * kWave;
 constexpr int kWideMaxTiles = 9;
@@ -507,7 +510,7 @@ __device__ __forceinline__ void wide_lds_load(__amdgpu_buffer_rsrc_t rs, uint32_
                                              0, 0, 0);
 }
 
-template <int G, bool MERGE>
+template <int G, bool MERGE, bool ROTK>
 __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b, int kvh) {
     constexpr int HD = 128, HALF = 64, KS = 8, DT = 4, W = kWideWaves, NT = kWideThreads;
     constexpr int KB = kTileKeys * attn_pipe::kRow;            // bytes of K (or V) of a tile
@@ -515,8 +518,11 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
     static_assert((W * G * HD + 2 * W * 32 + W * G + 2 * G) * 4 <= kWideMaxTiles * kWideTileBytes,
                   "merge buffers must fit the tiles");
     __shared__ __align__(1024) unsigned char smem[kWideMaxTiles * kWideTileBytes];   // tiles; then the merge
-    __shared__ __align__(1024) unsigned char sink[1024];      // destination of the skipped loads
     __shared__ float2 cs_qk[2][HALF];
+    __shared__ float sfreq[ROTK ? HALF : 1];
+    // ROTK: (cos, sin) as fp16 pairs for the keys of tile W (wave 0's second tile), row =
+    // key, 16-byte chunks XOR-swizzled by the row; built by every thread during set-up
+    __shared__ __align__(16) uint32_t cs9[ROTK ? kTileKeys * HALF : 1];
     __shared__ __align__(16) bf16_t qs[G * HD];
     __shared__ __align__(16) bf16_t qr[G * HD];
 
@@ -536,6 +542,28 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
     const float freq = (a.rope_q && tid < 2 * HALF) ? a.rope.inv_freq[tid % HALF] : 0.f;
     const int q_pos_off = __builtin_amdgcn_readfirstlane(a.q_pos_off);
     const int k_pos_off = __builtin_amdgcn_readfirstlane(a.k_pos_off);
+    // ROTK: cos / sin of this lane's key in its first tile (t0 + ql) for its d = 16 ks + 8 hh
+    // + e, ks < KS / 2. The tile loads are bound by the address unit, which takes the
+    // workgroup's requests in turn: waves W/2.. compute theirs before issuing their loads
+    // (while the unit works through the first half's requests), waves ..W/2-1 after
+    // issuing theirs (while it works through the second half's).
+    float2 ck[ROTK ? KS / 2 : 1][8];
+    const bool ck_early = ROTK && __builtin_amdgcn_readfirstlane(wave) >= W / 2;
+    if (ck_early) {
+        const float pos = (float)(start + wave * kTileKeys + ql + k_pos_off);
+#pragma unroll
+        for (int ks = 0; ks < KS / 2; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                // both candidates as uniform (scalar) loads, then a per-lane select
+                const float flo = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(a.rope.inv_freq[ks * 16 + e])));
+                const float fhi = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(a.rope.inv_freq[ks * 16 + 8 + e])));
+                const float f = hh ? fhi : flo;
+                float sn, cs;
+                sincos_reduced(pos * f, &sn, &cs);
+                ck[ks][e] = make_float2(cs, sn);
+            }
+    }
     {
         const int lim = min(a.row_bound, start + kps) - 1;   // last row this split may read
         const int nrec = __builtin_amdgcn_readfirstlane(a.row_bound * a.k_sn * 2);
@@ -546,16 +574,15 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
             const_cast<bf16_t*>(a.v + (size_t)kvh * a.v_sh), (short)0, nrecv, 0x00020000);
         const int pr = lane >> 4, pc = lane & 15;
         const int wu = __builtin_amdgcn_readfirstlane(wave);
-        // A missing tile's loads keep their place in the sequence (masks, not branches: the
-        // compiler counts loads only along straight-line code) but read nothing.
+        // Only wave 0 can have a second tile (ntiles <= W + 1); the other waves issue no
+        // loads for it (load requests that read nothing still take address-unit time: with
+        // seven waves issuing a skipped tile the 16k call took 1 us longer).
         const uint32_t smem_a = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)smem);
-        const uint32_t sink_a = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)sink);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int t = wu + i * W;
-            const uint32_t live = (uint32_t)__builtin_amdgcn_readfirstlane(t < ntiles ? -1 : 0);   // all ones or 0
-            const uint32_t slot = ((smem_a + (uint32_t)(t * kWideTileBytes)) & live) | (sink_a & ~live);
-            const uint32_t qstep = 1024u & live;
+            if (i == 1 && t >= ntiles) break;
+            const uint32_t slot = smem_a + (uint32_t)(t * kWideTileBytes);
             const int k0 = start + t * kTileKeys;
 #pragma unroll
             for (int q = 0; q < LPT; ++q) {
@@ -563,10 +590,10 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
                 const int row = (q % (KB / 1024)) * 4 + pr;       // row of the tile
                 const int c = isv ? (pc ^ ((row & 3) << 2)) : (pc ^ (row & 15));
                 // rows past the split's last readable row read nothing (zeros)
-                const uint32_t rowm = live & (k0 + row <= lim ? ~0u : 0u);
+                const uint32_t rowm = k0 + row <= lim ? ~0u : 0u;
                 const uint32_t off = ((uint32_t)((k0 + row) * (isv ? a.v_sn : a.k_sn) + c * 8) * 2u & rowm) |
                                      (kWloadSkipAttn & ~rowm);
-                wide_lds_load(isv ? rv : rk, slot + (uint32_t)q * qstep, off);
+                wide_lds_load(isv ? rv : rk, slot + (uint32_t)q * 1024u, off);
             }
         }
     }
@@ -587,6 +614,7 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
         float sn, cs;
         sincos_reduced((float)pos * freq, &sn, &cs);
         cs_qk[tid / HALF][tid % HALF] = make_float2(cs, sn);
+        if (ROTK && tid < HALF) sfreq[tid] = freq;
     }
     if (tid < G * (HD / 8)) *reinterpret_cast<uint4*>(&qs[tid * 8]) = qld;
     lds_barrier();
@@ -608,6 +636,18 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
             }
         }
     }
+    if (ROTK && ntiles > W && start + W * kTileKeys < end) {
+        // the (cos, sin) table of tile W: 32 keys x 64 frequencies, 4 entries per thread
+#pragma unroll
+        for (int k = 0; k < kTileKeys * HALF / NT; ++k) {
+            const int e = tid + k * NT, j = e / HALF, d = e % HALF;
+            float sn, cs;
+            sincos_reduced((float)(start + W * kTileKeys + j + k_pos_off) * sfreq[d], &sn, &cs);
+            typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+            const h2_t h = {(_Float16)cs, (_Float16)sn};
+            cs9[j * HALF + (((d >> 2) ^ (j & 15)) << 2) + (d & 3)] = __builtin_bit_cast(uint32_t, h);
+        }
+    }
     lds_barrier();
     bf16x8_t qf[KS];
     {
@@ -619,7 +659,7 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
             qf[ks] = pk.v;
         }
     }
-    const int fix_row = (a.rope_q && a.fix_last && L > 0) ? (int)L - 1 : -1;
+    const int fix_row = (!ROTK && a.rope_q && a.fix_last && L > 0) ? (int)L - 1 : -1;
     const bf16_t* kbase = a.k + (size_t)kvh * a.k_sh;
 
     f32x16_t oacc[DT];
@@ -634,7 +674,36 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
     for (int i = 0; i < 2; ++i) {
         const int t = wave + i * W;
         const int t0 = start + t * kTileKeys;
-        if (i == 0) attn_pipe::vm_wait<LPT>();   // tile i = 0 landed (the second may fly)
+        // ROTK: the first tile's cos / sin (waves below W/2: now, before the wait); the
+        // second tile, wave 0's ninth, reads them from the set-up table
+        if (ROTK && i == 0 && !ck_early && t < ntiles && t0 < end) {
+            const float pos = (float)(t0 + ql + k_pos_off);
+#pragma unroll
+            for (int ks = 0; ks < KS / 2; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float sn, cs;
+                    sincos_reduced(pos * sfreq[ks * 16 + hh * 8 + e], &sn, &cs);
+                    ck[ks][e] = make_float2(cs, sn);
+                }
+        } else if (ROTK && i == 1 && t < ntiles && t0 < end) {
+#pragma unroll
+            for (int ks = 0; ks < KS / 2; ++ks)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const int d0 = ks * 16 + hh * 8 + c * 4;   // 4 entries = one 16-byte chunk
+                    const uint4 w = *reinterpret_cast<const uint4*>(
+                        &cs9[ql * HALF + (((d0 >> 2) ^ (ql & 15)) << 2)]);
+                    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+                        const h2_t h = __builtin_bit_cast(h2_t, wv[e]);
+                        ck[ks][c * 4 + e] = make_float2((float)h.x, (float)h.y);
+                    }
+                }
+        }
+        if (i == 0 && wave + W < ntiles) attn_pipe::vm_wait<LPT>();   // tile 0 landed (the second may fly)
         else attn_pipe::vm_wait<0>();
         asm volatile("" ::: "memory");
         if (t >= ntiles || t0 >= end) continue;
@@ -664,9 +733,10 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
         asm volatile("s_waitcnt lgkmcnt(8)" ::: "memory");   // the K reads (issued first) are done
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kf[ks]));
-        if (t0 + ql == fix_row && fix_row < end) {
-            // the newest key: rotate at its position, use it and store it back rotated
-            bf16_t* kw = const_cast<bf16_t*>(kbase) + (size_t)fix_row * a.k_sn + hh * 8;
+        if (ROTK || (t0 + ql == fix_row && fix_row < end)) {
+            // rotate this lane's key: every key (ROTK) or the newest one, which is then
+            // stored back rotated
+            bf16_t* kw = const_cast<bf16_t*>(kbase) + (size_t)max(fix_row, 0) * a.k_sn + hh * 8;
 #pragma unroll
             for (int ks = 0; ks < KS / 2; ++ks) {
                 BfPack u0, u1;
@@ -677,7 +747,7 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
                 unpack8(u1.u, x1);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float2 c2 = cs_qk[1][ks * 16 + hh * 8 + e];
+                    const float2 c2 = ROTK ? ck[ks][e] : cs_qk[1][ks * 16 + hh * 8 + e];
                     const float y0 = x0[e] * c2.x - x1[e] * c2.y;
                     const float y1 = x1[e] * c2.x + x0[e] * c2.y;
                     x0[e] = y0;
@@ -687,8 +757,10 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
                 u1.u = pack8(x1);
                 kf[ks] = u0.v;
                 kf[ks + KS / 2] = u1.v;
-                *reinterpret_cast<uint4*>(kw + ks * 16) = u0.u;
-                *reinterpret_cast<uint4*>(kw + (ks + KS / 2) * 16) = u1.u;
+                if (!ROTK) {
+                    *reinterpret_cast<uint4*>(kw + ks * 16) = u0.u;
+                    *reinterpret_cast<uint4*>(kw + (ks + KS / 2) * 16) = u1.u;
+                }
             }
         }
         f32x16_t s = {};

@@ -1344,12 +1344,57 @@ def test_decode_attention_lds_kernel_matches_register_kernel(gpu, knob, hq, hkv,
     pytest.param(128, 64, 900, 1100, id="288keys-g2"),
     pytest.param(448, 64, 1100, 1100, id="288keys-g7-full"),
     pytest.param(256, 256, 257, 300, id="256keys-8-tiles"),
+    pytest.param(28, 4, 16448, 16512, id="c5-58-splits"),
+    pytest.param(28, 4, 16390, 16512, id="c5-short-last-split"),
+    pytest.param(28, 4, 18432, 18432, id="c5-64-splits-9-tiles"),
 ])
 def test_decode_attention_wide_kernel_matches_register_kernel(gpu, knob, hq, hkv, kv_len, max_kv):
-    """Plans past 512 splits of 128 keys run the 8-wave kernel (splits of 256-288 keys, every
-    tile in LDS; wave 0 takes a ninth tile): same checks as the 4-wave kernel, including a
-    split whose last tiles lie past the length and waves without a tile."""
+    """Plans past 512 splits of 128 keys run the 8-wave kernel (one workgroup per CU, splits
+    of 256-288 keys, every tile in LDS; wave 0 takes a ninth tile): same checks as the 4-wave kernel, including a split whose last tiles lie past the
+    length and waves without a tile."""
     _lds_vs_register(gpu, knob, hq, hkv, kv_len, max_kv)
+
+
+@pytest.mark.parametrize("hq,hkv,kv_len,max_kv,k_off", [
+    pytest.param(64, 64, 1057, 1100, 0, id="288keys-partial-last-split"),
+    pytest.param(64, 64, 1, 1100, 0, id="288keys-one-row"),
+    pytest.param(128, 64, 900, 1100, 3, id="288keys-g2-koff"),
+    pytest.param(448, 64, 1100, 1100, 0, id="288keys-g7-full"),
+    pytest.param(256, 256, 257, 300, 0, id="256keys-8-tiles"),
+    pytest.param(28, 4, 16448, 16512, 0, id="c5-7b-16k"),
+    pytest.param(28, 4, 18400, 18432, 5, id="288keys-9-tiles-koff"),
+])
+def test_decode_attention_wide_kernel_rotate_on_read(gpu, knob, hq, hkv, kv_len, max_kv, k_off):
+    """The reference's un-rotated cache (k_already_prerotated 0: every key rotated on read
+    at j + k_rope_pos_offset, qwen2_5.cpp:602,624-638 and attention.cu:135-139) on plans
+    that take the 8-wave kernel: against the oracle and the register-staged kernel, rows
+    past the length NaN, and the cache left as it was (nothing is stored back)."""
+    torch.manual_seed(kv_len + hq + 7)
+    hd = 128
+    q = torch.randn(1, hq, hd, dtype=torch.bfloat16)
+    k0 = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16)
+    v0 = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16)
+    ref = O.attention_decode(q, k0, v0, kv_len, O.AttnCtx(hq, hkv, hd, k_rope_pos_offset=k_off))
+    k0[kv_len:] = float("nan")
+    v0[kv_len:] = float("nan")
+    ctx = C.make_attention_ctx(hq, hkv, hd, k_rope_pos_offset=k_off)
+    assert ctx.k_already_prerotated == 0
+    qg, vg = q.reshape(1, hq * hd).to(gpu), v0.to(gpu)
+    d_len = torch.tensor([kv_len], dtype=torch.int32, device=gpu)
+    ws = torch.zeros(C.load().efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=gpu)
+    outs = []
+    for reg in (0, 1):
+        knob(C.EFM_KNOB_DECODE_REGISTER, reg)
+        k = k0.to(gpu)
+        o = torch.empty_like(qg)
+        C.call("efm_attention_decode", ctx, ptr(qg), ptr(k), ptr(vg), ptr(o), 0, ptr(d_len), max_kv, ptr(ws),
+               ws.numel(), stream())
+        torch.cuda.synchronize()
+        outs.append(o)
+        assert torch.equal(k[:kv_len].cpu(), k0[:kv_len]), "rotate-on-read must not store keys"
+    assert torch.isfinite(outs[0].float()).all()
+    assert_close_bf16(outs[0].reshape(1, hq, hd), ref, what=f"wide rotate-on-read L={kv_len}")
+    assert_close_bf16(outs[0], outs[1], what="wide rotate-on-read vs register kernel")
 
 
 def _lds_vs_register(gpu, knob, hq, hkv, kv_len, max_kv):
