@@ -11,7 +11,8 @@
 //   score_log2(i, j) = float(int32(Q8_i . K8_j)) * ((sq * sk) * (log2(e) / sqrt(hd)))
 //   causal: query i sees keys j <= i + (L - S); P rounded to bf16 for the PV product.
 //
-// Three launches: K mean (one workgroup per KV head and 8 channels, float64), block
+// Three launches: K column sums (float64; the attention entry point: per KV head and row
+// slice, coalesced rows; efm_sage_quantize: per KV head and 8 channels), block
 // quantisation of Q and K (one workgroup per block x head), attention (one workgroup =
 // 128 query rows of one head, 64-key tiles staged in LDS as int8 K and transposed V).
 #include "attn_pipe.hpp"
@@ -33,25 +34,26 @@ constexpr int kSageThreads = 256;
 constexpr int kSageQ = 128;   // query rows per attention workgroup
 constexpr int kSageKV = 64;   // keys per LDS tile
 
-// ---- K mean over tokens: grid (Hkv, hd / 8), 256 threads ------------------------
+// ---- K mean over tokens: grid (Hkv, hd / 8), 1024 threads --------------------------
 // Workgroup (h, c) owns channels [8c, 8c + 8) of KV head h; thread t adds rows
-// j = t (mod 256) with 16-byte loads (four rows in flight per step), then a fixed
-// LDS tree sums the 256 per-thread float64 partials. Sums of bf16 values in float64
-// are exact while their binary range fits the 53-bit significand, as it does for
-// cache contents, so the result matches any summation order.
-__global__ __launch_bounds__(kSageThreads) void sage_kmean_kernel(const bf16_t* k, int L, int k_sn, int k_sh, int hd,
-                                                                  float* kmean) {
-    __shared__ double part[8][kSageThreads];
+// j = t (mod 1024) with 16-byte loads (four rows in flight per step: one round trip up to
+// 4096 rows), then butterfly sums over each wave and a sum over the 16 waves. Sums of bf16
+// values in float64 are exact while their binary range fits the 53-bit significand, as
+// it does for cache contents, so the result matches any summation order.
+constexpr int kKmeanThreads = 1024;
+__global__ __launch_bounds__(kKmeanThreads) void sage_kmean_kernel(const bf16_t* k, int L, int k_sn, int k_sh, int hd,
+                                                                   float* kmean) {
+    __shared__ double part[kKmeanThreads / kWave][8];
     const int h = blockIdx.x, d0 = blockIdx.y * 8, t = threadIdx.x;
     const bf16_t* base = k + (size_t)h * k_sh + d0;
     double s[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) s[e] = 0.0;
     int j = t;
-    for (; j + 3 * kSageThreads < L; j += 4 * kSageThreads) {
+    for (; j + 3 * kKmeanThreads < L; j += 4 * kKmeanThreads) {
         uint4 u[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) u[r] = *reinterpret_cast<const uint4*>(base + (size_t)(j + r * kSageThreads) * k_sn);
+        for (int r = 0; r < 4; ++r) u[r] = *reinterpret_cast<const uint4*>(base + (size_t)(j + r * kKmeanThreads) * k_sn);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             float x[8];
@@ -60,32 +62,89 @@ __global__ __launch_bounds__(kSageThreads) void sage_kmean_kernel(const bf16_t* 
             for (int e = 0; e < 8; ++e) s[e] += (double)x[e];
         }
     }
-    for (; j < L; j += kSageThreads) {
+    for (; j < L; j += kKmeanThreads) {
         float x[8];
         unpack8(*reinterpret_cast<const uint4*>(base + (size_t)j * k_sn), x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) s[e] += (double)x[e];
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) part[e][t] = s[e];
-    __syncthreads();
-    for (int stride = kSageThreads / 2; stride > 0; stride >>= 1) {
-        if (t < stride) {
+    for (int e = 0; e < 8; ++e)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) part[e][t] += part[e][t + stride];
-        }
-        __syncthreads();
+        for (int off = kWave / 2; off >= 1; off >>= 1) s[e] += __shfl_xor(s[e], off, kWave);
+    if (t % kWave == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part[t / kWave][e] = s[e];
     }
-    if (t < 8) kmean[h * hd + d0 + t] = (float)(part[t][0] / (double)L);
+    __syncthreads();
+    if (t < 8) {
+        double sum = 0.0;
+#pragma unroll
+        for (int w = 0; w < kKmeanThreads / kWave; ++w) sum += part[w][t];
+        kmean[h * hd + d0 + t] = (float)(sum / (double)L);
+    }
+}
+
+// ---- K column sums in row slices: grid (Hkv, kKSlices), 256 threads -------------
+// The attention entry point's K mean: workgroup (h, sl) sums rows [sl * per, (sl + 1) *
+// per) of KV head h over every channel, 16 lanes (hd 128) per row, so a wave's 16-byte
+// loads cover four whole 256-byte rows; the quantisation kernel adds the slices (float64:
+// exact, so the mean equals sage_kmean_kernel's bit for bit).
+constexpr int kKSlices = 16;
+__global__ __launch_bounds__(kSageThreads) void sage_kpart_kernel(const bf16_t* k, int L, int k_sn, int k_sh, int hd,
+                                                                  double* part) {
+    __shared__ double red[kSageThreads][8];
+    const int h = blockIdx.x, sl = blockIdx.y, t = threadIdx.x;
+    const int cpr = hd / 8, c = t % cpr, r0 = t / cpr, rstep = kSageThreads / cpr;
+    const int per = (L + kKSlices - 1) / kKSlices;
+    const int j0 = sl * per, j1 = min(L, j0 + per);
+    const bf16_t* base = k + (size_t)h * k_sh + c * 8;
+    double s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = 0.0;
+    int j = j0 + r0;
+    for (; j + 3 * rstep < j1; j += 4 * rstep) {
+        uint4 u[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) u[r] = *reinterpret_cast<const uint4*>(base + (size_t)(j + r * rstep) * k_sn);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float x[8];
+            unpack8(u[r], x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[e] += (double)x[e];
+        }
+    }
+    for (; j < j1; j += rstep) {
+        float x[8];
+        unpack8(*reinterpret_cast<const uint4*>(base + (size_t)j * k_sn), x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] += (double)x[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[t][e] = s[e];
+    __syncthreads();
+    if (t < hd) {
+        const int cc = t / 8, e = t % 8;
+        double sum = 0.0;
+        for (int r = 0; r < rstep; ++r) sum += red[r * cpr + cc][e];
+        part[((size_t)sl * gridDim.x + h) * hd + t] = sum;
+    }
 }
 
 // ---- block quantisation: grid (blocks, H), 256 threads --------------------------
-// dst [T][H][hd] int8 (contiguous), scales [blocks][H].
+// dst [T][H][hd] int8 (contiguous), scales [blocks][H]. KM = 0: Q (no shift); 1: K with
+// its mean from kmean (sage_kmean_kernel); 2: K with its mean added up here from the
+// kKSlices row-slice sums in kpart (sage_kpart_kernel; block 0 stores it in kmean_out).
+// Every load is issued up front and branch-free (rows past the block's end are buffer
+// loads past the resource: zeros, no memory access), so one round trip covers them all.
+template <int KM>
 __global__ __launch_bounds__(kSageThreads) void sage_quant_kernel(const bf16_t* src, int T, int H, int sn, int sh,
-                                                                  int hd, const float* kmean, int8_t* dst,
-                                                                  float* scales) {
+                                                                  int hd, const float* kmean, const double* kpart,
+                                                                  float* kmean_out, int8_t* dst, float* scales) {
     __shared__ float red[kSageThreads / kWave];
-    const int b = blockIdx.x, h = blockIdx.y;
+    __shared__ float kms[KM == 2 ? 128 : 1];
+    const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const int t0 = b * kSageBlock;
     const int rows = min(kSageBlock, T - t0);
     const int cpr = hd / 8;  // 16-byte chunks per row
@@ -93,29 +152,49 @@ __global__ __launch_bounds__(kSageThreads) void sage_quant_kernel(const bf16_t* 
     constexpr int kMaxPer = kSageBlock * 128 / 8 / kSageThreads;  // 8
     // every chunk of a thread covers the same 8 channels (the thread count is a multiple
     // of the chunks per row), so their K means are loaded once, beside the data
-    const int d0 = (threadIdx.x % cpr) * 8;
-    float km[8];
-    if (kmean != nullptr) {
-        const float4 k0 = *reinterpret_cast<const float4*>(kmean + h * hd + d0);
-        const float4 k1 = *reinterpret_cast<const float4*>(kmean + h * hd + d0 + 4);
-        km[0] = k0.x; km[1] = k0.y; km[2] = k0.z; km[3] = k0.w;
-        km[4] = k1.x; km[5] = k1.y; km[6] = k1.z; km[7] = k1.w;
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) km[e] = 0.f;
+    const int d0 = (tid % cpr) * 8;
+    float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0;
+    if constexpr (KM == 1) {
+        k0 = *reinterpret_cast<const float4*>(kmean + h * hd + d0);
+        k1 = *reinterpret_cast<const float4*>(kmean + h * hd + d0 + 4);
     }
     uint4 raw[kMaxPer];
+    {
+        typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<bf16_t*>(src + (size_t)t0 * sn + (size_t)h * sh), (short)0, rows * sn * 2, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < kMaxPer; ++i) {
-        const int c = threadIdx.x + i * kSageThreads;
-        raw[i] = (c < nch) ? *reinterpret_cast<const uint4*>(src + (size_t)(t0 + c / cpr) * sn + (size_t)h * sh + d0)
-                           : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < kMaxPer; ++i) {
+            const int c = tid + i * kSageThreads;
+            const uint32_t off = (c < nch) ? (uint32_t)(((c / cpr) * sn + d0) * 2) : 0x80000000u;
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+            raw[i] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    double kv[KM == 2 ? kKSlices : 1];
+    if constexpr (KM == 2) {
+#pragma unroll
+        for (int sl = 0; sl < kKSlices; ++sl) kv[sl] = kpart[((size_t)sl * H + h) * hd + tid % hd];
+    }
+    float km[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    if constexpr (KM == 2) {
+        double sum = 0.0;
+#pragma unroll
+        for (int sl = 0; sl < kKSlices; ++sl) sum += kv[sl];
+        const float mean = (float)(sum / (double)T);
+        if (tid < hd) {
+            kms[tid] = mean;
+            if (b == 0) kmean_out[h * hd + tid] = mean;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) km[e] = kms[d0 + e];
     }
     float x[kMaxPer][8];
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < kMaxPer; ++i) {
-        const int c = threadIdx.x + i * kSageThreads;
+        const int c = tid + i * kSageThreads;
         unpack8(raw[i], x[i]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -125,16 +204,16 @@ __global__ __launch_bounds__(kSageThreads) void sage_quant_kernel(const bf16_t* 
         }
     }
     amax = wave_max(amax);
-    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = amax;
+    if (tid % kWave == 0) red[tid / kWave] = amax;
     __syncthreads();
     float m = 0.f;
 #pragma unroll
     for (int w = 0; w < kSageThreads / kWave; ++w) m = fmaxf(m, red[w]);
     const float scale = (m > 0.f) ? m / 127.0f : 1.0f;
-    if (threadIdx.x == 0) scales[b * H + h] = scale;
+    if (tid == 0) scales[b * H + h] = scale;
 #pragma unroll
     for (int i = 0; i < kMaxPer; ++i) {
-        const int c = threadIdx.x + i * kSageThreads;
+        const int c = tid + i * kSageThreads;
         if (c < nch) {
             const int r = c / cpr;
             uint32_t w[2] = {0u, 0u};
@@ -686,8 +765,8 @@ int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
 static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct SageWs {
-    size_t q8, k8, sq, sk, km;
-    size_t total() const { return q8 + k8 + sq + sk + km; }
+    size_t q8, k8, sq, sk, km, kp;
+    size_t total() const { return q8 + k8 + sq + sk + km + kp; }
 };
 
 static SageWs sage_ws(const efm_attention_ctx* c, uint32_t S, uint32_t L) {
@@ -698,31 +777,47 @@ static SageWs sage_ws(const efm_attention_ctx* c, uint32_t S, uint32_t L) {
     w.sq = al256((size_t)((S + kSageBlock - 1) / kSageBlock) * c->num_qo_heads * 4);
     w.sk = al256((size_t)((L + kSageBlock - 1) / kSageBlock) * c->num_kv_heads * 4);
     w.km = al256((size_t)c->num_kv_heads * hd * 4);
+    w.kp = al256((size_t)kKSlices * c->num_kv_heads * hd * 8);
     return w;
 }
 
+// kpart == nullptr (efm_sage_quantize): the K mean from one workgroup per (KV head, 8
+// channels); else (the attention entry point, whose workspace holds kpart) from row-slice
+// sums added up by the quantisation kernel, which also stores the mean in kmean.
 static int sage_quantize_impl(const efm_attention_ctx* c, const void* q, const void* k, uint32_t S, uint32_t L,
                               int8_t* q8, float* sq, int8_t* k8, float* sk, float* kmean, hipStream_t stream,
-                              bool quant_q = true) {
+                              bool quant_q = true, double* kpart = nullptr) {
     const int hd = (int)c->head_dim;
     const int q_sn = c->q_stride_n ? (int)c->q_stride_n : (int)(c->num_qo_heads * hd);
     const int q_sh = c->q_stride_h ? (int)c->q_stride_h : hd;
     const int k_sn = c->k_stride_n ? (int)c->k_stride_n : (int)(c->num_kv_heads * hd);
     const int k_sh = c->k_stride_h ? (int)c->k_stride_h : hd;
-    hipLaunchKernelGGL(sage_kmean_kernel, dim3(c->num_kv_heads, hd / 8), dim3(kSageThreads), 0, stream,
-                       static_cast<const bf16_t*>(k), (int)L, k_sn, k_sh, hd, kmean);
+    if (kpart != nullptr) {
+        hipLaunchKernelGGL(sage_kpart_kernel, dim3(c->num_kv_heads, kKSlices), dim3(kSageThreads), 0, stream,
+                           static_cast<const bf16_t*>(k), (int)L, k_sn, k_sh, hd, kpart);
+    } else {
+        hipLaunchKernelGGL(sage_kmean_kernel, dim3(c->num_kv_heads, hd / 8), dim3(kKmeanThreads), 0, stream,
+                           static_cast<const bf16_t*>(k), (int)L, k_sn, k_sh, hd, kmean);
+    }
     int rc = check_launch("sage kmean");
     if (rc) return rc;
     if (quant_q) {
-        hipLaunchKernelGGL(sage_quant_kernel, dim3((S + kSageBlock - 1) / kSageBlock, c->num_qo_heads),
+        hipLaunchKernelGGL(sage_quant_kernel<0>, dim3((S + kSageBlock - 1) / kSageBlock, c->num_qo_heads),
                            dim3(kSageThreads), 0, stream, static_cast<const bf16_t*>(q), (int)S,
-                           (int)c->num_qo_heads, q_sn, q_sh, hd, (const float*)nullptr, q8, sq);
+                           (int)c->num_qo_heads, q_sn, q_sh, hd, (const float*)nullptr, (const double*)nullptr,
+                           (float*)nullptr, q8, sq);
         rc = check_launch("sage quant q");
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(sage_quant_kernel, dim3((L + kSageBlock - 1) / kSageBlock, c->num_kv_heads),
-                       dim3(kSageThreads), 0, stream, static_cast<const bf16_t*>(k), (int)L, (int)c->num_kv_heads,
-                       k_sn, k_sh, hd, (const float*)kmean, k8, sk);
+    const dim3 kgrid((L + kSageBlock - 1) / kSageBlock, c->num_kv_heads);
+    if (kpart != nullptr)
+        hipLaunchKernelGGL(sage_quant_kernel<2>, kgrid, dim3(kSageThreads), 0, stream, static_cast<const bf16_t*>(k),
+                           (int)L, (int)c->num_kv_heads, k_sn, k_sh, hd, (const float*)nullptr, (const double*)kpart,
+                           kmean, k8, sk);
+    else
+        hipLaunchKernelGGL(sage_quant_kernel<1>, kgrid, dim3(kSageThreads), 0, stream, static_cast<const bf16_t*>(k),
+                           (int)L, (int)c->num_kv_heads, k_sn, k_sh, hd, (const float*)kmean, (const double*)nullptr,
+                           (float*)nullptr, k8, sk);
     return check_launch("sage quant k");
 }
 
@@ -776,10 +871,11 @@ extern "C" int efm_attention_prefill_sage_int8(const efm_attention_ctx* ctx, con
     float* sq = reinterpret_cast<float*>(p + w.q8 + w.k8);
     float* sk = reinterpret_cast<float*>(p + w.q8 + w.k8 + w.sq);
     float* km = reinterpret_cast<float*>(p + w.q8 + w.k8 + w.sq + w.sk);
+    double* kp = reinterpret_cast<double*>(p + w.q8 + w.k8 + w.sq + w.sk + w.km);
     const int hd = (int)ctx->head_dim;
     const bool pipe = hd == kSPHD && kernel_knob(EFM_KNOB_PREFILL_REGISTER) == 0;
     // the pipelined kernel quantises Q itself (one 128-row block per 4 waves)
-    rc = sage_quantize_impl(ctx, q, k, qo_len, kv_len, q8, sq, k8, sk, km, stream, !pipe);
+    rc = sage_quantize_impl(ctx, q, k, qo_len, kv_len, q8, sq, k8, sk, km, stream, !pipe, kp);
     if (rc) return rc;
     SageArgs a;
     a.q = static_cast<const bf16_t*>(q);

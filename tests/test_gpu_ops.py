@@ -1262,6 +1262,39 @@ def test_sage_quantize_bit_exact(gpu, S, L, hq, hkv, hd):
     assert torch.equal(k8.cpu(), rk8) and torch.equal(sk.cpu(), rsk)
 
 
+@pytest.mark.parametrize("S,L,hq,hkv,hd", [(300, 300, 28, 4, 128), (129, 257, 4, 2, 64), (1, 40, 8, 1, 128),
+                                           (4096, 4096, 28, 4, 128), (700, 1003, 8, 2, 128)])
+def test_sage_attention_quantisation_equals_quantize_entry(gpu, S, L, hq, hkv, hd):
+    """The attention entry point takes its K mean from float64 row-slice sums added up by
+    the quantisation kernel; its K8 / K scales / K mean (left in the workspace) must equal
+    efm_sage_quantize's (one workgroup per channel group) bit for bit."""
+    q, k, v = _sage_inputs(S, L, hq, hkv, hd, seed=3)
+    ctx = C.make_attention_ctx(hq, hkv, hd, rope=False)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    nbq, nbk = (S + 127) // 128, (L + 127) // 128
+    q8 = torch.empty(S, hq, hd, dtype=torch.int8, device=gpu)
+    k8 = torch.empty(L, hkv, hd, dtype=torch.int8, device=gpu)
+    sq = torch.empty(nbq, hq, dtype=torch.float32, device=gpu)
+    sk = torch.empty(nbk, hkv, dtype=torch.float32, device=gpu)
+    km = torch.empty(hkv, hd, dtype=torch.float32, device=gpu)
+    C.call("efm_sage_quantize", ctx, ptr(qg), ptr(kg), S, L, ptr(q8), ptr(sq), ptr(k8), ptr(sk), ptr(km), stream())
+    ws = torch.zeros(C.load().efm_attention_prefill_sage_int8_workspace_bytes(ctx, S, L), dtype=torch.uint8,
+                     device=gpu)
+    o = torch.empty(S, hq * hd, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_attention_prefill_sage_int8", ctx, ptr(qg), ptr(kg), ptr(vg), ptr(o), S, L, 1, ptr(ws), ws.numel(),
+           stream())
+    torch.cuda.synchronize()
+    al = lambda x: (x + 255) // 256 * 256
+    off_k8 = al(S * hq * hd)
+    off_sk = off_k8 + al(L * hkv * hd) + al(nbq * hq * 4)
+    off_km = off_sk + al(nbk * hkv * 4)
+    w = ws.cpu()
+    assert torch.equal(w[off_k8:off_k8 + L * hkv * hd].view(torch.int8).reshape(L, hkv, hd), k8.cpu())
+    assert torch.equal(w[off_sk:off_sk + nbk * hkv * 4].view(torch.float32).reshape(nbk, hkv), sk.cpu())
+    assert torch.equal(w[off_km:off_km + hkv * hd * 4].view(torch.float32).reshape(hkv, hd), km.cpu())
+    torch.testing.assert_close(km.cpu(), O.sage_kmean(k), rtol=2e-7, atol=1e-7)
+
+
 @pytest.mark.parametrize("S,L,hq,hkv,hd", [(512, 512, 28, 4, 128), (300, 700, 8, 2, 128), (200, 200, 14, 2, 64)])
 def test_sage_attention_matches_oracle(gpu, S, L, hq, hkv, hd):
     q, k, v = _sage_inputs(S, L, hq, hkv, hd, seed=1)
