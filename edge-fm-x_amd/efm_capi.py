@@ -118,12 +118,6 @@ SIGNATURES = {
     "efm_fused_gate_up_swiglu_ws": (c_int32, [c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
                                               c_size_t, c_void_p]),
     "efm_testing_set_kernel_path": (c_int32, [c_int32, c_int32]),
-    "efm_decode_stack_workspace_bytes": (c_size_t, [POINTER(AttentionCtx), c_int32, c_int32, c_int32, c_uint32]),
-    "efm_decode_stack_supported": (c_int32, [POINTER(AttentionCtx), c_int32, c_int32, c_int32, c_uint32]),
-    "efm_decode_stack": (c_int32, [POINTER(AttentionCtx), c_int32, c_int32, c_int32, c_float, c_void_p, c_void_p,
-                                   c_int64, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_size_t,
-                                   c_void_p]),
-    "efm_decode_stack_status": (c_int32, [c_void_p, c_void_p]),
     "efm_lm_head_top1_workspace_bytes": (c_size_t, [c_int64]),
     "efm_lm_head_top1": (c_int32, [c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "efm_sampler_greedy_workspace_bytes": (c_size_t, [c_int64, c_int64]),

@@ -116,7 +116,7 @@ def write_compact_vocab_mapping(path: str, original_vocab_size: int, new_to_old,
 def write_engine_config(path: str, model_dir: str, *, max_tokens: int = 4096, max_new_tokens: int = 256,
                         prefix_token_ids=None, use_graph: bool = True, temperature: float = 0.0,
                         top_p: float = 1.0, seed: int = 0, lm_head_top1: bool = True, model_name: str = "",
-                        operator_impl_table_path: str = "", extra_slots=None, decode_stack=None,
+                        operator_impl_table_path: str = "", extra_slots=None,
                         stop_token_ids=None, compact_vocab=None, decode_fused_qkv_attention=None,
                         debug_logits: bool = False) -> str:
     slots = [{"request_id": 0, "prefix_token_ids": list(prefix_token_ids or []), "max_tokens": max_tokens}]
@@ -131,8 +131,6 @@ def write_engine_config(path: str, model_dir: str, *, max_tokens: int = 4096, ma
         "sampling": {"max_new_tokens": max_new_tokens, "temperature": temperature, "top_p": top_p, "seed": seed,
                      "stop_token_ids": list(stop_token_ids or [])},
     }
-    if decode_stack is not None:
-        cfg["runtime"]["decode_stack"] = bool(decode_stack)
     if decode_fused_qkv_attention is not None:
         cfg["runtime"]["decode_fused_qkv_attention"] = bool(decode_fused_qkv_attention)
     if compact_vocab is not None:

@@ -221,11 +221,6 @@ bool EngineConfig::decode_fused_qkv_attention() const {
     if (env != nullptr && env[0] != '\0') return std::string(env) != "0";
     return json_.contains("runtime") ? json_.at("runtime").get_bool("decode_fused_qkv_attention", true) : true;
 }
-bool EngineConfig::decode_stack() const {
-    const char* env = std::getenv("EDGE_FM_DECODE_STACK");
-    if (env != nullptr && env[0] != '\0') return std::string(env) != "0";
-    return json_.contains("runtime") ? json_.at("runtime").get_bool("decode_stack", false) : false;
-}
 std::string EngineConfig::operator_table_path() const {
     std::string p = json_.get_string("operator_impl_table_path");
     if (!p.empty() && fs::path(p).is_relative() && !base_dir_.empty()) p = (fs::path(base_dir_) / p).string();
@@ -468,7 +463,6 @@ Qwen2_5::Qwen2_5(const EngineConfig& cfg, const ModelConfig& m, const std::unord
     : cfg_(cfg), m_(m), device_id_(device_id) {
     model_name_ = cfg.model_name();
     hw_profile_ = cfg.hw_profile();
-    stack_enabled_ = cfg.decode_stack() && !m.mrope;
     fused_front_enabled_ = cfg.decode_fused_qkv_attention() && !m.mrope;
     table_path_ = cfg.operator_table_path();
     hip_check(hipSetDevice(device_id), "hipSetDevice");
@@ -565,11 +559,6 @@ void Qwen2_5::reserve_decode(uint32_t max_kv_len) {
     const size_t bytes = efm_attention_decode_workspace_bytes(&c, max_kv_len);
     if (attn_ws_.empty() || attn_ws_.nbytes() < bytes)
         attn_ws_ = Tensor::zeros({(int64_t)bytes}, DType::UInt8, Device::GPU, device_id_);
-    if (uses_decode_stack(max_kv_len)) {
-        const size_t sb = efm_decode_stack_workspace_bytes(&c, m_.hidden, m_.inter, m_.layers, max_kv_len);
-        if (stack_ws_.empty() || stack_ws_.nbytes() < sb)
-            stack_ws_ = Tensor::zeros({(int64_t)sb}, DType::UInt8, Device::GPU, device_id_);
-    }
     // the decode plan for this cache length (impls resolved, their scratch prepared):
     // nothing is resolved or allocated while a decode step is captured
     if (!plans_.count(max_kv_len)) {
@@ -607,34 +596,9 @@ bool Qwen2_5::uses_fused_front(uint32_t max_kv_len) const {
     return false;
 }
 
-bool Qwen2_5::uses_decode_stack(uint32_t max_kv_len) const {
-    if (!stack_enabled_) return false;
-    const efm_attention_ctx c = decode_ctx();
-    return efm_decode_stack_supported(&c, m_.hidden, m_.inter, m_.layers, max_kv_len) == EFM_OK;
-}
-
-void Qwen2_5::prepare_decode_stack(uint32_t max_kv_len, void** k_caches, void** v_caches, hipStream_t stream) {
-    if (!uses_decode_stack(max_kv_len) || stack_tables_.count(k_caches[0])) return;
-    std::vector<efm_decode_stack_layer> tab((size_t)m_.layers);
-    for (int l = 0; l < m_.layers; ++l) {
-        const Layer& Ly = layers_[l];
-        tab[l] = efm_decode_stack_layer{Ly.in_norm.data_ptr(), Ly.qkv_w.data_ptr(), Ly.qkv_b.data_ptr(),
-                                        Ly.o_w.data_ptr(),     Ly.post_norm.data_ptr(), Ly.gu_w.data_ptr(),
-                                        Ly.down_w.data_ptr(),  k_caches[l],          v_caches[l]};
-    }
-    Tensor t = Tensor::empty({(int64_t)(tab.size() * sizeof(efm_decode_stack_layer))}, DType::UInt8, Device::GPU,
-                             device_id_);
-    hip_check(hipMemcpyAsync(t.data_ptr(), tab.data(), tab.size() * sizeof(efm_decode_stack_layer),
-                             hipMemcpyHostToDevice, stream),
-              "decode stack layer table");
-    hip_check(hipStreamSynchronize(stream), "decode stack layer table");
-    stack_tables_.emplace(k_caches[0], std::move(t));
-}
-
 void Qwen2_5::check_decode_status(hipStream_t stream) {
     if (!front_sync_ws_.empty())
         efm_check(efm_decode_qkv_attention_status(front_sync_ws_.data_ptr(), stream), "decode qkv + attention");
-    if (!stack_ws_.empty()) efm_check(efm_decode_stack_status(stack_ws_.data_ptr(), stream), "decode stack");
 }
 
 AttentionOpContext Qwen2_5::attn_ctx() const {
@@ -656,7 +620,7 @@ efm_attention_ctx Qwen2_5::decode_ctx() const {
     efm_attention_ctx c = to_c_ctx(attn_ctx());
     // text models: the cache holds keys rotated at their positions (prefill rotates
     // them before the cache write); this step's key, written un-rotated by the QKV
-    // projection of the fused front half / the decode stack, is rotated by the attention
+    // projection of the fused front half, is rotated by the attention
     // call that first reads it
     if (!m_.mrope) c.k_already_prerotated = EFM_K_PREROTATED_EXCEPT_NEWEST;
     return c;
@@ -802,30 +766,6 @@ void Qwen2_5::decode_step(int32_t* token_buf, const uint32_t* d_kv_len, uint32_t
     const efm_attention_ctx c = decode_ctx();
     check<InternalError>(!attn_ws_.empty() && attn_ws_.nbytes() >= efm_attention_decode_workspace_bytes(&c, max_kv_len),
                          "decode workspace not reserved for this cache length");
-    auto tab = stack_tables_.find(k_caches[0]);
-    if (!stack_ws_.empty() && tab != stack_tables_.end() && uses_decode_stack(max_kv_len)) {
-        // every layer in one persistent launch (embedding included); then the final norm
-        // and LM head on (h, residual) of the last layer
-        efm_check(efm_decode_stack(&c, H, m_.inter, m_.layers, m_.eps,
-                                   static_cast<const efm_decode_stack_layer*>(tab->second.data_ptr()),
-                                   embed_.data_ptr(), m_.vocab, token_buf, d_kv_len, max_kv_len, dec_h_.data_ptr(),
-                                   dec_res_[0].data_ptr(), stack_ws_.data_ptr(), stack_ws_.nbytes(), stream),
-                  "decode stack");
-        if (logits == nullptr) {
-            efm_check(efm_decode_norm_lm_head_top1(H, m_.vocab, m_.eps, dec_h_.data_ptr(), dec_res_[0].data_ptr(),
-                                                   final_norm_.data_ptr(), lm_head_.data_ptr(), token_buf,
-                                                   top1_ws_.data_ptr(), top1_ws_.nbytes(), stream),
-                      "decode lm head top1");
-        } else {
-            efm_check(efm_fused_add_rms_norm(1, (uint32_t)H, m_.eps, dec_h_.data_ptr(), dec_res_[0].data_ptr(),
-                                             final_norm_.data_ptr(), stream),
-                      "decode final norm");
-            efm_check(efm_linear(1, H, m_.vocab, dec_h_.data_ptr(), lm_head_.data_ptr(), nullptr, logits,
-                                 EFM_DTYPE_F32, stream),
-                      "decode lm head");
-        }
-        return;
-    }
     const std::vector<DecodeLayerPlan>& plan = decode_plan(max_kv_len);
     const efm_attention_ctx cr = decode_attn_ctx_rotated();
     for (int l = 0; l < m_.layers; ++l) {
@@ -1301,7 +1241,6 @@ Response StandardEngine::generate(const Request& request) {
     metrics_.clear();
     EventTimer pf, dc;
     auto kc = caches(req.request_id, true), vc = caches(req.request_id, false);
-    model_->prepare_decode_stack((uint32_t)slot.cfg.max_tokens, kc.data(), vc.data(), stream_);
     int32_t* st = static_cast<int32_t*>(state_.data_ptr());
     // decode state: d_kv_len = rows after prefill, step = 0, positions = last + 1
     int32_t init[6] = {base + S, 0, 0, last_pos[0] + 1, last_pos[1] + 1, last_pos[2] + 1};
@@ -1544,10 +1483,7 @@ Response StandardEngine::generate(const Request& request) {
     metrics_["response_tokens_capacity"] = (double)response_dev_.numel();
     metrics_["prefill_tokens"] = S;
     metrics_["prefill_tokens_per_second"] = prefill_ms > 0 ? S * 1000.0 / prefill_ms : 0.0;
-    const bool stack = model_->uses_decode_stack((uint32_t)slot.cfg.max_tokens);
-    metrics_["decode_stack"] = stack ? 1.0 : 0.0;
-    metrics_["decode_fused_qkv_attention"] =
-        (!stack && model_->uses_fused_front((uint32_t)slot.cfg.max_tokens)) ? 1.0 : 0.0;
+    metrics_["decode_fused_qkv_attention"] = model_->uses_fused_front((uint32_t)slot.cfg.max_tokens) ? 1.0 : 0.0;
     Response r;
     r.token_ids = compact_vocab_.restore_token_ids(host, "response token_ids");
     return r;

@@ -90,11 +90,6 @@ public:
     // (logits path instead of the fused LM-head top-1) and returned by
     // EdgeFM::last_logits() (test and debugging aid; off by default)
     bool debug_logits() const;
-    // Whole decode step of a text model in one persistent launch (efm_decode_stack;
-    // runtime.decode_stack, default off: on MI355X its six cross-workgroup hand-offs per
-    // layer cost more than the four kernel boundaries of the per-operator path;
-    // EDGE_FM_DECODE_STACK=1 / 0 overrides the config, read once when the engine is built).
-    bool decode_stack() const;
     // Whether the one-launch input norm + QKV + attention partials impl
     // (hip_gfx950_decode_fused_qkv_attention) may run when an operator-table record
     // selects it (runtime.decode_fused_qkv_attention, default on;
@@ -250,18 +245,12 @@ public:
     // valid only while this is unchanged.
     uint64_t prefill_buffers_epoch() const;
 
-    // Whether decode steps with caches of max_kv_len rows run every layer in one
-    // persistent launch (efm_decode_stack) instead of the per-operator kernels.
-    bool uses_decode_stack(uint32_t max_kv_len) const;
-    // Builds the decode stack's device layer table for one request slot's caches (outside
-    // graph capture; no-op when the stack is not used or the table exists).
-    void prepare_decode_stack(uint32_t max_kv_len, void** k_caches, void** v_caches, hipStream_t stream);
     // Whether decode steps run efm_decode_norm_qkv_attention (input norm + QKV +
     // attention partials in one launch per layer) in every layer.
     bool uses_fused_front(uint32_t max_kv_len) const;
     // The decode plan for caches of max_kv_len rows (resolved by reserve_decode).
     const std::vector<DecodeLayerPlan>& decode_plan(uint32_t max_kv_len) const;
-    // Throws DeviceError if a decode-stack or fused QKV + attention launch since the last
+    // Throws DeviceError if a fused QKV + attention launch since the last
     // check could not exchange its vectors in time (synchronises the stream).
     void check_decode_status(hipStream_t stream);
 
@@ -290,9 +279,6 @@ private:
     // decode scratch
     Tensor dec_h_, dec_res_[2], dec_q_, dec_attn_, dec_a_, dec_mid_, dec_kvtmp_, dec_one_, top1_ws_;
     Tensor attn_ws_;
-    bool stack_enabled_ = false;   // config switch (text models only)
-    Tensor stack_ws_;
-    std::map<void*, Tensor> stack_tables_;   // per request slot, keyed by its layer-0 K cache
     bool fused_front_enabled_ = false;
     Tensor front_sync_ws_;
     // prefill scratch (grow-only)

@@ -288,58 +288,6 @@ int efm_fused_gate_up_swiglu_ws(int64_t m, int64_t hidden, int64_t inter, const 
                                 const void* w_up_gate, void* out, void* workspace, size_t workspace_bytes,
                                 hipStream_t stream);
 
-
-/* ------------------------------------------------------------------------------------
- * One whole decode step of a Qwen2.5 text decoder in one persistent launch: the embedding
- * of the previous token and every layer's RMSNorm (+ residual) -> fused QKV + bias -> KV
- * write -> GQA attention (RoPE-Llama at L - 1, rotated cache) -> split merge -> o_proj ->
- * add + RMSNorm -> gate/up + SwiGLU -> down_proj. Replaces the per-layer operator
- * sequence of Qwen2_5::forward_impl for one decode token
- * (src/models/qwen2_5/qwen2_5.cpp:534-930, the layers' LinearImpl / NormOp / AttentionOp
- * calls). It leaves the last layer's h and residual in h_out / residual_out for the final
- * norm + LM head (efm_decode_norm_lm_head_top1 or efm_fused_add_rms_norm + efm_linear).
- *
- * layer_table: device array of `layers` entries (weights in the layouts of the other
- * entry points: fused [Q;K;V] + bias, [up; gate], RMSNorm weights; per-layer K / V cache
- * rows of num_kv_heads * 128). token: device int32, the previous token (out of range ->
- * zero embedding). d_kv_len: device, rows after this step (this token's K / V go to row
- * d_kv_len - 1); max_kv_len bounds it. ctx: head_dim 128, RoPE-Llama,
- * k_already_prerotated = EFM_K_PREROTATED_EXCEPT_NEWEST, contiguous q and caches.
- * Limits: hidden <= 4096, intermediate <= 20480, ceil(max_kv_len / 128) <= 16 splits per
- * KV head and num_kv_heads * splits <= 64; efm_decode_stack_supported reports the reason
- * when a shape is outside them.
- *
- * The launch runs one workgroup per CU and needs them all resident at once: do not run
- * other kernels concurrently on the device. Hand-offs between workgroups are bounded
- * waits; if one times out the step's outputs are invalid, the launch still finishes,
- * and efm_decode_stack_status (synchronising; call it outside graph capture) reports
- * EFM_ERR_DEVICE once and re-arms. workspace: efm_decode_stack_workspace_bytes bytes,
- * 256-byte aligned, zero-filled before its first use and then reused as is (every launch
- * tags its hand-offs with a fresh epoch kept in the workspace); launches sharing a
- * workspace must be stream-ordered. Graph-capture safe.
- * ---------------------------------------------------------------------------------- */
-typedef struct efm_decode_stack_layer {
-    const void* in_norm;   /* [hidden] input RMSNorm weight                    */
-    const void* w_qkv;     /* [Hq*128 + 2*Hkv*128, hidden]                      */
-    const void* b_qkv;     /* [Hq*128 + 2*Hkv*128] or NULL                      */
-    const void* w_o;       /* [hidden, Hq*128]                                  */
-    const void* post_norm; /* [hidden] post-attention RMSNorm weight           */
-    const void* w_up_gate; /* [2*inter, hidden], rows [up; gate]                */
-    const void* w_down;    /* [hidden, inter]                                   */
-    void* k_cache;         /* [max_kv_len, Hkv*128] (rows [0, L-1) rotated)     */
-    void* v_cache;         /* [max_kv_len, Hkv*128]                             */
-} efm_decode_stack_layer;
-
-size_t efm_decode_stack_workspace_bytes(const efm_attention_ctx* ctx, int32_t hidden, int32_t inter, int32_t layers,
-                                        uint32_t max_kv_len);
-int efm_decode_stack_supported(const efm_attention_ctx* ctx, int32_t hidden, int32_t inter, int32_t layers,
-                               uint32_t max_kv_len);
-int efm_decode_stack(const efm_attention_ctx* ctx, int32_t hidden, int32_t inter, int32_t layers, float eps,
-                     const efm_decode_stack_layer* layer_table, const void* embed, int64_t vocab,
-                     const int32_t* token, const uint32_t* d_kv_len, uint32_t max_kv_len, void* h_out,
-                     void* residual_out, void* workspace, size_t workspace_bytes, hipStream_t stream);
-int efm_decode_stack_status(void* workspace, hipStream_t stream);
-
 /* ------------------------------------------------------------------------------------
  * LM head with fused greedy top-1 (src/layers/linear.cu:140-276, 2288-2369):
  * token_out[0] = argmax_v (x . W[v,:]) with ties to the lowest id (a NaN score never
