@@ -601,9 +601,10 @@ def run_c1(args):
     mid = torch.empty(1, I, device=dev, dtype=torch.bfloat16)
     out = torch.empty(1, H, device=dev, dtype=torch.bfloat16)
     state = {"i": 0}
-    # as the engine: the split merge folds into o_proj when the cache needs <= 8 splits of
-    # 128 keys (1024 rows); 1025 rows take the attention kernel's own merge + o_proj GEMV
-    fused_merge = max_kv <= 1024
+    # as the engine: the split merge folds into o_proj wherever the partials plan fits an
+    # o_proj merge prologue (here 17 one-wave splits of 64 keys, the narrow prologue);
+    # otherwise the attention kernel's own merge + the o_proj GEMV
+    fused_merge = C.load().efm_decode_attention_merge_o_proj_supported(ctx, max_kv) == C.EFM_OK
 
     def step(stream_handle):
         # the engine's per-layer decode sequence (Qwen2_5::decode_step): norm + QKV + KV
@@ -661,7 +662,8 @@ def run_c1(args):
                    "head_dim": hd, "intermediate": I, "copies_rotated": ncopy},
         "roofline": {"bound": "hbm", "achieved": round(nbytes / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_step": nbytes, "note": "launches: norm+qkv+kv write, attention (+ merge), o_proj, norm+gate/up+swiglu, down"},
+                     "bytes_per_step": nbytes, "note": "launches: norm+qkv+kv write, attention partials, merge+o_proj, norm+gate/up+swiglu, down"
+                     if fused_merge else "launches: norm+qkv+kv write, attention + merge, o_proj, norm+gate/up+swiglu, down"},
         "cpu_baseline": cpu,
     }))
 

@@ -663,7 +663,7 @@ __global__ __launch_bounds__(kWave) void decode_attn_tile_kernel(DecodeArgs a) {
     // ---- 4. the split's partial (o unnormalised, m, l), or with one split the output;
     //         lane (ql, hh) holds d = 32 tt + 8 eb + 4 hh + 0..3 of head ql
     if (ql < G) {
-        if (a.split_cap == 1) {
+        if (a.split_cap == 1 && a.o != nullptr) {
             const float inv = (l_run > 0.f) ? 1.f / l_run : 0.f;
             bf16_t* o = a.o + (size_t)(kvh * G + ql) * HD;
 #pragma unroll
@@ -848,6 +848,37 @@ static int tile_keys_per_split(int num_kv_heads, uint32_t max_kv_len) {
     return 0;
 }
 
+// Partials plan (efm_decode_attention_partials, read back by
+// efm_decode_attention_merge_o_proj): head_dim-64 models whose query width fits the narrow
+// merge prologue take one-wave splits of 1 or 2 tiles (the fewest tiles that keep the
+// splits within kMergeNarrowMaxSplits), twice the workgroups of the 4-wave plan at a
+// 1k-row cache, merged without a separate kernel; every other shape takes the plan above.
+DecodePartialsPlan decode_partials_plan(const efm_attention_ctx* c, uint32_t max_kv_len) {
+    const uint32_t bound = std::max<uint32_t>(max_kv_len, 1u);
+    const int Hkv = std::max(1, (int)c->num_kv_heads), hd = (int)c->head_dim;
+    DecodePartialsPlan p;
+    p.keys_per_split = decode_keys_per_split(Hkv, bound);
+    p.split_cap = (int)((bound + p.keys_per_split - 1) / p.keys_per_split);
+    p.narrow = false;
+    const int64_t k_sn = c->k_stride_n ? (int64_t)c->k_stride_n : (int64_t)Hkv * hd;
+    const int64_t v_sn = c->kv_stride_n ? (int64_t)c->kv_stride_n : (int64_t)Hkv * hd;
+    const bool offsets_fit = (int64_t)bound * k_sn * 2 < 0x7fffffffLL && (int64_t)bound * v_sn * 2 < 0x7fffffffLL;
+    if (hd != 64 || (int64_t)c->num_qo_heads * hd > kMergeNarrowMaxWidth || !offsets_fit ||
+        kernel_knob(EFM_KNOB_DECODE_TILE) != 0)
+        return p;
+    const uint32_t tiles = (bound + kTileKeys - 1) / kTileKeys;
+    for (int t = 1; t <= kTileMaxT; ++t) {
+        const uint32_t cap = (tiles + t - 1) / t;
+        if (cap <= (uint32_t)kMergeNarrowMaxSplits && cap * (uint32_t)Hkv <= (uint32_t)kTileMaxWG) {
+            p.keys_per_split = t * kTileKeys;
+            p.split_cap = (int)cap;
+            p.narrow = true;
+            return p;
+        }
+    }
+    return p;
+}
+
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct DecodeWs {
@@ -861,6 +892,7 @@ static DecodeWs decode_ws(const efm_attention_ctx* c, uint32_t max_kv_len) {
     int cap = decode_split_cap(c->num_kv_heads, bound);
     if (const int tk = tile_keys_per_split((int)c->num_kv_heads, bound))
         cap = std::max(cap, (int)((bound + tk - 1) / tk));
+    cap = std::max(cap, decode_partials_plan(c, bound).split_cap);
     DecodeWs w;
     w.o_bytes = align256((size_t)c->num_kv_heads * cap * G * c->head_dim * sizeof(float));
     w.ml_bytes = align256((size_t)c->num_kv_heads * cap * G * 2 * sizeof(float));
@@ -950,9 +982,11 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
     a.counter = reinterpret_cast<uint32_t*>(wsb + ws.o_bytes + ws.ml_bytes);
 
     // Merged calls on short and mid contexts: one-wave splits, then the merge kernel (or,
-    // with one split, the output written by that wave).
-    const int tile_kps = tile_keys_per_split((int)ctx->num_kv_heads, a.row_bound);
-    if (merge && tile_kps > 0 && decode_lds_offsets_fit(a) && kernel_knob(EFM_KNOB_DECODE_TILE) == 0) {
+    // with one split, the output written by that wave). Partials calls take them where
+    // their plan says so (narrow plan), and end with the partials.
+    const DecodePartialsPlan pp = merge ? DecodePartialsPlan{0, 0, false} : decode_partials_plan(ctx, bound);
+    const int tile_kps = merge ? tile_keys_per_split((int)ctx->num_kv_heads, a.row_bound) : (pp.narrow ? pp.keys_per_split : 0);
+    if (tile_kps > 0 && decode_lds_offsets_fit(a) && kernel_knob(EFM_KNOB_DECODE_TILE) == 0) {
         a.keys_per_split = tile_kps;
         a.split_cap = (a.row_bound + tile_kps - 1) / tile_kps;
         const dim3 tgrid(a.split_cap, ctx->num_kv_heads), tblock(kWave);
@@ -963,7 +997,7 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
             else if (rotk) hipLaunchKernelGGL((decode_attn_tile_kernel<HDV, GV, 2, true>), tgrid, tblock, 0, stream, a);      \
             else if (T == 1) hipLaunchKernelGGL((decode_attn_tile_kernel<HDV, GV, 1, false>), tgrid, tblock, 0, stream, a);  \
             else hipLaunchKernelGGL((decode_attn_tile_kernel<HDV, GV, 2, false>), tgrid, tblock, 0, stream, a);              \
-            if (a.split_cap > 1)                                                                               \
+            if (merge && a.split_cap > 1)                                                                      \
                 hipLaunchKernelGGL((decode_merge_kernel<HDV>), dim3(ctx->num_qo_heads, kMergeSlices), dim3(kAttnThreads), 0, \
                                    stream, a, G);                                                              \
             return check_launch("attention_decode");                                                           \

@@ -16,6 +16,18 @@ constexpr int kWave = 64;
 // Split-KV decode partials that the o_proj GEMV's merge prologue holds (one register
 // slot per split): caches of up to 8 x 128 rows.
 constexpr int kMergeMaxSplits = 8;
+// The narrow merge prologue (query widths up to 1024): one register slot per split for up
+// to 24 splits, e.g. a 1.5k-row cache in 64-row splits.
+constexpr int kMergeNarrowMaxSplits = 24;
+constexpr int kMergeNarrowMaxWidth = 1024;
+
+// Split plan of the decode partials (efm_decode_attention_partials) that every consumer of
+// them reads back: keys per split, splits, and whether the one-wave tile kernel writes
+// them (narrow: merged by the narrow o_proj prologue).
+struct DecodePartialsPlan {
+    int keys_per_split, split_cap;
+    bool narrow;
+};
 
 typedef uint16_t bf16_t;
 

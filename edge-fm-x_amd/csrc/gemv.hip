@@ -248,36 +248,52 @@ extern "C" int efm_decode_norm_gate_up_swiglu(int32_t hidden, int32_t inter, flo
 }
 
 namespace efm {
-int decode_split_cap(int num_kv_heads, uint32_t max_kv_len);
-int decode_keys_per_split(int num_kv_heads, uint32_t max_kv_len);
 size_t decode_workspace_bytes(const efm_attention_ctx* ctx, uint32_t max_kv_len);
 size_t decode_ml_offset(const efm_attention_ctx* ctx, uint32_t max_kv_len);
+DecodePartialsPlan decode_partials_plan(const efm_attention_ctx* c, uint32_t max_kv_len);
 int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
+
+// The partials plan's splits fit one of the merge prologues: the narrow one (its plan's
+// own shapes) or the wide one (up to kMergeMaxSplits splits, kMergeMaxHeads heads).
+static int merge_o_proj_supported(const efm_attention_ctx* ctx, uint32_t max_kv_len, DecodePartialsPlan* plan) {
+    int rc = validate_attention_ctx(ctx, "attention_merge_o_proj");
+    if (rc) return rc;
+    if (max_kv_len == 0) return set_error(EFM_ERR_INVALID_ARGUMENT, "attention_merge_o_proj: max_kv_len is 0");
+    const DecodePartialsPlan p = decode_partials_plan(ctx, max_kv_len);
+    if (plan != nullptr) *plan = p;
+    if (p.narrow) return EFM_OK;
+    if (p.split_cap > kMergeMaxSplits || (int)ctx->num_qo_heads > kMergeMaxHeads ||
+        (int64_t)ctx->num_qo_heads * ctx->head_dim > 2 * 4 * kGemvThreads)
+        return set_error(EFM_ERR_UNSUPPORTED, "attention_merge_o_proj: %d splits / %u heads exceed the fused merge",
+                         p.split_cap, ctx->num_qo_heads);
+    return EFM_OK;
+}
 }  // namespace efm
+
+extern "C" int efm_decode_attention_merge_o_proj_supported(const efm_attention_ctx* ctx, uint32_t max_kv_len) {
+    return merge_o_proj_supported(ctx, max_kv_len, nullptr);
+}
 
 extern "C" int efm_decode_attention_merge_o_proj(const efm_attention_ctx* ctx, const uint32_t* d_kv_len,
                                                  uint32_t max_kv_len, const void* workspace,
                                                  size_t workspace_bytes, const void* w_o, int32_t hidden, void* out,
                                                  hipStream_t stream) {
-    int rc = validate_attention_ctx(ctx, "attention_merge_o_proj");
+    DecodePartialsPlan plan;
+    int rc = merge_o_proj_supported(ctx, max_kv_len, &plan);
     if (rc) return rc;
     if (d_kv_len == nullptr || workspace == nullptr || w_o == nullptr || out == nullptr)
         return set_error(EFM_ERR_INVALID_ARGUMENT, "attention_merge_o_proj: null pointer");
     const int q_dim = (int)(ctx->num_qo_heads * ctx->head_dim);
     rc = gemv_check(q_dim, hidden, w_o, workspace, out, false);
     if (rc) return rc;
-    const int cap = decode_split_cap((int)ctx->num_kv_heads, max_kv_len);
-    if ((int64_t)cap > kMergeMaxSplits || (int)ctx->num_qo_heads > kMergeMaxHeads)
-        return set_error(EFM_ERR_UNSUPPORTED, "attention_merge_o_proj: %d splits / %u heads exceed the fused merge",
-                         cap, ctx->num_qo_heads);
     if (workspace_bytes < decode_workspace_bytes(ctx, max_kv_len))
         return set_error(EFM_ERR_WORKSPACE, "attention_merge_o_proj: workspace too small");
     GemvArgs a = gemv_args(q_dim, hidden, w_o, workspace);
     a.y = out;
     a.o_part = static_cast<const float*>(workspace);
     a.ml_part = reinterpret_cast<const float*>(static_cast<const char*>(workspace) + decode_ml_offset(ctx, max_kv_len));
-    a.split_cap = cap;
-    a.keys_per_split = decode_keys_per_split((int)ctx->num_kv_heads, max_kv_len);
+    a.split_cap = plan.split_cap;
+    a.keys_per_split = plan.keys_per_split;
     a.head_dim = (int)ctx->head_dim;
     a.group = (int)(ctx->num_qo_heads / ctx->num_kv_heads);
     a.attn_len = d_kv_len;
@@ -285,6 +301,7 @@ extern "C" int efm_decode_attention_merge_o_proj(const efm_attention_ctx* ctx, c
     // every workgroup repeats the split merge: two rows per wave group (gemv_pick's choice
     // with one wave per row) halve the workgroups and the repeats
     const GemvCfg g = gemv_pick(q_dim, hidden, 1, 1024, false);
+    if (plan.narrow) return gemv_launch<PRO_ATTN_MERGE_N, EPI_BF16>(g, a, stream);
     return gemv_launch<PRO_ATTN_MERGE, EPI_BF16>(g, a, stream);
 }
 

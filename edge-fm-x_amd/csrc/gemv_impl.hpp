@@ -28,7 +28,7 @@
 
 namespace efm {
 
-enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ADD_NORM = 2, PRO_ATTN_MERGE = 3 };
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ADD_NORM = 2, PRO_ATTN_MERGE = 3, PRO_ATTN_MERGE_N = 4 };
 enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_TOP1 = 4, EPI_QKV_TAG = 5, EPI_QKV_ROPE = 6 };
 
 // Weight-stream load of the GEMV main loop: a non-temporal 16-byte buffer load (weights
@@ -90,63 +90,136 @@ constexpr int kMergeMaxHeads = 64;
 constexpr int kPlainPre = 4;   // PLAIN input chunks per thread loaded ahead of the weights
 constexpr int kNormPre = 2;    // NORM / ADD_NORM chunks per thread loaded ahead (K <= 4096)
 
+// Attention-merge prologues: ATTN_MERGE takes up to kMergeMaxSplits splits of inputs up
+// to 2048 wide (two float4 of every split per thread), ATTN_MERGE_N up to
+// kMergeNarrowMaxSplits splits of inputs up to 1024 wide (one float4 per split: the same
+// registers hold three times the splits).
+constexpr bool pro_merge(int PRO) { return PRO == PRO_ATTN_MERGE || PRO == PRO_ATTN_MERGE_N; }
+template <int PRO>
+struct MergeShape {
+    static constexpr int MS = (PRO == PRO_ATTN_MERGE_N) ? kMergeNarrowMaxSplits : (PRO == PRO_ATTN_MERGE ? kMergeMaxSplits : 1);
+    static constexpr int NQ = (PRO == PRO_ATTN_MERGE) ? 2 : 1;   // float4 of the input per thread
+    // (m, l) loads per wave and input slice: lanes cover (head, split) pairs, 64 / heads
+    // per slice splits per load (at least 16: head_dim 64 puts 4 heads in a wave's slice)
+    static constexpr int ML = (MS + 15) / 16;
+};
+static_assert(MergeShape<PRO_ATTN_MERGE_N>::NQ * 4 * kGemvThreads == kMergeNarrowMaxWidth,
+              "narrow merge width");
+static_assert(MergeShape<PRO_ATTN_MERGE>::MS % 4 == 0 && MergeShape<PRO_ATTN_MERGE_N>::MS % 4 == 0,
+              "merge weights are read four splits at a time");
+
 // The prologue's own loads (input vector, residual, norm weight), issued before the first
 // weight loads of the workgroup: loads return in issue order, so issued after the weight
 // stream they would wait for all of it, and the norm's reduction would start only then.
 template <int PRO>
 struct ProLoads {
-    static constexpr int N = (PRO == PRO_PLAIN) ? kPlainPre : (PRO == PRO_ATTN_MERGE ? 0 : kNormPre);
-    static constexpr int MS = (PRO == PRO_ATTN_MERGE) ? kMergeMaxSplits : 1;
+    static constexpr int N = (PRO == PRO_PLAIN) ? kPlainPre : (pro_merge(PRO) ? 0 : kNormPre);
+    static constexpr int MS = MergeShape<PRO>::MS, NQ = MergeShape<PRO>::NQ;
     uint4 x[N > 0 ? N : 1], r[PRO == PRO_ADD_NORM ? N : 1], w[(PRO == PRO_NORM || PRO == PRO_ADD_NORM) ? N : 1];
-    float2 ml[MS];      // ATTN_MERGE: this thread's head's split statistics (m, l)
-    float4 op[2][MS];   // ATTN_MERGE: this thread's 2 x 4 output elements of every split
+    float2 ml[NQ][MergeShape<PRO>::ML];   // ATTN_MERGE*: (m, l) of this lane's (head, split) pairs
+    float4 op[NQ][MS];   // ATTN_MERGE*: this thread's NQ x 4 input elements of every split
+    uint32_t len;        // ATTN_MERGE*: attended rows
 };
 
 // The one-round-trip attention merge (prologue of merge + o_proj) covers these shapes.
+template <int PRO>
 __device__ __forceinline__ bool merge_fast(const GemvArgs& a) {
-    return a.K <= 2 * 4 * kGemvThreads && a.split_cap <= kMergeMaxSplits;
+    return a.K <= MergeShape<PRO>::NQ * 4 * kGemvThreads && a.split_cap <= MergeShape<PRO>::MS;
+}
+
+// Max / sum over each aligned group of 16 lanes (or 32 with wide), the result in every lane
+// of the group: four DPP steps within a row (xor 1, xor 2, half-row mirror, row mirror),
+// plus one swizzle (xor 16) across the row pair for 32 lanes. No LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lane_group_max(float v, bool wide) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f32<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f32<0x141>(v));   // row_half_mirror
+    v = fmaxf(v, dpp_f32<0x140>(v));   // row_mirror
+    if (wide) v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
+    return v;
+}
+// Sum over the 64 lanes of a wave, returned uniform: the 16-lane DPP steps above, then
+// row broadcasts (lane 15 into rows 1 and 3, lane 31 into rows 2 and 3) leave the total in
+// lane 63, which is read out. Every decode GEMV reduces its dot products with this.
+__device__ __forceinline__ float wave_total(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));   // row_bcast:15
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));   // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float lane_group_sum(float v, bool wide) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    if (wide) v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+    return v;
 }
 
 // Branch-free like the weight loads (chunks past K read as zero), so that the compiler
 // waits for each of them by its exact position in the wave's load sequence.
 template <int PRO>
 __device__ __forceinline__ void gemv_prologue_load(const GemvArgs& a, ProLoads<PRO>& p) {
-    if constexpr (PRO == PRO_ATTN_MERGE) {
-        // every split slot of this thread's elements (slots past split_cap, threads past
-        // the heads / elements and shapes outside merge_fast read zeros)
+    if constexpr (pro_merge(PRO)) {
+        // Every split slot of this thread's elements: the head offset is computed once,
+        // slot j adds j splits (one add per load). Slots at or past split_cap read entries
+        // of the next KV head (or zeros past the last): the merge never uses them, since
+        // the live split count is at most split_cap. The split statistics come once per
+        // wave: the slice's hpw = 256 / head_dim heads take 64 / hpw lanes each, lane l
+        // holding (head l / (64 / hpw), split l % (64 / hpw) + i * 64 / hpw). Threads past
+        // the elements and shapes outside merge_fast read zeros.
         typedef float f32x2_t __attribute__((ext_vector_type(2)));
         typedef float f32x4_t __attribute__((ext_vector_type(4)));
-        const bool fast = merge_fast(a);
+        constexpr int MS = MergeShape<PRO>::MS, NQ = MergeShape<PRO>::NQ, ML = MergeShape<PRO>::ML;
+        const bool fast = merge_fast<PRO>(a);
+        p.len = fast ? min(a.attn_len[0], a.attn_max_len) : 0u;
         const int hd = a.head_dim, G = a.group, cap = a.split_cap;
         const int Hq = a.K / hd, Hkv = Hq / G;
-        const int ml_bytes = fast ? Hkv * cap * G * 8 : 0, op_bytes = fast ? Hkv * cap * G * hd * 4 : 0;
+        const int hd_shift = __builtin_ctz((unsigned)hd);   // head_dim 64 or 128
+        const int hpw_shift = 8 - hd_shift;                 // log2(256 / head_dim)
+        const uint32_t ml_split = (uint32_t)(G * 8), op_split = (uint32_t)(G * hd * 4);
         const __amdgpu_buffer_rsrc_t rml = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(a.ml_part), (short)0, __builtin_amdgcn_readfirstlane(ml_bytes), 0x00020000);
+            const_cast<float*>(a.ml_part), (short)0, fast ? (int)((uint32_t)Hkv * cap * ml_split) : 0, 0x00020000);
         const __amdgpu_buffer_rsrc_t rop = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(a.o_part), (short)0, __builtin_amdgcn_readfirstlane(op_bytes), 0x00020000);
-        {
-            const int h = threadIdx.x;
+            const_cast<float*>(a.o_part), (short)0, fast ? (int)((uint32_t)Hkv * cap * op_split) : 0, 0x00020000);
+        const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+        uint32_t vml[NQ], vop[NQ];
 #pragma unroll
-            for (int j = 0; j < kMergeMaxSplits; ++j) {
-                const uint32_t off = (h < Hq && j < cap) ? (uint32_t)((((h / G) * cap + j) * G + (h % G)) * 8) : kWloadSkip;
-                const f32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rml, off, 0, 0);
-                p.ml[j] = make_float2(v[0], v[1]);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < NQ; ++q) {
             const int c = threadIdx.x + q * kGemvThreads;
-            const int n0 = c * 4, h = n0 / hd, d0 = n0 % hd;
-            const uint32_t base = (uint32_t)((((h / G) * cap * G + (h % G)) * hd + d0) * 4);
+            const int n0 = c * 4, h = n0 >> hd_shift, d0 = n0 & (hd - 1);
+            const int kvh = h / G, g = h - kvh * G;
+            vop[q] = (c < (a.K >> 2)) ? ((uint32_t)(kvh * cap * G + g) * (uint32_t)hd + (uint32_t)d0) * 4u : kWloadSkip;
+            const int hs = (((wave + q * (kGemvThreads / kWave)) * kWave * 4) >> hd_shift) + (lane >> (6 - hpw_shift));
+            const int kvs = hs / G, gs = hs - kvs * G;
+            vml[q] = (hs < Hq) ? (uint32_t)(kvs * cap * G + gs) * 8u : kWloadSkip;
+        }
+        const int jl = lane & ((kWave >> hpw_shift) - 1);
 #pragma unroll
-            for (int j = 0; j < kMergeMaxSplits; ++j) {
-                const uint32_t off = (c < (a.K >> 2) && j < cap) ? base + (uint32_t)(j * G * hd * 4) : kWloadSkip;
-                const f32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rop, off, 0, 0);
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+            for (int i = 0; i < ML; ++i) {
+                const int js = jl + (i << (6 - hpw_shift));
+                const uint32_t off = (js < cap) ? vml[q] + (uint32_t)js * ml_split : kWloadSkip;
+                const f32x2_t m = __builtin_amdgcn_raw_buffer_load_b64(rml, off, 0, 0);
+                p.ml[q][i] = make_float2(m[0], m[1]);
+            }
+#pragma unroll
+        for (int j = 0; j < MS; ++j)
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const f32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rop, vop[q] + j * op_split, 0, 0);
                 p.op[q][j] = make_float4(v[0], v[1], v[2], v[3]);
             }
-        }
     }
-    if constexpr (PRO != PRO_ATTN_MERGE) {
+    if constexpr (!pro_merge(PRO)) {
         const int nbytes = a.K * 2;
         auto rsrc = [&](const bf16_t* v) {
             return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(v), (short)0, nbytes, 0x00020000);
@@ -182,7 +255,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, const ProLoads<
         for (int c = threadIdx.x + kPlainPre * kGemvThreads; c < C; c += kGemvThreads) xs4[c] = x4[c];
         return;
     }
-    if constexpr (PRO != PRO_ATTN_MERGE) {
+    if constexpr (!pro_merge(PRO)) {
         // Chunks past K hold zeros: they add nothing to the sum of squares. Chunks beyond the
         // preloaded ones (K > 4096) are loaded here, behind the weights, and read again for
         // the normalisation instead of being kept in registers.
@@ -252,56 +325,77 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, const ProLoads<
         }
         return;
     }
-    if constexpr (PRO == PRO_ATTN_MERGE) {
-    if (merge_fast(a)) {
+    if constexpr (pro_merge(PRO)) {
+    constexpr int MS = MergeShape<PRO>::MS, NQ = MergeShape<PRO>::NQ;
+    if (merge_fast<PRO>(a)) {
         // Same merge as below with every load issued up front, ahead of the weight stream
-        // (gemv_prologue_load: each head's split statistics and this thread's partial
-        // outputs for every split slot; slots beyond the live split count get weight 0):
-        // one memory round trip, under the weights' instead of after them.
-        __shared__ float swf[kMergeMaxHeads * kMergeMaxSplits];
-        const int hd = a.head_dim;
-        const int Hq = a.K / hd;
-        const uint32_t L = min(a.attn_len[0], a.attn_max_len);
-        const float2 (&ml)[kMergeMaxSplits] = pl.ml;
-        const float4 (&op)[2][kMergeMaxSplits] = pl.op;
+        // (gemv_prologue_load): one memory round trip, under the weights' instead of after
+        // them. Each wave merges its own input slice: the lanes holding a head's split
+        // statistics reduce its max and denominator across lanes, write the head's split
+        // weights to the wave's own LDS rows, and every lane applies its head's weights to
+        // its partial outputs. Slots past the live split count take no part.
+        constexpr int ML = MergeShape<PRO>::ML;
+        __shared__ __align__(16) float swl[kGemvThreads / kWave][NQ][4 * MS];   // [wave][slice][head][split]
+        const uint32_t L = pl.len;
         const int kps = a.keys_per_split;
         const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
-        if ((int)threadIdx.x < Hq) {
-            const int h = threadIdx.x;
+        const int hd_shift = __builtin_ctz((unsigned)a.head_dim);
+        const int hpw_shift = 8 - hd_shift;
+        const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+        const int hl = lane >> (6 - hpw_shift), jl = lane & ((kWave >> hpw_shift) - 1);
+        const bool wide_group = hd_shift == 7;   // 32 lanes per head (head_dim 128), else 16
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
             float M = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < kMergeMaxSplits; ++j)
-                if (j < nsplit) M = fmaxf(M, ml[j].x);
-            float den = 0.f, w[kMergeMaxSplits];
-#pragma unroll
-            for (int j = 0; j < kMergeMaxSplits; ++j) {
-                if (j < nsplit) {
-                    w[j] = (ml[j].x == -INFINITY) ? 0.f : exp2f(ml[j].x - M);
-                    den = fmaf(w[j], ml[j].y, den);
-                }
+            for (int i = 0; i < ML; ++i) {
+                const int js = jl + (i << (6 - hpw_shift));
+                if (js < nsplit) M = fmaxf(M, pl.ml[q][i].x);
             }
+            M = lane_group_max(M, wide_group);
+            float e[ML], den = 0.f;
+#pragma unroll
+            for (int i = 0; i < ML; ++i) {
+                const int js = jl + (i << (6 - hpw_shift));
+                const float m = pl.ml[q][i].x;
+                e[i] = (js < nsplit && m != -INFINITY) ? exp2f(m - M) : 0.f;
+                den = fmaf(e[i], pl.ml[q][i].y, den);
+            }
+            den = lane_group_sum(den, wide_group);
             const float inv = (den > 0.f) ? 1.f / den : 0.f;
 #pragma unroll
-            for (int j = 0; j < kMergeMaxSplits; ++j)
-                if (j < nsplit) swf[h * nsplit + j] = w[j] * inv;
+            for (int i = 0; i < ML; ++i) {
+                const int js = jl + (i << (6 - hpw_shift));
+                if (js < MS) swl[wave][q][hl * MS + js] = e[i] * inv;
+            }
         }
-        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int he = (lane * 4) >> hd_shift;   // head of this lane's elements in the slice
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < NQ; ++q) {
             const int c = threadIdx.x + q * kGemvThreads;
-            if (c < (a.K >> 2)) {
-                const int h = (c * 4) / hd;
-                float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            const float* w = &swl[wave][q][he * MS];
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int j = 0; j < kMergeMaxSplits; ++j) {
-                    if (j < nsplit) {
-                        const float wj = swf[h * nsplit + j];
-                        acc[0] = fmaf(wj, op[q][j].x, acc[0]);
-                        acc[1] = fmaf(wj, op[q][j].y, acc[1]);
-                        acc[2] = fmaf(wj, op[q][j].z, acc[2]);
-                        acc[3] = fmaf(wj, op[q][j].w, acc[3]);
+            for (int j = 0; j < MS; j += 4) {
+                if (j < nsplit) {
+                    const float4 w4 = *reinterpret_cast<const float4*>(w + j);
+                    const float wj[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        if (j + t < nsplit) {
+                            const float4 o = pl.op[q][j + t];
+                            acc[0] = fmaf(wj[t], o.x, acc[0]);
+                            acc[1] = fmaf(wj[t], o.y, acc[1]);
+                            acc[2] = fmaf(wj[t], o.z, acc[2]);
+                            acc[3] = fmaf(wj[t], o.w, acc[3]);
+                        }
                     }
                 }
+            }
+            if (c < (a.K >> 2)) {
                 uint2 pk;
                 pk.x = pack_bf16x2(acc[0], acc[1]);
                 pk.y = pack_bf16x2(acc[2], acc[3]);
@@ -310,7 +404,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, const ProLoads<
         }
         return;
     }
-    {
+    if constexpr (PRO == PRO_ATTN_MERGE) {
         // x[h*hd + d] = bf16( sum_s w[h][s] * o_part[kvh][s][g][d] ),
         // w[h][s] = exp2(m_s - M) / sum_s exp2(m_s - M) l_s  (log-sum-exp merge of the splits)
         __shared__ float sw[kMergeMaxHeads * kMergeMaxSplits];
@@ -495,7 +589,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int p = 0; p < P; ++p) acc[r][p] = wave_sum(acc[r][p]);
+            for (int p = 0; p < P; ++p) acc[r][p] = wave_total(acc[r][p]);
         if (KS > 1) {
             if (lane == 0) {
 #pragma unroll

@@ -88,6 +88,7 @@ SIGNATURES = {
                                                 c_uint32, c_void_p, c_size_t, c_void_p]),
     "efm_decode_attention_merge_o_proj": (c_int32, [POINTER(AttentionCtx), c_void_p, c_uint32, c_void_p, c_size_t,
                                                     c_void_p, c_int32, c_void_p, c_void_p]),
+    "efm_decode_attention_merge_o_proj_supported": (c_int32, [POINTER(AttentionCtx), c_uint32]),
     "efm_attention_prefill": (c_int32, [POINTER(AttentionCtx), c_void_p, c_void_p, c_void_p, c_void_p, c_uint32,
                                         c_uint32, c_int32, c_void_p]),
     "efm_attention_prefill_sage_int8_workspace_bytes": (c_size_t, [POINTER(AttentionCtx), c_uint32, c_uint32]),

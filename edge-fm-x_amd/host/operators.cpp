@@ -271,15 +271,17 @@ public:
 //       launch (efm_decode_norm_qkv_attention), partials merged in the o_proj prologue
 //   hip_gfx950_decode_split_attention      norm + QKV, then the split attention, partials
 //       merged in the o_proj prologue
-// Both need the merge to fold into o_proj: at most 8 splits (1024 cached rows) and 64
-// query heads; the fused launch also a text model (rotate-on-read cache), head_dim 128
-// and efm_decode_norm_qkv_attention_supported.
+// Both need the merge to fold into o_proj (efm_decode_attention_merge_o_proj_supported:
+// up to 8 splits of 128 keys, or for head_dim 64 and query widths up to 1024, 24 splits
+// of 32 or 64 keys); the fused launch also a text model (rotate-on-read cache), head_dim
+// 128 and efm_decode_norm_qkv_attention_supported.
 class HipDecodeSplitAttentionOp : public HipAttentionOp {
 public:
     std::string impl_id() const override { return "hip_gfx950_decode_split_attention"; }
     bool supports(const AttentionOpContext& c) const override {
-        return HipAttentionOp::supports(c) && c.decode_max_kv_len > 0 && c.decode_max_kv_len <= 1024 &&
-               c.num_qo_heads <= 64;
+        if (!HipAttentionOp::supports(c) || c.decode_max_kv_len == 0) return false;
+        const efm_attention_ctx cc = to_c_ctx(c);
+        return efm_decode_attention_merge_o_proj_supported(&cc, c.decode_max_kv_len) == EFM_OK;
     }
 };
 

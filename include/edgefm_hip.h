@@ -170,12 +170,21 @@ int efm_decode_attention_partials(const efm_attention_ctx* ctx, const void* q, c
  * where merge is the log-sum-exp combination of the splits written by
  * efm_decode_attention_partials with the same ctx, d_kv_len, max_kv_len and workspace;
  * the merged vector is rounded to bf16 before the projection, as the unfused
- * attention output would be. Supports up to 8 splits (max_kv_len <= 1024) and 64 query
- * heads. Replaces the o_proj LinearImpl::forward (role attention_output,
- * src/layers/linear.cu:41-58). */
+ * attention output would be. Supports the split plans that
+ * efm_decode_attention_merge_o_proj_supported accepts: head_dim 64 with query widths up
+ * to 1024 and caches up to 1536 rows (up to 24 splits of 32 or 64 keys), otherwise up to
+ * 8 splits (max_kv_len <= 1024) and 64 query heads. Replaces the o_proj
+ * LinearImpl::forward (role attention_output, src/layers/linear.cu:41-58). */
 int efm_decode_attention_merge_o_proj(const efm_attention_ctx* ctx, const uint32_t* d_kv_len, uint32_t max_kv_len,
                                       const void* workspace, size_t workspace_bytes, const void* w_o, int32_t hidden,
                                       void* out, hipStream_t stream);
+
+/* EFM_OK when efm_decode_attention_merge_o_proj takes the partials that
+ * efm_decode_attention_partials writes for (ctx, max_kv_len); otherwise the error code it
+ * would return (callers then use efm_attention_decode and efm_linear). Host-side only.
+ * Part of the same split of the reference's attention + o_proj pair
+ * (src/models/qwen2_5/qwen2_5.cpp:831-847). */
+int efm_decode_attention_merge_o_proj_supported(const efm_attention_ctx* ctx, uint32_t max_kv_len);
 
 /* Causal / non-causal GQA prefill attention on the matrix cores. q [qo_len, Hq, hd]
  * (q_stride_* may point into a fused QKV buffer), k, v [kv_len, Hkv, hd] with

@@ -85,3 +85,22 @@ def test_testing_kernel_path_setter_validates():
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_DECODE_TILE, 2) == C.EFM_ERR_INVALID_ARGUMENT
     assert lib.efm_testing_set_kernel_path(6, 0) == C.EFM_ERR_INVALID_ARGUMENT
     assert lib.efm_testing_set_kernel_path(99, 0) == C.EFM_ERR_INVALID_ARGUMENT
+
+
+def test_merge_o_proj_plan_query_without_gpu():
+    """The partials plan that efm_decode_attention_merge_o_proj reads back: head_dim 64
+    with query widths up to 1024 merges up to 24 splits of 32 / 64 keys (1536 rows); other
+    shapes up to 8 splits of 128 keys (1024 rows) and 64 query heads."""
+    lib = C.load()
+    sup = lib.efm_decode_attention_merge_o_proj_supported
+    assert sup(C.make_attention_ctx(14, 2, 64), 1025) == C.EFM_OK
+    assert sup(C.make_attention_ctx(16, 2, 64), 1536) == C.EFM_OK
+    assert sup(C.make_attention_ctx(14, 2, 64), 1537) == C.EFM_ERR_UNSUPPORTED
+    assert sup(C.make_attention_ctx(32, 8, 64), 1024) == C.EFM_OK          # wide prologue, 8 splits
+    assert sup(C.make_attention_ctx(32, 8, 64), 1025) == C.EFM_ERR_UNSUPPORTED
+    assert sup(C.make_attention_ctx(12, 2, 128), 1024) == C.EFM_OK
+    assert sup(C.make_attention_ctx(12, 2, 128), 1025) == C.EFM_ERR_UNSUPPORTED
+    assert sup(C.make_attention_ctx(14, 2, 64), 0) == C.EFM_ERR_INVALID_ARGUMENT
+    # the narrow plan's splits fit the workspace the size query reports
+    ctx = C.make_attention_ctx(14, 2, 64)
+    assert lib.efm_attention_decode_workspace_bytes(ctx, 1536) >= 2 * 24 * 7 * 64 * 4 + 2 * 24 * 7 * 2 * 4
