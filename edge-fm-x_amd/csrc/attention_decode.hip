@@ -849,30 +849,35 @@ static int tile_keys_per_split(int num_kv_heads, uint32_t max_kv_len) {
 }
 
 // Partials plan (efm_decode_attention_partials, read back by
-// efm_decode_attention_merge_o_proj): head_dim-64 models whose query width fits the narrow
-// merge prologue take one-wave splits of 1 or 2 tiles (the fewest tiles that keep the
-// splits within kMergeNarrowMaxSplits), twice the workgroups of the 4-wave plan at a
-// 1k-row cache, merged without a separate kernel; every other shape takes the plan above.
+// efm_decode_attention_merge_o_proj): one-wave splits of 1 or 2 tiles (the fewest tiles
+// that keep the splits within what the o_proj merge prologue holds for this query width)
+// where they fit: more workgroups than the 4-wave plan and no merge across waves
+// (head_dim 64, 14 / 2 heads: partials + merge + o_proj 7.1-8.8 us against 9.4-10.6 up to
+// 1.5k rows); longer caches take the plan above.
 DecodePartialsPlan decode_partials_plan(const efm_attention_ctx* c, uint32_t max_kv_len) {
     const uint32_t bound = std::max<uint32_t>(max_kv_len, 1u);
     const int Hkv = std::max(1, (int)c->num_kv_heads), hd = (int)c->head_dim;
     DecodePartialsPlan p;
     p.keys_per_split = decode_keys_per_split(Hkv, bound);
     p.split_cap = (int)((bound + p.keys_per_split - 1) / p.keys_per_split);
-    p.narrow = false;
+    p.tile = false;
     const int64_t k_sn = c->k_stride_n ? (int64_t)c->k_stride_n : (int64_t)Hkv * hd;
     const int64_t v_sn = c->kv_stride_n ? (int64_t)c->kv_stride_n : (int64_t)Hkv * hd;
     const bool offsets_fit = (int64_t)bound * k_sn * 2 < 0x7fffffffLL && (int64_t)bound * v_sn * 2 < 0x7fffffffLL;
-    if (hd != 64 || (int64_t)c->num_qo_heads * hd > kMergeNarrowMaxWidth || !offsets_fit ||
-        kernel_knob(EFM_KNOB_DECODE_TILE) != 0)
-        return p;
+    const int ms = merge_max_splits((int64_t)c->num_qo_heads * hd);
+    if (ms == 0 || !offsets_fit || kernel_knob(EFM_KNOB_DECODE_TILE) != 0) return p;
+    // head_dim 128 takes one-tile splits only, at most kMergeMaxSplits of them: two-tile
+    // splits load 32 KB through one wave and were measured slower than the 4-wave plan
+    // (12 / 2 heads at 768 rows: 10.4 against 9.5 us for partials + merge + o_proj)
     const uint32_t tiles = (bound + kTileKeys - 1) / kTileKeys;
-    for (int t = 1; t <= kTileMaxT; ++t) {
+    const int max_t = (hd == 64) ? kTileMaxT : 1;
+    const int max_cap = (hd == 64) ? ms : std::min(ms, kMergeMaxSplits);
+    for (int t = 1; t <= max_t; ++t) {
         const uint32_t cap = (tiles + t - 1) / t;
-        if (cap <= (uint32_t)kMergeNarrowMaxSplits && cap * (uint32_t)Hkv <= (uint32_t)kTileMaxWG) {
+        if (cap <= (uint32_t)max_cap && cap * (uint32_t)Hkv <= (uint32_t)kTileMaxWG) {
             p.keys_per_split = t * kTileKeys;
             p.split_cap = (int)cap;
-            p.narrow = true;
+            p.tile = true;
             return p;
         }
     }
@@ -983,9 +988,9 @@ static int decode_launch(const efm_attention_ctx* ctx, const void* q, const void
 
     // Merged calls on short and mid contexts: one-wave splits, then the merge kernel (or,
     // with one split, the output written by that wave). Partials calls take them where
-    // their plan says so (narrow plan), and end with the partials.
+    // their plan says so, and end with the partials.
     const DecodePartialsPlan pp = merge ? DecodePartialsPlan{0, 0, false} : decode_partials_plan(ctx, bound);
-    const int tile_kps = merge ? tile_keys_per_split((int)ctx->num_kv_heads, a.row_bound) : (pp.narrow ? pp.keys_per_split : 0);
+    const int tile_kps = merge ? tile_keys_per_split((int)ctx->num_kv_heads, a.row_bound) : (pp.tile ? pp.keys_per_split : 0);
     if (tile_kps > 0 && decode_lds_offsets_fit(a) && kernel_knob(EFM_KNOB_DECODE_TILE) == 0) {
         a.keys_per_split = tile_kps;
         a.split_cap = (a.row_bound + tile_kps - 1) / tile_kps;

@@ -14,19 +14,26 @@ namespace efm {
 
 constexpr int kWave = 64;
 // Split-KV decode partials that the o_proj GEMV's merge prologue holds (one register
-// slot per split): caches of up to 8 x 128 rows.
-constexpr int kMergeMaxSplits = 8;
-// The narrow merge prologue (query widths up to 1024): one register slot per split for up
-// to 24 splits, e.g. a 1.5k-row cache in 64-row splits.
+// slot per split and input float4): query widths up to 2048 (two float4 per thread) with
+// up to 12 splits (a variant with 8 slots takes up to 8: fewer instructions ahead of the
+// weight stream), or up to 1024 (one float4) with up to 24.
+constexpr int kMergeMaxSplits = 12;
+constexpr int kMergeShortSplits = 8;
+constexpr int kMergeMaxWidth = 2048;
 constexpr int kMergeNarrowMaxSplits = 24;
 constexpr int kMergeNarrowMaxWidth = 1024;
 
+// Splits the o_proj merge prologue takes for a query width (0: none).
+__host__ __device__ constexpr int merge_max_splits(int64_t q_width) {
+    return q_width <= kMergeNarrowMaxWidth ? kMergeNarrowMaxSplits : (q_width <= kMergeMaxWidth ? kMergeMaxSplits : 0);
+}
+
 // Split plan of the decode partials (efm_decode_attention_partials) that every consumer of
 // them reads back: keys per split, splits, and whether the one-wave tile kernel writes
-// them (narrow: merged by the narrow o_proj prologue).
+// them (else the 4- / 8-wave kernels).
 struct DecodePartialsPlan {
     int keys_per_split, split_cap;
-    bool narrow;
+    bool tile;
 };
 
 typedef uint16_t bf16_t;

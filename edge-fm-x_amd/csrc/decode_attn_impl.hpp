@@ -143,7 +143,7 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
     constexpr int TILE = RK * attn_pipe::kRow;                 // bytes of K (or V) per round
     constexpr int LPW = 2 * TILE / 1024 / kAttnWaves;          // 1 KB wave loads per wave per round
     static_assert(G <= 32, "group too large");
-    static_assert((kAttnWaves * G * HD + 2 * kAttnWaves * 32 + kAttnWaves * G + 2 * G) * 4 <= 2 * TILE,
+    static_assert((kAttnWaves * G * (HD + 8) + 2 * kAttnWaves * 32) * 4 <= 2 * TILE,
                   "merge buffers must fit the tiles");
     __shared__ __align__(1024) unsigned char smem[2 * TILE];   // K | V of one round; then the wave merge
     __shared__ float2 cs_qk[2][HALF];
@@ -424,15 +424,17 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
             }
     }
 
-    // ---- merge the 4 waves through LDS (the tile buffers are free now): per head the
-    //      running max M, the wave weights sc_w = exp2(m_w - M) and den = sum sc_w l_w are
-    //      computed once, then every output is the fixed-order sum of sc_w o_w
+    // ---- merge the 4 waves through LDS (the tile buffers are free now): every output is
+    //      the fixed-order sum of sc_w o_w with the wave weights sc_w = exp2(m_w - M) of
+    //      its head (M the running max over the waves) and den = sum sc_w l_w. A wave's 64
+    //      outputs of one pass all belong to one head, so each wave derives that head's
+    //      weights itself from the (m, l) words (no second barrier). Rows of o_w are padded
+    //      to HD + 8 floats: the 16-byte writes of lanes (ql, hh) then fall in distinct banks.
+    constexpr int OBS = HD + 8;
     __syncthreads();
     float* om = reinterpret_cast<float*>(smem);                  // [4][32]
     float* ol = om + kAttnWaves * 32;                            // [4][32]
-    float* ob = ol + kAttnWaves * 32;                            // [4][G][HD]
-    float* sw = ob + kAttnWaves * G * HD;                        // [4][G]
-    float* md = sw + kAttnWaves * G;                             // [G][2]: M, den
+    float* ob = ol + kAttnWaves * 32;                            // [4][G][OBS]
     if (hh == 0) {
         om[wave * 32 + ql] = m_run;
         ol[wave * 32 + ql] = l_run;
@@ -442,44 +444,38 @@ __device__ __forceinline__ void decode_attn_lds_body(const DecodeArgs& a, int b,
         for (int tt = 0; tt < DT; ++tt)
 #pragma unroll
             for (int eb = 0; eb < 4; ++eb)
-                *reinterpret_cast<float4*>(&ob[(wave * G + ql) * HD + tt * 32 + eb * 8 + hh * 4]) =
+                *reinterpret_cast<float4*>(&ob[(wave * G + ql) * OBS + tt * 32 + eb * 8 + hh * 4]) =
                     make_float4(oacc[tt][eb * 4 + 0], oacc[tt][eb * 4 + 1], oacc[tt][eb * 4 + 2], oacc[tt][eb * 4 + 3]);
-    }
-    __syncthreads();
-    if (tid < G) {
-        const int g = tid;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, om[w * 32 + g]);
-        float den = 0.f;
-#pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) {
-            const float mw = om[w * 32 + g];
-            const float sc = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-            sw[w * G + g] = sc;
-            den = fmaf(sc, ol[w * 32 + g], den);
-        }
-        md[g * 2 + 0] = M;
-        md[g * 2 + 1] = den;
     }
     __syncthreads();
     float* o_part = a.o_part + ((size_t)kvh * a.split_cap + b) * G * HD;
     float* ml_part = a.ml_part + ((size_t)kvh * a.split_cap + b) * G * 2;
     constexpr int NO = (G * HD + kAttnThreads - 1) / kAttnThreads;
+    static_assert(HD % kWave == 0 && kAttnWaves == 4, "a wave's outputs of one pass share a head; quads hold the waves");
 #pragma unroll
     for (int k = 0; k < NO; ++k) {
         const int i = tid + k * kAttnThreads;
         if (i >= G * HD) break;
         const int g = i / HD, d = i % HD;
-        float num = 0.f;
+        // lane w of every quad takes wave w's (m, l): one exp for the four weights, the
+        // max over the quad through DPP, the weights handed to the wave by readlane
+        const int wl = lane & (kAttnWaves - 1);
+        const float mw = om[wl * 32 + g], lw = ol[wl * 32 + g];
+        float M = fmaxf(mw, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mw), 0xB1, 0xf, 0xf, false)));
+        M = fmaxf(M, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(M), 0x4E, 0xf, 0xf, false)));
+        const float scl = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+        float num = 0.f, den = 0.f;
 #pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) num = fmaf(sw[w * G + g], ob[(w * G + g) * HD + d], num);
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scl), w));
+            den = fmaf(sc, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lw), w)), den);
+            num = fmaf(sc, ob[(w * G + g) * OBS + d], num);
+        }
         if (MERGE) {
-            const float den = md[g * 2 + 1];
             a.o[(size_t)(kvh * G + g) * HD + d] = (bf16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
         } else {
             o_part[i] = num;
-            if (d == 0) *reinterpret_cast<float2*>(&ml_part[g * 2]) = make_float2(md[g * 2 + 0], md[g * 2 + 1]);
+            if (d == 0) *reinterpret_cast<float2*>(&ml_part[g * 2]) = make_float2(M, den);
         }
     }
     // FUSED: counted in only now (the returning atomic stays off the critical path); every

@@ -26,6 +26,7 @@ int decode_split_cap(int num_kv_heads, uint32_t max_kv_len);
 int decode_keys_per_split(int num_kv_heads, uint32_t max_kv_len);
 size_t decode_workspace_bytes(const efm_attention_ctx* ctx, uint32_t max_kv_len);
 size_t decode_ml_offset(const efm_attention_ctx* ctx, uint32_t max_kv_len);
+DecodePartialsPlan decode_partials_plan(const efm_attention_ctx* c, uint32_t max_kv_len);
 int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
 
 constexpr int kFusedMaxAttn = 128;       // attention workgroups (a quarter of the slots)
@@ -83,6 +84,10 @@ static int fused_supported(const efm_attention_ctx* ctx, int32_t hidden, uint32_
         return set_error(EFM_ERR_UNSUPPORTED, "decode_norm_qkv_attention: K / V caches past 2 GB per layer");
     const int kps = decode_keys_per_split(Hkv, max_kv_len);
     const int n_attn = Hkv * decode_split_cap(Hkv, max_kv_len);
+    // the partials this launch writes are the plan efm_decode_attention_merge_o_proj reads
+    if (decode_partials_plan(ctx, max_kv_len).tile)
+        return set_error(EFM_ERR_UNSUPPORTED,
+                         "decode_norm_qkv_attention: this cache length takes one-wave splits in the partials plan");
     if (kps != kAttnWaves * kTileKeys || n_attn > kFusedMaxAttn)
         return set_error(EFM_ERR_UNSUPPORTED,
                          "decode_norm_qkv_attention: %d attention workgroups of %d keys (needs <= %d of %d)", n_attn,

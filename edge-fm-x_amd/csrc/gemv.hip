@@ -253,19 +253,19 @@ size_t decode_ml_offset(const efm_attention_ctx* ctx, uint32_t max_kv_len);
 DecodePartialsPlan decode_partials_plan(const efm_attention_ctx* c, uint32_t max_kv_len);
 int validate_attention_ctx(const efm_attention_ctx* c, const char* who);
 
-// The partials plan's splits fit one of the merge prologues: the narrow one (its plan's
-// own shapes) or the wide one (up to kMergeMaxSplits splits, kMergeMaxHeads heads).
+// The partials plan's splits fit the merge prologue of this query width: up to 24 splits
+// for widths up to 1024, 12 up to 2048.
 static int merge_o_proj_supported(const efm_attention_ctx* ctx, uint32_t max_kv_len, DecodePartialsPlan* plan) {
     int rc = validate_attention_ctx(ctx, "attention_merge_o_proj");
     if (rc) return rc;
     if (max_kv_len == 0) return set_error(EFM_ERR_INVALID_ARGUMENT, "attention_merge_o_proj: max_kv_len is 0");
     const DecodePartialsPlan p = decode_partials_plan(ctx, max_kv_len);
     if (plan != nullptr) *plan = p;
-    if (p.narrow) return EFM_OK;
-    if (p.split_cap > kMergeMaxSplits || (int)ctx->num_qo_heads > kMergeMaxHeads ||
-        (int64_t)ctx->num_qo_heads * ctx->head_dim > 2 * 4 * kGemvThreads)
-        return set_error(EFM_ERR_UNSUPPORTED, "attention_merge_o_proj: %d splits / %u heads exceed the fused merge",
-                         p.split_cap, ctx->num_qo_heads);
+    const int64_t width = (int64_t)ctx->num_qo_heads * ctx->head_dim;
+    if (p.split_cap > merge_max_splits(width))
+        return set_error(EFM_ERR_UNSUPPORTED,
+                         "attention_merge_o_proj: %d splits of a %lld-wide query exceed the fused merge (%d)",
+                         p.split_cap, (long long)width, merge_max_splits(width));
     return EFM_OK;
 }
 }  // namespace efm
@@ -301,8 +301,9 @@ extern "C" int efm_decode_attention_merge_o_proj(const efm_attention_ctx* ctx, c
     // every workgroup repeats the split merge: two rows per wave group (gemv_pick's choice
     // with one wave per row) halve the workgroups and the repeats
     const GemvCfg g = gemv_pick(q_dim, hidden, 1, 1024, false);
-    if (plan.narrow) return gemv_launch<PRO_ATTN_MERGE_N, EPI_BF16>(g, a, stream);
-    return gemv_launch<PRO_ATTN_MERGE, EPI_BF16>(g, a, stream);
+    if (q_dim <= kMergeNarrowMaxWidth) return gemv_launch<PRO_ATTN_MERGE_N, EPI_BF16>(g, a, stream);
+    if (plan.split_cap <= kMergeShortSplits) return gemv_launch<PRO_ATTN_MERGE, EPI_BF16>(g, a, stream);
+    return gemv_launch<PRO_ATTN_MERGE_W, EPI_BF16>(g, a, stream);
 }
 
 extern "C" int efm_decode_norm_lm_head_top1(int32_t hidden, int64_t vocab, float eps, const void* h,

@@ -28,7 +28,7 @@
 
 namespace efm {
 
-enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ADD_NORM = 2, PRO_ATTN_MERGE = 3, PRO_ATTN_MERGE_N = 4 };
+enum { PRO_PLAIN = 0, PRO_NORM = 1, PRO_ADD_NORM = 2, PRO_ATTN_MERGE = 3, PRO_ATTN_MERGE_N = 4, PRO_ATTN_MERGE_W = 5 };
 enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_TOP1 = 4, EPI_QKV_TAG = 5, EPI_QKV_ROPE = 6 };
 
 // Weight-stream load of the GEMV main loop: a non-temporal 16-byte buffer load (weights
@@ -85,27 +85,27 @@ struct GemvArgs {
 };
 
 
-constexpr int kMergeMaxHeads = 64;
-
 constexpr int kPlainPre = 4;   // PLAIN input chunks per thread loaded ahead of the weights
 constexpr int kNormPre = 2;    // NORM / ADD_NORM chunks per thread loaded ahead (K <= 4096)
 
-// Attention-merge prologues: ATTN_MERGE takes up to kMergeMaxSplits splits of inputs up
-// to 2048 wide (two float4 of every split per thread), ATTN_MERGE_N up to
-// kMergeNarrowMaxSplits splits of inputs up to 1024 wide (one float4 per split: the same
-// registers hold three times the splits).
-constexpr bool pro_merge(int PRO) { return PRO == PRO_ATTN_MERGE || PRO == PRO_ATTN_MERGE_N; }
+// Attention-merge prologues: ATTN_MERGE takes up to kMergeShortSplits splits of inputs up
+// to 2048 wide (two float4 of every split per thread), ATTN_MERGE_W up to kMergeMaxSplits
+// of them, ATTN_MERGE_N up to kMergeNarrowMaxSplits splits of inputs up to 1024 wide (one
+// float4 per split: the same registers hold twice the splits).
+constexpr bool pro_merge(int PRO) { return PRO == PRO_ATTN_MERGE || PRO == PRO_ATTN_MERGE_N || PRO == PRO_ATTN_MERGE_W; }
 template <int PRO>
 struct MergeShape {
-    static constexpr int MS = (PRO == PRO_ATTN_MERGE_N) ? kMergeNarrowMaxSplits : (PRO == PRO_ATTN_MERGE ? kMergeMaxSplits : 1);
-    static constexpr int NQ = (PRO == PRO_ATTN_MERGE) ? 2 : 1;   // float4 of the input per thread
+    static constexpr int MS = (PRO == PRO_ATTN_MERGE_N) ? kMergeNarrowMaxSplits
+                            : (PRO == PRO_ATTN_MERGE_W ? kMergeMaxSplits : (PRO == PRO_ATTN_MERGE ? kMergeShortSplits : 1));
+    static constexpr int NQ = (PRO == PRO_ATTN_MERGE || PRO == PRO_ATTN_MERGE_W) ? 2 : 1;   // float4 of the input per thread
     // (m, l) loads per wave and input slice: lanes cover (head, split) pairs, 64 / heads
     // per slice splits per load (at least 16: head_dim 64 puts 4 heads in a wave's slice)
     static constexpr int ML = (MS + 15) / 16;
 };
-static_assert(MergeShape<PRO_ATTN_MERGE_N>::NQ * 4 * kGemvThreads == kMergeNarrowMaxWidth,
-              "narrow merge width");
-static_assert(MergeShape<PRO_ATTN_MERGE>::MS % 4 == 0 && MergeShape<PRO_ATTN_MERGE_N>::MS % 4 == 0,
+static_assert(MergeShape<PRO_ATTN_MERGE_N>::NQ * 4 * kGemvThreads == kMergeNarrowMaxWidth &&
+              MergeShape<PRO_ATTN_MERGE>::NQ * 4 * kGemvThreads == kMergeMaxWidth, "merge widths");
+static_assert(MergeShape<PRO_ATTN_MERGE>::MS % 4 == 0 && MergeShape<PRO_ATTN_MERGE_N>::MS % 4 == 0 &&
+              MergeShape<PRO_ATTN_MERGE_W>::MS % 4 == 0,
               "merge weights are read four splits at a time");
 
 // The prologue's own loads (input vector, residual, norm weight), issued before the first
@@ -168,10 +168,10 @@ __device__ __forceinline__ float lane_group_sum(float v, bool wide) {
 template <int PRO>
 __device__ __forceinline__ void gemv_prologue_load(const GemvArgs& a, ProLoads<PRO>& p) {
     if constexpr (pro_merge(PRO)) {
-        // Every split slot of this thread's elements: the head offset is computed once,
-        // slot j adds j splits (one add per load). Slots at or past split_cap read entries
-        // of the next KV head (or zeros past the last): the merge never uses them, since
-        // the live split count is at most split_cap. The split statistics come once per
+        // The split slots of this thread's elements: the head offset is computed once, slot
+        // j adds j splits (one add per load); the merge never uses the slots past
+        // split_cap, since the live split count is at most split_cap. The split
+        // statistics come once per
         // wave: the slice's hpw = 256 / head_dim heads take 64 / hpw lanes each, lane l
         // holding (head l / (64 / hpw), split l % (64 / hpw) + i * 64 / hpw). Threads past
         // the elements and shapes outside merge_fast read zeros.
@@ -211,13 +211,28 @@ __device__ __forceinline__ void gemv_prologue_load(const GemvArgs& a, ProLoads<P
                 const f32x2_t m = __builtin_amdgcn_raw_buffer_load_b64(rml, off, 0, 0);
                 p.ml[q][i] = make_float2(m[0], m[1]);
             }
+        // With more than kMergeShortSplits slots, groups of four slots wholly past
+        // split_cap issue no load (one uniform branch per group: a load costs the address
+        // unit the same whether its data is used or not); the 8-slot variant loads every
+        // slot (its few dead loads cost less than the branches). Slots past split_cap that
+        // do load read entries of the next KV head, or zeros past the last.
 #pragma unroll
-        for (int j = 0; j < MS; ++j)
+        for (int j0 = 0; j0 < MS; j0 += 4) {
+            if (MS <= kMergeShortSplits || j0 < cap) {
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-                const f32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rop, vop[q] + j * op_split, 0, 0);
-                p.op[q][j] = make_float4(v[0], v[1], v[2], v[3]);
+                for (int j = j0; j < j0 + 4; ++j)
+#pragma unroll
+                    for (int q = 0; q < NQ; ++q) {
+                        const f32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rop, vop[q] + j * op_split, 0, 0);
+                        p.op[q][j] = make_float4(v[0], v[1], v[2], v[3]);
+                    }
+            } else {
+#pragma unroll
+                for (int j = j0; j < j0 + 4; ++j)
+#pragma unroll
+                    for (int q = 0; q < NQ; ++q) p.op[q][j] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
+        }
     }
     if constexpr (!pro_merge(PRO)) {
         const int nbytes = a.K * 2;
@@ -327,10 +342,13 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, const ProLoads<
     }
     if constexpr (pro_merge(PRO)) {
     constexpr int MS = MergeShape<PRO>::MS, NQ = MergeShape<PRO>::NQ;
-    if (merge_fast<PRO>(a)) {
-        // Same merge as below with every load issued up front, ahead of the weight stream
-        // (gemv_prologue_load): one memory round trip, under the weights' instead of after
-        // them. Each wave merges its own input slice: the lanes holding a head's split
+    {
+        // x[h*hd + d] = bf16( sum_s w[h][s] * o_part[kvh][s][g][d] ), w[h][s] = exp2(m_s - M)
+        // / sum_s exp2(m_s - M) l_s (log-sum-exp merge of the splits), with every load
+        // issued up front, ahead of the weight stream (gemv_prologue_load): one memory
+        // round trip, under the weights' instead of after them. The host admits only shapes
+        // within merge_fast (outside it the loads read zeros and so does the projection's
+        // input). Each wave merges its own input slice: the lanes holding a head's split
         // statistics reduce its max and denominator across lanes, write the head's split
         // weights to the wave's own LDS rows, and every lane applies its head's weights to
         // its partial outputs. Slots past the live split count take no part.
@@ -401,55 +419,6 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, const ProLoads<
                 pk.y = pack_bf16x2(acc[2], acc[3]);
                 reinterpret_cast<uint2*>(xs)[c] = pk;
             }
-        }
-        return;
-    }
-    if constexpr (PRO == PRO_ATTN_MERGE) {
-        // x[h*hd + d] = bf16( sum_s w[h][s] * o_part[kvh][s][g][d] ),
-        // w[h][s] = exp2(m_s - M) / sum_s exp2(m_s - M) l_s  (log-sum-exp merge of the splits)
-        __shared__ float sw[kMergeMaxHeads * kMergeMaxSplits];
-        const uint32_t L = min(a.attn_len[0], a.attn_max_len);
-        const int kps = a.keys_per_split;
-        const int nsplit = (L == 0) ? 1 : (int)((L + kps - 1) / kps);
-        const int hd = a.head_dim, G = a.group;
-        const int Hq = a.K / hd;
-        for (int i = threadIdx.x; i < Hq * nsplit; i += kGemvThreads) {
-            const int h = i / nsplit, sidx = i % nsplit;
-            const size_t idx = ((size_t)(h / G) * a.split_cap + sidx) * G + (h % G);
-            sw[i] = a.ml_part[idx * 2];
-        }
-        __syncthreads();
-        if (threadIdx.x < Hq) {
-            const int h = threadIdx.x;
-            float M = -INFINITY;
-            for (int j = 0; j < nsplit; ++j) M = fmaxf(M, sw[h * nsplit + j]);
-            float den = 0.f, w[kMergeMaxSplits];
-            for (int j = 0; j < nsplit; ++j) {
-                const size_t idx = ((size_t)(h / G) * a.split_cap + j) * G + (h % G);
-                const float m = sw[h * nsplit + j];
-                w[j] = (m == -INFINITY) ? 0.f : exp2f(m - M);
-                den = fmaf(w[j], a.ml_part[idx * 2 + 1], den);
-            }
-            const float inv = (den > 0.f) ? 1.f / den : 0.f;
-            for (int j = 0; j < nsplit; ++j) sw[h * nsplit + j] = w[j] * inv;
-        }
-        __syncthreads();
-        for (int c = threadIdx.x; c < (a.K >> 2); c += kGemvThreads) {
-            const int n0 = c * 4, h = n0 / hd, d0 = n0 % hd;
-            const float* op = a.o_part + ((size_t)(h / G) * a.split_cap * G + (h % G)) * hd + d0;
-            float acc[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int j = 0; j < nsplit; ++j) {
-                const float4 v = *reinterpret_cast<const float4*>(op + (size_t)j * G * hd);
-                const float wj = sw[h * nsplit + j];
-                acc[0] = fmaf(wj, v.x, acc[0]);
-                acc[1] = fmaf(wj, v.y, acc[1]);
-                acc[2] = fmaf(wj, v.z, acc[2]);
-                acc[3] = fmaf(wj, v.w, acc[3]);
-            }
-            uint2 pk;
-            pk.x = pack_bf16x2(acc[0], acc[1]);
-            pk.y = pack_bf16x2(acc[2], acc[3]);
-            reinterpret_cast<uint2*>(xs)[c] = pk;
         }
         return;
     }

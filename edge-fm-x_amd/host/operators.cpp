@@ -272,9 +272,9 @@ public:
 //   hip_gfx950_decode_split_attention      norm + QKV, then the split attention, partials
 //       merged in the o_proj prologue
 // Both need the merge to fold into o_proj (efm_decode_attention_merge_o_proj_supported:
-// up to 8 splits of 128 keys, or for head_dim 64 and query widths up to 1024, 24 splits
-// of 32 or 64 keys); the fused launch also a text model (rotate-on-read cache), head_dim
-// 128 and efm_decode_norm_qkv_attention_supported.
+// up to 24 splits for query widths up to 1024, 12 up to 2048); the fused launch also a
+// text model (rotate-on-read cache), head_dim 128 and
+// efm_decode_norm_qkv_attention_supported (128-key splits).
 class HipDecodeSplitAttentionOp : public HipAttentionOp {
 public:
     std::string impl_id() const override { return "hip_gfx950_decode_split_attention"; }

@@ -171,9 +171,9 @@ int efm_decode_attention_partials(const efm_attention_ctx* ctx, const void* q, c
  * efm_decode_attention_partials with the same ctx, d_kv_len, max_kv_len and workspace;
  * the merged vector is rounded to bf16 before the projection, as the unfused
  * attention output would be. Supports the split plans that
- * efm_decode_attention_merge_o_proj_supported accepts: head_dim 64 with query widths up
- * to 1024 and caches up to 1536 rows (up to 24 splits of 32 or 64 keys), otherwise up to
- * 8 splits (max_kv_len <= 1024) and 64 query heads. Replaces the o_proj
+ * efm_decode_attention_merge_o_proj_supported accepts: up to 24 splits for query widths
+ * up to 1024 and up to 12 for widths up to 2048 (splits of 32 or 64 keys where those fit,
+ * else of 128: e.g. head_dim 128 caches up to 1536 rows). Replaces the o_proj
  * LinearImpl::forward (role attention_output, src/layers/linear.cu:41-58). */
 int efm_decode_attention_merge_o_proj(const efm_attention_ctx* ctx, const uint32_t* d_kv_len, uint32_t max_kv_len,
                                       const void* workspace, size_t workspace_bytes, const void* w_o, int32_t hidden,
@@ -446,9 +446,10 @@ int efm_decode_norm_qkv_rope(const efm_attention_ctx* ctx, int32_t hidden, float
  * soon as any other workgroup on the GPU ends, so the waits end. They are bounded all the
  * same (2^20 polls): a split that does not receive its inputs in time goes on with zeros
  * and flags the workspace, and efm_decode_qkv_attention_status reports EFM_ERR_DEVICE and
- * clears the flag (it synchronises the stream); launches after it compute correctly. efm_decode_norm_qkv_attention_supported tells whether a shape qualifies
- * (hidden <= 4096, at most 128 attention splits of 128 keys, contiguous cache rows);
- * otherwise call the two unfused entry points. */
+ * clears the flag (it synchronises the stream); launches after it compute correctly.
+ * efm_decode_norm_qkv_attention_supported tells whether a shape qualifies (hidden <= 4096,
+ * at most 128 attention splits of 128 keys, a cache length whose partials plan is not the
+ * one-wave one, contiguous cache rows); otherwise call the two unfused entry points. */
 size_t efm_decode_qkv_attention_sync_bytes(int32_t q_dim, int32_t kv_dim);
 int efm_decode_norm_qkv_attention_supported(const efm_attention_ctx* ctx, int32_t hidden, uint32_t max_kv_len);
 int efm_decode_norm_qkv_attention(const efm_attention_ctx* ctx, int32_t hidden, float eps, const void* h,

@@ -88,19 +88,24 @@ def test_testing_kernel_path_setter_validates():
 
 
 def test_merge_o_proj_plan_query_without_gpu():
-    """The partials plan that efm_decode_attention_merge_o_proj reads back: head_dim 64
-    with query widths up to 1024 merges up to 24 splits of 32 / 64 keys (1536 rows); other
-    shapes up to 8 splits of 128 keys (1024 rows) and 64 query heads."""
+    """The partials plan that efm_decode_attention_merge_o_proj reads back: query widths up
+    to 1024 merge up to 24 splits, widths up to 2048 up to 12 (splits of 32 / 64 keys from
+    the one-wave kernel where they fit, else of 128 keys)."""
     lib = C.load()
     sup = lib.efm_decode_attention_merge_o_proj_supported
-    assert sup(C.make_attention_ctx(14, 2, 64), 1025) == C.EFM_OK
-    assert sup(C.make_attention_ctx(16, 2, 64), 1536) == C.EFM_OK
-    assert sup(C.make_attention_ctx(14, 2, 64), 1537) == C.EFM_ERR_UNSUPPORTED
-    assert sup(C.make_attention_ctx(32, 8, 64), 1024) == C.EFM_OK          # wide prologue, 8 splits
-    assert sup(C.make_attention_ctx(32, 8, 64), 1025) == C.EFM_ERR_UNSUPPORTED
-    assert sup(C.make_attention_ctx(12, 2, 128), 1024) == C.EFM_OK
-    assert sup(C.make_attention_ctx(12, 2, 128), 1025) == C.EFM_ERR_UNSUPPORTED
+    assert sup(C.make_attention_ctx(14, 2, 64), 1025) == C.EFM_OK          # 17 splits of 64 keys
+    assert sup(C.make_attention_ctx(16, 2, 64), 1536) == C.EFM_OK          # 24 splits of 64 keys
+    assert sup(C.make_attention_ctx(14, 2, 64), 3072) == C.EFM_OK          # 24 splits of 128 keys
+    assert sup(C.make_attention_ctx(14, 2, 64), 3073) == C.EFM_ERR_UNSUPPORTED
+    assert sup(C.make_attention_ctx(32, 8, 64), 1536) == C.EFM_OK          # width 2048: 12 of 128
+    assert sup(C.make_attention_ctx(32, 8, 64), 1537) == C.EFM_ERR_UNSUPPORTED
+    assert sup(C.make_attention_ctx(12, 2, 128), 768) == C.EFM_OK          # 12 splits of 64 keys
+    assert sup(C.make_attention_ctx(12, 2, 128), 1536) == C.EFM_OK
+    assert sup(C.make_attention_ctx(12, 2, 128), 1537) == C.EFM_ERR_UNSUPPORTED
+    assert sup(C.make_attention_ctx(28, 4, 128), 64) == C.EFM_ERR_UNSUPPORTED   # width 3584
     assert sup(C.make_attention_ctx(14, 2, 64), 0) == C.EFM_ERR_INVALID_ARGUMENT
-    # the narrow plan's splits fit the workspace the size query reports
+    # the one-wave plan's splits fit the workspace the size query reports
     ctx = C.make_attention_ctx(14, 2, 64)
     assert lib.efm_attention_decode_workspace_bytes(ctx, 1536) >= 2 * 24 * 7 * 64 * 4 + 2 * 24 * 7 * 2 * 4
+    ctx = C.make_attention_ctx(12, 2, 128)
+    assert lib.efm_attention_decode_workspace_bytes(ctx, 768) >= 2 * 12 * 6 * 128 * 4 + 2 * 12 * 6 * 2 * 4

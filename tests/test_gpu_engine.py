@@ -385,11 +385,14 @@ def test_compact_vocab_generate_matches_unmapped_run(gpu):
 
 
 @pytest.mark.parametrize("table", ["generic", "fused", "split_o1_plain"])
-def test_decode_impls_switched_by_table_match_oracle(gpu, table):
+def test_decode_impls_switched_by_table_match_oracle(gpu, knob, table):
     """Operator-table records switch the decode attention impl (all layers) or one layer's
     o_proj; every variant generates the oracle's tokens (teacher-forced, near-tie rule)
-    and agrees with the default plan's run at every clear step."""
+    and agrees with the default plan's run at every clear step. The fused launch writes
+    128-key split partials, so its run keeps the partials plan off one-tile splits (which
+    a 128-row bound would otherwise take) with EFM_KNOB_DECODE_TILE."""
     import json
+    import efm_capi as C
 
     fused = "hip_gfx950_decode_fused_qkv_attention"
     recs = {"generic": [{"op_kind": "attention", "stage": "decode", "impl_id": "hip_gfx950_attention"}],
@@ -405,6 +408,7 @@ def test_decode_impls_switched_by_table_match_oracle(gpu, table):
             json.dump({"schema": "edgefm_operator_impl_table_v1", "records": recs}, f)
         runs = {}
         for name, tpath in (("default", ""), (table, path)):
+            knob(C.EFM_KNOB_DECODE_TILE, 1 if name == "fused" else 0)
             eng, keep = _engine(tmp, shape, w, max_tokens=96, max_new_tokens=24, operator_impl_table_path=tpath)
             plan = edge_fm.plan_decode(os.path.join(tmp, "engine.json"), 96)
             req = edge_fm.Request(0, prompt.tolist())
@@ -433,7 +437,9 @@ def test_front_wait_timeout_raises_device_error_then_recovers(gpu, knob, use_gra
     carries, 64 polls; every kernel still drains): generate() raises DeviceError and
     returns no tokens. With the knob back at 0 the same engine's next generate() returns
     the tokens of an engine that never failed (after the error the engine drops its
-    captured decode graphs, so the graph case captures the next call afresh)."""
+    captured decode graphs, so the graph case captures the next call afresh). The fused
+    launch writes 128-key split partials: EFM_KNOB_DECODE_TILE keeps the partials plan of
+    the short bounds on them."""
     import json
     import efm_capi as C
 
@@ -446,6 +452,7 @@ def test_front_wait_timeout_raises_device_error_then_recovers(gpu, knob, use_gra
             json.dump({"schema": "edgefm_operator_impl_table_v1",
                        "records": [{"op_kind": "attention", "stage": "decode",
                                     "impl_id": "hip_gfx950_decode_fused_qkv_attention"}]}, f)
+        knob(C.EFM_KNOB_DECODE_TILE, 1)
         cfg = dict(max_tokens=96, max_new_tokens=16, use_graph=use_graph, operator_impl_table_path=table)
         eng, keep = _engine(tmp, shape, w, **cfg)
         plan = edge_fm.plan_decode(os.path.join(tmp, "engine.json"), 96)

@@ -63,18 +63,20 @@ def test_default_plan_follows_the_shape(tmp_path):
                and l["down"] == LINEAR for l in p)
     assert [l["attention"] for l in _plan(tmp_path, TEXT64, name="b")] == [SPLIT, SPLIT]
     assert [l["attention"] for l in _plan(tmp_path, VL128, name="c")] == [SPLIT, SPLIT]
-    # more than 8 splits of 128 rows cannot merge in o_proj: generic attention, plain GEMV
-    # o_proj (splits of 160-256 rows that would keep 8 were measured slower than this)
-    p = _plan(tmp_path, TEXT128, max_kv=1024, name="d0")
+    # more than 24 splits of 128 rows (query widths up to 1024; 12 up to 2048) cannot merge
+    # in o_proj: generic attention, plain GEMV o_proj
+    p = _plan(tmp_path, TEXT128, max_kv=3072, name="d0")
     assert all(l["attention"] == SPLIT and l["partials_to_o_proj"] for l in p)
-    p = _plan(tmp_path, TEXT128, max_kv=1025, name="d1")
+    p = _plan(tmp_path, TEXT128, max_kv=3073, name="d1")
     assert all(l["attention"] == GENERIC and not l["partials_to_o_proj"] for l in p)
     p = _plan(tmp_path, TEXT128, max_kv=4096, name="d")
     assert all(l["attention"] == GENERIC and not l["partials_to_o_proj"] for l in p)
-    # a record selects the one-launch impl; the engine config can forbid it
+    # a record selects the one-launch impl where the partials plan has 128-key splits (past
+    # 12 one-tile splits at head_dim 128); the engine config can forbid it
     fused = [_record(op_kind="attention", stage="decode", impl_id=FUSED)]
-    assert [l["attention"] for l in _plan(tmp_path, TEXT128, fused, name="e")] == [FUSED, FUSED]
-    p = _plan(tmp_path, TEXT128, fused, name="e2", decode_fused_qkv_attention=False)
+    assert [l["attention"] for l in _plan(tmp_path, TEXT128, fused, max_kv=448, name="e")] == [FUSED, FUSED]
+    assert [l["attention"] for l in _plan(tmp_path, TEXT128, fused, max_kv=384, name="e1")] == [SPLIT, SPLIT]
+    p = _plan(tmp_path, TEXT128, fused, max_kv=448, name="e2", decode_fused_qkv_attention=False)
     assert [l["attention"] for l in p] == [SPLIT, SPLIT]
     # head_dim 64 and M-RoPE (rotation before the cache write) cannot run it: registry default
     assert [l["attention"] for l in _plan(tmp_path, TEXT64, fused, name="e3")] == [SPLIT, SPLIT]
@@ -121,7 +123,7 @@ def test_per_layer_linear_records(tmp_path):
     # the fused launch needs its partials merged in o_proj
     fused = _record(op_kind="attention", stage="decode", impl_id=FUSED)
     with pytest.raises(edge_fm.ConfigurationError, match="cannot merge"):
-        _plan(tmp_path, TEXT128, [fused, o1], name="l")
+        _plan(tmp_path, TEXT128, [fused, o1], max_kv=448, name="l")
     # shape_sig of the m = 1 down projection selects the same impl explicitly
     down = _record(op_kind="linear", layer_role="mlp_down", stage="decode",
                    shape_sig="m=1|input=2|weight=2|output=2|in_features=512|out_features=256", impl_id=LINEAR)
