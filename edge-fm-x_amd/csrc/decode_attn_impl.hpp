@@ -511,7 +511,7 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
     constexpr int HD = 128, HALF = 64, KS = 8, DT = 4, W = kWideWaves, NT = kWideThreads;
     constexpr int KB = kTileKeys * attn_pipe::kRow;            // bytes of K (or V) of a tile
     constexpr int LPT = 2 * KB / 1024;                         // 1 KB wave loads per tile
-    static_assert((W * G * HD + 2 * W * 32 + W * G + 2 * G) * 4 <= kWideMaxTiles * kWideTileBytes,
+    static_assert((W * G * (HD + 8) + 2 * W * 32) * 4 <= kWideMaxTiles * kWideTileBytes,
                   "merge buffers must fit the tiles");
     __shared__ __align__(1024) unsigned char smem[kWideMaxTiles * kWideTileBytes];   // tiles; then the merge
     __shared__ float2 cs_qk[2][HALF];
@@ -822,13 +822,16 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
             }
     }
 
-    // ---- merge the 8 waves through LDS (every tile load has landed: the waits above)
+    // ---- merge the 8 waves through LDS (every tile load has landed: the waits above), as
+    //      the 4-wave kernel's merge: rows of o_w padded to HD + 8 floats (distinct banks for
+    //      the lanes' 16-byte writes), each wave deriving its head's wave weights itself
+    //      (lane w of every octet takes wave w's (m, l): one exp, a DPP max over the octet,
+    //      the weights handed to the wave by readlane), the fixed-order sum of sc_w o_w
+    constexpr int OBS = HD + 8;
     __syncthreads();
     float* om = reinterpret_cast<float*>(smem);                  // [W][32]
     float* ol = om + W * 32;                                     // [W][32]
-    float* ob = ol + W * 32;                                     // [W][G][HD]
-    float* sw = ob + W * G * HD;                                 // [W][G]
-    float* md = sw + W * G;                                      // [G][2]: M, den
+    float* ob = ol + W * 32;                                     // [W][G][OBS]
     if (hh == 0) {
         om[wave * 32 + ql] = m_run;
         ol[wave * 32 + ql] = l_run;
@@ -838,44 +841,37 @@ __device__ __forceinline__ void decode_attn_wide_body(const DecodeArgs& a, int b
         for (int tt = 0; tt < DT; ++tt)
 #pragma unroll
             for (int eb = 0; eb < 4; ++eb)
-                *reinterpret_cast<float4*>(&ob[(wave * G + ql) * HD + tt * 32 + eb * 8 + hh * 4]) =
+                *reinterpret_cast<float4*>(&ob[(wave * G + ql) * OBS + tt * 32 + eb * 8 + hh * 4]) =
                     make_float4(oacc[tt][eb * 4 + 0], oacc[tt][eb * 4 + 1], oacc[tt][eb * 4 + 2], oacc[tt][eb * 4 + 3]);
-    }
-    __syncthreads();
-    if (tid < G) {
-        const int g = tid;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < W; ++w) M = fmaxf(M, om[w * 32 + g]);
-        float den = 0.f;
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-            const float mw = om[w * 32 + g];
-            const float sc = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-            sw[w * G + g] = sc;
-            den = fmaf(sc, ol[w * 32 + g], den);
-        }
-        md[g * 2 + 0] = M;
-        md[g * 2 + 1] = den;
     }
     __syncthreads();
     float* o_part = a.o_part + ((size_t)kvh * a.split_cap + b) * G * HD;
     float* ml_part = a.ml_part + ((size_t)kvh * a.split_cap + b) * G * 2;
     constexpr int NO = (G * HD + NT - 1) / NT;
+    static_assert(HD % kWave == 0 && W == 8, "a wave's outputs of one pass share a head; octets hold the waves");
 #pragma unroll
     for (int k = 0; k < NO; ++k) {
         const int i = tid + k * NT;
         if (i >= G * HD) break;
         const int g = i / HD, d = i % HD;
-        float num = 0.f;
+        const int wl = lane & (W - 1);
+        const float mw = om[wl * 32 + g], lw = ol[wl * 32 + g];
+        float M = fmaxf(mw, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mw), 0xB1, 0xf, 0xf, false)));
+        M = fmaxf(M, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(M), 0x4E, 0xf, 0xf, false)));
+        M = fmaxf(M, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(M), 0x141, 0xf, 0xf, false)));
+        const float scl = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+        float num = 0.f, den = 0.f;
 #pragma unroll
-        for (int w = 0; w < W; ++w) num = fmaf(sw[w * G + g], ob[(w * G + g) * HD + d], num);
+        for (int w = 0; w < W; ++w) {
+            const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scl), w));
+            den = fmaf(sc, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lw), w)), den);
+            num = fmaf(sc, ob[(w * G + g) * OBS + d], num);
+        }
         if (MERGE) {
-            const float den = md[g * 2 + 1];
             a.o[(size_t)(kvh * G + g) * HD + d] = (bf16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
         } else {
             o_part[i] = num;
-            if (d == 0) *reinterpret_cast<float2*>(&ml_part[g * 2]) = make_float2(md[g * 2 + 0], md[g * 2 + 1]);
+            if (d == 0) *reinterpret_cast<float2*>(&ml_part[g * 2]) = make_float2(M, den);
         }
     }
 }
