@@ -1277,6 +1277,52 @@ def test_decode_attention_partials_merge_o_proj_narrow(gpu, hq, hkv, hidden, max
     assert_close_bf16(outs[0], ref_gpu, rtol=2e-2, atol=2e-2, what=what + " vs attention_decode + linear")
 
 
+@pytest.mark.parametrize("hq,hkv,hidden", [pytest.param(12, 2, 1536, id="1p5b"), pytest.param(16, 2, 2048, id="vl3b"),
+                                            pytest.param(16, 4, 2048, id="g4")])
+@pytest.mark.parametrize("max_kv,kv_len", [(96, 96), (256, 1), (384, 200), (1025, 1025), (1280, 700), (1536, 1536),
+                                           (1536, 1)])
+def test_decode_attention_partials_merge_o_proj_head_dim_128_plans(gpu, hq, hkv, hidden, max_kv, kv_len):
+    """head_dim 128 beyond the 8-split merge: one-tile (32-key) partials up to 12 splits at
+    short caches, and 9-12 splits of 128 keys (the 12-slot prologue) at 1025-1536 rows, ==
+    the oracle's attention then o_proj, and == efm_attention_decode + efm_linear to rounding.
+    Rows past the length hold Inf / NaN; two calls in a row agree bit for bit."""
+    hd = 128
+    torch.manual_seed(4)
+    q = torch.randn(1, hq, hd, dtype=torch.bfloat16)
+    k = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16)
+    v = torch.randn(max_kv, hkv, hd, dtype=torch.bfloat16)
+    wo = (torch.randn(hidden, hq * hd) * 0.02).to(torch.bfloat16)
+    ctx = C.make_attention_ctx(hq, hkv, hd, rope=False)
+    lib = C.load()
+    assert lib.efm_decode_attention_merge_o_proj_supported(ctx, max_kv) == C.EFM_OK
+    qg, kg, vg, wg = q.to(gpu), k.to(gpu), v.to(gpu), wo.to(gpu)
+    kg[kv_len:] = float("inf")
+    vg[kv_len:] = float("nan")
+    d_len = torch.tensor([kv_len], dtype=torch.int32, device=gpu)
+    ws = torch.zeros(lib.efm_attention_decode_workspace_bytes(ctx, max_kv), dtype=torch.uint8, device=gpu)
+    outs = []
+    for _ in range(2):
+        out = torch.empty(1, hidden, dtype=torch.bfloat16, device=gpu)
+        C.call("efm_decode_attention_partials", ctx, ptr(qg), ptr(kg), ptr(vg), ptr(d_len), max_kv, ptr(ws),
+               ws.numel(), stream())
+        C.call("efm_decode_attention_merge_o_proj", ctx, ptr(d_len), max_kv, ptr(ws), ws.numel(), ptr(wg), hidden,
+               ptr(out), stream())
+        outs.append(out)
+    att = torch.empty(1, hq * hd, dtype=torch.bfloat16, device=gpu)
+    ref_gpu = torch.empty(1, hidden, dtype=torch.bfloat16, device=gpu)
+    C.call("efm_attention_decode", ctx, ptr(qg), ptr(kg), ptr(vg), ptr(att), 0, ptr(d_len), max_kv, ptr(ws),
+           ws.numel(), stream())
+    C.call("efm_linear", 1, hq * hd, hidden, ptr(att), ptr(wg), None, ptr(ref_gpu), C.EFM_DTYPE_BF16, stream())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert torch.isfinite(outs[0].float()).all()
+    ref = O.linear(O.attention_decode(q, k[:kv_len], v[:kv_len], kv_len, O.AttnCtx(hq, hkv, hd, rope=False))
+                   .reshape(1, hq * hd), wo)
+    what = f"head_dim 128 partials+merge {hq}/{hkv} max={max_kv} kv={kv_len}"
+    assert_close_bf16(outs[0], ref, rtol=2e-2, atol=2e-2, what=what)
+    assert_close_bf16(outs[0], ref_gpu, rtol=2e-2, atol=2e-2, what=what + " vs attention_decode + linear")
+
+
 def _sage_inputs(S, L, hq, hkv, hd, seed=0, gpu=None):
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(S, hq, hd, generator=g).to(torch.bfloat16)
