@@ -741,11 +741,11 @@ __global__ __launch_bounds__(kAttnThreads) void decode_merge_kernel(DecodeArgs a
             }
             M = fmaxf(M, ms[k]);
         }
-        M = wave_max(M);
+        M = wave_max_uniform(M);
         float den = 0.f;
 #pragma unroll
         for (int k = 0; k < kPerLane; ++k) den += (ms[k] == -INFINITY) ? 0.f : exp2f(ms[k] - M) * ls[k];
-        den = wave_sum(den);
+        den = wave_total(den);
         const float inv = (den > 0.f) ? 1.f / den : 0.f;
 #pragma unroll
         for (int k = 0; k < kPerLane; ++k) {

@@ -136,6 +136,39 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// DPP move of a float across lanes (CTRL: quad_perm 0x00-0xff, row_mirror 0x140,
+// row_half_mirror 0x141, ...; every source lane valid).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave, returned uniform: four 16-lane DPP steps (xor 1, xor 2,
+// half-row mirror, row mirror), then row broadcasts (lane 15 into rows 1 and 3, lane 31
+// into rows 2 and 3) leave the total in lane 63, which is read out. No LDS-crossbar round
+// trips: every decode GEMV reduces its dot products with this.
+__device__ __forceinline__ float wave_total(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));   // row_bcast:15
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));   // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// Max over the 64 lanes of a wave, returned uniform (as wave_total; rows outside a
+// broadcast's row mask keep -inf).
+__device__ __forceinline__ float wave_max_uniform(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    const int ninf = __float_as_int(-INFINITY);
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x142, 0xA, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x143, 0xC, 0xF, false)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {

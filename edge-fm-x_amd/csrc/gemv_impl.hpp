@@ -130,10 +130,6 @@ __device__ __forceinline__ bool merge_fast(const GemvArgs& a) {
 // Max / sum over each aligned group of 16 lanes (or 32 with wide), the result in every lane
 // of the group: four DPP steps within a row (xor 1, xor 2, half-row mirror, row mirror),
 // plus one swizzle (xor 16) across the row pair for 32 lanes. No LDS round trips.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
 __device__ __forceinline__ float lane_group_max(float v, bool wide) {
     v = fmaxf(v, dpp_f32<0xB1>(v));    // quad_perm [1,0,3,2]
     v = fmaxf(v, dpp_f32<0x4E>(v));    // quad_perm [2,3,0,1]
@@ -142,17 +138,16 @@ __device__ __forceinline__ float lane_group_max(float v, bool wide) {
     if (wide) v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
     return v;
 }
-// Sum over the 64 lanes of a wave, returned uniform: the 16-lane DPP steps above, then
-// row broadcasts (lane 15 into rows 1 and 3, lane 31 into rows 2 and 3) leave the total in
-// lane 63, which is read out. Every decode GEMV reduces its dot products with this.
-__device__ __forceinline__ float wave_total(float v) {
-    v += dpp_f32<0xB1>(v);
-    v += dpp_f32<0x4E>(v);
-    v += dpp_f32<0x141>(v);
-    v += dpp_f32<0x140>(v);
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));   // row_bcast:15
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));   // row_bcast:31
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+// Sum over the GEMV's 256 threads, valid in every thread: DPP wave totals, one LDS word
+// per wave, one barrier (`red` is not read before this in the launch).
+__device__ __forceinline__ float block_total(float v, float* red) {
+    v = wave_total(v);
+    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int i = 1; i < kGemvThreads / kWave; ++i) t += red[i];
+    return t;
 }
 __device__ __forceinline__ float lane_group_sum(float v, bool wide) {
     v += dpp_f32<0xB1>(v);
@@ -317,7 +312,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, const ProLoads<
             for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
             if (store_r) reinterpret_cast<uint4*>(a.r_out)[c] = pack8(v);
         }
-        const float tot = block_sum<kGemvThreads>(ss, red);
+        const float tot = block_total(ss, red);
         const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
 #pragma unroll
         for (int i = 0; i < kNormPre; ++i) {
