@@ -169,6 +169,20 @@ __device__ __forceinline__ float wave_max_uniform(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Sum over a 1-D block of `nthreads` (multiple of 64), valid in every thread: DPP wave
+// totals, one LDS word per wave (`red`, nthreads / 64 floats, not read before in the
+// launch), one barrier.
+template <int nthreads>
+__device__ __forceinline__ float block_total(float v, float* red) {
+    v = wave_total(v);
+    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int i = 1; i < nthreads / kWave; ++i) t += red[i];
+    return t;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {

@@ -26,6 +26,14 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(const bf16_t* in, 
     uint4* r4 = FUSED ? reinterpret_cast<uint4*>(residual + row * hidden) : nullptr;
     float s[kRowMaxChunks][8];
     float ss = 0.f;
+    // the norm weight's chunks go out with the row's (not after the reduction)
+    const uint4* w4 = reinterpret_cast<const uint4*>(w);
+    uint4 wv[kRowMaxChunks];
+#pragma unroll
+    for (int i = 0; i < kRowMaxChunks; ++i) {
+        const int c = threadIdx.x + i * kRowThreads;
+        wv[i] = (c < C) ? w4[c] : make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
     for (int i = 0; i < kRowMaxChunks; ++i) {
         const int c = threadIdx.x + i * kRowThreads;
@@ -42,16 +50,15 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(const bf16_t* in, 
             for (int e = 0; e < 8; ++e) ss = fmaf(s[i][e], s[i][e], ss);
         }
     }
-    const float tot = block_sum<kRowThreads>(ss, red);
+    const float tot = block_total<kRowThreads>(ss, red);
     const float inv = 1.0f / sqrtf(tot / (float)hidden + eps);
-    const uint4* w4 = reinterpret_cast<const uint4*>(w);
     uint4* o4 = reinterpret_cast<uint4*>(out + row * hidden);
 #pragma unroll
     for (int i = 0; i < kRowMaxChunks; ++i) {
         const int c = threadIdx.x + i * kRowThreads;
         if (c < C) {
             float wf[8], o[8];
-            unpack8(w4[c], wf);
+            unpack8(wv[i], wf);
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = (s[i][e] * inv) * wf[e];
             o4[c] = pack8(o);

@@ -138,17 +138,6 @@ __device__ __forceinline__ float lane_group_max(float v, bool wide) {
     if (wide) v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
     return v;
 }
-// Sum over the GEMV's 256 threads, valid in every thread: DPP wave totals, one LDS word
-// per wave, one barrier (`red` is not read before this in the launch).
-__device__ __forceinline__ float block_total(float v, float* red) {
-    v = wave_total(v);
-    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
-    __syncthreads();
-    float t = red[0];
-#pragma unroll
-    for (int i = 1; i < kGemvThreads / kWave; ++i) t += red[i];
-    return t;
-}
 __device__ __forceinline__ float lane_group_sum(float v, bool wide) {
     v += dpp_f32<0xB1>(v);
     v += dpp_f32<0x4E>(v);
@@ -312,7 +301,7 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, const ProLoads<
             for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
             if (store_r) reinterpret_cast<uint4*>(a.r_out)[c] = pack8(v);
         }
-        const float tot = block_total(ss, red);
+        const float tot = block_total<kGemvThreads>(ss, red);
         const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
 #pragma unroll
         for (int i = 0; i < kNormPre; ++i) {
