@@ -7,9 +7,9 @@
 
 namespace efm {
 
-template <int R, int KS, int PRO, int EPI>
+template <int R, int KS, int PRO, int EPI, int NJM>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a, int nj, int nseg) {
-    gemv_body<R, KS, PRO, EPI>(a, nj, nseg, blockIdx.x, gridDim.x);
+    gemv_body<R, KS, PRO, EPI, NJM>(a, nj, nseg, blockIdx.x, gridDim.x);
 }
 
 }  // namespace efm
@@ -58,10 +58,16 @@ template <int PRO, int EPI>
 static int gemv_launch(const GemvCfg& g, const GemvArgs& a, hipStream_t stream) {
     const size_t smem = (size_t)a.K * sizeof(bf16_t);
     dim3 grid(g.grid), block(kGemvThreads);
+    // rows of at most three chunks per lane (one wave per row, K <= 1536) take 3 load slots
 #define EFM_GEMV_CASE(RR, KK)                                                                  \
     if (g.R == RR && g.KS == KK) {                                                             \
-        hipLaunchKernelGGL((gemv_kernel<RR, KK, PRO, EPI>), grid, block, smem, stream, a, g.nj, \
-                           g.nseg);                                                            \
+        if constexpr (KK == 1) {                                                               \
+            if (g.nseg == 1 && g.nj <= 3) {                                                    \
+                hipLaunchKernelGGL((gemv_kernel<RR, KK, PRO, EPI, 3>), grid, block, smem, stream, a, g.nj, g.nseg); \
+                return check_launch("gemv");                                                   \
+            }                                                                                  \
+        }                                                                                      \
+        hipLaunchKernelGGL((gemv_kernel<RR, KK, PRO, EPI, kNJMax>), grid, block, smem, stream, a, g.nj, g.nseg); \
         return check_launch("gemv");                                                           \
     }
     EFM_GEMV_CASE(1, 1) EFM_GEMV_CASE(2, 1) EFM_GEMV_CASE(4, 1)

@@ -444,7 +444,7 @@ __device__ __forceinline__ float2 qkv_rope_cs(const GemvArgs& a, int n, uint32_t
 
 // Body of the GEMV kernel for workgroup `blk` of `nblk` (grid-stride over row blocks),
 // shared by gemv_kernel and the fused QKV + attention kernel.
-template <int R, int KS, int PRO, int EPI>
+template <int R, int KS, int PRO, int EPI, int NJM = kNJMax>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, int blk, int nblk) {
     constexpr int P = (EPI == EPI_SWIGLU || EPI == EPI_QKV_ROPE) ? 2 : 1;
     constexpr int G = 4 / KS;          // row groups per block
@@ -469,7 +469,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
 
     // Weight loads of row block rb, segment seg: one buffer resource per block and part
     // (uniform across the workgroup) covering the block's rows below N.
-    uint4 wr[R][P][kNJMax];
+    // NJM: load slots per lane and row (nj <= NJM live; a launch shape whose rows need at most
+    // three chunks per lane takes NJM = 3, so no slot past the row is issued: an unused slot
+    // costs the address unit as much as a used one)
+    uint4 wr[R][P][NJM];
     const int grpu = __builtin_amdgcn_readfirstlane(grp);
     const int kwu = __builtin_amdgcn_readfirstlane(kw);
     auto issue = [&](int rb, int seg) {
@@ -485,7 +488,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
             for (int r = 0; r < R; ++r) {
                 const uint32_t roff = (uint32_t)((grpu * R + r) * a.K) * 2u;
 #pragma unroll
-                for (int j = 0; j < kNJMax; ++j) {
+                for (int j = 0; j < NJM; ++j) {
                     const int c = seg * segC + kwu * kWave + lane + j * kWave * KS;
                     const uint32_t off = (j < nj && c < C) ? roff + (uint32_t)c * 16u : kWloadSkip;
                     wr[r][p][j] = gemv_wload(rs, off);
@@ -525,7 +528,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
         for (int seg = 0; seg < nseg; ++seg) {
             if (seg > 0) issue(rb, seg);
 #pragma unroll
-            for (int j = 0; j < kNJMax; ++j) {
+            for (int j = 0; j < NJM; ++j) {
                 const int c = seg * segC + kw * kWave + lane + j * kWave * KS;
                 if (j < nj && c < C) {
                     const uint4 xv = xs4[c];
