@@ -54,20 +54,35 @@ GemvCfg gemv_pick_config(int K, int N, int P, int max_grid, bool tall, bool sing
     return gemv_pick(K, N, P, max_grid, tall, single_row);
 }
 
+// Launch with the fewest load slots per lane and row that hold a row's chunks (an unused
+// slot costs the address unit as much as a used one): 2-4 with one wave per row, 3-4 with
+// two, 3-6 with four.
+template <int RR, int KK, int PRO, int EPI>
+static void gemv_launch_slots(const GemvCfg& g, dim3 grid, dim3 block, size_t smem, const GemvArgs& a,
+                              hipStream_t stream) {
+#define EFM_GEMV_SLOTS(NJV)                                                                    \
+    if (g.nj <= NJV) {                                                                         \
+        hipLaunchKernelGGL((gemv_kernel<RR, KK, PRO, EPI, NJV>), grid, block, smem, stream, a, g.nj, g.nseg); \
+        return;                                                                                \
+    }
+    if constexpr (KK == 1) {
+        EFM_GEMV_SLOTS(2) EFM_GEMV_SLOTS(3) EFM_GEMV_SLOTS(4)
+    } else if constexpr (KK == 2) {
+        EFM_GEMV_SLOTS(3) EFM_GEMV_SLOTS(4)
+    } else {
+        EFM_GEMV_SLOTS(3) EFM_GEMV_SLOTS(4) EFM_GEMV_SLOTS(5)
+    }
+#undef EFM_GEMV_SLOTS
+    hipLaunchKernelGGL((gemv_kernel<RR, KK, PRO, EPI, kNJMax>), grid, block, smem, stream, a, g.nj, g.nseg);
+}
+
 template <int PRO, int EPI>
 static int gemv_launch(const GemvCfg& g, const GemvArgs& a, hipStream_t stream) {
     const size_t smem = (size_t)a.K * sizeof(bf16_t);
     dim3 grid(g.grid), block(kGemvThreads);
-    // rows of at most three chunks per lane (one wave per row, K <= 1536) take 3 load slots
 #define EFM_GEMV_CASE(RR, KK)                                                                  \
     if (g.R == RR && g.KS == KK) {                                                             \
-        if constexpr (KK == 1) {                                                               \
-            if (g.nseg == 1 && g.nj <= 3) {                                                    \
-                hipLaunchKernelGGL((gemv_kernel<RR, KK, PRO, EPI, 3>), grid, block, smem, stream, a, g.nj, g.nseg); \
-                return check_launch("gemv");                                                   \
-            }                                                                                  \
-        }                                                                                      \
-        hipLaunchKernelGGL((gemv_kernel<RR, KK, PRO, EPI, kNJMax>), grid, block, smem, stream, a, g.nj, g.nseg); \
+        gemv_launch_slots<RR, KK, PRO, EPI>(g, grid, block, smem, a, stream);                  \
         return check_launch("gemv");                                                           \
     }
     EFM_GEMV_CASE(1, 1) EFM_GEMV_CASE(2, 1) EFM_GEMV_CASE(4, 1)

@@ -469,9 +469,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int nj, int nseg, i
 
     // Weight loads of row block rb, segment seg: one buffer resource per block and part
     // (uniform across the workgroup) covering the block's rows below N.
-    // NJM: load slots per lane and row (nj <= NJM live; a launch shape whose rows need at most
-    // three chunks per lane takes NJM = 3, so no slot past the row is issued: an unused slot
-    // costs the address unit as much as a used one)
+    // NJM: load slots per lane and row (nj <= NJM live; launches take the fewest slots that
+    // hold their rows, so no slot past a row is issued: an unused slot costs the address
+    // unit as much as a used one)
     uint4 wr[R][P][NJM];
     const int grpu = __builtin_amdgcn_readfirstlane(grp);
     const int kwu = __builtin_amdgcn_readfirstlane(kw);
