@@ -719,21 +719,36 @@ static void gemm_wide_launch(int M, int N, int K, const bf16_t* A, const bf16_t*
                        B, bias, C, M, N, K, ldc, mt, nt);
 }
 
-// Split-K plan for a plain (non-SwiGLU) projection with K % 64 == 0: worth it when the
-// 128 x 128 tiles cannot fill half the chip's workgroup slots and K >= 4096 (measured:
-// 512 x 8960 -> 1536 goes 51 -> 32 us; at 176 tiles, 1344 x 11008 -> 2048, it gains
-// nothing); 0 = no split.
+int prefill_cus();
+
+// Split-K plan for a plain (non-SwiGLU) projection with K % 64 == 0 and K >= 4096 whose
+// 128 x 128 tiles leave the chip's workgroup slots empty; ksplit 0 = no split. Each slice
+// covers at least 16 slabs (1024 keys). Measured on MI355X (us):
+//  * tiles for at most a third of the CUs: as many slices as fill every CU once (at most
+//    8), one workgroup per CU over a 4-deep ring: 512 x 8960 -> 1536 33.6 -> 28.3 (5
+//    slices, against 8 slices over 2-deep rings, two workgroups per CU), 512 x 11008 ->
+//    2048 47.7 -> 39.1 (4 against 6), 768 x 8960 -> 1536 40.9 -> 39.7 (3 against 6);
+//  * up to 128 tiles: about 384 workgroups over 2-deep rings, two per CU (two slices over
+//    4-deep rings: 1024 x 8960 -> 1536 46.1 -> 50.9, 512 x 18944 -> 3584 101.2 -> 102.9).
 struct SplitK {
     int ksplit = 0, kt_per = 0;
+    bool deep = false;  // 4-deep ring, one workgroup per CU (else 2-deep, two per CU)
 };
 static SplitK splitk_plan(int M, int N, int K) {
     SplitK p;
     if (K % kPBK != 0 || N % 4 != 0) return p;
     const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
     const int nk = K / kPBK;
-    if (tiles >= 128 || nk < 64) return p;
-    int ks = (int)std::min<long>(8, (384 + tiles - 1) / tiles);
-    ks = std::min(ks, nk / 16);                 // at least 16 slabs (1024 keys) per slice
+    if (tiles > 128 || nk < 64) return p;
+    const int fill = (int)std::min<long>({8L, prefill_cus() / tiles, (long)(nk / 16)});
+    int ks;
+    if (fill >= 3) {
+        ks = fill;
+        p.deep = true;
+    } else {
+        ks = (int)std::min<long>(8, (384 + tiles - 1) / tiles);
+        ks = std::min(ks, nk / 16);
+    }
     if (ks < 2) return p;
     p.kt_per = (nk + ks - 1) / ks;
     p.ksplit = (nk + p.kt_per - 1) / p.kt_per;
@@ -750,8 +765,12 @@ static void gemm_splitk_launch(int M, int N, int K, const bf16_t* A, const bf16_
                                bool f32out, float* part, const SplitK& p, hipStream_t stream) {
     const int mt = (M + 127) / 128, nt = (N + 127) / 128;
     const int grid = 8 * ((mt * nt * p.ksplit + 7) / 8);
-    hipLaunchKernelGGL((gemm_pipe_kernel<128, 128, 2, GEPI_PARTIAL>), dim3(grid), dim3(kGemmThreads), 0, stream, A, B,
-                       nullptr, part, M, N, K, N, mt, nt, p.ksplit, p.kt_per);
+    if (p.deep)
+        hipLaunchKernelGGL((gemm_pipe_kernel<128, 128, 4, GEPI_PARTIAL>), dim3(grid), dim3(kGemmThreads), 0, stream, A,
+                           B, nullptr, part, M, N, K, N, mt, nt, p.ksplit, p.kt_per);
+    else
+        hipLaunchKernelGGL((gemm_pipe_kernel<128, 128, 2, GEPI_PARTIAL>), dim3(grid), dim3(kGemmThreads), 0, stream, A,
+                           B, nullptr, part, M, N, K, N, mt, nt, p.ksplit, p.kt_per);
     const size_t quads = (size_t)M * N / 4;
     const dim3 rgrid((unsigned)((quads + 255) / 256));
     if (f32out) hipLaunchKernelGGL((gemm_splitk_reduce_kernel<true>), rgrid, dim3(256), 0, stream, part, p.ksplit, M, N, bias, C);
@@ -784,17 +803,28 @@ static int gemm_dispatch(int M, int N, int K, const bf16_t* A, const bf16_t* B, 
         }
     }
     if (K % kPBK == 0) {
-        // Tile choice from a sweep of the prefill shapes on MI355X: 128 x 128 double-
+        // Tile choice from sweeps of the prefill shapes on MI355X: 128 x 128 double-
         // buffered (two workgroups per CU) once there are >= 1.5 tiles per CU (>= 1 for
-        // SwiGLU); else 128 x 64 double-buffered; else 64 x 64 (64 x 128 for SwiGLU) with
-        // shallow pipelines. Every tile shape sums each output over K in the same order:
-        // results are bit-identical whichever is chosen.
+        // SwiGLU); K >= 4096 with 129 to one-per-CU 128 x 128 tiles: those tiles over a
+        // 4-deep ring, one workgroup per CU (1344 x 11008 -> 2048 129.2 -> 106.6 us,
+        // 1024 x 18944 -> 3584 237.6 -> 182.8; at 132 tiles, 1344 x 8960 -> 1536, 80.2 ->
+        // 86.1); else 128 x 64 over a 3-deep ring (two per CU; 1024 x 1536 -> 2048 20.2 ->
+        // 18.3 against the 2-deep ring, no shape slower); else 64 x 64 (64 x 128 for
+        // SwiGLU) with shallow pipelines. Every tile shape sums each output over K in the
+        // same order: results are bit-identical whichever is chosen.
+        if constexpr (EPI != GEPI_SWIGLU) {
+            const long t = tiles(128, 128);
+            if (K / kPBK >= 64 && t > 128 && t < 384 && t <= prefill_cus()) {
+                gemm_pipe_launch<128, 128, 4, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+                return check_launch("gemm_bf16");
+            }
+        }
         if (tiles(128, 128) >= ((EPI == GEPI_SWIGLU) ? 256 : 384)) {
             gemm_pipe_launch<128, 128, 2, EPI>(M, N, K, A, B, bias, C, ldc, stream);
         } else if constexpr (EPI == GEPI_SWIGLU) {
             gemm_pipe_launch<64, 128, 3, EPI>(M, N, K, A, B, bias, C, ldc, stream);
         } else {
-            if (tiles(128, 64) >= 256) gemm_pipe_launch<128, 64, 2, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+            if (tiles(128, 64) >= 256) gemm_pipe_launch<128, 64, 3, EPI>(M, N, K, A, B, bias, C, ldc, stream);
             else gemm_pipe_launch<64, 64, 4, EPI>(M, N, K, A, B, bias, C, ldc, stream);
         }
         return check_launch("gemm_bf16");

@@ -610,6 +610,7 @@ def test_gemm_wide_kernel_matches_narrow_bit_exact(gpu, knob, m, k, n, kind):
     pytest.param(300, 18944, 3584, "bf16", id="7b_down"),
     pytest.param(300, 4096, 1000, "bias", id="ragged_bias"),
     pytest.param(200, 8192, 2048, "f32", id="f32"),
+    pytest.param(1024, 8960, 1536, "bf16", id="shallow_split"),
 ])
 def test_linear_split_k_matches_unsplit_and_oracle(gpu, m, k, n, kind):
     """efm_linear_ws splits K for these under-filled, long-K shapes: its result equals
@@ -646,6 +647,30 @@ def test_linear_split_k_matches_unsplit_and_oracle(gpu, m, k, n, kind):
         torch.testing.assert_close(outs[0][rows].cpu(), exp, rtol=1e-4, atol=1e-4)
     else:
         assert_close_bf16(outs[0][rows], exp)
+
+
+def test_gemm_long_k_tiles_agree_bit_exact(gpu):
+    """K = 11008 (the VL-3B down projection) at three M: 100 rows run 64 x 64 tiles, 1344
+    rows (176 tiles of 128 x 128, at most one per CU) 128 x 128 tiles over a 4-deep ring
+    with one workgroup per CU, 2300 rows 128 x 64 tiles over a 3-deep ring. All sum each
+    output over K in the same order: the first 100 rows agree bit for bit, and a row
+    sample of each launch matches the oracle."""
+    torch.manual_seed(29)
+    k, n = 11008, 2048
+    x = torch.randn(2300, k, dtype=torch.bfloat16, device=gpu)
+    w = (torch.randn(n, k, device=gpu) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(n, device=gpu) * 0.05).to(torch.bfloat16)
+    outs = {}
+    for m in (100, 1344, 2300):
+        y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+        C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), C.EFM_DTYPE_BF16, stream())
+        torch.cuda.synchronize()
+        assert not torch.isnan(y).any(), f"M={m}: outputs left unwritten"
+        outs[m] = y
+    for m in (1344, 2300):
+        assert torch.equal(outs[m][:100], outs[100]), f"rows of the M={m} launch differ from the M=100 launch"
+        rows = torch.tensor([0, m // 2, m - 1])
+        assert_close_bf16(outs[m][rows], O.linear(x[rows].cpu(), w.cpu(), b.cpu()))
 
 
 def test_linear_workspace_bytes_zero_without_split(gpu):
