@@ -55,7 +55,7 @@ extern "C" int efm_testing_set_kernel_path(int32_t knob, int32_t value) {
     if (knob < 0 || knob >= EFM_KNOB_COUNT)
         return set_error(EFM_ERR_INVALID_ARGUMENT, "testing_set_kernel_path: unknown knob %d", knob);
     const bool ok = (knob == EFM_KNOB_PREFILL_SHAPE) ? (value == 0 || value == 2 || value == 4 || value == 8)
-                    : (knob == EFM_KNOB_GEMM_TILE)   ? (value >= 0 && value <= 2)
+                    : (knob == EFM_KNOB_GEMM_TILE)   ? (value >= 0 && value <= 3)
                                                      : (value == 0 || value == 1);
     if (!ok) return set_error(EFM_ERR_INVALID_ARGUMENT, "testing_set_kernel_path: bad value %d for knob %d", value, knob);
     g_knobs[knob].store(value, std::memory_order_relaxed);

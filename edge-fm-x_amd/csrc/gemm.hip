@@ -461,15 +461,28 @@ __device__ __forceinline__ void lgkm_wait() {
 
 // DMA of one stage's operand rows: per-lane byte offsets (row, swizzled chunk) of each
 // of the wave's loads from the operand base; the stage's base pointers and LDS slot are
-// uniform values computed once per stage.
-template <int LPW, int LA, int NW>
+// uniform values computed once per stage. EXACT: both operands' 1 KB blocks divide evenly
+// over the waves, so load i of every wave reads A for i < LA and lands i * NW blocks past
+// the wave's first. Otherwise (192-row tiles: 12 A + 16 B blocks over 8 waves) each load
+// carries a wave-uniform operand choice and LDS offset.
+template <int LPW, int LA, int NW, bool EXACT>
 struct WideDma {
     uint32_t voff[LPW];
+    uint32_t dst[EXACT ? 1 : LPW];
+    bool from_a[EXACT ? 1 : LPW];
     __device__ __forceinline__ void issue(int i, const unsigned char* sa, const unsigned char* sb,
                                           unsigned char* slot_wave) const {
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>((i < LA ? sa : sb) + voff[i]),
-                                         (__attribute__((address_space(3))) void*)(slot_wave + i * NW * 1024), 16, 0,
-                                         0);
+        const unsigned char* base;
+        unsigned char* d;
+        if constexpr (EXACT) {
+            base = i < LA ? sa : sb;
+            d = slot_wave + i * NW * 1024;
+        } else {
+            base = from_a[i] ? sa : sb;
+            d = slot_wave + dst[i];
+        }
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(base + voff[i]),
+                                         (__attribute__((address_space(3))) void*)d, 16, 0, 0);
     }
 };
 
@@ -508,9 +521,11 @@ __global__ __launch_bounds__(WGM * WGN * kWave, 1) void gemm_wide_kernel(const b
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr int STAGE = (BM + BN) * kWRow;
     constexpr int QA = BM / 16, QB = BN / 16;   // 1 KB wave loads per operand per stage
-    constexpr int LA = QA / NW, LPW = (QA + QB) / NW;
+    constexpr int Q = QA + QB;
+    constexpr bool kExact = QA % NW == 0 && QB % NW == 0;
+    constexpr int LA = QA / NW, LPW = (Q + NW - 1) / NW;
     constexpr int NR = TM + TN;                 // operand reads per key step
-    static_assert(QA % NW == 0 && QB % NW == 0 && S >= 2 && (S - 2) * LPW <= 63, "bad wide GEMM shape");
+    static_assert(QA >= NW && S >= 2 && (S - 2) * LPW <= 63, "bad wide GEMM shape");
     static_assert(LPW <= TM * TN && NR <= TM * TN && NR <= 15, "interleave slots");
     static_assert(EPI != GEPI_SWIGLU || TN % 2 == 0, "SwiGLU needs paired N tiles");
     static_assert(EPI != GEPI_PARTIAL, "no split-K in the wide kernel");
@@ -540,7 +555,7 @@ __global__ __launch_bounds__(WGM * WGN * kWave, 1) void gemm_wide_kernel(const b
     };
 
     // DMA sources (the host keeps both operands under 2 GB: 32-bit byte offsets)
-    WideDma<LPW, LA, NW> dma;
+    WideDma<LPW, LA, NW, kExact> dma;
     const unsigned char* pa = reinterpret_cast<const unsigned char*>(A);
     const unsigned char* pb = reinterpret_cast<const unsigned char*>(B);
     auto issue_stage = [&](int stage) {
@@ -554,8 +569,16 @@ __global__ __launch_bounds__(WGM * WGN * kWave, 1) void gemm_wide_kernel(const b
         const int rr = lane >> 2, cs = lane & 3;
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
-            const int q = wave + NW * i;
-            if (i < LA) {
+            // Block q of the stage; past the last block (Q % NW != 0), a repeat of the
+            // wave's first load (same source, same LDS bytes), so that every wave issues
+            // LPW loads per stage and the vmcnt waits below count alike in all waves.
+            int q = wave + NW * i;
+            if (q >= Q) q = wave;
+            if constexpr (!kExact) {
+                dma.from_a[i] = q < QA;
+                dma.dst[i] = (uint32_t)((q - wave) * 1024);
+            }
+            if (q < QA) {
                 const int row = q * 16 + rr;
                 const int grow = min(m0 + row, M - 1);
                 dma.voff[i] = (uint32_t)((grow * K + ((cs ^ wide_swz(row)) << 3)) * 2);
@@ -797,6 +820,15 @@ static int gemm_dispatch(int M, int N, int K, const bf16_t* A, const bf16_t* B, 
     const bool wide_ok = K % kPBK == 0 && (long)M * K * 2 < 0x7fffffffL && b_rows * K * 2 < 0x7fffffffL;
     if (wide_ok && tile_knob != 1) {
         const long r_wide = (tiles(256, 256) + 255) / 256, r_pipe = (tiles(128, 128) + 511) / 512;
+        // 192 x 256 tiles (six MFMA tiles per wave instead of eight) take 0.9 of a 256 x
+        // 256 round (measured, SwiGLU: 512 x 1536 -> 2 x 8960 48.3 -> 43.3 us in one round
+        // of 210 tiles against 140; 512 x 3584 -> 2 x 18944 198.2 -> 177.3 in two rounds,
+        // against 196.5 for the 128 x 128 kernel); the fewest weighted rounds wins.
+        const long r_192 = (tiles(192, 256) + 255) / 256;
+        if (tile_knob == 3 || (tile_knob == 0 && 171 * r_192 < std::min(190 * r_wide, 115 * r_pipe))) {
+            gemm_wide_launch<192, 256, 2, 4, 4, EPI>(M, N, K, A, B, bias, C, ldc, stream);
+            return check_launch("gemm_bf16");
+        }
         if (tile_knob == 2 || 190 * r_wide < 115 * r_pipe) {
             gemm_wide_launch<256, 256, 2, 4, 4, EPI>(M, N, K, A, B, bias, C, ldc, stream);
             return check_launch("gemm_bf16");

@@ -71,7 +71,8 @@ int efm_init(void);
  *                              kernel treats 2 as 4)
  *   EFM_KNOB_GEMM_TILE         prefill GEMM kernel (K % 64 == 0): 1 the two-workgroup-
  *                              per-CU 128 x 128 / 128 x 64 / 64 x 64 kernel, 2 the
- *                              one-workgroup-per-CU 256 x 256 kernel
+ *                              one-workgroup-per-CU 256 x 256 kernel, 3 the same kernel
+ *                              with 192 x 256 tiles
  *   EFM_KNOB_FRONT_WAIT_TIMEOUT 1: efm_decode_norm_qkv_attention launches whose attention
  *                              workgroups wait for a tag that no projected word carries,
  *                              with a 64-poll limit: every wait gives up, the launch

@@ -76,7 +76,9 @@ def test_testing_kernel_path_setter_validates():
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_PREFILL_REGISTER, 2) == C.EFM_ERR_INVALID_ARGUMENT
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_GEMM_TILE, 2) == C.EFM_OK
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_GEMM_TILE, 0) == C.EFM_OK
-    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_GEMM_TILE, 3) == C.EFM_ERR_INVALID_ARGUMENT
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_GEMM_TILE, 3) == C.EFM_OK
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_GEMM_TILE, 0) == C.EFM_OK
+    assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_GEMM_TILE, 4) == C.EFM_ERR_INVALID_ARGUMENT
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 1) == C.EFM_OK
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 0) == C.EFM_OK
     assert lib.efm_testing_set_kernel_path(C.EFM_KNOB_FRONT_WAIT_TIMEOUT, 2) == C.EFM_ERR_INVALID_ARGUMENT

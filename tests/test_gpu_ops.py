@@ -572,9 +572,10 @@ def test_gemm_tile_shapes_agree_bit_exact(gpu, kind):
     pytest.param(512, 1536, 8960, "swiglu", id="c2_gate_up"),
 ])
 def test_gemm_wide_kernel_matches_narrow_bit_exact(gpu, knob, m, k, n, kind):
-    """The 256 x 256 wide kernel (EFM_KNOB_GEMM_TILE 2) against the 128 x 128 family
-    (knob 1) on aligned and ragged shapes and every epilogue: bit-identical outputs (both
-    sum keys 16 at a time in increasing order), and a row sample against the oracle."""
+    """The 256 x 256 wide kernel (EFM_KNOB_GEMM_TILE 2) and its 192 x 256 tiles (knob 3:
+    12 A and 16 B blocks per stage over 8 waves) against the 128 x 128 family (knob 1) on
+    aligned and ragged shapes and every epilogue: bit-identical outputs (all sum keys 16
+    at a time in increasing order), and a row sample against the oracle."""
     torch.manual_seed(m + n)
     x = torch.randn(m, k, dtype=torch.bfloat16, device=gpu)
     nw = 2 * n if kind == "swiglu" else n
@@ -582,7 +583,7 @@ def test_gemm_wide_kernel_matches_narrow_bit_exact(gpu, knob, m, k, n, kind):
     b = (torch.randn(n, device=gpu) * 0.05).to(torch.bfloat16) if kind in ("bias", "f32") else None
     odt = torch.float32 if kind == "f32" else torch.bfloat16
     outs = []
-    for path in (1, 2):
+    for path in (1, 2, 3):
         knob(C.EFM_KNOB_GEMM_TILE, path)
         y = torch.full((m, n), float("nan"), dtype=odt, device=gpu)
         if kind == "swiglu":
@@ -592,8 +593,9 @@ def test_gemm_wide_kernel_matches_narrow_bit_exact(gpu, knob, m, k, n, kind):
             C.call("efm_linear", m, k, n, ptr(x), ptr(w), ptr(b), ptr(y), cd, stream())
         torch.cuda.synchronize()
         outs.append(y)
-    assert not torch.isnan(outs[1]).any(), "wide kernel left outputs unwritten"
-    assert torch.equal(outs[0], outs[1]), f"{kind}: wide and narrow kernels differ"
+    for path, y in zip((2, 3), outs[1:]):
+        assert not torch.isnan(y).any(), f"wide kernel (knob {path}) left outputs unwritten"
+        assert torch.equal(outs[0], y), f"{kind}: wide (knob {path}) and narrow kernels differ"
     rows = torch.tensor([0, m // 2, m - 1])
     xs = x[rows].cpu()
     if kind == "swiglu":
